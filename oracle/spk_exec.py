@@ -1,0 +1,285 @@
+"""Runs an SPK package on the CPU oracle (oracle/liboracle.so), node by node.
+
+TEST INFRASTRUCTURE ONLY: the checker the parity tests compare the MI355X
+runtime against.  It parses the package with its own minimal reader (not the
+product's loader or writer), keeps every tensor as a separate numpy array (so
+a wrong arena plan in the product shows up as a mismatch), and calls the C
+restatement of each reference kernel.  Dispatch order and per-op semantics
+follow the reference executor (runtime/core/executor.c:500-537) and kernels.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import struct
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_LIB = Path(__file__).resolve().parent / "liboracle.so"
+
+_HDR = struct.Struct("<IHHHHIIIIIIQQQII")
+_SEC = struct.Struct("<IIQQII")
+_TEN = struct.Struct("<IHHHH8IQQII")
+_NODE = struct.Struct("<IHHHH8I4IIIII")
+_ATTR = struct.Struct("<Iiii4i2i2i2i2i2fii8i3i")
+_QP = struct.Struct("<IHHIQ")
+
+OPS = {1: "Add", 2: "Conv", 3: "Flatten", 4: "Gemm", 5: "MaxPool", 6: "Relu", 7: "Softmax", 8: "Mul", 9: "Sub",
+       10: "Div", 11: "Mod", 12: "Sigmoid", 13: "Reshape", 15: "Concat", 17: "ReduceMean", 18: "ReduceMax",
+       19: "MatMul", 20: "Resize", 22: "Unsqueeze", 25: "Cast", 28: "AveragePool", 29: "GlobalAveragePool"}
+
+
+@dataclass
+class TensorInfo:
+    id: int
+    dtype: int
+    role: int
+    shape: tuple
+    size: int
+    offset: int
+
+
+@dataclass
+class NodeInfo:
+    id: int
+    op: int
+    inputs: list
+    outputs: list
+    attr: dict
+
+
+def _lib():
+    if not ORACLE_LIB.exists():
+        raise FileNotFoundError(f"{ORACLE_LIB} not built (make -C oracle oracle)")
+    lib = ctypes.CDLL(str(ORACLE_LIB))
+    return lib
+
+
+class Package:
+    """Minimal independent reader of an SPK v0.3 blob."""
+
+    def __init__(self, blob: bytes) -> None:
+        h = _HDR.unpack_from(blob, 0)
+        assert h[0] == 0x32564B50, "bad magic"
+        self.num_tensors, self.num_nodes = h[7], h[8]
+        secs = {}
+        for i in range(h[5]):
+            kind, _, off, size, _, _ = _SEC.unpack_from(blob, h[4] + i * _SEC.size)
+            secs[kind] = (off, size)
+        toff = secs[3][0]
+        self.tensors = []
+        for i in range(self.num_tensors):
+            f = _TEN.unpack_from(blob, toff + i * _TEN.size)
+            self.tensors.append(TensorInfo(f[0], f[1], f[2], tuple(f[5:5 + f[3]]), f[13], f[14]))
+        noff = secs[4][0]
+        aoff = secs[5][0]
+        self.nodes = []
+        for i in range(self.num_nodes):
+            f = _NODE.unpack_from(blob, noff + i * _NODE.size)
+            nin, nout = f[3], f[4]
+            a = _ATTR.unpack_from(blob, aoff + f[17])
+            attr = dict(op=a[0], axis=a[1], group=a[2], act=a[3], pads=a[4:8], strides=a[8:10], kernel=a[10:12],
+                        dil=a[12:14], trans_a=a[14], trans_b=a[15], alpha=a[16], beta=a[17], extra_count=a[18],
+                        keepdims=a[19], extra=a[20:28])
+            self.nodes.append(NodeInfo(f[0], f[1], list(f[5:5 + nin]), list(f[13:13 + nout]), attr))
+        woff = secs[6][0]
+        self.weights = {}
+        for t in self.tensors:
+            if t.role == 3:
+                raw = blob[woff + t.offset: woff + t.offset + t.size]
+                dt = np.int8 if t.dtype == 2 else np.float32
+                self.weights[t.id] = np.frombuffer(raw, dtype=dt).reshape(t.shape).copy()
+        self.quant = {}
+        if 9 in secs:
+            qoff, qsize = secs[9]
+            first = _QP.unpack_from(blob, qoff)
+            count = first[4] // _QP.size
+            for i in range(count):
+                tid, scheme, axis, nch, doff = _QP.unpack_from(blob, qoff + i * _QP.size)
+                self.quant[tid] = np.frombuffer(blob[qoff + doff: qoff + doff + 4 * nch], dtype="<f4").copy()
+        meta = json.loads(blob[secs[1][0]: secs[1][0] + secs[1][1]].decode())
+        self.inputs = [t.id for t in self.tensors if t.role == 1]
+        self.outputs = list(meta.get("outputs", [t.id for t in self.tensors if t.role == 2]))
+
+
+def _f(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+class OracleExecutor:
+    def __init__(self, blob: bytes) -> None:
+        self.pkg = Package(blob)
+        self.lib = _lib()
+        self.acc: dict[int, np.ndarray] = {}  # int8 conv node id -> int32 accumulators of the last run
+
+    def run(self, *inputs: np.ndarray, keep: bool = False) -> list[np.ndarray] | dict[int, np.ndarray]:
+        pkg = self.pkg
+        vals: dict[int, np.ndarray] = dict(pkg.weights)
+        for tid, x in zip(pkg.inputs, inputs):
+            vals[tid] = np.ascontiguousarray(x, dtype=np.float32).reshape(pkg.tensors[tid].shape)
+        for n in pkg.nodes:
+            op = OPS.get(n.op)
+            if op is None:
+                raise NotImplementedError(f"oracle has no op code {n.op}")
+            getattr(self, "_" + op.lower())(n, vals)
+        if keep:
+            return vals
+        return [vals[t] for t in pkg.outputs]
+
+    # ------------------------------------------------------------------ ops
+    def _shape(self, tid):
+        return self.pkg.tensors[tid].shape
+
+    def _out(self, n, vals, dtype=np.float32):
+        y = np.zeros(self._shape(n.outputs[0]), dtype=dtype)
+        vals[n.outputs[0]] = y
+        return y
+
+    def _conv(self, n, vals):
+        x = vals[n.inputs[0]]
+        w = vals[n.inputs[1]]
+        b = vals[n.inputs[2]] if len(n.inputs) > 2 else None
+        r = np.ascontiguousarray(vals[n.inputs[3]]) if len(n.inputs) > 3 else None
+        y = self._out(n, vals)
+        N, C, H, W = x.shape
+        M, _, KH, KW = w.shape
+        OH, OW = y.shape[2], y.shape[3]
+        a = n.attr
+        geo = (N, C, H, W, M, KH, KW, OH, OW, a["strides"][0], a["strides"][1], a["pads"][0], a["pads"][1],
+               a["dil"][0], a["dil"][1])
+        if w.dtype == np.int8:
+            ws = self.pkg.quant[n.inputs[1]]
+            xs = self.pkg.quant[n.inputs[0]][0]
+            acc = np.zeros(y.shape, dtype=np.int32)
+            rc = self.lib.oracle_conv2d_int8(_f(x), _f(w), _f(ws), ctypes.c_float(xs), _f(b), _f(r), _f(y), _f(acc),
+                                             *geo, a["act"])
+            self.acc[n.id] = acc
+        else:
+            rc = self.lib.oracle_conv2d_f32(_f(x), _f(w), _f(b), _f(r), _f(y), *geo, a["group"], a["act"])
+        assert rc == 0, rc
+
+    def _gemm(self, n, vals):
+        a_, b_ = vals[n.inputs[0]], vals[n.inputs[1]]
+        c = vals[n.inputs[2]] if len(n.inputs) > 2 else None
+        y = self._out(n, vals)
+        at = n.attr["trans_a"]
+        rows = a_.shape[1] if at else a_.shape[0]
+        k = a_.shape[0] if at else a_.shape[1]
+        nout = b_.shape[0] if n.attr["trans_b"] else b_.shape[1]
+        self.lib.oracle_gemm_f32(_f(a_), _f(b_), _f(c), _f(y), rows, k, nout, at, n.attr["trans_b"],
+                                 ctypes.c_float(n.attr["alpha"]))
+
+    def _matmul(self, n, vals):
+        a_, b_ = vals[n.inputs[0]], vals[n.inputs[1]]
+        y = self._out(n, vals)
+        M, N = y.shape[-2], y.shape[-1]
+        K = a_.shape[-1]
+        lead = y.shape[:-2]
+        ai = np.broadcast_to(np.arange(int(np.prod(a_.shape[:-2]))).reshape(a_.shape[:-2] or (1,)), lead or (1,))
+        bi = np.broadcast_to(np.arange(int(np.prod(b_.shape[:-2]))).reshape(b_.shape[:-2] or (1,)), lead or (1,))
+        aoff = np.ascontiguousarray(ai.reshape(-1) * M * K, dtype=np.int64)
+        boff = np.ascontiguousarray(bi.reshape(-1) * K * N, dtype=np.int64)
+        self.lib.oracle_matmul_f32(_f(a_), _f(b_), _f(y), len(aoff), _f(aoff), _f(boff), M, K, N)
+
+    def _pool_args(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        a = n.attr
+        return x, y, (*x.shape, y.shape[2], y.shape[3], a["kernel"][0], a["kernel"][1], a["strides"][0],
+                      a["strides"][1], a["pads"][0], a["pads"][1])
+
+    def _maxpool(self, n, vals):
+        x, y, g = self._pool_args(n, vals)
+        self.lib.oracle_maxpool_f32(_f(x), _f(y), *g)
+
+    def _averagepool(self, n, vals):
+        x, y, g = self._pool_args(n, vals)
+        self.lib.oracle_avgpool_f32(_f(x), _f(y), *g)
+
+    def _globalaveragepool(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        self.lib.oracle_global_avgpool_f32(_f(x), _f(y), x.shape[0], x.shape[1], x.shape[2] * x.shape[3])
+
+    def _binary(self, n, vals, code):
+        a_, b_ = vals[n.inputs[0]], vals[n.inputs[1]]
+        y = self._out(n, vals)
+        sh = lambda t: (ctypes.c_uint32 * 8)(*t.shape)  # noqa: E731
+        rc = self.lib.oracle_binary_f32(code, _f(a_), sh(a_), a_.ndim, _f(b_), sh(b_), b_.ndim, _f(y), sh(y), y.ndim,
+                                        n.attr["act"] if code == 1 else 0)
+        assert rc == 0
+
+    def _add(self, n, vals):
+        self._binary(n, vals, 1)
+
+    def _mul(self, n, vals):
+        self._binary(n, vals, 8)
+
+    def _sub(self, n, vals):
+        self._binary(n, vals, 9)
+
+    def _div(self, n, vals):
+        self._binary(n, vals, 10)
+
+    def _mod(self, n, vals):
+        self._binary(n, vals, 11)
+
+    def _relu(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        self.lib.oracle_relu_f32(_f(x), _f(y), ctypes.c_size_t(x.size))
+
+    def _sigmoid(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        self.lib.oracle_sigmoid_f32(_f(x), _f(y), ctypes.c_size_t(x.size))
+
+    def _softmax(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        ax = n.attr["axis"] % x.ndim
+        outer = int(np.prod(x.shape[:ax]))
+        inner = int(np.prod(x.shape[ax + 1:]))
+        self.lib.oracle_softmax_f32(_f(x), _f(y), ctypes.c_size_t(outer), ctypes.c_size_t(x.shape[ax]),
+                                    ctypes.c_size_t(inner))
+
+    def _reduce(self, n, vals, is_max):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        a = n.attr
+        if a["extra_count"] > 0:
+            axes = [v % x.ndim for v in a["extra"][:a["extra_count"]]]
+        else:
+            axes = list(range(x.ndim))
+        mask = 0
+        for ax in axes:
+            mask |= 1 << ax
+        shp = (ctypes.c_uint32 * 8)(*x.shape)
+        self.lib.oracle_reduce_f32(_f(x), shp, x.ndim, ctypes.c_uint32(mask), int(is_max), _f(y))
+
+    def _reducemean(self, n, vals):
+        self._reduce(n, vals, False)
+
+    def _reducemax(self, n, vals):
+        self._reduce(n, vals, True)
+
+    def _resize(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        self.lib.oracle_resize_nearest_f32(_f(x), _f(y), *x.shape, y.shape[2], y.shape[3])
+
+    def _copy(self, n, vals):
+        vals[n.outputs[0]] = vals[n.inputs[0]].reshape(self._shape(n.outputs[0])).copy()
+
+    _flatten = _reshape = _unsqueeze = _cast = _copy
+
+    def _concat(self, n, vals):
+        ax = n.attr["axis"] % len(self._shape(n.outputs[0]))
+        vals[n.outputs[0]] = np.concatenate([vals[t] for t in n.inputs], axis=ax)
+
+
+def _setup_signatures() -> None:
+    pass

@@ -1,0 +1,52 @@
+// Convolution geometry and the per-node plan kept in node_cache.
+#pragma once
+
+#include <cstdint>
+#include <string>
+
+#include "common.hpp"
+
+namespace spk::kern {
+
+// Shapes and attributes of one Conv node, read the way the reference kernel
+// reads them (runtime/kernels/reference/conv/conv.c:5-30): x = inputs[0]
+// NCHW, w = inputs[1] OIHW, bias = inputs[2] if present, residual =
+// inputs[3] if present (FuseConvAdd), y = outputs[0] NCHW whose H/W come
+// from the tensor record.
+struct ConvGeom {
+    int N, C, H, W;
+    int M, KH, KW, OH, OW;
+    int sh, sw, ph, pw, dh, dw;
+    int group, act;
+    bool has_bias, has_res;
+    int x_dtype, w_dtype;
+    int64_t x_elems, y_elems;
+};
+
+int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeom *g);
+
+enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2 };
+
+struct ConvPlan {
+    ConvPath path;
+    ConvGeom g;
+    int cfg;             // index of the tile configuration
+    int BM, BN, BK;      // tile shape
+    int m_tiles, n_tiles, k_tiles;
+    int splitk, kt_per_split;
+    int K, Kpad;
+    void *wpack;         // device: packed weight panels (fp32 or int8)
+    void *ktab;          // device: per-k gather table
+    float *scales;       // device, int8 path: w_scale[m] * x_scale
+    float x_scale;       // int8 path: activation scale
+    int quant_split;     // int8 path: first element index of the per-image tail (round half away)
+    size_t workspace;    // bytes of runtime workspace needed per run
+};
+
+void conv_plan_free(void *p);
+
+// int8 path entry points (conv_i8.hip)
+int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan);
+int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *plan, int32_t *raw_acc_out);
+
+}  // namespace spk::kern

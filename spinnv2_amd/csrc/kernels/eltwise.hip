@@ -1,0 +1,707 @@
+// Memory-bound node kernels: binary/unary elementwise, copies, Concat, pools,
+// Softmax, Reduce, Resize, plus the reliability helpers.  All are coalesced
+// wavefront kernels: consecutive lanes touch consecutive addresses of the
+// NCHW output, wide (float4) accesses where shapes allow, one wave per row for
+// row reductions.
+#include <cmath>
+#include <cstring>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace spk::kern {
+
+namespace {
+
+constexpr int kMaxRank = 8;
+
+struct BcastDesc {
+    int rank;
+    int64_t ydim[kMaxRank];
+    int64_t astride[kMaxRank];
+    int64_t bstride[kMaxRank];
+};
+
+// Right-aligned numpy broadcasting of a and b onto y: size-1 dims get
+// stride 0 (reference kernel_common.c:37-48).
+void make_bcast(const Spkv2TensorRecord *a, const Spkv2TensorRecord *b, const Spkv2TensorRecord *y, BcastDesc *d) {
+    d->rank = y->rank;
+    for (int i = 0; i < kMaxRank; i++) d->ydim[i] = 1, d->astride[i] = 0, d->bstride[i] = 0;
+    for (int i = 0; i < y->rank; i++) d->ydim[i] = y->shape[i];
+    auto fill = [&](const Spkv2TensorRecord *t, int64_t *stride) {
+        int64_t s = 1;
+        const int delta = y->rank - t->rank;
+        for (int i = t->rank - 1; i >= 0; i--) {
+            stride[i + delta] = t->shape[i] == 1 ? 0 : s;
+            s *= t->shape[i];
+        }
+    };
+    fill(a, d->astride);
+    fill(b, d->bstride);
+}
+
+enum BinOp { BIN_ADD = 0, BIN_MUL, BIN_SUB, BIN_DIV, BIN_MOD };
+
+template <int OP>
+__device__ __forceinline__ float bin(float a, float b) {
+    if constexpr (OP == BIN_ADD) return a + b;
+    if constexpr (OP == BIN_MUL) return a * b;
+    if constexpr (OP == BIN_SUB) return a - b;
+    if constexpr (OP == BIN_DIV) return a / b;
+    // Mod as the reference computes it: C integer remainder of truncated
+    // operands (reference math/binary.c:27); a zero divisor yields 0 here
+    const int ib = static_cast<int>(b);
+    return ib == 0 ? 0.0f : static_cast<float>(static_cast<int>(a) % ib);
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256) binary_same4(const float4 *__restrict__ a, const float4 *__restrict__ b,
+                                                    float4 *__restrict__ y, size_t n4, int act) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += static_cast<size_t>(gridDim.x) * 256) {
+        const float4 u = a[i], v = b[i];
+        float4 r;
+        r.x = apply_act(bin<OP>(u.x, v.x), act);
+        r.y = apply_act(bin<OP>(u.y, v.y), act);
+        r.z = apply_act(bin<OP>(u.z, v.z), act);
+        r.w = apply_act(bin<OP>(u.w, v.w), act);
+        y[i] = r;
+    }
+}
+
+template <int OP>
+__global__ void __launch_bounds__(256) binary_bcast(const float *__restrict__ a, const float *__restrict__ b,
+                                                    float *__restrict__ y, size_t n, BcastDesc d, int act) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        size_t t = i;
+        int64_t ao = 0, bo = 0;
+        for (int k = d.rank - 1; k >= 0; k--) {
+            const int64_t c = static_cast<int64_t>(t % d.ydim[k]);
+            t /= d.ydim[k];
+            ao += c * d.astride[k];
+            bo += c * d.bstride[k];
+        }
+        y[i] = apply_act(bin<OP>(a[ao], b[bo]), act);
+    }
+}
+
+template <int OP>
+int launch_binary(hipStream_t s, const Spkv2TensorRecord *ar, const Spkv2TensorRecord *br, const Spkv2TensorRecord *yr,
+                  const float *a, const float *b, float *y, int act) {
+    const size_t n = elem_count(yr);
+    if (n == 0) return 0;
+    const bool same = elem_count(ar) == n && elem_count(br) == n && ar->rank == yr->rank && br->rank == yr->rank;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+                           reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+    if (same && aligned && n % 4 == 0) {
+        hipLaunchKernelGGL((binary_same4<OP>), dim3(grid_for(n / 4, 256)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
+                           reinterpret_cast<float4 *>(y), n / 4, act);
+    } else {
+        BcastDesc d;
+        make_bcast(ar, br, yr, &d);
+        hipLaunchKernelGGL((binary_bcast<OP>), dim3(grid_for(n, 256)), dim3(256), 0, s, a, b, y, n, d, act);
+    }
+    return launch_status("binary");
+}
+
+enum UnOp { UN_RELU = 0, UN_SIGMOID, UN_CLIP, UN_LEAKY };
+
+template <int OP>
+__global__ void __launch_bounds__(256) unary_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n,
+                                                    const float *__restrict__ lo, const float *__restrict__ hi,
+                                                    float alpha) {
+    const float minv = (OP == UN_CLIP && lo) ? *lo : -INFINITY;
+    const float maxv = (OP == UN_CLIP && hi) ? *hi : INFINITY;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        float v = x[i];
+        if constexpr (OP == UN_RELU) v = v > 0.0f ? v : 0.0f;                  // relu.c:11
+        if constexpr (OP == UN_SIGMOID) v = 1.0f / (1.0f + expf(-v));          // sigmoid.c:11
+        if constexpr (OP == UN_CLIP) {                                         // clip_leakyrelu.c:23-27
+            if (v < minv) v = minv;
+            if (v > maxv) v = maxv;
+        }
+        if constexpr (OP == UN_LEAKY) v = v >= 0.0f ? v : v * alpha;           // clip_leakyrelu.c:47
+        y[i] = v;
+    }
+}
+
+__global__ void __launch_bounds__(256) copy_kernel(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                   size_t n) {
+    const size_t n16 = n / 16;
+    const int4 *s4 = reinterpret_cast<const int4 *>(src);
+    int4 *d4 = reinterpret_cast<int4 *>(dst);
+    const size_t stride = static_cast<size_t>(gridDim.x) * 256;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n16; i += stride) d4[i] = s4[i];
+    for (size_t i = n16 * 16 + static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+__global__ void __launch_bounds__(256) copy_kernel_bytes(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst,
+                                                         size_t n) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        dst[i] = src[i];
+}
+
+int launch_copy(hipStream_t s, const void *src, void *dst, size_t bytes) {
+    if (bytes == 0 || src == dst) return 0;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    if (aligned)
+        hipLaunchKernelGGL(copy_kernel, dim3(grid_for(bytes / 16 + 1, 256)), dim3(256), 0, s,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), bytes);
+    else
+        hipLaunchKernelGGL(copy_kernel_bytes, dim3(grid_for(bytes, 256)), dim3(256), 0, s,
+                           static_cast<const uint8_t *>(src), static_cast<uint8_t *>(dst), bytes);
+    return launch_status("copy");
+}
+
+// Strided block copy for Concat: `outer` blocks of `block` floats from src
+// (contiguous) into dst with row pitch `dst_pitch`.
+__global__ void __launch_bounds__(256) concat_copy(const float *__restrict__ src, float *__restrict__ dst, size_t outer,
+                                                   size_t block, size_t dst_pitch) {
+    const size_t total = outer * block;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t o = i / block, r = i - o * block;
+        dst[o * dst_pitch + r] = src[i];
+    }
+}
+
+struct PoolArgs {
+    const float *__restrict__ x;
+    float *__restrict__ y;
+    int N, C, H, W, OH, OW, kh, kw, sh, sw, ph, pw;
+};
+
+// reference pool/maxpool.c:20-40: -inf start, out-of-bounds taps skipped
+__global__ void __launch_bounds__(256) maxpool_kernel(PoolArgs a) {
+    const size_t total = static_cast<size_t>(a.N) * a.C * a.OH * a.OW;
+    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+         idx += static_cast<size_t>(gridDim.x) * 256) {
+        const int ow = static_cast<int>(idx % a.OW);
+        const size_t t = idx / a.OW;
+        const int oh = static_cast<int>(t % a.OH);
+        const size_t plane = t / a.OH;
+        const float *xp = a.x + plane * a.H * a.W;
+        float m = -INFINITY;
+        for (int i = 0; i < a.kh; i++) {
+            const int ih = oh * a.sh + i - a.ph;
+            if (ih < 0 || ih >= a.H) continue;
+            for (int j = 0; j < a.kw; j++) {
+                const int iw = ow * a.sw + j - a.pw;
+                if (iw < 0 || iw >= a.W) continue;
+                const float v = xp[ih * a.W + iw];
+                if (v > m) m = v;
+            }
+        }
+        a.y[idx] = m;
+    }
+}
+
+// reference pool/avgpool.c:21-45: mean over the in-bounds taps
+__global__ void __launch_bounds__(256) avgpool_kernel(PoolArgs a) {
+    const size_t total = static_cast<size_t>(a.N) * a.C * a.OH * a.OW;
+    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+         idx += static_cast<size_t>(gridDim.x) * 256) {
+        const int ow = static_cast<int>(idx % a.OW);
+        const size_t t = idx / a.OW;
+        const int oh = static_cast<int>(t % a.OH);
+        const size_t plane = t / a.OH;
+        const float *xp = a.x + plane * a.H * a.W;
+        float sum = 0.0f;
+        int count = 0;
+        for (int i = 0; i < a.kh; i++) {
+            const int ih = oh * a.sh + i - a.ph;
+            if (ih < 0 || ih >= a.H) continue;
+            for (int j = 0; j < a.kw; j++) {
+                const int iw = ow * a.sw + j - a.pw;
+                if (iw < 0 || iw >= a.W) continue;
+                sum += xp[ih * a.W + iw];
+                count++;
+            }
+        }
+        a.y[idx] = count > 0 ? sum / static_cast<float>(count) : 0.0f;
+    }
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+    for (int off = 32; off > 0; off >>= 1) {
+        const float o = __shfl_xor(v, off, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// One wave per contiguous row of `len` elements.  MODE 0: mean of x/denom
+// terms (ReduceMean, reference reduce.c:37-40); 1: max (ReduceMax);
+// 2: sum * inv (GlobalAveragePool, avgpool.c:62-67).
+template <int MODE>
+__global__ void __launch_bounds__(256) row_reduce(const float *__restrict__ x, float *__restrict__ y, size_t rows,
+                                                  int len, float denom) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = static_cast<size_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * len;
+    float acc = MODE == 1 ? -INFINITY : 0.0f;
+    for (int i = lane; i < len; i += 64) {
+        const float v = xr[i];
+        if (MODE == 0) acc += v / denom;
+        else if (MODE == 1) acc = v > acc ? v : acc;
+        else acc += v;
+    }
+    acc = MODE == 1 ? wave_max(acc) : wave_sum(acc);
+    if (lane == 0) y[row] = MODE == 2 ? acc * (1.0f / denom) : acc;
+}
+
+// Generic reduction: thread per output element, walking the reduced
+// sub-space.  rdim/rstride describe the reduced axes, odim/ostride the kept
+// axes (in x strides), in row-major order of the output.
+struct ReduceDesc {
+    int nr, no;
+    int64_t rdim[kMaxRank], rstride[kMaxRank];
+    int64_t odim[kMaxRank], ostride[kMaxRank];
+    int64_t rcount;
+};
+
+template <int MODE>
+__global__ void __launch_bounds__(256) generic_reduce(const float *__restrict__ x, float *__restrict__ y, size_t nout,
+                                                      ReduceDesc d, float denom) {
+    for (size_t o = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; o < nout; o += static_cast<size_t>(gridDim.x) * 256) {
+        size_t t = o;
+        int64_t base = 0;
+        for (int k = d.no - 1; k >= 0; k--) {
+            base += static_cast<int64_t>(t % d.odim[k]) * d.ostride[k];
+            t /= d.odim[k];
+        }
+        float acc = MODE == 1 ? -INFINITY : 0.0f;
+        for (int64_t r = 0; r < d.rcount; r++) {
+            int64_t rr = r, off = 0;
+            for (int k = d.nr - 1; k >= 0; k--) {
+                off += (rr % d.rdim[k]) * d.rstride[k];
+                rr /= d.rdim[k];
+            }
+            const float v = x[base + off];
+            if (MODE == 0) acc += v / denom;
+            else acc = v > acc ? v : acc;
+        }
+        y[o] = acc;
+    }
+}
+
+// Softmax over contiguous rows (inner == 1): one wave per row.
+__global__ void __launch_bounds__(256) softmax_rows(const float *__restrict__ x, float *__restrict__ y, size_t rows,
+                                                    int dim) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = static_cast<size_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * dim;
+    float *yr = y + row * dim;
+    float m = -INFINITY;
+    for (int i = lane; i < dim; i += 64) m = fmaxf(m, xr[i]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int i = lane; i < dim; i += 64) {
+        const float e = expf(xr[i] - m);
+        yr[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    for (int i = lane; i < dim; i += 64) yr[i] = yr[i] / s;
+}
+
+// Softmax along a strided axis: thread per (outer, inner) column, lanes
+// adjacent in `inner` so every pass over d is coalesced.
+__global__ void __launch_bounds__(256) softmax_strided(const float *__restrict__ x, float *__restrict__ y, size_t outer,
+                                                       int dim, size_t inner) {
+    const size_t cols = outer * inner;
+    for (size_t c = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; c < cols; c += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t o = c / inner, in = c - o * inner;
+        const float *xc = x + o * dim * inner + in;
+        float *yc = y + o * dim * inner + in;
+        float m = -INFINITY;
+        for (int d = 0; d < dim; d++) m = fmaxf(m, xc[static_cast<size_t>(d) * inner]);
+        float s = 0.0f;
+        for (int d = 0; d < dim; d++) {
+            const float e = expf(xc[static_cast<size_t>(d) * inner] - m);
+            yc[static_cast<size_t>(d) * inner] = e;
+            s += e;
+        }
+        for (int d = 0; d < dim; d++) yc[static_cast<size_t>(d) * inner] = yc[static_cast<size_t>(d) * inner] / s;
+    }
+}
+
+// Nearest resize with the reference index rule (reference shape/resize.c:15-26).
+__global__ void __launch_bounds__(256) resize_nearest(const float *__restrict__ x, float *__restrict__ y, int N, int C,
+                                                      int H, int W, int OH, int OW, float scale_h, float scale_w) {
+    const size_t total = static_cast<size_t>(N) * C * OH * OW;
+    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+         idx += static_cast<size_t>(gridDim.x) * 256) {
+        const int ow = static_cast<int>(idx % OW);
+        const size_t t = idx / OW;
+        const int oh = static_cast<int>(t % OH);
+        const size_t plane = t / OH;
+        int ih = static_cast<int>(floorf(static_cast<float>(oh) / scale_h));
+        if (ih >= H) ih = H - 1;
+        int iw = static_cast<int>(floorf(static_cast<float>(ow) / scale_w));
+        if (iw >= W) iw = W - 1;
+        y[idx] = x[(plane * H + ih) * W + iw];
+    }
+}
+
+// ------------------------------------------------ reliability helpers
+
+__global__ void flip_bit_kernel(uint32_t *p, uint32_t bit) { *p ^= (1u << bit); }
+
+__global__ void __launch_bounds__(256) minmax_kernel(const float *__restrict__ x, size_t n, float *__restrict__ out) {
+    __shared__ float smin[4], smax[4], snan[4];
+    float lo = INFINITY, hi = -INFINITY, bad = 0.0f;
+    for (size_t i = threadIdx.x; i < n; i += 256) {
+        const float v = x[i];
+        if (!isfinite(v)) bad += 1.0f;
+        else {
+            lo = fminf(lo, v);
+            hi = fmaxf(hi, v);
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        lo = fminf(lo, __shfl_xor(lo, off, 64));
+        hi = fmaxf(hi, __shfl_xor(hi, off, 64));
+        bad += __shfl_xor(bad, off, 64);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        smin[w] = lo;
+        smax[w] = hi;
+        snan[w] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < 4; i++) {
+            lo = fminf(lo, smin[i]);
+            hi = fmaxf(hi, smax[i]);
+            bad += snan[i];
+        }
+        lo = fminf(lo, smin[0]);
+        hi = fmaxf(hi, smax[0]);
+        out[0] = lo;
+        out[1] = hi;
+        out[2] = snan[0] + snan[1] + snan[2] + snan[3];
+        out[3] = 0.0f;
+    }
+}
+
+__global__ void __launch_bounds__(256) compare_kernel(const uint8_t *__restrict__ a, const uint8_t *__restrict__ b,
+                                                      size_t n, uint32_t *flag) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        if (a[i] != b[i]) *flag = 1u;
+}
+
+__global__ void fill_u32_kernel(uint32_t *p, size_t n, uint32_t v) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256)
+        p[i] = v;
+}
+
+int axis_norm(int axis, int rank) { return axis < 0 ? axis + rank : axis; }
+
+}  // namespace
+
+// ================================================================ node kernels
+
+int binary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    if (node->input_count < 2 || node->output_count < 1) return -11;
+    int act = 0;
+    if (node->op_type == SPKV2_OP_ADD) {
+        Spkv2AttrRecord attr;
+        if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+        act = attr.fused_activation;
+    }
+    const Spkv2TensorRecord *ar = rec(ctx, node->inputs[0]), *br = rec(ctx, node->inputs[1]), *yr = rec(ctx, node->outputs[0]);
+    const float *a = dptr<const float>(ctx, node->inputs[0]), *b = dptr<const float>(ctx, node->inputs[1]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    hipStream_t s = ctx->stream;
+    set_kernel_name(ctx, node, "binary");
+    switch (node->op_type) {
+    case SPKV2_OP_ADD: return launch_binary<BIN_ADD>(s, ar, br, yr, a, b, y, act);
+    case SPKV2_OP_MUL: return launch_binary<BIN_MUL>(s, ar, br, yr, a, b, y, 0);
+    case SPKV2_OP_SUB: return launch_binary<BIN_SUB>(s, ar, br, yr, a, b, y, 0);
+    case SPKV2_OP_DIV: return launch_binary<BIN_DIV>(s, ar, br, yr, a, b, y, 0);
+    case SPKV2_OP_MOD: return launch_binary<BIN_MOD>(s, ar, br, yr, a, b, y, 0);
+    }
+    return -99;
+}
+
+int unary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    const size_t n = elem_count(xr);
+    if (n == 0) return 0;
+    const dim3 grid(grid_for(n, 256));
+    hipStream_t s = ctx->stream;
+    set_kernel_name(ctx, node, "unary");
+    switch (node->op_type) {
+    case SPKV2_OP_RELU: hipLaunchKernelGGL(unary_kernel<UN_RELU>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, 0.0f); break;
+    case SPKV2_OP_SIGMOID:
+        hipLaunchKernelGGL(unary_kernel<UN_SIGMOID>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, 0.0f);
+        break;
+    case SPKV2_OP_CLIP: {
+        const float *lo = node->input_count >= 2 ? dptr<const float>(ctx, node->inputs[1]) : nullptr;
+        const float *hi = node->input_count >= 3 ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
+        hipLaunchKernelGGL(unary_kernel<UN_CLIP>, grid, dim3(256), 0, s, x, y, n, lo, hi, 0.0f);
+        break;
+    }
+    case SPKV2_OP_LEAKYRELU: {
+        Spkv2AttrRecord attr;
+        if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+        hipLaunchKernelGGL(unary_kernel<UN_LEAKY>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, attr.alpha);
+        break;
+    }
+    default: return -99;
+    }
+    return launch_status("unary");
+}
+
+// Flatten / Reshape / Cast / Unsqueeze: a byte copy unless the planner
+// aliased output and input (reference shape/copy.c, shape/flatten.c).
+int copy_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    const size_t bytes = node->op_type == SPKV2_OP_FLATTEN ? rec(ctx, node->inputs[0])->size_bytes
+                                                           : rec(ctx, node->outputs[0])->size_bytes;
+    set_kernel_name(ctx, node, "copy");
+    return launch_copy(ctx->stream, ctx->tensors[node->inputs[0]].data, ctx->tensors[node->outputs[0]].data, bytes);
+}
+
+// reference tensor/concat.c; inputs the planner placed inside the output
+// (memory_plan.py Concat aliases) are already in place and are skipped.
+int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *yr = rec(ctx, node->outputs[0]);
+    const int axis = axis_norm(attr.axis, yr->rank);
+    if (axis < 0 || axis >= yr->rank) return -11;
+    size_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= yr->shape[i];
+    for (int i = axis + 1; i < yr->rank; i++) inner *= yr->shape[i];
+    const size_t y_axis = yr->shape[axis];
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    size_t axis_off = 0;
+    set_kernel_name(ctx, node, "concat");
+    for (uint16_t i = 0; i < node->input_count; i++) {
+        const Spkv2TensorRecord *xr = rec(ctx, node->inputs[i]);
+        const float *x = dptr<const float>(ctx, node->inputs[i]);
+        const size_t block = static_cast<size_t>(xr->shape[axis]) * inner;
+        float *dst = y + axis_off * inner;
+        if (!(outer == 1 && dst == x) && outer * block > 0) {
+            hipLaunchKernelGGL(concat_copy, dim3(grid_for(outer * block, 256)), dim3(256), 0, ctx->stream, x, dst,
+                               outer, block, y_axis * inner);
+            if (int rc = launch_status("concat")) return rc;
+        }
+        axis_off += xr->shape[axis];
+    }
+    return 0;
+}
+
+static int pool_args(Spkv2Context *ctx, const Spkv2NodeRecord *node, PoolArgs *p) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]), *yr = rec(ctx, node->outputs[0]);
+    if (xr->rank != 4 || yr->rank != 4) return -11;
+    p->x = dptr<const float>(ctx, node->inputs[0]);
+    p->y = dptr<float>(ctx, node->outputs[0]);
+    p->N = xr->shape[0];
+    p->C = xr->shape[1];
+    p->H = xr->shape[2];
+    p->W = xr->shape[3];
+    p->OH = yr->shape[2];
+    p->OW = yr->shape[3];
+    p->kh = attr.kernel_shape[0];
+    p->kw = attr.kernel_shape[1];
+    p->sh = attr.strides[0];
+    p->sw = attr.strides[1];
+    p->ph = attr.pads[0];
+    p->pw = attr.pads[1];
+    return 0;
+}
+
+int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    PoolArgs p;
+    if (int rc = pool_args(ctx, node, &p)) return rc;
+    const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
+    if (total == 0) return 0;
+    set_kernel_name(ctx, node, "maxpool");
+    hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, p);
+    return launch_status("maxpool");
+}
+
+int avgpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    PoolArgs p;
+    if (int rc = pool_args(ctx, node, &p)) return rc;
+    const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
+    if (total == 0) return 0;
+    set_kernel_name(ctx, node, "avgpool");
+    hipLaunchKernelGGL(avgpool_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, p);
+    return launch_status("avgpool");
+}
+
+int global_avgpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    if (xr->rank != 4) return -11;
+    const size_t rows = static_cast<size_t>(xr->shape[0]) * xr->shape[1];
+    const int len = static_cast<int>(xr->shape[2] * xr->shape[3]);
+    if (rows == 0) return 0;
+    set_kernel_name(ctx, node, "global_avgpool");
+    hipLaunchKernelGGL(row_reduce<2>, dim3(blocks_for(rows, 4)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]), rows, len,
+                       static_cast<float>(len));
+    return launch_status("global_avgpool");
+}
+
+int softmax_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    const int axis = axis_norm(attr.axis, xr->rank);
+    if (axis < 0 || axis >= xr->rank) return -11;
+    size_t outer = 1, inner = 1;
+    const int dim = static_cast<int>(xr->shape[axis]);
+    for (int i = 0; i < axis; i++) outer *= xr->shape[i];
+    for (int i = axis + 1; i < xr->rank; i++) inner *= xr->shape[i];
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    if (outer * inner == 0 || dim == 0) return 0;
+    set_kernel_name(ctx, node, "softmax");
+    if (inner == 1)
+        hipLaunchKernelGGL(softmax_rows, dim3(blocks_for(outer, 4)), dim3(256), 0, ctx->stream, x, y, outer, dim);
+    else
+        hipLaunchKernelGGL(softmax_strided, dim3(grid_for(outer * inner, 256)), dim3(256), 0, ctx->stream, x, y, outer,
+                           dim, inner);
+    return launch_status("softmax");
+}
+
+// ReduceMean / ReduceMax (reference reduce/reduce.c).  Axes come from a
+// second (weight) input holding float axis values, else from the attr extra
+// list, else all axes (kernel_common.c:50-81).
+int reduce_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    const int rank = xr->rank;
+    bool reduced[kMaxRank] = {false};
+    int naxes = 0;
+    if (node->input_count > 1) {
+        const Spkv2TensorRecord *ar = rec(ctx, node->inputs[1]);
+        const float *av = reinterpret_cast<const float *>(host_weight_data(ctx, node->inputs[1]));
+        if (!av) return SPKV2_E_UNSUPPORTED;  // axes computed at run time
+        const size_t cnt = elem_count(ar);
+        if (cnt > 8) return -11;
+        for (size_t i = 0; i < cnt; i++) {
+            const int ax = axis_norm(static_cast<int>(av[i]), rank);
+            if (ax < 0 || ax >= rank) return -11;
+            if (!reduced[ax]) naxes++;
+            reduced[ax] = true;
+        }
+    } else if (attr.extra_count > 0) {
+        if (attr.extra_count > 8) return -11;
+        for (int i = 0; i < attr.extra_count; i++) {
+            const int ax = axis_norm(attr.extra[i], rank);
+            if (ax < 0 || ax >= rank) return -11;
+            if (!reduced[ax]) naxes++;
+            reduced[ax] = true;
+        }
+    } else {
+        for (int i = 0; i < rank; i++) reduced[i] = true;
+        naxes = rank;
+    }
+    float denom = 1.0f;
+    for (int i = 0; i < rank; i++)
+        if (reduced[i]) denom *= static_cast<float>(xr->shape[i]);
+    const bool is_max = node->op_type == SPKV2_OP_REDUCEMAX;
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    set_kernel_name(ctx, node, is_max ? "reduce_max" : "reduce_mean");
+
+    // trailing contiguous axes -> one wave per output row
+    int first = rank;
+    for (int i = rank - 1; i >= 0 && reduced[i]; i--) first = i;
+    int n_trailing = rank - first;
+    if (n_trailing == naxes && naxes > 0) {
+        size_t rows = 1, len = 1;
+        for (int i = 0; i < first; i++) rows *= xr->shape[i];
+        for (int i = first; i < rank; i++) len *= xr->shape[i];
+        if (rows * len == 0) return 0;
+        if (is_max)
+            hipLaunchKernelGGL(row_reduce<1>, dim3(blocks_for(rows, 4)), dim3(256), 0, ctx->stream, x, y, rows,
+                               static_cast<int>(len), denom);
+        else
+            hipLaunchKernelGGL(row_reduce<0>, dim3(blocks_for(rows, 4)), dim3(256), 0, ctx->stream, x, y, rows,
+                               static_cast<int>(len), denom);
+        return launch_status("reduce");
+    }
+    ReduceDesc d{};
+    int64_t stride[kMaxRank];
+    int64_t s = 1;
+    for (int i = rank - 1; i >= 0; i--) {
+        stride[i] = s;
+        s *= xr->shape[i];
+    }
+    d.rcount = 1;
+    size_t nout = 1;
+    for (int i = 0; i < rank; i++) {
+        if (reduced[i]) {
+            d.rdim[d.nr] = xr->shape[i];
+            d.rstride[d.nr++] = stride[i];
+            d.rcount *= xr->shape[i];
+        } else {
+            d.odim[d.no] = xr->shape[i];
+            d.ostride[d.no++] = stride[i];
+            nout *= xr->shape[i];
+        }
+    }
+    if (nout == 0) return 0;
+    if (is_max)
+        hipLaunchKernelGGL(generic_reduce<1>, dim3(grid_for(nout, 256)), dim3(256), 0, ctx->stream, x, y, nout, d, denom);
+    else
+        hipLaunchKernelGGL(generic_reduce<0>, dim3(grid_for(nout, 256)), dim3(256), 0, ctx->stream, x, y, nout, d, denom);
+    return launch_status("reduce");
+}
+
+int resize_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]), *yr = rec(ctx, node->outputs[0]);
+    if (xr->rank != 4 || yr->rank != 4) return -11;
+    const int N = yr->shape[0], C = yr->shape[1], OH = yr->shape[2], OW = yr->shape[3];
+    const int H = xr->shape[2], W = xr->shape[3];
+    const size_t total = static_cast<size_t>(N) * C * OH * OW;
+    if (total == 0) return 0;
+    const float scale_h = static_cast<float>(OH) / static_cast<float>(H);
+    const float scale_w = static_cast<float>(OW) / static_cast<float>(W);
+    set_kernel_name(ctx, node, "resize_nearest");
+    hipLaunchKernelGGL(resize_nearest, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]), N, C, H, W, OH, OW,
+                       scale_h, scale_w);
+    return launch_status("resize");
+}
+
+int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit) {
+    hipLaunchKernelGGL(flip_bit_kernel, dim3(1), dim3(1), 0, s, static_cast<uint32_t *>(data) + element, bit);
+    return launch_status("flip_bit");
+}
+
+int minmax(hipStream_t s, const float *x, size_t n, float *dev_out4) {
+    hipLaunchKernelGGL(minmax_kernel, dim3(1), dim3(256), 0, s, x, n, dev_out4);
+    return launch_status("minmax");
+}
+
+int fill_u32(hipStream_t s, uint32_t *p, size_t n, uint32_t v) {
+    hipLaunchKernelGGL(fill_u32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, v);
+    return launch_status("fill_u32");
+}
+
+int compare_bytes(hipStream_t s, const void *a, const void *b, size_t n, uint32_t *dev_flag) {
+    if (int rc = fill_u32(s, dev_flag, 1, 0u)) return rc;
+    if (n == 0) return 0;
+    hipLaunchKernelGGL(compare_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, static_cast<const uint8_t *>(a),
+                       static_cast<const uint8_t *>(b), n, dev_flag);
+    return launch_status("compare");
+}
+
+}  // namespace spk::kern

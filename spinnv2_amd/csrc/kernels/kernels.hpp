@@ -1,0 +1,47 @@
+// Built-in device node kernels of the MI355X backend.
+//
+// Each `*_run` has the plug-in signature of Spkv2NodeKernelFn and enqueues HIP
+// work on the context stream; each `*_prepare` runs once per node inside
+// spkv2_prepare (weight upload/repack, launch planning) and reports the
+// runtime workspace it needs.
+#pragma once
+
+#include <cstddef>
+
+#include "../runtime/context.hpp"
+
+namespace spk::kern {
+
+using RunFn = int (*)(Spkv2Context *, const Spkv2NodeRecord *, void *);
+using PrepFn = int (*)(Spkv2Context *, const Spkv2NodeRecord *, size_t *workspace_bytes);
+
+// convolution: fp32 MFMA implicit GEMM (group 1), direct kernels (grouped,
+// fallback), int8 MFMA implicit GEMM when the weight tensor is int8
+int conv_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int conv_prepare(Spkv2Context *, const Spkv2NodeRecord *, size_t *);
+int conv_direct_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+// int8 accumulator test hook
+int conv_int8_accumulators(Spkv2Context *, const Spkv2NodeRecord *, int32_t *dev_out);
+
+int gemm_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int gemm_prepare(Spkv2Context *, const Spkv2NodeRecord *, size_t *);
+int matmul_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+
+int binary_run(Spkv2Context *, const Spkv2NodeRecord *, void *);  // Add Mul Sub Div Mod
+int unary_run(Spkv2Context *, const Spkv2NodeRecord *, void *);   // Relu Sigmoid Clip LeakyRelu
+int copy_run(Spkv2Context *, const Spkv2NodeRecord *, void *);    // Flatten Reshape Cast Unsqueeze
+int concat_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int maxpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int avgpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int global_avgpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int softmax_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int reduce_run(Spkv2Context *, const Spkv2NodeRecord *, void *);  // ReduceMean ReduceMax
+int resize_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+
+// reliability helpers used by the executor
+int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);
+int minmax(hipStream_t s, const float *x, size_t n, float *dev_out4);
+int compare_bytes(hipStream_t s, const void *a, const void *b, size_t n, uint32_t *dev_flag);
+int fill_u32(hipStream_t s, uint32_t *p, size_t n, uint32_t v);
+
+}  // namespace spk::kern

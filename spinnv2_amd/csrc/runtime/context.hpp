@@ -1,0 +1,105 @@
+// Private state of one loaded SPK model on one GPU.
+//
+// The reference keeps an equivalent struct (runtime/core/context.h:15-59) and
+// lets kernels dereference it; here it is opaque to everything outside
+// libspkv2_mi355x.so and kernels use the accessors of spkv2_mi355x.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "spkv2_format.h"
+#include "spkv2_runtime.h"
+
+struct Spkv2TensorSlot {
+    const Spkv2TensorRecord *record = nullptr;
+    uint8_t *data = nullptr;  // device address (or a caller-bound device buffer)
+};
+
+struct Spkv2Context {
+    // ---- the package (host memory, zero-copy views into the blob) ----
+    uint8_t *owned_model = nullptr;
+    const uint8_t *model = nullptr;
+    size_t model_size = 0;
+    Spkv2Header header{};
+    const Spkv2SectionEntry *sections = nullptr;
+    const Spkv2TensorRecord *tensor_records = nullptr;
+    const Spkv2NodeRecord *node_records = nullptr;
+    const Spkv2MemoryPlanRecord *plan_records = nullptr;
+    size_t plan_count = 0;
+    const Spkv2KernelSpecRecord *spec_records = nullptr;
+    size_t spec_count = 0;
+    const Spkv2ProtectionRecord *protection_records = nullptr;
+    size_t protection_count = 0;
+    const uint8_t *attrs = nullptr;
+    size_t attrs_size = 0;
+    const uint8_t *weights_host = nullptr;
+    size_t weights_size = 0;
+    const Spkv2QuantParamRecord *quant_records = nullptr;
+    size_t quant_count = 0;
+    const uint8_t *quant_data = nullptr;
+    size_t quant_data_size = 0;
+    uint32_t *output_ids = nullptr;  // graph output order from the metadata JSON
+    size_t output_count = 0;
+    Spkv2TensorSlot *tensors = nullptr;
+
+    // ---- device state (valid after prepare) ----
+    bool prepared = false;
+    int device = -1;
+    hipStream_t stream = nullptr;
+    uint8_t *weights_dev = nullptr;
+    uint8_t *arena = nullptr;
+    bool owns_arena = false;
+    size_t arena_size = 0;
+    uint8_t *scratch = nullptr;
+    bool owns_scratch = false;
+    size_t scratch_size = 0;
+    uint8_t *workspace = nullptr;  // runtime-owned device workspace (split-K partials)
+    size_t workspace_size = 0;
+
+    // per-node state
+    size_t node_count = 0;
+    void **node_cache = nullptr;
+    void (**node_cache_dtors)(void *) = nullptr;
+    std::vector<std::string> node_kernel_names;
+
+    // ---- reliability (reference executor.c:335-498) ----
+    Spkv2FaultEvent fault_event{};
+    Spkv2ReliabilityStats stats{};
+    Spkv2RangeObservation *ranges = nullptr;
+    uint32_t *invocations = nullptr;
+    float *dev_minmax = nullptr;  // 4 floats: min, max, nonfinite count, pad
+    uint32_t *dev_flag = nullptr;
+
+    // ---- execution controls ----
+    bool graph_mode = false;
+    hipGraphExec_t graph_exec = nullptr;
+    uint64_t binding_epoch = 1;  // bumped by every bind_*
+    uint64_t graph_epoch = 0;    // binding_epoch the graph was captured at
+    bool profiling = false;
+    std::vector<hipEvent_t> ev_begin, ev_end;
+    std::vector<double> node_ms;
+    std::vector<uint32_t> node_runs;
+};
+
+// ---- internal helpers shared by the runtime translation units ----
+namespace spk {
+
+int execute_node(Spkv2Context *ctx, const Spkv2NodeRecord *node);
+int prepare_node(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *workspace_bytes);
+const Spkv2KernelSpecRecord *spec_by_id(const Spkv2Context *ctx, uint32_t id);
+void set_last_error(const char *what, hipError_t err);
+void set_last_error_text(const std::string &text);
+int hip_check(hipError_t err, const char *what);
+
+inline const uint8_t *host_weight_data(const Spkv2Context *ctx, uint32_t tensor_id) {
+    const Spkv2TensorRecord *r = &ctx->tensor_records[tensor_id];
+    if (r->role != SPKV2_ROLE_WEIGHT) return nullptr;
+    return ctx->weights_host + r->data_offset;
+}
+
+}  // namespace spk

@@ -1,0 +1,223 @@
+"""A small static-shape graph IR for building SPK packages without ONNX.
+
+Tensors and nodes carry dense ids in creation order, as the reference IR does
+(compiler/ir/graph.py:63-75).  Builders add ONNX-level ops (Conv,
+BatchNormalization, Relu, Add, ...); `spinnv2_amd.spk.passes` then applies
+the reference's fusion semantics before packaging.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+@dataclass
+class Tensor:
+    id: int
+    name: str
+    shape: list[int]
+    dtype: str = "fp32"  # fp32 | int8
+    role: str = "activation"  # input | output | weight | activation
+    data: np.ndarray | None = None
+    producer: int | None = None
+    consumers: list[int] = field(default_factory=list)
+
+    @property
+    def size_bytes(self) -> int:
+        n = 1
+        for d in self.shape:
+            n *= int(d)
+        return n * (1 if self.dtype == "int8" else 4)
+
+
+@dataclass
+class Node:
+    id: int
+    op_type: str
+    inputs: list[int]
+    outputs: list[int]
+    attrs: dict = field(default_factory=dict)
+
+
+def conv_out(size: int, k: int, s: int, p0: int, p1: int, d: int = 1) -> int:
+    return (size + p0 + p1 - d * (k - 1) - 1) // s + 1
+
+
+class Graph:
+    def __init__(self, name: str = "model") -> None:
+        self.model_name = name
+        self.tensors: list[Tensor] = []
+        self.nodes: list[Node] = []
+        self.inputs: list[int] = []
+        self.outputs: list[int] = []
+        self.metadata: dict = {}
+
+    # ------------------------------------------------------------ tensors
+    def _tensor(self, name, shape, dtype="fp32", role="activation", data=None) -> int:
+        t = Tensor(len(self.tensors), name, [int(d) for d in shape], dtype, role, data)
+        self.tensors.append(t)
+        return t.id
+
+    def input(self, name: str, shape) -> int:
+        tid = self._tensor(name, shape, role="input")
+        self.inputs.append(tid)
+        return tid
+
+    def weight(self, name: str, array: np.ndarray) -> int:
+        arr = np.ascontiguousarray(array)
+        dtype = "int8" if arr.dtype == np.int8 else "fp32"
+        if dtype == "fp32":
+            arr = arr.astype(np.float32, copy=False)
+        return self._tensor(name, list(arr.shape), dtype, "weight", arr)
+
+    def mark_output(self, tid: int) -> None:
+        self.tensors[tid].role = "output"
+        self.outputs.append(tid)
+
+    def shape(self, tid: int) -> list[int]:
+        return self.tensors[tid].shape
+
+    # -------------------------------------------------------------- nodes
+    def node(self, op: str, inputs: list[int], out_shapes: list[list[int]], attrs=None, name=None) -> list[int]:
+        nid = len(self.nodes)
+        outs = [self._tensor(f"{name or op.lower()}_{nid}_out{i}", s) for i, s in enumerate(out_shapes)]
+        self.nodes.append(Node(nid, op, list(inputs), outs, dict(attrs or {})))
+        self.relink()
+        return outs
+
+    def relink(self) -> None:
+        for t in self.tensors:
+            t.producer = None
+            t.consumers = []
+        for n in self.nodes:
+            for tid in n.outputs:
+                self.tensors[tid].producer = n.id
+            for tid in n.inputs:
+                if n.id not in self.tensors[tid].consumers:
+                    self.tensors[tid].consumers.append(n.id)
+
+    # ------------------------------------------------------- op builders
+    def conv(self, x: int, w: np.ndarray, b: np.ndarray | None = None, *, stride=1, pad=0, dilation=1, group=1,
+             name=None) -> int:
+        n, c, h, wd = self.shape(x)
+        m, cg, kh, kw = w.shape
+        assert cg * group == c, (w.shape, c, group)
+        s = [stride, stride] if isinstance(stride, int) else list(stride)
+        p = [pad] * 4 if isinstance(pad, int) else list(pad)
+        d = [dilation, dilation] if isinstance(dilation, int) else list(dilation)
+        oh = conv_out(h, kh, s[0], p[0], p[2], d[0])
+        ow = conv_out(wd, kw, s[1], p[1], p[3], d[1])
+        ins = [x, self.weight(f"{name or 'conv'}_w{len(self.nodes)}", w)]
+        if b is not None:
+            ins.append(self.weight(f"{name or 'conv'}_b{len(self.nodes)}", b))
+        attrs = {"kernel_shape": [kh, kw], "strides": s, "pads": p, "dilations": d, "group": group}
+        return self.node("Conv", ins, [[n, m, oh, ow]], attrs, name)[0]
+
+    def batchnorm(self, x: int, gamma, beta, mean, var, eps=1e-5, name=None) -> int:
+        ins = [x] + [self.weight(f"{name or 'bn'}_{k}{len(self.nodes)}", np.asarray(a, np.float32))
+                     for k, a in (("g", gamma), ("b", beta), ("m", mean), ("v", var))]
+        return self.node("BatchNormalization", ins, [self.shape(x)], {"epsilon": eps}, name)[0]
+
+    def unary(self, op: str, x: int, attrs=None) -> int:
+        return self.node(op, [x], [self.shape(x)], attrs)[0]
+
+    def relu(self, x: int) -> int:
+        return self.unary("Relu", x)
+
+    def silu(self, x: int) -> int:
+        """x * sigmoid(x) as the two ONNX nodes FuseConvSilu matches."""
+        s = self.unary("Sigmoid", x)
+        return self.binary("Mul", x, s)
+
+    def binary(self, op: str, a: int, b: int) -> int:
+        sa, sb = self.shape(a), self.shape(b)
+        r = max(len(sa), len(sb))
+        pa = [1] * (r - len(sa)) + sa
+        pb = [1] * (r - len(sb)) + sb
+        out = [max(x, y) if 1 in (x, y) else x for x, y in zip(pa, pb)]
+        return self.node(op, [a, b], [out])[0]
+
+    def add(self, a: int, b: int) -> int:
+        return self.binary("Add", a, b)
+
+    def maxpool(self, x: int, k: int, s: int, p: int = 0) -> int:
+        n, c, h, w = self.shape(x)
+        out = [n, c, conv_out(h, k, s, p, p), conv_out(w, k, s, p, p)]
+        return self.node("MaxPool", [x], [out], {"kernel_shape": [k, k], "strides": [s, s], "pads": [p] * 4})[0]
+
+    def avgpool(self, x: int, k: int, s: int, p: int = 0) -> int:
+        n, c, h, w = self.shape(x)
+        out = [n, c, conv_out(h, k, s, p, p), conv_out(w, k, s, p, p)]
+        return self.node("AveragePool", [x], [out], {"kernel_shape": [k, k], "strides": [s, s], "pads": [p] * 4})[0]
+
+    def global_avgpool(self, x: int) -> int:
+        n, c, _, _ = self.shape(x)
+        return self.node("GlobalAveragePool", [x], [[n, c, 1, 1]])[0]
+
+    def reduce_mean(self, x: int, axes, keepdims=1) -> int:
+        shape = self.shape(x)
+        axes = [a % len(shape) for a in axes]
+        out = [1 if i in axes else d for i, d in enumerate(shape)] if keepdims else \
+            [d for i, d in enumerate(shape) if i not in axes]
+        return self.node("ReduceMean", [x], [out], {"axes": axes, "keepdims": keepdims})[0]
+
+    def flatten(self, x: int, axis: int = 1) -> int:
+        shape = self.shape(x)
+        lead = int(np.prod(shape[:axis])) if axis > 0 else 1
+        return self.node("Flatten", [x], [[lead, int(np.prod(shape[axis:]))]], {"axis": axis})[0]
+
+    def reshape(self, x: int, shape) -> int:
+        return self.node("Reshape", [x], [list(shape)])[0]
+
+    def gemm(self, a: int, b: np.ndarray, c: np.ndarray | None = None, *, alpha=1.0, beta=1.0, trans_b=0,
+             name=None) -> int:
+        rows = self.shape(a)[0]
+        nout = b.shape[0] if trans_b else b.shape[1]
+        ins = [a, self.weight(f"{name or 'fc'}_w{len(self.nodes)}", b)]
+        if c is not None:
+            ins.append(self.weight(f"{name or 'fc'}_b{len(self.nodes)}", c))
+        attrs = {"alpha": alpha, "beta": beta, "transB": trans_b}
+        return self.node("Gemm", ins, [[rows, nout]], attrs, name)[0]
+
+    def matmul(self, a: int, b: int) -> int:
+        sa, sb = self.shape(a), self.shape(b)
+        lead_a, lead_b = sa[:-2], sb[:-2]
+        r = max(len(lead_a), len(lead_b))
+        la = [1] * (r - len(lead_a)) + lead_a
+        lb = [1] * (r - len(lead_b)) + lead_b
+        lead = [max(x, y) for x, y in zip(la, lb)]
+        return self.node("MatMul", [a, b], [lead + [sa[-2], sb[-1]]])[0]
+
+    def softmax(self, x: int, axis: int = -1) -> int:
+        return self.node("Softmax", [x], [self.shape(x)], {"axis": axis})[0]
+
+    def resize(self, x: int, scale: int = 2) -> int:
+        n, c, h, w = self.shape(x)
+        return self.node("Resize", [x], [[n, c, h * scale, w * scale]], {"mode": "nearest"})[0]
+
+    def concat(self, xs: list[int], axis: int = 1) -> int:
+        shape = list(self.shape(xs[0]))
+        shape[axis] = sum(self.shape(t)[axis] for t in xs)
+        return self.node("Concat", xs, [shape], {"axis": axis})[0]
+
+    # ---------------------------------------------------------- compaction
+    def compact(self) -> None:
+        """Drops tensors no node or graph IO refers to, renumbers ids densely."""
+        used = set(self.inputs) | set(self.outputs)
+        for n in self.nodes:
+            used.update(n.inputs)
+            used.update(n.outputs)
+        keep = [t for t in self.tensors if t.id in used]
+        remap = {t.id: i for i, t in enumerate(keep)}
+        for i, t in enumerate(keep):
+            t.id = i
+        self.tensors = keep
+        for i, n in enumerate(self.nodes):
+            n.id = i
+            n.inputs = [remap[t] for t in n.inputs]
+            n.outputs = [remap[t] for t in n.outputs]
+        self.inputs = [remap[t] for t in self.inputs]
+        self.outputs = [remap[t] for t in self.outputs]
+        self.relink()

@@ -1,0 +1,201 @@
+"""GPU parity: the MI355X runtime against the CPU oracle on the same packages.
+
+fp32 tolerance: tensor-normalized max error <= 1e-4 (FP32_TOL); selection /
+copy ops (MaxPool, Add, Resize, Relu) bit-exact; INT8 accumulators and
+dequantized outputs bit-exact.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from spinnv2_amd.spk import models, write_spk
+from spinnv2_amd.spk.quantize import calibrate_activation_scales, quantize_conv_weights
+
+from .helpers import FP32_TOL, rng_inputs, run_gpu, run_oracle, tnorm_err
+
+pytestmark = pytest.mark.gpu
+
+# (N, Cin, H, W, Cout, k, stride, pad, dilation, group, act, bias, residual)
+CONV_CASES = [
+    (1, 3, 17, 19, 8, 3, 1, 1, 1, 1, "Relu", True, False),
+    (2, 16, 12, 12, 32, 1, 1, 0, 1, 1, None, True, False),
+    (1, 3, 32, 32, 64, 7, 2, 3, 1, 1, "Relu", True, False),      # stem-like
+    (2, 64, 14, 14, 64, 3, 1, 1, 1, 1, "Relu", True, True),      # residual + relu
+    (1, 32, 15, 15, 48, 3, 2, 1, 1, 1, "Silu", True, False),
+    (1, 8, 16, 16, 8, 3, 1, 2, 2, 1, None, False, False),        # dilation, no bias
+    (1, 16, 10, 10, 16, 3, 1, 1, 1, 16, "Relu", True, False),    # depthwise -> direct kernel
+    (1, 16, 10, 10, 32, 3, 1, 1, 1, 4, None, True, False),       # grouped
+    (1, 130, 9, 9, 70, 1, 1, 0, 1, 1, "Relu", True, False),      # ragged M, K, N
+    (3, 5, 7, 7, 3, 3, 1, 1, 1, 1, None, True, True),            # tiny
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[f"conv{i}" for i in range(len(CONV_CASES))])
+def test_conv_f32_vs_oracle(gpu, case):
+    n, cin, h, w, cout, k, s, p, d, grp, act, bias, res = case
+    g = models.single_conv(n, cin, h, w, cout, k, s, p, d, grp, act, bias, res)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    print(f"conv case {case}", flush=True)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+# ResNet-101 layers at their real shapes, batch 1 (split-K path) and batch 8
+RESNET_LAYERS = [
+    (64, 56, 64, 3, 1, 1),     # s1 3x3
+    (256, 56, 64, 1, 1, 0),    # s1 1x1 reduce
+    (128, 28, 128, 3, 1, 1),   # s2 3x3
+    (256, 14, 256, 3, 1, 1),   # s3 3x3
+    (1024, 14, 256, 1, 1, 0),  # s3 1x1 reduce
+    (256, 14, 1024, 1, 1, 0),  # s3 1x1 expand
+    (512, 7, 512, 3, 1, 1),    # s4 3x3
+    (512, 7, 2048, 1, 1, 0),   # s4 1x1 expand
+    (512, 28, 1024, 1, 2, 0),  # s3 projection 1x1/2
+]
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("layer", RESNET_LAYERS, ids=[f"L{i}" for i in range(len(RESNET_LAYERS))])
+def test_resnet_layer_shapes(gpu, layer, batch):
+    cin, hw, cout, k, s, p = layer
+    g = models.single_conv(batch, cin, hw, hw, cout, k, s, p, act="Relu", residual=False)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    print(f"resnet layer {layer} b={batch}", flush=True)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+@pytest.mark.parametrize("rows,k,nout,trans_b,alpha", [(1, 400, 120, 0, 1.0), (64, 2048, 1000, 0, 1.0),
+                                                       (3, 84, 10, 1, 0.5), (1, 2048, 1000, 1, 1.0)])
+def test_gemm_vs_oracle(gpu, rows, k, nout, trans_b, alpha):
+    g = models.single_gemm(rows, k, nout, alpha=alpha, trans_b=trans_b)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+EXACT_OPS = [
+    ("MaxPool", [2, 8, 23, 23], dict(k=3, s=2, p=1)),
+    ("MaxPool", [1, 4, 8, 8], dict(k=2, s=2, p=0)),
+    ("Add", [2, 16, 9, 9], {}),
+    ("Add", [2, 16, 9, 9], dict(b_shape=[1, 16, 1, 1])),
+    ("Add", [1, 8, 5, 5], dict(relu=True)),
+    ("Relu", [3, 7, 11], {}),
+    ("Resize", [1, 4, 10, 12], dict(scale=2)),
+]
+
+
+@pytest.mark.parametrize("op,shape,kw", EXACT_OPS, ids=[f"{o}{i}" for i, (o, _, _) in enumerate(EXACT_OPS)])
+def test_exact_ops_bitwise(gpu, op, shape, kw):
+    g = models.single_op(op, shape, **kw)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+FLOAT_OPS = [
+    ("Softmax", [4, 1000], dict(axis=-1)),
+    ("Softmax", [2, 16, 50], dict(axis=1)),
+    ("ReduceMean", [4, 2048, 7, 7], dict(axes=[2, 3])),
+    ("ReduceMean", [2, 6, 5, 4], dict(axes=[1])),
+    ("GlobalAveragePool", [2, 32, 7, 7], {}),
+    ("AveragePool", [1, 4, 9, 9], dict(k=3, s=2, p=1)),
+    ("Sigmoid", [2, 300], {}),
+    ("Mul", [2, 8, 4, 4], dict(b_shape=[8, 1, 1])),
+]
+
+
+@pytest.mark.parametrize("op,shape,kw", FLOAT_OPS, ids=[f"{o}{i}" for i, (o, _, _) in enumerate(FLOAT_OPS)])
+def test_float_ops(gpu, op, shape, kw):
+    g = models.single_op(op, shape, **kw)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= 1e-5
+
+
+def test_lenet_e2e(gpu):
+    g = models.lenet()
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g, dist="uniform")
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+    assert np.argmax(got) == np.argmax(want)
+
+
+def test_resnet18_e2e_b1(gpu):
+    g = models.resnet(18, 1)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+    assert np.argmax(got) == np.argmax(want)
+
+
+def test_cpu_generic_package_runs_on_gpu(gpu):
+    """A package compiled for cpu_generic (bnns / simd kinds) runs unchanged."""
+    g = models.resnet(18, 1)
+    xs = rng_inputs(g)
+    got_generic = run_gpu(write_spk(g, "cpu_generic"), xs)[0]
+    got_mi = run_gpu(write_spk(g, "mi355x"), xs)[0]
+    np.testing.assert_array_equal(got_generic, got_mi)
+
+
+INT8_CASES = [
+    (1, 16, 14, 14, 32, 3, 1, 1, "Relu", False),
+    (2, 64, 14, 14, 64, 1, 1, 0, None, True),
+    (1, 3, 32, 32, 64, 7, 2, 3, "Relu", False),     # C % 16 != 0: byte gather
+    (1, 128, 7, 7, 256, 3, 2, 1, "Relu", False),    # split-K
+]
+
+
+@pytest.mark.parametrize("case", INT8_CASES, ids=[f"i8_{i}" for i in range(len(INT8_CASES))])
+def test_int8_conv_bit_exact(gpu, case):
+    from spinnv2_amd.runtime import Model
+    from oracle.spk_exec import OracleExecutor
+
+    n, cin, h, w, cout, k, s, p, act, res = case
+    g = models.single_conv(n, cin, h, w, cout, k, s, p, act=act, residual=res)
+    xs = rng_inputs(g)
+    qp = calibrate_activation_scales(g, [xs]) + quantize_conv_weights(g)
+    blob = write_spk(g, "mi355x", quant_params=qp)
+    ora = OracleExecutor(blob)
+    want = ora.run(*xs)[0].ravel()
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        got = m.get_output(0)
+        acc = m.int8_accumulators(0, want.nbytes)
+    np.testing.assert_array_equal(acc, ora.acc[0].ravel())
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_graph_mode_matches_eager(gpu):
+    from spinnv2_amd.runtime import Model
+
+    g = models.resnet(18, 2)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        eager = m.get_output(0)
+        m.set_graph_mode(True)
+        for _ in range(3):
+            m.set_input(0, xs[0])
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0), eager)
