@@ -1,0 +1,191 @@
+"""Benchmark: ResNet-101 fp32 224x224 on one MI355X through the SPINNV2 C API.
+
+A step is one spkv2_run of the whole network over one batch whose input is
+already resident in HBM (a device buffer bound with spkv2_bind_input).
+Workload: ResNet-101-style bottleneck CNN, batch
+64, He-normal weights with BN folded, N(0,1) input, seed 42 (synthetic data,
+random-init weights of the real architecture).
+
+Reported:
+  value          images/sec at batch 64 over the timed K steps (eager node
+                 loop with HIP events around every node on the run stream);
+  roofline       conv implicit-GEMM throughput: sum of conv FLOP per step /
+                 sum of conv node device time per step (HIP events), against
+                 the fp32 MFMA peak;
+  b1_*           batch-1 latency and images/sec (HIP-graph replay);
+  cpu_baseline   the reference runtime (cpu_generic package: naive conv on
+                 x86) on one batch-1 image, timed on the host.
+
+    python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--batch 64] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+FP32_MFMA_PEAK_TFLOPS = 157.3
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(timeout_s: float = 300.0) -> dict | None:
+    from oracle.ref_runtime import available
+
+    if not available():
+        log("cpu baseline skipped: oracle/_ref/libspkv2_ref.so not built")
+        return None
+    env = dict(os.environ)
+    env["OMP_NUM_THREADS"] = "1"
+    cmd = [sys.executable, "-m", "oracle.cpu_baseline", "--model", "resnet101", "--batch", "1",
+           "--profile", "cpu_generic", "--runs", "1"]
+    log("cpu baseline: reference cpu_generic runtime, ResNet-101 b=1, one image, 1 thread")
+    try:
+        out = subprocess.run(cmd, cwd=ROOT, env=env, capture_output=True, text=True, timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        log("cpu baseline timed out")
+        return None
+    if out.returncode != 0:
+        log(f"cpu baseline failed: {out.stderr[-400:]}")
+        return None
+    r = json.loads(out.stdout.strip().splitlines()[-1])
+    return {"value": r["images_per_sec"], "unit": "images/sec", "cores": 1, "kind": "reference",
+            "sample": "ResNet-101 fp32 b=1, one 224x224 image, reference cpu_generic package "
+                      "(bnns kind -> naive reference conv on x86), OMP_NUM_THREADS=1",
+            "seconds": r["avg_s"]}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--depth", type=int, default=101)
+    ap.add_argument("--b1-steps", type=int, default=50)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build targets a single MI355X); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    from spinnv2_amd.runtime import DeviceBuffer, Model, load_library
+    from spinnv2_amd.spk import models, write_spk
+
+    lib = load_library()
+    base = None if args.no_cpu_baseline else cpu_baseline()
+
+    # ---------------------------------------------------------- batch B
+    t0 = time.time()
+    g = models.resnet(args.depth, args.batch)
+    blob = write_spk(g, "mi355x")
+    conv_nodes = [n.id for n in g.nodes if n.op_type == "Conv"]
+    flops_per_node = {}
+    for n in g.nodes:
+        if n.op_type == "Conv":
+            y = g.shape(n.outputs[0])
+            w = g.tensors[n.inputs[1]].shape
+            flops_per_node[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
+    conv_flops = sum(flops_per_node.values())
+    x = models.make_input(g.tensors[g.inputs[0]].shape)
+    log(f"resnet{args.depth} b={args.batch}: package {len(blob) / 1e6:.1f} MB built in {time.time() - t0:.1f}s")
+
+    m = Model(blob, lib=lib)
+    xin = DeviceBuffer(x.nbytes, lib)
+    xin.upload(x)
+    m.bind_input(0, xin)
+    m.set_profiling(True)
+    for _ in range(args.warmup):
+        m.run()
+    m.reset_node_times()
+    lib.spkv2_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        m.run()
+    lib.spkv2_device_synchronize()
+    elapsed = time.perf_counter() - t0
+    logits = m.get_output(0).reshape(args.batch, -1)
+    conv_ms = 0.0
+    node_ms = {}
+    for nid in range(len(g.nodes)):
+        ms, cnt = m.node_time(nid)
+        node_ms[nid] = ms / max(cnt, 1)
+        if nid in flops_per_node:
+            conv_ms += node_ms[nid]
+    total_node_ms = sum(node_ms.values())
+    if args.node_report:
+        for nid, ms in node_ms.items():
+            n = g.nodes[nid]
+            extra = ""
+            if nid in flops_per_node:
+                extra = f" {flops_per_node[nid] / ms / 1e9:.1f} TFLOP/s"
+            log(f"node {nid:3d} {n.op_type:18s} {m.kernel_name(nid):44s} {ms:8.3f} ms{extra}")
+    m.close()
+    xin.free()
+    ms_per_step = elapsed * 1e3 / args.steps
+    conv_tflops = conv_flops / (conv_ms * 1e-3) / 1e12
+
+    # ---------------------------------------------------------- batch 1
+    g1 = models.resnet(args.depth, 1)
+    m1 = Model(write_spk(g1, "mi355x"), lib=lib)
+    x1 = models.make_input(g1.tensors[g1.inputs[0]].shape)
+    x1buf = DeviceBuffer(x1.nbytes, lib)
+    x1buf.upload(x1)
+    m1.bind_input(0, x1buf)
+    m1.set_graph_mode(True)
+    for _ in range(5):
+        m1.run()
+    lib.spkv2_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.b1_steps):
+        m1.run()
+    lib.spkv2_device_synchronize()
+    b1_ms = (time.perf_counter() - t0) * 1e3 / args.b1_steps
+    m1.close()
+    x1buf.free()
+
+    result = {
+        "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
+        "value": args.batch * args.steps / elapsed,
+        "unit": "images/sec",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic N(0,1) input, random-init He-normal weights, BN folded (seed 42)",
+        "config": {"workload": f"resnet{args.depth}_fp32_224", "batch": args.batch, "image": 224,
+                   "conv_gflop_per_image": conv_flops / args.batch / 1e9, "conv_nodes": len(conv_nodes),
+                   "parallelism": "single GPU"},
+        "b1_ms_per_image": b1_ms,
+        "b1_images_per_sec": 1e3 / b1_ms,
+        "conv_ms_per_step": conv_ms,
+        "node_ms_per_step": total_node_ms,
+        "roofline": {"bound": "mfma", "achieved": conv_tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": conv_tflops / FP32_MFMA_PEAK_TFLOPS, "traffic": None,
+                     "kernel": "conv_igemm_f32 (all conv nodes; HIP events per node on the run stream)"},
+        "cpu_baseline": base,
+        "top1_image0": int(logits[0].argmax()),
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

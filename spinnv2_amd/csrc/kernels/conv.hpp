@@ -33,10 +33,13 @@ struct ConvPlan {
     int cfg;             // index of the tile configuration
     int BM, BN, BK;      // tile shape
     int m_tiles, n_tiles, k_tiles;
-    int splitk, kt_per_split;
+    int splitk, kt_per_split;  // split-K factor and k-tiles per slice
     int K, Kpad;
     void *wpack;         // device: packed weight panels (fp32 or int8)
-    void *ktab;          // device: per-k gather table
+    void *ktab;          // device: per-k gather table (byte offsets into the B source)
+    int Hp, Wp, pt, pl;  // fp32 path: zero-padded input geometry (Hp == H, Wp == W, no copy, when unpadded)
+    bool padded;         // fp32 path: the input is copied into a padded workspace buffer first
+    size_t pad_bytes;    // fp32 path: workspace bytes of that padded copy
     float *scales;       // device, int8 path: w_scale[m] * x_scale
     float x_scale;       // int8 path: activation scale
     int quant_split;     // int8 path: first element index of the per-image tail (round half away)

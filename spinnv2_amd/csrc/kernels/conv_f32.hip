@@ -11,9 +11,10 @@
 // GEMM view (group == 1): M = Cout, N = batch*OH*OW, K = Cin*KH*KW.
 //   A[m][k] = w (OIHW flattened), repacked once at prepare into contiguous
 //             BM x BK panels per (m-tile, k-tile), zero padded;
-//   B[k][n] = x gathered on the fly (no im2col buffer): each k has an entry
-//             {c*H*W + kh*d*W + kw*d, kh*d, kw*d} in a per-layer table, each
-//             n a base offset (img, oh*s-p, ow*s-p);
+//   B[k][n] = x gathered on the fly (no im2col buffer) from the input, or
+//             from a zero-padded copy of it when the conv pads, so that every
+//             tap is in bounds: element (k, n) is at col(n) + koff(k), a
+//             per-lane base plus a per-layer table entry;
 //   C[m][n] = y in NCHW, written from the MFMA accumulators with bias,
 //             residual and activation applied in registers.
 // Tiles: 256 threads = 4 waves in a WAVES_M x WAVES_N grid; each wave owns
@@ -23,6 +24,7 @@
 // k = 8j+s and lanes 32-63 k = 8j+4+s for step s, the same mapping for A and
 // B, so every k is summed exactly once.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -85,27 +87,48 @@ void conv_plan_free(void *p) {
 
 // ------------------------------------------------------- implicit GEMM kernel
 
+// gfx9 buffer resource word 3 (raw, untyped loads); loads whose offset is at
+// or beyond num_records return 0.
+constexpr int kBufferWord3 = 0x00020000;
+// byte offset that is out of range for every tensor (they are < 2 GiB), and
+// still does not wrap when a valid offset is added to it
+constexpr int kOobOffset = 0x7fff0000;
+
 struct IgemmArgs {
-    const float *__restrict__ x;
-    const float *__restrict__ wp;    // [m_tiles][k_tiles][BM][BK]
-    const int2 *__restrict__ ktab;   // [Kpad] {offset, (kh*d << 16) | kw*d}
+    const float *__restrict__ x;     // B-operand source: NCHW input, zero-padded when the conv pads
+    const float *__restrict__ wp;    // [m_tiles][k_tiles][BM][BK] packed weights
+    const int *__restrict__ koff;    // [Kpad + 2*BK] byte offset of k = (c, kh, kw) in x, kOobOffset past K
     const float *__restrict__ bias;  // [M] or null
     const float *__restrict__ res;   // like y, or null
     float *__restrict__ y;
     float *__restrict__ ws;          // split-K partials [splitk][M][Ntot]
-    int H, W, M, OW, OHW, Ntot;
-    int sh, sw, ph, pw;
-    int x_img_stride;
+    int x_bytes;                     // extent of x for the bounds-checked loads
+    int y_bytes;                     // extent of y (and of the residual)
+    int ws_bytes;                    // extent of the split-K partials
+    int Wp;                          // row pitch of x (padded width)
+    int M, OW, OHW, Ntot;
+    int sh, sw;
+    int x_img_stride;                // elements between images in x
     int m_tiles, k_tiles, kt_per_split;
     int act;
     float alpha;
 };
 
+
+// Implicit GEMM: one BM x BN output tile per 256-thread workgroup
+// (blockIdx.x), the k range optionally split over blockIdx.y (split-K
+// partials are summed by splitk_epilogue).
+//
+// B gather: every tap of the (padded) input is in bounds, so element (k, n)
+// sits at byte offset col(n) + koff[k]: col(n) is a per-lane VGPR, koff[k] a
+// wave-uniform SGPR from the per-layer table, and each element is a single
+// buffer_load with (voffset, soffset) = (col(n), koff[k]).  Columns past N
+// and k past K use out-of-range offsets and load 0.
 template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     constexpr int TM = BM / (32 * WAVES_M);
     constexpr int TN = BN / (32 * WAVES_N);
-    constexpr int LDK = BK + 4;
+    constexpr int LDK = BK + (BK == 16 ? 8 : 4);  // row pitch (floats): keeps b128 LDS traffic conflict-free
     constexpr int KPT = BK * BN / 256;  // B elements per thread per k-tile
     constexpr int APT = BM * BK / 1024; // A float4 per thread per k-tile
     static_assert(WAVES_M * WAVES_N == 4, "four waves");
@@ -129,125 +152,193 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
     const int mt = bid % a.m_tiles;
     const int nt = bid / a.m_tiles;
+    const int kt0 = blockIdx.y * a.kt_per_split;
+    const int kt1 = min(kt0 + a.kt_per_split, a.k_tiles);
 
-    const int kt_begin = blockIdx.y * a.kt_per_split;
-    const int kt_end = min(kt_begin + a.kt_per_split, a.k_tiles);
-
-    // B gather: thread owns column bcol and KPT consecutive k rows of the tile
     const int bcol = tid % BN;
     const int bgrp = __builtin_amdgcn_readfirstlane(tid / BN);  // wave-uniform: BN >= 64
-    int ih0 = -0x40000000, iw0 = 0, col_off = 0;
-    {
-        const int n = nt * BN + bcol;
-        if (n < a.Ntot) {
-            const int img = n / a.OHW;
-            const int sp = n - img * a.OHW;
-            const int oh = sp / a.OW;
-            const int ow = sp - oh * a.OW;
-            ih0 = oh * a.sh - a.ph;
-            iw0 = ow * a.sw - a.pw;
-            col_off = img * a.x_img_stride + ih0 * a.W + iw0;
-        }
-    }
-
-    float4 areg[APT];
-    float breg[KPT];
-
-    auto load_tile = [&](int kt) {
-        const float4 *src = reinterpret_cast<const float4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt) * (BM * BK));
-#pragma unroll
-        for (int i = 0; i < APT; i++) areg[i] = src[tid + i * 256];
-        const int kbase = kt * BK + bgrp * KPT;
-#pragma unroll
-        for (int j = 0; j < KPT; j++) {
-            const int2 e = a.ktab[kbase + j];
-            const int ih = ih0 + (e.y >> 16);
-            const int iw = iw0 + (e.y & 0xffff);
-            const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
-                            static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
-            const float v = a.x[ok ? col_off + e.x : 0];
-            breg[j] = ok ? v : 0.0f;
-        }
-    };
-
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < APT; i++) {
-            const int f = (tid + i * 256) * 4;
-            *reinterpret_cast<float4 *>(&As[buf][(f / BK) * LDK + (f % BK)]) = areg[i];
-        }
-#pragma unroll
-        for (int j = 0; j < KPT; j += 4)
-            *reinterpret_cast<float4 *>(&Bs[buf][bcol * LDK + bgrp * KPT + j]) =
-                make_float4(breg[j], breg[j + 1], breg[j + 2], breg[j + 3]);
-    };
-
-    floatx16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
     const int row = lane & 31;
     const int khalf = 4 * (lane >> 5);
-    if (kt_begin < kt_end) {
-        load_tile(kt_begin);
-        store_tile(0);
-        __syncthreads();
-        for (int kt = kt_begin; kt < kt_end; kt++) {
-            const int cur = (kt - kt_begin) & 1;
-            if (kt + 1 < kt_end) load_tile(kt + 1);
-#pragma unroll
-            for (int k8 = 0; k8 < BK / 8; k8++) {
-                floatx4 af[TM], bf[TN];
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    af[i] = *reinterpret_cast<const floatx4 *>(
-                        &As[cur][((wm * TM + i) * 32 + row) * LDK + k8 * 8 + khalf]);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bf[j] = *reinterpret_cast<const floatx4 *>(
-                        &Bs[cur][((wn * TN + j) * 32 + row) * LDK + k8 * 8 + khalf]);
-#pragma unroll
-                for (int s = 0; s < 4; s++)
-#pragma unroll
-                    for (int i = 0; i < TM; i++)
-#pragma unroll
-                        for (int j = 0; j < TN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);
+    const int rsub = 4 * (lane >> 5);
+
+    {
+        int col = kOobOffset;
+        {
+            const int n = nt * BN + bcol;
+            if (n < a.Ntot) {
+                const int img = n / a.OHW;
+                const int sp = n - img * a.OHW;
+                const int oh = sp / a.OW;
+                const int ow = sp - oh * a.OW;
+                col = (img * a.x_img_stride + oh * a.sh * a.Wp + ow * a.sw) * 4;
             }
-            if (kt + 1 < kt_end) store_tile(cur ^ 1);
-            __syncthreads();
         }
+
+        // Two register sets, each holding one k-tile in flight: the loads of
+        // tile t+2 are issued while tile t is multiplied.  Native vector
+        // types: arrays of HIP's float4 class are not promoted to registers.
+        floatx4 ar0[APT], ar1[APT];
+        float br0[KPT], br1[KPT];
+
+#define IGEMM_LOAD_TILE(KT, AR, BR)                                                                                  \
+    {                                                                                                                \
+        const int kt_ = min((KT), a.k_tiles - 1);                                                                    \
+        const floatx4 *src =                                                                                         \
+            reinterpret_cast<const floatx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt_) * (BM * BK));       \
+        _Pragma("unroll") for (int i = 0; i < APT; i++) AR[i] = src[tid + i * 256];                                   \
+        /* the table has two tiles of out-of-range entries past Kpad */                                           \
+        const int *ko = a.koff + (KT) * BK + bgrp * KPT;                                                              \
+        _Pragma("unroll") for (int j = 0; j < KPT; j++) BR[j] = __builtin_bit_cast(                                  \
+            float, __builtin_amdgcn_raw_buffer_load_b32(xrs, col, ko[j], 0));                                        \
     }
 
-    // Epilogue.  32x32 accumulator layout: lane holds column (lane & 31) and
-    // rows 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.
-    const int rsub = 4 * (lane >> 5);
+#define IGEMM_STORE_TILE(BUF, AR, BR)                                                                                \
+    {                                                                                                                \
+        _Pragma("unroll") for (int i = 0; i < APT; i++) {                                                            \
+            const int f = (tid + i * 256) * 4;                                                                       \
+            *reinterpret_cast<floatx4 *>(&As[BUF][(f / BK) * LDK + (f % BK)]) = AR[i];                               \
+        }                                                                                                             \
+        _Pragma("unroll") for (int j = 0; j < KPT; j += 4) *reinterpret_cast<floatx4 *>(                             \
+            &Bs[BUF][bcol * LDK + bgrp * KPT + j]) = floatx4{BR[j], BR[j + 1], BR[j + 2], BR[j + 3]};                \
+    }
+
+#define IGEMM_COMPUTE(BUF)                                                                                           \
+    _Pragma("unroll") for (int k8 = 0; k8 < BK / 8; k8++) {                                                          \
+        floatx4 af[TM], bf[TN];                                                                                      \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) af[i] =                                                       \
+            *reinterpret_cast<const floatx4 *>(&As[BUF][((wm * TM + i) * 32 + row) * LDK + k8 * 8 + khalf]);         \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) bf[j] =                                                       \
+            *reinterpret_cast<const floatx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + k8 * 8 + khalf]);         \
+        _Pragma("unroll") for (int s = 0; s < 4; s++) _Pragma("unroll") for (int i = 0; i < TM; i++)                 \
+            _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =                                               \
+                __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);                        \
+    }
+
+    // One pipeline step: tile KT is in LDS buffer BUF, tile KT+1 is in flight
+    // in (AN, BNX), the free register set (AF, BF) receives tile KT+2.
+#define IGEMM_STEP(KT, BUF, AN, BNX, AF, BF)                                                                         \
+    {                                                                                                                \
+        IGEMM_LOAD_TILE((KT) + 2, AF, BF);                                                                           \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        IGEMM_COMPUTE(BUF);                                                                                          \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        IGEMM_STORE_TILE((BUF) ^ 1, AN, BNX);                                                                        \
+        __syncthreads();                                                                                             \
+    }
+
+        floatx16 acc[TM][TN];
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-        const int n = nt * BN + (wn * TN + j) * 32 + row;
-        if (n >= a.Ntot) continue;
-        const int img = n / a.OHW;
-        const int sp = n - img * a.OHW;
-        const size_t ybase = static_cast<size_t>(img) * a.M * a.OHW + sp;
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+            for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = mt * BM + (wm * TM + i) * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                if (m >= a.M) continue;
-                float v = acc[i][j][r];
-                if (a.ws) {
-                    a.ws[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.Ntot + n] = v;
-                } else {
-                    v = a.alpha * v;
-                    if (a.bias) v += a.bias[m];
-                    const size_t yi = ybase + static_cast<size_t>(m) * a.OHW;
-                    if (a.res) v += a.res[yi];
-                    a.y[yi] = apply_act(v, a.act);
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+        if (kt0 >= kt1) return;  // empty split-K slice
+        IGEMM_LOAD_TILE(kt0, ar0, br0);
+        IGEMM_LOAD_TILE(kt0 + 1, ar1, br1);
+        IGEMM_STORE_TILE(0, ar0, br0);
+        __syncthreads();
+        int kt = kt0;
+        // Tiles past kt1 are loaded and ignored, which keeps the loop free of
+        // data-dependent branches.
+        for (; kt + 1 < kt1; kt += 2) {
+            IGEMM_STEP(kt, 0, ar1, br1, ar0, br0);
+            IGEMM_STEP(kt + 1, 1, ar0, br0, ar1, br1);
+        }
+        if (kt < kt1) {
+            IGEMM_COMPUTE(0);
+        }
+#undef IGEMM_STEP
+#undef IGEMM_COMPUTE
+#undef IGEMM_LOAD_TILE
+#undef IGEMM_STORE_TILE
+
+        // 32x32 accumulator layout: lane holds column (lane & 31) and rows
+        // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.  Output offsets are
+        // 32-bit (tensors < 2 GiB); rows past M and columns past N get an
+        // out-of-range offset, so the buffer stores drop them.
+        int obase[TN];  // byte offset of (row 0, this lane's column) in y / res / ws
+        int mrow[TM];   // first row of this lane in block i
+#pragma unroll
+        for (int i = 0; i < TM; i++) mrow[i] = mt * BM + (wm * TM + i) * 32 + rsub;
+        if (a.ws) {
+            // split-K partials: ws[slice][m][n]
+            const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+                a.ws, static_cast<short>(0), a.ws_bytes, kBufferWord3);
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = nt * BN + (wn * TN + j) * 32 + row;
+                obase[j] = n < a.Ntot ? (blockIdx.y * a.M * a.Ntot + n) * 4 : kOobOffset;
+            }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                        const int off = m < a.M ? obase[j] + m * a.Ntot * 4 : kOobOffset;
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), wrs, off, 0, 0);
+                    }
+        } else {
+            const int ohw4 = a.OHW * 4;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = nt * BN + (wn * TN + j) * 32 + row;
+                const int img = n / a.OHW;
+                const int sp = n - img * a.OHW;
+                obase[j] = n < a.Ntot ? (img * a.M * a.OHW + sp) * 4 : kOobOffset;
+            }
+            const __amdgpu_buffer_rsrc_t yrs =
+                __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), a.y_bytes, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(a.res ? a.res : a.y), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(a.bias ? a.bias : a.y), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufferWord3);
+            // one 32x32 block at a time: its 16 bias and 16 residual loads are
+            // all in flight before the first use
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    floatx16 v = acc[i][j];
+                    if (a.alpha != 1.0f) v *= a.alpha;
+                    if (a.bias) {
+                        floatx16 bv;
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            bv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                  brs, (mrow[i] + 8 * (r >> 2) + (r & 3)) * 4, 0, 0));
+                        v += bv;
+                    }
+                    if (a.res) {
+                        floatx16 rv;
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                            rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                                  rrs, m < a.M ? obase[j] + m * ohw4 : kOobOffset, 0, 0));
+                        }
+                        v += rv;
+                    }
+                    if (a.act == 1) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+                    } else if (a.act == 2) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                        // __float_as_uint takes the element by value (a bit
+                        // cast applied to a vector element reads element 0)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
+                                                              m < a.M ? obase[j] + m * ohw4 : kOobOffset, 0, 0);
+                    }
                 }
             }
         }
@@ -260,13 +351,12 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
                                                        const float *__restrict__ res, float *__restrict__ y, int act,
                                                        float alpha) {
     const size_t total = static_cast<size_t>(M) * Ntot;
-    const size_t plane = total;
     for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
          idx += static_cast<size_t>(gridDim.x) * 256) {
         const int m = static_cast<int>(idx / Ntot);
         const int n = static_cast<int>(idx - static_cast<size_t>(m) * Ntot);
         float v = 0.0f;
-        for (int s = 0; s < splitk; s++) v += ws[s * plane + idx];
+        for (int s = 0; s < splitk; s++) v += ws[s * total + idx];
         v = alpha * v;
         if (bias) v += bias[m];
         const int img = n / OHW;
@@ -276,6 +366,26 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
         y[yi] = apply_act(v, act);
     }
 }
+
+// Zero-padded copy of an NCHW tensor: xp[p][pt + h][pl + w] = x[p][h][w],
+// every other element of the Hp x Wp planes 0.  One block per plane, 32-bit
+// index math, coalesced on both sides.
+__global__ void __launch_bounds__(256) pad_nchw(const float *__restrict__ x, float *__restrict__ xp, int H, int W,
+                                                int Hp, int Wp, int pt, int pl) {
+    const size_t plane = blockIdx.x;
+    const float *src = x + plane * H * W;
+    float *dst = xp + plane * Hp * Wp;
+    const int total = Hp * Wp;
+    for (int i = threadIdx.x; i < total; i += 256) {
+        const int hq = i / Wp;
+        const int wq = i - hq * Wp;
+        const int h = hq - pt, w = wq - pl;
+        dst[i] = (static_cast<unsigned>(h) < static_cast<unsigned>(H) && static_cast<unsigned>(w) < static_cast<unsigned>(W))
+                     ? src[h * W + w]
+                     : 0.0f;
+    }
+}
+
 
 // ------------------------------------------------------------ direct kernel
 
@@ -327,18 +437,21 @@ __global__ void __launch_bounds__(256) conv_direct_f32(DirectArgs a) {
 
 namespace {
 
+using IgemmKernel = void (*)(IgemmArgs);
+
 struct TileCfg {
     int BM, BN, BK;
     const char *name;
+    IgemmKernel kernel;
+    double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
 };
 
-// Index order must match the dispatch switch in launch_igemm.
+#define CFG(BM, BN, BK, EFF) {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, 2, 2>, EFF}
 const TileCfg kCfgs[] = {
-    {128, 128, 16, "128x128x16"},
-    {64, 128, 16, "64x128x16"},
-    {128, 64, 16, "128x64x16"},
-    {64, 64, 16, "64x64x16"},
+    CFG(128, 128, 16, 0.85), CFG(128, 128, 32, 0.85), CFG(64, 128, 16, 0.90), CFG(64, 128, 32, 0.88),
+    CFG(128, 64, 16, 1.00),  CFG(128, 64, 32, 0.95),  CFG(64, 64, 16, 0.96),  CFG(64, 64, 32, 0.98),
 };
+#undef CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 int device_cu_count() {
@@ -354,33 +467,48 @@ int device_cu_count() {
     return cus;
 }
 
-// Picks the tile shape and split-K factor for an (M, N, K) problem.  The cost
-// model counts the MFMA work of the padded tiles, divided over the waves of
-// workgroups the GPU can hold at once, with a per-shape efficiency factor
-// (smaller tiles re-read more from L2 per flop).
+// Workgroups of configuration c one CU holds at once.
+int resident_wgs(int c) {
+    static int cache[kNumCfgs] = {0};
+    if (cache[c] == 0) {
+        int n = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(kCfgs[c].kernel), 256, 0) !=
+                hipSuccess ||
+            n < 1) {
+            (void)hipGetLastError();
+            n = 1;
+        }
+        cache[c] = n;
+    }
+    return cache[c];
+}
+
+// Picks the tile shape and split-K factor for an (M, N, K) problem.  Cost =
+// rounds of workgroups the GPU runs at once x work of one round per CU /
+// per-shape efficiency, + the split-K partial traffic.  SPKV2_CONV_CFG and
+// SPKV2_CONV_SPLITK force a choice (tuning sweeps).
 void choose_tiles(int M, int Ntot, int K, int *cfg_out, int *splitk_out) {
     const int cus = device_cu_count();
-    const double eff[kNumCfgs] = {1.0, 0.92, 0.92, 0.8};
-    const int resident[kNumCfgs] = {2, 2, 2, 4};
     double best = 1e300;
     int best_cfg = 0, best_split = 1;
     for (int c = 0; c < kNumCfgs; c++) {
         const TileCfg &t = kCfgs[c];
+        const int res = resident_wgs(c);
         const int mt = (M + t.BM - 1) / t.BM;
         const int nt = (Ntot + t.BN - 1) / t.BN;
         const int kt = (K + t.BK - 1) / t.BK;
-        const int tiles = mt * nt;
+        const long tiles = static_cast<long>(mt) * nt;
         for (int split = 1; split <= 16; split *= 2) {
-            if (split > 1 && kt / split < 4) break;
+            if (split > 1 && kt / split < 2) break;
             const int kps = (kt + split - 1) / split;
-            const long wgs = static_cast<long>(tiles) * split;
-            const long slots = static_cast<long>(cus) * resident[c];
+            const long wgs = tiles * split;
+            const long slots = static_cast<long>(cus) * res;
             const long rounds = (wgs + slots - 1) / slots;
-            // time ~ rounds * work per WG / efficiency; WGs in one round share a CU
-            double work = static_cast<double>(t.BM) * t.BN * kps * t.BK;
-            double per_round = work * std::min<long>(resident[c], (wgs + cus - 1) / cus);
-            double cost = rounds * per_round / eff[c];
-            if (split > 1) cost += static_cast<double>(M) * Ntot * split * 8.0 / 64.0;  // partial write + re-read
+            // a CU's matrix cores are shared by the workgroups it runs: one
+            // round costs the work of the busiest CU
+            const long per_cu = std::min<long>(res, (wgs + cus - 1) / cus);
+            double cost = static_cast<double>(rounds) * per_cu * t.BM * t.BN * kps * t.BK / t.eff;
+            if (split > 1) cost += static_cast<double>(M) * Ntot * split * 24.0;  // partials written + re-read
             if (cost < best * 0.999) {
                 best = cost;
                 best_cfg = c;
@@ -388,23 +516,16 @@ void choose_tiles(int M, int Ntot, int K, int *cfg_out, int *splitk_out) {
             }
         }
     }
+    if (const char *e = getenv("SPKV2_CONV_CFG")) {
+        const int c = atoi(e);
+        if (c >= 0 && c < kNumCfgs) best_cfg = c;
+    }
+    if (const char *e = getenv("SPKV2_CONV_SPLITK")) {
+        const int sk = atoi(e);
+        if (sk >= 1 && sk <= 64) best_split = sk;
+    }
     *cfg_out = best_cfg;
     *splitk_out = best_split;
-}
-
-template <int BM, int BN, int BK, int WM, int WN>
-void launch_cfg(const IgemmArgs &a, int m_tiles, int n_tiles, int splitk, hipStream_t s) {
-    dim3 grid(static_cast<unsigned>(m_tiles * n_tiles), static_cast<unsigned>(splitk));
-    hipLaunchKernelGGL((conv_igemm_f32<BM, BN, BK, WM, WN>), grid, dim3(256), 0, s, a);
-}
-
-void launch_igemm(int cfg, const IgemmArgs &a, int m_tiles, int n_tiles, int splitk, hipStream_t s) {
-    switch (cfg) {
-    case 0: launch_cfg<128, 128, 16, 2, 2>(a, m_tiles, n_tiles, splitk, s); break;
-    case 1: launch_cfg<64, 128, 16, 2, 2>(a, m_tiles, n_tiles, splitk, s); break;
-    case 2: launch_cfg<128, 64, 16, 2, 2>(a, m_tiles, n_tiles, splitk, s); break;
-    default: launch_cfg<64, 64, 16, 2, 2>(a, m_tiles, n_tiles, splitk, s); break;
-    }
 }
 
 // Packs A[m][k] (row-major, lda = K) into [m_tiles][k_tiles][BM][BK] panels,
@@ -429,37 +550,18 @@ int upload_packed_f32(const float *w, int M, int K, int BM, int BK, int m_tiles,
     return hip_check(hipMemcpy(*out, packed.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy packed weights");
 }
 
-}  // namespace
-
-// Gather table for the implicit-GEMM B operand: entry k = (c, kh, kw) holds
-// the input offset relative to the output pixel's window origin and the tap
-// displacement used for the bounds test.  Entries past K point at a tap that
-// is always out of bounds, so padded k contribute zeros.
-int upload_ktab(const ConvGeom &g, int Kpad, void **out) {
-    const int K = g.C / g.group * g.KH * g.KW;
-    std::vector<int2> tab(static_cast<size_t>(Kpad));
-    for (int k = 0; k < Kpad; k++) {
-        if (k < K) {
-            const int c = k / (g.KH * g.KW);
-            const int r = k % (g.KH * g.KW);
-            const int kh = r / g.KW;
-            const int kw = r % g.KW;
-            tab[k].x = c * g.H * g.W + kh * g.dh * g.W + kw * g.dw;
-            tab[k].y = ((kh * g.dh) << 16) | (kw * g.dw);
-        } else {
-            tab[k].x = 0;
-            tab[k].y = 0x7fff << 16;
-        }
-    }
-    const size_t bytes = tab.size() * sizeof(int2);
-    if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc ktab")) return rc;
-    return hip_check(hipMemcpy(*out, tab.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy ktab");
+int upload_koff(const std::vector<int> &koff, void **out) {
+    const size_t bytes = koff.size() * sizeof(int);
+    if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc koff")) return rc;
+    return hip_check(hipMemcpy(*out, koff.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy koff");
 }
 
-// Shared with Gemm: plans an fp32 implicit GEMM for geometry g whose
-// weight matrix is w[M][K] on the host.
-int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan) {
-    const int K = g.C * g.KH * g.KW;
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+}  // namespace
+
+// Tiles, split-K and packed weights for an (M x K) weight matrix on the host.
+static int plan_tiles_and_weights(const ConvGeom &g, int K, const float *w_host, ConvPlan *plan) {
     const int Ntot = g.N * g.OH * g.OW;
     int cfg = 0, split = 1;
     choose_tiles(g.M, Ntot, K, &cfg, &split);
@@ -476,47 +578,104 @@ int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan) {
     plan->Kpad = plan->k_tiles * t.BK;
     plan->kt_per_split = (plan->k_tiles + split - 1) / split;
     plan->splitk = (plan->k_tiles + plan->kt_per_split - 1) / plan->kt_per_split;
-    plan->workspace = plan->splitk > 1 ? static_cast<size_t>(plan->splitk) * g.M * Ntot * sizeof(float) : 0;
-    if (int rc = upload_packed_f32(w_host, g.M, K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack)) return rc;
-    return upload_ktab(g, plan->Kpad, &plan->ktab);
+    return upload_packed_f32(w_host, g.M, K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack);
+}
+
+static size_t partial_bytes(const ConvPlan *p) {
+    return p->splitk > 1 ? static_cast<size_t>(p->splitk) * p->g.M * p->g.N * p->g.OH * p->g.OW * sizeof(float) : 0;
+}
+
+// Plans an fp32 implicit GEMM for convolution g (group 1) with weights
+// w_host[M][C*KH*KW].  When some tap falls outside the input, the input is
+// first copied into a zero-padded buffer so the kernel needs no bounds tests.
+int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan) {
+    const int K = g.C * g.KH * g.KW;
+    if (int rc = plan_tiles_and_weights(g, K, w_host, plan)) return rc;
+    const int hspan = (g.OH - 1) * g.sh + (g.KH - 1) * g.dh + 1;  // rows the taps touch, from -ph
+    const int wspan = (g.OW - 1) * g.sw + (g.KW - 1) * g.dw + 1;
+    plan->padded = g.ph > 0 || g.pw > 0 || hspan - g.ph > g.H || wspan - g.pw > g.W;
+    plan->pt = plan->padded ? g.ph : 0;
+    plan->pl = plan->padded ? g.pw : 0;
+    plan->Hp = plan->padded ? std::max(g.H + g.ph, hspan) : g.H;
+    plan->Wp = plan->padded ? std::max(g.W + g.pw, wspan) : g.W;
+    const int64_t xp_elems = static_cast<int64_t>(g.N) * g.C * plan->Hp * plan->Wp;
+    if (xp_elems * 4 >= 0x7fff0000LL) return SPKV2_E_UNSUPPORTED;  // byte offsets are 31-bit
+    plan->pad_bytes = plan->padded ? align256(static_cast<size_t>(xp_elems) * 4) : 0;
+    if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
+    plan->workspace = plan->pad_bytes + partial_bytes(plan);
+    // two extra tiles of out-of-range entries: the pipeline prefetches up to
+    // two tiles past the last one
+    std::vector<int> koff(static_cast<size_t>(plan->Kpad + 2 * plan->BK), kOobOffset);
+    for (int k = 0; k < K; k++) {
+        const int c = k / (g.KH * g.KW), r = k % (g.KH * g.KW);
+        const int kh = r / g.KW, kw = r % g.KW;
+        koff[k] = ((c * plan->Hp + kh * g.dh) * plan->Wp + kw * g.dw) * 4;
+    }
+    return upload_koff(koff, &plan->ktab);
+}
+
+// Plans the implicit GEMM of a Gemm node: B source is A [rows][K]
+// (k_stride 1) or, with trans_a, [K][rows] (k_stride rows).
+int plan_igemm_gemm(const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan) {
+    const int K = g.C;
+    if (int rc = plan_tiles_and_weights(g, K, w_host, plan)) return rc;
+    plan->padded = false;
+    plan->Hp = plan->Wp = 1;
+    if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
+    plan->workspace = partial_bytes(plan);
+    std::vector<int> koff(static_cast<size_t>(plan->Kpad + 2 * plan->BK), kOobOffset);
+    for (int k = 0; k < K; k++) koff[k] = k * k_stride * 4;
+    return upload_koff(koff, &plan->ktab);
 }
 
 std::string igemm_name(const ConvPlan *p) {
-    return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name + ",splitk=" + std::to_string(p->splitk) + ">";
+    return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") +
+           ",splitk=" + std::to_string(p->splitk) + ">";
 }
 
+// x_img_stride: elements between consecutive "images" of the B source (a
+// Gemm with trans_a reads A as [K][rows]: stride 1).
 static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res,
                           float *y, float alpha, int x_img_stride) {
     const ConvGeom &g = p->g;
+    const TileCfg &t = kCfgs[p->cfg];
+    if (ctx->workspace_size < p->workspace) return SPKV2_E_UNSUPPORTED;
     IgemmArgs a{};
     a.x = x;
+    a.x_bytes = static_cast<int>(g.x_elems * 4);
+    a.x_img_stride = x_img_stride;
+    if (p->padded) {
+        float *xp = reinterpret_cast<float *>(ctx->workspace);
+        const unsigned planes = static_cast<unsigned>(g.N * g.C);
+        hipLaunchKernelGGL(pad_nchw, dim3(planes), dim3(256), 0, ctx->stream, x, xp, g.H, g.W, p->Hp, p->Wp, p->pt,
+                           p->pl);
+        if (int rc = launch_status("pad_nchw")) return rc;
+        a.x = xp;
+        a.x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);
+        a.x_img_stride = g.C * p->Hp * p->Wp;
+    }
     a.wp = static_cast<const float *>(p->wpack);
-    a.ktab = static_cast<const int2 *>(p->ktab);
+    a.koff = static_cast<const int *>(p->ktab);
     a.bias = bias;
     a.res = res;
     a.y = y;
-    a.H = g.H;
-    a.W = g.W;
+    a.Wp = p->Wp;
     a.M = g.M;
     a.OW = g.OW;
     a.OHW = g.OH * g.OW;
     a.Ntot = g.N * a.OHW;
     a.sh = g.sh;
     a.sw = g.sw;
-    a.ph = g.ph;
-    a.pw = g.pw;
-    a.x_img_stride = x_img_stride;
     a.m_tiles = p->m_tiles;
     a.k_tiles = p->k_tiles;
     a.kt_per_split = p->kt_per_split;
     a.act = g.act;
     a.alpha = alpha;
-    a.ws = nullptr;
-    if (p->splitk > 1) {
-        if (ctx->workspace_size < p->workspace) return SPKV2_E_UNSUPPORTED;
-        a.ws = reinterpret_cast<float *>(ctx->workspace);
-    }
-    launch_igemm(p->cfg, a, p->m_tiles, p->n_tiles, p->splitk, ctx->stream);
+    a.ws = p->splitk > 1 ? reinterpret_cast<float *>(ctx->workspace + p->pad_bytes) : nullptr;
+    a.y_bytes = static_cast<int>(g.y_elems * 4);
+    a.ws_bytes = static_cast<int>(partial_bytes(p));
+    dim3 grid(static_cast<unsigned>(p->m_tiles * p->n_tiles), static_cast<unsigned>(p->splitk));
+    t.kernel<<<grid, dim3(256), 0, ctx->stream>>>(a);
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (p->splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.Ntot;
@@ -532,7 +691,7 @@ int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const fl
     return run_igemm_impl(ctx, p, x, bias, res, y, alpha, p->g.C * p->g.H * p->g.W);
 }
 
-// Gemm entry: no residual, caller-chosen row stride of the B operand source.
+// Gemm entry: no residual, caller-chosen row stride of the B source.
 int run_igemm_f32_strided(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, float *y,
                           float alpha, int x_img_stride) {
     return run_igemm_impl(ctx, p, x, bias, nullptr, y, alpha, x_img_stride);

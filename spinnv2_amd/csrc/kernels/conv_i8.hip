@@ -124,11 +124,12 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
         }
     }
 
-    int4 areg[2];
-    int4 breg[2];
+    // native vector types: arrays of HIP's int4 class stay in scratch memory
+    intx4 areg[2];
+    intx4 breg[2];
 
     auto load_tile = [&](int kt) {
-        const int4 *src = reinterpret_cast<const int4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt) * (BM * BK));
+        const intx4 *src = reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt) * (BM * BK));
         areg[0] = src[tid];
         areg[1] = src[tid + 256];
         const int kbase = kt * BK + bhalf * 32;
@@ -140,8 +141,8 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
                 const int iw = iw0 + (e.y & 0xffff);
                 const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
                                 static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
-                const int4 v = *reinterpret_cast<const int4 *>(a.xq + (ok ? col_off + e.x : 0));
-                breg[g] = ok ? v : make_int4(0, 0, 0, 0);
+                const intx4 v = *reinterpret_cast<const intx4 *>(a.xq + (ok ? col_off + e.x : 0));
+                breg[g] = ok ? v : intx4{0, 0, 0, 0};
             }
         } else {
             uint32_t words[8];
@@ -160,8 +161,10 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
                 }
                 words[w] = packed;
             }
-            breg[0] = make_int4(words[0], words[1], words[2], words[3]);
-            breg[1] = make_int4(words[4], words[5], words[6], words[7]);
+            breg[0] = intx4{static_cast<int>(words[0]), static_cast<int>(words[1]), static_cast<int>(words[2]),
+                            static_cast<int>(words[3])};
+            breg[1] = intx4{static_cast<int>(words[4]), static_cast<int>(words[5]), static_cast<int>(words[6]),
+                            static_cast<int>(words[7])};
         }
     };
 
@@ -169,10 +172,10 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int f = (tid + i * 256) * 16;  // byte index within the BM x BK tile
-            *reinterpret_cast<int4 *>(&As[buf][(f / BK) * LDK + (f % BK)]) = areg[i];
+            *reinterpret_cast<intx4 *>(&As[buf][(f / BK) * LDK + (f % BK)]) = areg[i];
         }
-        *reinterpret_cast<int4 *>(&Bs[buf][bcol * LDK + bhalf * 32]) = breg[0];
-        *reinterpret_cast<int4 *>(&Bs[buf][bcol * LDK + bhalf * 32 + 16]) = breg[1];
+        *reinterpret_cast<intx4 *>(&Bs[buf][bcol * LDK + bhalf * 32]) = breg[0];
+        *reinterpret_cast<intx4 *>(&Bs[buf][bcol * LDK + bhalf * 32 + 16]) = breg[1];
     };
 
     intx16 acc[TM][TN];

@@ -7,7 +7,7 @@
 // the fp32 MFMA implicit GEMM of a 1x1 convolution over an [rows, K, 1, 1]
 // input: the GEMM's M is the output feature dimension, its N the rows.  B is
 // constant weight data, transposed into [n][k] panels at prepare time;
-// trans_a only changes the gather table and the per-row stride.
+// trans_a only changes the k-offset table and the per-row stride.
 //
 // MatMul (reference mm/matmul.c:3-49): batched, numpy-broadcast leading
 // dimensions; one thread per output element, k inner, lanes along n.
@@ -19,8 +19,7 @@
 
 namespace spk::kern {
 
-int upload_ktab(const ConvGeom &g, int Kpad, void **out);
-int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan);
+int plan_igemm_gemm(const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan);
 int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res, float *y,
                   float alpha);
 std::string igemm_name(const ConvPlan *p);
@@ -127,21 +126,7 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     g.x_elems = static_cast<int64_t>(gp->rows) * gp->K;
     g.y_elems = static_cast<int64_t>(gp->rows) * gp->Nout;
     gp->conv.g = g;
-    if (int rc = plan_igemm_f32(g, w.data(), &gp->conv)) return rc;
-    if (attr.trans_a) {
-        // A stored [K][rows]: element (row r, k) at k*rows + r
-        (void)hipFree(gp->conv.ktab);
-        gp->conv.ktab = nullptr;
-        std::vector<int2> tab(static_cast<size_t>(gp->conv.Kpad));
-        for (int k = 0; k < gp->conv.Kpad; k++) {
-            tab[k].x = k < gp->K ? k * gp->rows : 0;
-            tab[k].y = k < gp->K ? 0 : (0x7fff << 16);
-        }
-        if (int rc = hip_check(hipMalloc(&gp->conv.ktab, tab.size() * sizeof(int2)), "hipMalloc")) return rc;
-        if (int rc = hip_check(hipMemcpy(gp->conv.ktab, tab.data(), tab.size() * sizeof(int2), hipMemcpyHostToDevice),
-                               "hipMemcpy"))
-            return rc;
-    }
+    if (int rc = plan_igemm_gemm(g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
     set_kernel_name(ctx, node, "gemm:" + igemm_name(&gp->conv));
     *ws = gp->conv.workspace;
     return 0;
@@ -156,6 +141,7 @@ int gemm_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const float *a = dptr<const float>(ctx, node->inputs[0]);
     const float *c = node->input_count > 2 ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
     float *y = dptr<float>(ctx, node->outputs[0]);
+    // A is [rows][K] (one "image" of K channels per row), or [K][rows] with trans_a
     return run_igemm_f32_strided(ctx, &gp->conv, a, c, y, gp->alpha, gp->trans_a ? 1 : gp->K);
 }
 
