@@ -2,9 +2,14 @@
  * CPU oracle for the MI355X hot path: plain C restatement of the reference
  * kernels.  TEST INFRASTRUCTURE ONLY (see spk_oracle.h).
  *
- * Built with -ffp-contract=off so every multiply-add rounds twice, as the
- * C source of the reference reads; the INT8 dequantize uses an explicit
- * fmaf where the reference's vector path fuses (vfmaq_f32).
+ * Built with -ffp-contract=off, so the compiler fuses nothing on its own;
+ * the multiply-adds the reference's release build fuses are written as
+ * explicit fmaf.  The reference's CMake build (runtime/CMakeLists.txt:8-14)
+ * adds -mfma on x86, and gcc then contracts `sum += a * b` in the conv,
+ * Gemm and MatMul loops and `alpha * sum + bias` in Gemm into one fused
+ * multiply-add each; the INT8 dequantize is an fmaf because the
+ * reference's vector path fuses it (vfmaq_f32).  With this, the oracle's
+ * conv / Gemm / MatMul outputs equal the reference runtime's bit for bit.
  * OpenMP splits work across output planes only, so each output element is
  * computed by exactly the sequential arithmetic shown.
  */
@@ -43,8 +48,8 @@ int oracle_conv2d_f32(const float *x, const float *w, const float *bias, const f
                             for (int kw = 0; kw < KW; kw++) {
                                 const int iw = ow * sw + kw * dw - pw;
                                 if (iw < 0 || iw >= W) continue;
-                                sum += x[(((size_t)n * C + c0 + c) * H + ih) * W + iw] *
-                                       w[(((size_t)m * Cg + c) * KH + kh) * KW + kw];
+                                sum = fmaf(x[(((size_t)n * C + c0 + c) * H + ih) * W + iw],
+                                           w[(((size_t)m * Cg + c) * KH + kh) * KW + kw], sum);
                             }
                         }
                     }
@@ -58,9 +63,15 @@ int oracle_conv2d_f32(const float *x, const float *w, const float *bias, const f
     return 0;
 }
 
-/* reference kernels/reference/mm/gemm.c:17-31 */
+/* reference kernels/reference/mm/gemm.c:17-31.  Rounding of the k loop as
+ * the reference's release build executes it: when both operands run
+ * contiguously along k (trans_a == 0, trans_b == 1) gcc vectorizes the
+ * products (8- then 4-wide multiplies, each rounded) and adds them to the
+ * sum one by one in k order, and only the last K % 4 terms are fused
+ * multiply-adds; otherwise every term is a fused multiply-add. */
 void oracle_gemm_f32(const float *a, const float *b, const float *c, float *y, int rows, int K, int nout,
                      int trans_a, int trans_b, float alpha) {
+    const int k_split = (!trans_a && trans_b) ? (K & ~3) : 0;
 #pragma omp parallel for schedule(static)
     for (int m = 0; m < rows; m++) {
         for (int n = 0; n < nout; n++) {
@@ -68,9 +79,14 @@ void oracle_gemm_f32(const float *a, const float *b, const float *c, float *y, i
             for (int k = 0; k < K; k++) {
                 const float av = trans_a ? a[(size_t)k * rows + m] : a[(size_t)m * K + k];
                 const float bv = trans_b ? b[(size_t)n * K + k] : b[(size_t)k * nout + n];
-                sum += av * bv;
+                if (k < k_split) {
+                    const float prod = av * bv;
+                    sum = sum + prod;
+                } else {
+                    sum = fmaf(av, bv, sum);
+                }
             }
-            y[(size_t)m * nout + n] = alpha * sum + (c ? c[n] : 0.0f);
+            y[(size_t)m * nout + n] = fmaf(alpha, sum, c ? c[n] : 0.0f);
         }
     }
 }
@@ -85,7 +101,7 @@ void oracle_matmul_f32(const float *a, const float *b, float *y, int batch, cons
             const float *bb = b + b_off[bi];
             for (int n = 0; n < N; n++) {
                 float sum = 0.0f;
-                for (int k = 0; k < K; k++) sum += ab[(size_t)m * K + k] * bb[(size_t)k * N + n];
+                for (int k = 0; k < K; k++) sum = fmaf(ab[(size_t)m * K + k], bb[(size_t)k * N + n], sum);
                 y[((size_t)bi * M + m) * N + n] = sum;
             }
         }

@@ -1,0 +1,131 @@
+"""Writes the golden fixtures in tests/golden/ from the reference SPINNV2 C runtime.
+
+The reference runtime is compiled from its own sources under
+/root/reference/runtime into oracle/_ref/libspkv2_ref.so (`make -C oracle
+ref`); this script runs it on packages written by this repo's SPK writer with
+the `cpu_ref` profile (every node on the reference kernels,
+runtime/kernels/reference/*) and stores, per case, the builder call, the
+inputs and the reference runtime's output.  The fixtures are data only: the
+tests re-create each package with the same builder call and compare the CPU
+oracle (and, on the GPU box, the MI355X runtime) against the stored output.
+
+    python tests/golden/make_golden.py          # rewrites tests/golden/*.npz
+
+Needs /root/reference; the GPU box never runs this.
+"""
+
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent.parent
+sys.path.insert(0, str(ROOT))
+
+from oracle.ref_runtime import RefModel, available  # noqa: E402
+from spinnv2_amd.spk import models, write_spk  # noqa: E402
+
+# (fixture name, builder, kwargs, input distribution)
+CASES: list[tuple[str, str, dict, str]] = []
+
+# Conv shapes: the reference test suite's CONV_CASES flavour
+# (tests/e2e/test_single_ops.py:72-80: kernel, stride, pad, group, dilation
+# variations) at sizes the naive reference conv finishes quickly.
+_CONV = [
+    dict(n=1, cin=3, h=17, w=19, cout=8, k=3, stride=1, pad=1, act="Relu"),
+    dict(n=2, cin=16, h=12, w=12, cout=32, k=1, stride=1, pad=0, act=None),
+    dict(n=1, cin=3, h=32, w=32, cout=64, k=7, stride=2, pad=3, act="Relu"),
+    dict(n=2, cin=64, h=14, w=14, cout=64, k=3, stride=1, pad=1, act="Relu", residual=True),
+    dict(n=1, cin=32, h=15, w=15, cout=48, k=3, stride=2, pad=1, act="Silu"),
+    dict(n=1, cin=8, h=16, w=16, cout=8, k=3, stride=1, pad=2, dilation=2, act=None, bias=False),
+    dict(n=1, cin=16, h=10, w=10, cout=16, k=3, stride=1, pad=1, group=16, act="Relu"),
+    dict(n=1, cin=16, h=10, w=10, cout=32, k=3, stride=1, pad=1, group=4, act=None),
+    dict(n=1, cin=130, h=9, w=9, cout=70, k=1, stride=1, pad=0, act="Relu"),
+    dict(n=3, cin=5, h=7, w=7, cout=3, k=3, stride=1, pad=1, act=None, residual=True),
+    dict(n=1, cin=4, h=9, w=11, cout=6, k=3, stride=2, pad=0, act=None, pads=[0, 1, 1, 0]),
+]
+for i, kw in enumerate(_CONV):
+    CASES.append((f"conv{i}", "single_conv", kw, "normal"))
+
+_GEMM = [
+    dict(rows=3, k=50, nout=20),
+    dict(rows=5, k=64, nout=10, trans_b=1, alpha=0.5),
+    dict(rows=1, k=2048, nout=100),
+    dict(rows=7, k=33, nout=65, bias=False),
+    dict(rows=4, k=33, nout=9, trans_b=1),
+    dict(rows=3, k=7, nout=5, trans_b=1, alpha=2.0),
+    dict(rows=2, k=3, nout=4, trans_b=1),
+]
+for i, kw in enumerate(_GEMM):
+    CASES.append((f"gemm{i}", "single_gemm", kw, "normal"))
+
+_OPS = [
+    ("MaxPool", [2, 8, 23, 23], dict(k=3, s=2, p=1)),
+    ("MaxPool", [1, 4, 8, 8], dict(k=2, s=2, p=0)),
+    ("Add", [2, 16, 9, 9], {}),
+    ("Add", [2, 16, 9, 9], dict(b_shape=[1, 16, 1, 1])),
+    ("Add", [1, 8, 5, 5], dict(relu=True)),
+    ("Relu", [3, 7, 11], {}),
+    ("Resize", [1, 4, 10, 12], dict(scale=2)),
+    ("Softmax", [4, 1000], dict(axis=-1)),
+    ("Softmax", [2, 16, 50], dict(axis=1)),
+    ("ReduceMean", [2, 64, 7, 7], dict(axes=[2, 3])),
+    ("ReduceMean", [2, 6, 5, 4], dict(axes=[1])),
+    ("GlobalAveragePool", [2, 32, 7, 7], {}),
+    ("AveragePool", [1, 4, 9, 9], dict(k=3, s=2, p=1)),
+    ("Sigmoid", [2, 300], {}),
+    ("Mul", [2, 8, 4, 4], dict(b_shape=[8, 1, 1])),
+    ("Sub", [2, 3, 4], dict(b_shape=[4])),
+    ("Div", [2, 3, 4], dict(b_shape=[3, 1])),
+]
+for i, (op, shape, kw) in enumerate(_OPS):
+    CASES.append((f"op{i}_{op}", "single_op", dict(op=op, shape=shape, **kw), "normal"))
+
+# End to end: the LeNet config on U[0,1) input, and a
+# ResNet-18 at 32x32 (every ResNet node kind: stem, pools, basic blocks with
+# projections, ReduceMean, Gemm).
+CASES.append(("lenet", "lenet", {}, "uniform"))
+CASES.append(("resnet18_32px", "resnet", dict(depth=18, batch=2, image=32, classes=10), "normal"))
+CASES.append(("resnet50_32px", "resnet", dict(depth=50, batch=1, image=32, classes=10), "normal"))
+
+
+def build_graph(builder: str, kw: dict):
+    kw = dict(kw)
+    if builder == "single_op":
+        op = kw.pop("op")
+        shape = kw.pop("shape")
+        return models.single_op(op, shape, **kw)
+    return getattr(models, builder)(**kw)
+
+
+def case_inputs(g, dist: str, seed: int = 42) -> list[np.ndarray]:
+    return [models.make_input(g.tensors[t].shape, seed + i, dist) for i, t in enumerate(g.inputs)]
+
+
+def main() -> None:
+    if not available():
+        sys.exit("oracle/_ref/libspkv2_ref.so is not built: make -C oracle ref (needs /root/reference)")
+    only = set(sys.argv[1:])
+    for name, builder, kw, dist in CASES:
+        if only and name not in only:
+            continue
+        g = build_graph(builder, kw)
+        blob = write_spk(g, "cpu_ref")
+        xs = case_inputs(g, dist)
+        ref = RefModel(blob)
+        y = ref.run(*xs)
+        ref.close()
+        meta = {"builder": builder, "kwargs": kw, "dist": dist, "seed": 42, "profile": "cpu_ref",
+                "source": "reference runtime (runtime/core + runtime/kernels/reference) built by oracle/Makefile"}
+        arrays = {f"x{i}": x for i, x in enumerate(xs)}
+        np.savez_compressed(HERE / f"{name}.npz", meta=np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8),
+                            y=y, **arrays)
+        print(f"{name:24s} inputs {[list(x.shape) for x in xs]} -> {y.size} values")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,53 @@
+"""Loads the golden fixtures written by tests/golden/make_golden.py.
+
+Each fixture holds a builder call (re-run here with this repo's SPK writer),
+the inputs, and the output the reference SPINNV2 C runtime produced on the
+`cpu_ref` package of that graph.
+"""
+
+from __future__ import annotations
+
+import json
+from dataclasses import dataclass
+from pathlib import Path
+
+import numpy as np
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+# ops whose reference kernels are a pure selection, copy or one IEEE add per
+# element: any correct restatement is bit-exact
+EXACT_BUILDER_OPS = {"MaxPool", "Add", "Relu", "Resize", "Sub", "Mul", "Div"}
+
+
+@dataclass
+class GoldenCase:
+    name: str
+    builder: str
+    kwargs: dict
+    inputs: list
+    expected: np.ndarray
+
+    def graph(self):
+        from spinnv2_amd.spk import models
+
+        kw = dict(self.kwargs)
+        if self.builder == "single_op":
+            op = kw.pop("op")
+            shape = kw.pop("shape")
+            return models.single_op(op, shape, **kw)
+        return getattr(models, self.builder)(**kw)
+
+    @property
+    def exact(self) -> bool:
+        return self.builder == "single_op" and self.kwargs["op"] in EXACT_BUILDER_OPS
+
+
+def load_cases() -> list[GoldenCase]:
+    cases = []
+    for p in sorted(GOLDEN.glob("*.npz")):
+        with np.load(p, allow_pickle=False) as z:
+            meta = json.loads(bytes(z["meta"]).decode())
+            xs = [z[f"x{i}"] for i in range(len([k for k in z.files if k.startswith("x")]))]
+            cases.append(GoldenCase(p.stem, meta["builder"], meta["kwargs"], xs, z["y"]))
+    return cases

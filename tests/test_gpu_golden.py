@@ -1,0 +1,38 @@
+"""MI355X runtime against the reference runtime's own outputs.
+
+The fixtures in tests/golden/ hold what the reference SPINNV2 C runtime
+computed on the same graphs and inputs (tests/golden/make_golden.py); here
+the `mi355x` package of each graph runs on the GPU through the C ABI.
+Bar: bit-exact for selection / copy / single-add ops, fp32 tensor-normalized
+error <= 1e-4 for contractions, plus top-1 agreement for the networks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from spinnv2_amd.spk import write_spk
+
+from .golden_cases import load_cases
+from .helpers import FP32_TOL, run_gpu, tnorm_err
+
+CASES = load_cases()
+NETWORKS = {"lenet", "resnet18_32px", "resnet50_32px"}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", CASES, ids=[c.name for c in CASES])
+def test_mi355x_matches_reference_runtime(gpu, case):
+    print(f"[golden] {case.name}", flush=True)
+    blob = write_spk(case.graph(), "mi355x")
+    got = run_gpu(blob, case.inputs)[0].ravel()
+    assert got.shape == case.expected.shape
+    if case.exact:
+        np.testing.assert_array_equal(got.view(np.uint32), case.expected.view(np.uint32))
+    else:
+        assert tnorm_err(got, case.expected) <= FP32_TOL
+    if case.name in NETWORKS:
+        rows = got.reshape(case.inputs[0].shape[0], -1)
+        want = case.expected.reshape(rows.shape)
+        assert (rows.argmax(axis=1) == want.argmax(axis=1)).all()
