@@ -67,6 +67,73 @@ def cpu_baseline(timeout_s: float = 300.0) -> dict | None:
             "seconds": r["avg_s"]}
 
 
+def copy_calibration(mib: int, reps: int) -> None:
+    """Runs the runtime's plain copy kernel (a Flatten node whose output the
+    planner cannot alias to the graph input) over `mib` MiB, `reps` times:
+    the known-size reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    from spinnv2_amd.runtime import DeviceBuffer, Model, load_library
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk import write_spk
+
+    lib = load_library()
+    n = mib * (1 << 20) // 4
+    g = Graph("copy")
+    x = g.input("x", [1, n])
+    g.mark_output(g.flatten(x))
+    m = Model(write_spk(g, "mi355x"), lib=lib)
+    buf = DeviceBuffer(n * 4, lib)
+    buf.upload(np.zeros(n, np.float32))
+    m.bind_input(0, buf)
+    for _ in range(reps):
+        m.run()
+    lib.spkv2_device_synchronize()
+    assert m.kernel_name(0) == "copy", m.kernel_name(0)
+    print(json.dumps({"copy_kernel_bytes_read": n * 4, "copy_kernel_bytes_written": n * 4, "dispatches": reps}))
+    m.close()
+    buf.free()
+
+
+def pmc_traffic() -> dict | None:
+    """HBM bytes of the conv kernels per step, from the committed rocprofv3
+    --pmc summary (FETCH_SIZE and WRITE_SIZE passes scaled by the copy
+    kernel's reading).  None when no summary is committed."""
+    p = ROOT / "profiles" / "conv_igemm_f32_resnet101_b64_traffic.txt"
+    if not p.exists():
+        return None
+    vals = {}
+    for line in p.read_text().splitlines():
+        if line.startswith("result "):
+            k, v = line[len("result "):].split("=", 1)
+            vals[k.strip()] = float(v)
+    return vals or None
+
+
+def batch1_latency(depth: int, steps: int, lib) -> float:
+    """Batch-1 latency: ms per spkv2_run of a HIP-graph-captured node loop,
+    input already resident on the device."""
+    from spinnv2_amd.runtime import DeviceBuffer, Model
+    from spinnv2_amd.spk import models, write_spk
+
+    g1 = models.resnet(depth, 1)
+    m1 = Model(write_spk(g1, "mi355x"), lib=lib)
+    x1 = models.make_input(g1.tensors[g1.inputs[0]].shape)
+    x1buf = DeviceBuffer(x1.nbytes, lib)
+    x1buf.upload(x1)
+    m1.bind_input(0, x1buf)
+    m1.set_graph_mode(True)
+    for _ in range(5):
+        m1.run()
+    lib.spkv2_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m1.run()
+    lib.spkv2_device_synchronize()
+    b1_ms = (time.perf_counter() - t0) * 1e3 / steps
+    m1.close()
+    x1buf.free()
+    return b1_ms
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,11 +144,16 @@ def main() -> None:
     ap.add_argument("--b1-steps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build targets a single MI355X); got --gpus {args.gpus}",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration_mib:
+        copy_calibration(args.copy_calibration_mib, args.steps)
+        return
 
     from spinnv2_amd.runtime import DeviceBuffer, Model, load_library
     from spinnv2_amd.spk import models, write_spk
@@ -101,6 +173,13 @@ def main() -> None:
             w = g.tensors[n.inputs[1]].shape
             flops_per_node[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
     conv_flops = sum(flops_per_node.values())
+    # minimum HBM bytes of the conv nodes: weights + input + output (+ residual) read/written once
+    conv_alg_bytes = 0
+    for n in g.nodes:
+        if n.op_type == "Conv":
+            conv_alg_bytes += 4 * sum(int(np.prod(g.tensors[t].shape)) for t in n.inputs)
+            conv_alg_bytes += 4 * int(np.prod(g.shape(n.outputs[0])))
+    traffic = pmc_traffic()
     x = models.make_input(g.tensors[g.inputs[0]].shape)
     log(f"resnet{args.depth} b={args.batch}: package {len(blob) / 1e6:.1f} MB built in {time.time() - t0:.1f}s")
 
@@ -119,6 +198,16 @@ def main() -> None:
     lib.spkv2_device_synchronize()
     elapsed = time.perf_counter() - t0
     logits = m.get_output(0).reshape(args.batch, -1)
+    # host-buffer interface (spkv2_set_input / spkv2_get_output copy over PCIe
+    # each step): reported beside, never as, the value
+    pcie_steps = max(1, min(args.steps, 5))
+    t0 = time.perf_counter()
+    for _ in range(pcie_steps):
+        m.set_input(0, x)
+        m.run()
+        m.get_output(0)
+    pcie_ips = args.batch * pcie_steps / (time.perf_counter() - t0)
+    m.bind_input(0, xin)
     conv_ms = 0.0
     node_ms = {}
     for nid in range(len(g.nodes)):
@@ -140,23 +229,7 @@ def main() -> None:
     conv_tflops = conv_flops / (conv_ms * 1e-3) / 1e12
 
     # ---------------------------------------------------------- batch 1
-    g1 = models.resnet(args.depth, 1)
-    m1 = Model(write_spk(g1, "mi355x"), lib=lib)
-    x1 = models.make_input(g1.tensors[g1.inputs[0]].shape)
-    x1buf = DeviceBuffer(x1.nbytes, lib)
-    x1buf.upload(x1)
-    m1.bind_input(0, x1buf)
-    m1.set_graph_mode(True)
-    for _ in range(5):
-        m1.run()
-    lib.spkv2_device_synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.b1_steps):
-        m1.run()
-    lib.spkv2_device_synchronize()
-    b1_ms = (time.perf_counter() - t0) * 1e3 / args.b1_steps
-    m1.close()
-    x1buf.free()
+    b1_ms = batch1_latency(args.depth, args.b1_steps, lib) if args.b1_steps > 0 else None
 
     result = {
         "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
@@ -174,12 +247,17 @@ def main() -> None:
         "config": {"workload": f"resnet{args.depth}_fp32_224", "batch": args.batch, "image": 224,
                    "conv_gflop_per_image": conv_flops / args.batch / 1e9, "conv_nodes": len(conv_nodes),
                    "parallelism": "single GPU"},
+        "host_io_images_per_sec": pcie_ips,
         "b1_ms_per_image": b1_ms,
-        "b1_images_per_sec": 1e3 / b1_ms,
+        "b1_images_per_sec": 1e3 / b1_ms if b1_ms else None,
         "conv_ms_per_step": conv_ms,
         "node_ms_per_step": total_node_ms,
         "roofline": {"bound": "mfma", "achieved": conv_tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": conv_tflops / FP32_MFMA_PEAK_TFLOPS, "traffic": None,
+                     "frac": conv_tflops / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": traffic.get("conv_hbm_bytes_per_step") if traffic else None,
+                     "traffic_basis": "HBM bytes of all conv launches of one step (rocprofv3 FETCH_SIZE + "
+                                      "WRITE_SIZE, copy-kernel scaled; profiles/)" if traffic else None,
+                     "algorithmic_bytes": conv_alg_bytes,
                      "kernel": "conv_igemm_f32 (all conv nodes; HIP events per node on the run stream)"},
         "cpu_baseline": base,
         "top1_image0": int(logits[0].argmax()),
