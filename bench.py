@@ -183,7 +183,9 @@ def main() -> None:
     x = models.make_input(g.tensors[g.inputs[0]].shape)
     log(f"resnet{args.depth} b={args.batch}: package {len(blob) / 1e6:.1f} MB built in {time.time() - t0:.1f}s")
 
+    t0 = time.time()
     m = Model(blob, lib=lib)
+    log(f"load + prepare (weights upload, tile tuning) {time.time() - t0:.2f}s")
     xin = DeviceBuffer(x.nbytes, lib)
     xin.upload(x)
     m.bind_input(0, xin)

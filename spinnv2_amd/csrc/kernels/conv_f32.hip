@@ -24,8 +24,13 @@
 // k = 8j+s and lanes 32-63 k = 8j+4+s for step s, the same mapping for A and
 // B, so every k is summed exactly once.
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "conv.hpp"
@@ -483,36 +488,269 @@ int resident_wgs(int c) {
     return cache[c];
 }
 
-// Picks the tile shape and split-K factor for an (M, N, K) problem.  Cost =
-// rounds of workgroups the GPU runs at once x work of one round per CU /
-// per-shape efficiency, + the split-K partial traffic.  SPKV2_CONV_CFG and
-// SPKV2_CONV_SPLITK force a choice (tuning sweeps).
-void choose_tiles(int M, int Ntot, int K, int *cfg_out, int *splitk_out) {
+// Tile counts of configuration c for an (M, Ntot, K) problem with split-K
+// request `split`, as a plan stores them.
+struct TileCounts {
+    int m_tiles, n_tiles, k_tiles, kt_per_split, splitk;
+};
+
+TileCounts tile_counts(int c, int M, int Ntot, int K, int split) {
+    const TileCfg &t = kCfgs[c];
+    TileCounts tc;
+    tc.m_tiles = (M + t.BM - 1) / t.BM;
+    tc.n_tiles = (Ntot + t.BN - 1) / t.BN;
+    tc.k_tiles = (K + t.BK - 1) / t.BK;
+    tc.kt_per_split = (tc.k_tiles + split - 1) / split;
+    tc.splitk = (tc.k_tiles + tc.kt_per_split - 1) / tc.kt_per_split;
+    return tc;
+}
+
+size_t partial_bytes_of(const TileCounts &tc, int M, int Ntot) {
+    return tc.splitk > 1 ? static_cast<size_t>(tc.splitk) * M * Ntot * sizeof(float) : 0;
+}
+
+// Modelled time (us) of a candidate: the MFMA work of the busiest CU over
+// the rounds of resident workgroups, floored by the serial latency of one
+// workgroup's k loop (a k-tile step costs ~35 ns per k when a workgroup
+// runs alone on its CU), plus split-K partial traffic and the extra
+// epilogue launch.  Used to prune the candidates the tuner times, and alone
+// when tuning is off.
+double model_us(int c, const TileCounts &tc, int M, int Ntot) {
+    const TileCfg &t = kCfgs[c];
     const int cus = device_cu_count();
-    double best = 1e300;
-    int best_cfg = 0, best_split = 1;
+    const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles * tc.splitk;
+    const long slots = static_cast<long>(cus) * resident_wgs(c);
+    const long rounds = (wgs + slots - 1) / slots;
+    const long per_cu = std::min<long>(resident_wgs(c), (wgs + cus - 1) / cus);
+    const double tile_us = 2.0 * t.BM * t.BN * t.BK / (256.0 * 2400.0 * t.eff);  // one k-tile on a whole CU
+    const double mfma = static_cast<double>(rounds) * per_cu * tc.kt_per_split * tile_us;
+    const double latency = static_cast<double>(rounds) * tc.kt_per_split * t.BK * 0.035;
+    double us = std::max(mfma, latency) + 2.0;
+    if (tc.splitk > 1) us += 4.0 * M * static_cast<double>(Ntot) * (tc.splitk + 1) / 4.0e6 + 3.0;
+    return us;
+}
+
+const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
+
+// What the tuner needs to launch a candidate: the B source geometry and
+// the k -> byte offset rule of the layer.
+struct GatherSpec {
+    int K;
+    int Wp;            // row pitch of the B source
+    int x_bytes;       // extent of the B source
+    int x_img_stride;  // elements between images of the B source
+    std::function<int(int)> koff;  // byte offset of k < K
+    std::string key;   // everything the timing depends on
+};
+
+std::vector<int> build_koff(const GatherSpec &gs, int BK) {
+    const int kpad = (gs.K + BK - 1) / BK * BK;
+    // two extra tiles of out-of-range entries: the pipeline prefetches up to
+    // two tiles past the last one
+    std::vector<int> koff(static_cast<size_t>(kpad + 2 * BK), kOobOffset);
+    for (int k = 0; k < gs.K; k++) koff[k] = gs.koff(k);
+    return koff;
+}
+
+}  // namespace
+
+// Launches the implicit GEMM of configuration cfg with tile counts tc over
+// an already prepared (padded) B source, then the split-K epilogue.
+static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
+                        int x_bytes, int x_img_stride, const float *wpack, const int *koff, const float *bias,
+                        const float *res, float *y, float alpha, float *ws) {
+    const TileCfg &t = kCfgs[cfg];
+    IgemmArgs a{};
+    a.x = xs;
+    a.x_bytes = x_bytes;
+    a.x_img_stride = x_img_stride;
+    a.wp = wpack;
+    a.koff = koff;
+    a.bias = bias;
+    a.res = res;
+    a.y = y;
+    a.Wp = Wp;
+    a.M = g.M;
+    a.OW = g.OW;
+    a.OHW = g.OH * g.OW;
+    a.Ntot = g.N * a.OHW;
+    a.sh = g.sh;
+    a.sw = g.sw;
+    a.m_tiles = tc.m_tiles;
+    a.k_tiles = tc.k_tiles;
+    a.kt_per_split = tc.kt_per_split;
+    a.act = g.act;
+    a.alpha = alpha;
+    a.ws = tc.splitk > 1 ? ws : nullptr;
+    a.y_bytes = static_cast<int>(g.y_elems * 4);
+    a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
+    dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
+    t.kernel<<<grid, dim3(256), 0, st>>>(a);
+    if (int rc = launch_status("conv_igemm_f32")) return rc;
+    if (tc.splitk > 1) {
+        const size_t total = static_cast<size_t>(g.M) * a.Ntot;
+        hipLaunchKernelGGL(splitk_epilogue, dim3(grid_for(total, 256)), dim3(256), 0, st, ws, tc.splitk, g.M, a.Ntot,
+                           a.OHW, bias, res, y, g.act, alpha);
+        if (int rc = launch_status("splitk_epilogue")) return rc;
+    }
+    return 0;
+}
+
+namespace {
+
+std::mutex g_tune_mu;
+std::map<std::string, std::pair<int, int>> g_tuned;  // key -> (cfg, split request)
+
+// Device buffers of one tuning session, freed on scope exit.
+struct TuneBuffers {
+    std::vector<void *> ptrs;
+    void *alloc(size_t bytes) {
+        void *p = nullptr;
+        if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        ptrs.push_back(p);
+        return p;
+    }
+    ~TuneBuffers() {
+        for (void *p : ptrs) (void)hipFree(p);
+    }
+};
+
+// Times every candidate (configuration x split-K) the model does not rule
+// out on scratch buffers of the layer's real shape, and returns the fastest
+// (cfg, split request).  Results are cached per shape for the process, so
+// every context sees the same choice for the same layer.  Returns false
+// when the device could not be used (the caller then trusts the model).
+bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
+    {
+        std::lock_guard<std::mutex> lk(g_tune_mu);
+        auto it = g_tuned.find(gs.key);
+        if (it != g_tuned.end()) {
+            *cfg_out = it->second.first;
+            *split_out = it->second.second;
+            return true;
+        }
+    }
+    const int Ntot = g.N * g.OH * g.OW;
+    struct Cand {
+        int cfg, split;
+        TileCounts tc;
+        double model, t;
+    };
+    std::vector<Cand> cands;
+    double best_model = 1e300;
     for (int c = 0; c < kNumCfgs; c++) {
-        const TileCfg &t = kCfgs[c];
-        const int res = resident_wgs(c);
-        const int mt = (M + t.BM - 1) / t.BM;
-        const int nt = (Ntot + t.BN - 1) / t.BN;
-        const int kt = (K + t.BK - 1) / t.BK;
-        const long tiles = static_cast<long>(mt) * nt;
-        for (int split = 1; split <= 16; split *= 2) {
-            if (split > 1 && kt / split < 2) break;
-            const int kps = (kt + split - 1) / split;
-            const long wgs = tiles * split;
-            const long slots = static_cast<long>(cus) * res;
-            const long rounds = (wgs + slots - 1) / slots;
-            // a CU's matrix cores are shared by the workgroups it runs: one
-            // round costs the work of the busiest CU
-            const long per_cu = std::min<long>(res, (wgs + cus - 1) / cus);
-            double cost = static_cast<double>(rounds) * per_cu * t.BM * t.BN * kps * t.BK / t.eff;
-            if (split > 1) cost += static_cast<double>(M) * Ntot * split * 24.0;  // partials written + re-read
-            if (cost < best * 0.999) {
-                best = cost;
-                best_cfg = c;
-                best_split = split;
+        int last_splitk = -1;
+        for (int split : kSplits) {
+            const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, split);
+            if (tc.splitk == last_splitk) continue;
+            if (split > 1 && tc.kt_per_split < 2) break;
+            last_splitk = tc.splitk;
+            if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
+            const double m = model_us(c, tc, g.M, Ntot);
+            best_model = std::min(best_model, m);
+            cands.push_back({c, split, tc, m, 0.0});
+        }
+    }
+    std::vector<Cand> keep;
+    for (const Cand &cd : cands)
+        if (cd.model <= 3.0 * best_model) keep.push_back(cd);
+    if (keep.empty()) return false;
+
+    TuneBuffers tb;
+    size_t wpack_bytes = 0, ws_bytes = 16;
+    for (const Cand &cd : keep) {
+        const TileCfg &t = kCfgs[cd.cfg];
+        wpack_bytes = std::max(wpack_bytes, static_cast<size_t>(cd.tc.m_tiles) * cd.tc.k_tiles * t.BM * t.BK * 4);
+        ws_bytes = std::max(ws_bytes, partial_bytes_of(cd.tc, g.M, Ntot));
+    }
+    const size_t y_bytes = static_cast<size_t>(g.y_elems) * 4;
+    float *xs = static_cast<float *>(tb.alloc(gs.x_bytes));
+    float *wp = static_cast<float *>(tb.alloc(wpack_bytes));
+    float *y = static_cast<float *>(tb.alloc(y_bytes));
+    float *ws = static_cast<float *>(tb.alloc(ws_bytes));
+    float *bias = g.has_bias ? static_cast<float *>(tb.alloc(static_cast<size_t>(g.M) * 4)) : nullptr;
+    float *res = g.has_res ? static_cast<float *>(tb.alloc(y_bytes)) : nullptr;
+    int *koff[2] = {nullptr, nullptr};  // BK 16, BK 32
+    for (int i = 0; i < 2; i++) {
+        const std::vector<int> kv = build_koff(gs, 16 << i);
+        koff[i] = static_cast<int *>(tb.alloc(kv.size() * sizeof(int)));
+        if (koff[i] && hipMemcpy(koff[i], kv.data(), kv.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+            koff[i] = nullptr;
+    }
+    if (!xs || !wp || !y || !ws || (g.has_bias && !bias) || (g.has_res && !res) || !koff[0] || !koff[1]) return false;
+    // operands of zeros: the timing does not depend on the values
+    (void)hipMemsetAsync(xs, 0, gs.x_bytes, st);
+    (void)hipMemsetAsync(wp, 0, wpack_bytes, st);
+    if (bias) (void)hipMemsetAsync(bias, 0, static_cast<size_t>(g.M) * 4, st);
+    if (res) (void)hipMemsetAsync(res, 0, y_bytes, st);
+
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    auto time_it = [&](const Cand &cd, int reps) -> double {
+        const int *ko = koff[kCfgs[cd.cfg].BK == 16 ? 0 : 1];
+        if (hipEventRecord(e0, st) != hipSuccess) return 1e300;
+        for (int r = 0; r < reps; r++)
+            if (launch_igemm(st, cd.cfg, cd.tc, g, gs.Wp, xs, gs.x_bytes, gs.x_img_stride, wp, ko, bias, res, y, 1.0f,
+                             ws) != 0)
+                return 1e300;
+        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e300;
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e300;
+        return 1e3 * ms / reps;
+    };
+    bool ok = true;
+    for (Cand &cd : keep) {
+        (void)time_it(cd, 1);  // warm-up (first launch of a kernel variant)
+        cd.t = time_it(cd, 1);
+        if (cd.t >= 1e300) ok = false;
+    }
+    std::sort(keep.begin(), keep.end(), [](const Cand &a, const Cand &b) { return a.t < b.t; });
+    const size_t finalists = std::min<size_t>(keep.size(), 4);
+    for (size_t i = 0; i < finalists && ok; i++) {
+        const double t = time_it(keep[i], 3);
+        keep[i].t = std::min(keep[i].t, t);
+    }
+    std::sort(keep.begin(), keep.begin() + finalists, [](const Cand &a, const Cand &b) { return a.t < b.t; });
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (!ok || hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    *cfg_out = keep[0].cfg;
+    *split_out = keep[0].split;
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tuned[gs.key] = {keep[0].cfg, keep[0].split};
+    return true;
+}
+
+// Picks (cfg, split) for a layer: SPKV2_CONV_CFG / SPKV2_CONV_SPLITK force a
+// choice; otherwise the tuner measures unless SPKV2_CONV_TUNE=0, and the
+// model decides when it does not.
+void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
+    const int Ntot = g.N * g.OH * g.OW;
+    int best_cfg = 0, best_split = 1;
+    const char *tune_env = getenv("SPKV2_CONV_TUNE");
+    const bool tune = !(tune_env && tune_env[0] == '0');
+    if (!(tune && tune_tiles(st, g, gs, &best_cfg, &best_split))) {
+        double best = 1e300;
+        for (int c = 0; c < kNumCfgs; c++) {
+            for (int split : kSplits) {
+                const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, split);
+                if (split > 1 && tc.kt_per_split < 2) break;
+                if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
+                const double m = model_us(c, tc, g.M, Ntot);
+                if (m < best * 0.999) {
+                    best = m;
+                    best_cfg = c;
+                    best_split = split;
+                }
             }
         }
     }
@@ -525,7 +763,7 @@ void choose_tiles(int M, int Ntot, int K, int *cfg_out, int *splitk_out) {
         if (sk >= 1 && sk <= 64) best_split = sk;
     }
     *cfg_out = best_cfg;
-    *splitk_out = best_split;
+    *split_out = best_split;
 }
 
 // Packs A[m][k] (row-major, lda = K) into [m_tiles][k_tiles][BM][BK] panels,
@@ -560,37 +798,54 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 }  // namespace
 
-// Tiles, split-K and packed weights for an (M x K) weight matrix on the host.
-static int plan_tiles_and_weights(const ConvGeom &g, int K, const float *w_host, ConvPlan *plan) {
+static TileCounts plan_counts(const ConvPlan *p) {
+    return TileCounts{p->m_tiles, p->n_tiles, p->k_tiles, p->kt_per_split, p->splitk};
+}
+
+static size_t partial_bytes(const ConvPlan *p) {
+    return partial_bytes_of(plan_counts(p), p->g.M, p->g.N * p->g.OH * p->g.OW);
+}
+
+// Chooses tiles and split-K for the layer, packs and uploads its weights and
+// k-offset table.
+static int plan_tiles_and_weights(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, const float *w_host,
+                                  ConvPlan *plan) {
     const int Ntot = g.N * g.OH * g.OW;
     int cfg = 0, split = 1;
-    choose_tiles(g.M, Ntot, K, &cfg, &split);
+    choose_tiles(st, g, gs, &cfg, &split);
     const TileCfg &t = kCfgs[cfg];
+    const TileCounts tc = tile_counts(cfg, g.M, Ntot, gs.K, split);
     plan->path = CONV_IGEMM_F32;
     plan->cfg = cfg;
     plan->BM = t.BM;
     plan->BN = t.BN;
     plan->BK = t.BK;
-    plan->K = K;
-    plan->m_tiles = (g.M + t.BM - 1) / t.BM;
-    plan->n_tiles = (Ntot + t.BN - 1) / t.BN;
-    plan->k_tiles = (K + t.BK - 1) / t.BK;
-    plan->Kpad = plan->k_tiles * t.BK;
-    plan->kt_per_split = (plan->k_tiles + split - 1) / split;
-    plan->splitk = (plan->k_tiles + plan->kt_per_split - 1) / plan->kt_per_split;
-    return upload_packed_f32(w_host, g.M, K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack);
+    plan->K = gs.K;
+    plan->m_tiles = tc.m_tiles;
+    plan->n_tiles = tc.n_tiles;
+    plan->k_tiles = tc.k_tiles;
+    plan->Kpad = tc.k_tiles * t.BK;
+    plan->kt_per_split = tc.kt_per_split;
+    plan->splitk = tc.splitk;
+    if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
+    if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack))
+        return rc;
+    return upload_koff(build_koff(gs, t.BK), &plan->ktab);
 }
 
-static size_t partial_bytes(const ConvPlan *p) {
-    return p->splitk > 1 ? static_cast<size_t>(p->splitk) * p->g.M * p->g.N * p->g.OH * p->g.OW * sizeof(float) : 0;
+static std::string shape_key(const char *kind, const ConvGeom &g, const ConvPlan *p, int x_img_stride) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "%s|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d|%d,%d,%d,%d", kind, g.N, g.C, g.H, g.W,
+             g.M, g.KH, g.KW, g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, p->Hp, p->Wp, x_img_stride, g.has_bias ? 1 : 0,
+             g.has_res ? 1 : 0, g.act);
+    return buf;
 }
 
 // Plans an fp32 implicit GEMM for convolution g (group 1) with weights
 // w_host[M][C*KH*KW].  When some tap falls outside the input, the input is
 // first copied into a zero-padded buffer so the kernel needs no bounds tests.
-int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan) {
+int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvPlan *plan) {
     const int K = g.C * g.KH * g.KW;
-    if (int rc = plan_tiles_and_weights(g, K, w_host, plan)) return rc;
     const int hspan = (g.OH - 1) * g.sh + (g.KH - 1) * g.dh + 1;  // rows the taps touch, from -ph
     const int wspan = (g.OW - 1) * g.sw + (g.KW - 1) * g.dw + 1;
     plan->padded = g.ph > 0 || g.pw > 0 || hspan - g.ph > g.H || wspan - g.pw > g.W;
@@ -601,31 +856,39 @@ int plan_igemm_f32(const ConvGeom &g, const float *w_host, ConvPlan *plan) {
     const int64_t xp_elems = static_cast<int64_t>(g.N) * g.C * plan->Hp * plan->Wp;
     if (xp_elems * 4 >= 0x7fff0000LL) return SPKV2_E_UNSUPPORTED;  // byte offsets are 31-bit
     plan->pad_bytes = plan->padded ? align256(static_cast<size_t>(xp_elems) * 4) : 0;
-    if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
-    plan->workspace = plan->pad_bytes + partial_bytes(plan);
-    // two extra tiles of out-of-range entries: the pipeline prefetches up to
-    // two tiles past the last one
-    std::vector<int> koff(static_cast<size_t>(plan->Kpad + 2 * plan->BK), kOobOffset);
-    for (int k = 0; k < K; k++) {
+    GatherSpec gs;
+    gs.K = K;
+    gs.Wp = plan->Wp;
+    gs.x_bytes = static_cast<int>(xp_elems * 4);
+    gs.x_img_stride = g.C * plan->Hp * plan->Wp;
+    const int Hp = plan->Hp, Wp = plan->Wp;
+    gs.koff = [g, Hp, Wp](int k) {
         const int c = k / (g.KH * g.KW), r = k % (g.KH * g.KW);
         const int kh = r / g.KW, kw = r % g.KW;
-        koff[k] = ((c * plan->Hp + kh * g.dh) * plan->Wp + kw * g.dw) * 4;
-    }
-    return upload_koff(koff, &plan->ktab);
+        return ((c * Hp + kh * g.dh) * Wp + kw * g.dw) * 4;
+    };
+    gs.key = shape_key("conv", g, plan, gs.x_img_stride);
+    if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
+    plan->workspace = plan->pad_bytes + partial_bytes(plan);
+    return 0;
 }
 
-// Plans the implicit GEMM of a Gemm node: B source is A [rows][K]
-// (k_stride 1) or, with trans_a, [K][rows] (k_stride rows).
-int plan_igemm_gemm(const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan) {
-    const int K = g.C;
-    if (int rc = plan_tiles_and_weights(g, K, w_host, plan)) return rc;
+// Plans the implicit GEMM of a Gemm node: the B source is A [rows][K]
+// (k_stride 1, rows K apart) or, with trans_a, [K][rows] (k_stride rows,
+// rows 1 apart).
+int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan) {
     plan->padded = false;
     plan->Hp = plan->Wp = 1;
-    if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
+    GatherSpec gs;
+    gs.K = g.C;
+    gs.Wp = 1;
+    gs.x_bytes = static_cast<int>(g.x_elems * 4);
+    gs.x_img_stride = k_stride == 1 ? g.C : 1;
+    gs.koff = [k_stride](int k) { return k * k_stride * 4; };
+    gs.key = shape_key(k_stride == 1 ? "gemm" : "gemm_ta", g, plan, gs.x_img_stride);
+    if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = partial_bytes(plan);
-    std::vector<int> koff(static_cast<size_t>(plan->Kpad + 2 * plan->BK), kOobOffset);
-    for (int k = 0; k < K; k++) koff[k] = k * k_stride * 4;
-    return upload_koff(koff, &plan->ktab);
+    return 0;
 }
 
 std::string igemm_name(const ConvPlan *p) {
@@ -638,52 +901,23 @@ std::string igemm_name(const ConvPlan *p) {
 static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res,
                           float *y, float alpha, int x_img_stride) {
     const ConvGeom &g = p->g;
-    const TileCfg &t = kCfgs[p->cfg];
     if (ctx->workspace_size < p->workspace) return SPKV2_E_UNSUPPORTED;
-    IgemmArgs a{};
-    a.x = x;
-    a.x_bytes = static_cast<int>(g.x_elems * 4);
-    a.x_img_stride = x_img_stride;
+    const float *xs = x;
+    int x_bytes = static_cast<int>(g.x_elems * 4);
     if (p->padded) {
         float *xp = reinterpret_cast<float *>(ctx->workspace);
         const unsigned planes = static_cast<unsigned>(g.N * g.C);
         hipLaunchKernelGGL(pad_nchw, dim3(planes), dim3(256), 0, ctx->stream, x, xp, g.H, g.W, p->Hp, p->Wp, p->pt,
                            p->pl);
         if (int rc = launch_status("pad_nchw")) return rc;
-        a.x = xp;
-        a.x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);
-        a.x_img_stride = g.C * p->Hp * p->Wp;
+        xs = xp;
+        x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);
+        x_img_stride = g.C * p->Hp * p->Wp;
     }
-    a.wp = static_cast<const float *>(p->wpack);
-    a.koff = static_cast<const int *>(p->ktab);
-    a.bias = bias;
-    a.res = res;
-    a.y = y;
-    a.Wp = p->Wp;
-    a.M = g.M;
-    a.OW = g.OW;
-    a.OHW = g.OH * g.OW;
-    a.Ntot = g.N * a.OHW;
-    a.sh = g.sh;
-    a.sw = g.sw;
-    a.m_tiles = p->m_tiles;
-    a.k_tiles = p->k_tiles;
-    a.kt_per_split = p->kt_per_split;
-    a.act = g.act;
-    a.alpha = alpha;
-    a.ws = p->splitk > 1 ? reinterpret_cast<float *>(ctx->workspace + p->pad_bytes) : nullptr;
-    a.y_bytes = static_cast<int>(g.y_elems * 4);
-    a.ws_bytes = static_cast<int>(partial_bytes(p));
-    dim3 grid(static_cast<unsigned>(p->m_tiles * p->n_tiles), static_cast<unsigned>(p->splitk));
-    t.kernel<<<grid, dim3(256), 0, ctx->stream>>>(a);
-    if (int rc = launch_status("conv_igemm_f32")) return rc;
-    if (p->splitk > 1) {
-        const size_t total = static_cast<size_t>(g.M) * a.Ntot;
-        hipLaunchKernelGGL(splitk_epilogue, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, a.ws, p->splitk,
-                           g.M, a.Ntot, a.OHW, bias, res, y, g.act, alpha);
-        if (int rc = launch_status("splitk_epilogue")) return rc;
-    }
-    return 0;
+    float *ws = reinterpret_cast<float *>(ctx->workspace + p->pad_bytes);
+    return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
+                        static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res, y, alpha,
+                        ws);
 }
 
 int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res, float *y,
@@ -750,7 +984,7 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
         if (!w) {
             rc = SPKV2_E_UNSUPPORTED;  // weights produced at run time
         } else {
-            rc = plan_igemm_f32(g, w, plan);
+            rc = plan_igemm_f32(ctx->stream, g, w, plan);
             if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan));
         }
     } else {

@@ -19,7 +19,7 @@
 
 namespace spk::kern {
 
-int plan_igemm_gemm(const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan);
+int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int k_stride, ConvPlan *plan);
 int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res, float *y,
                   float alpha);
 std::string igemm_name(const ConvPlan *p);
@@ -126,7 +126,7 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     g.x_elems = static_cast<int64_t>(gp->rows) * gp->K;
     g.y_elems = static_cast<int64_t>(gp->rows) * gp->Nout;
     gp->conv.g = g;
-    if (int rc = plan_igemm_gemm(g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
+    if (int rc = plan_igemm_gemm(ctx->stream, g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
     set_kernel_name(ctx, node, "gemm:" + igemm_name(&gp->conv));
     *ws = gp->conv.workspace;
     return 0;
