@@ -144,6 +144,7 @@ def main() -> None:
     ap.add_argument("--b1-steps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
+    ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
     args = ap.parse_args()
@@ -202,14 +203,16 @@ def main() -> None:
     logits = m.get_output(0).reshape(args.batch, -1)
     # host-buffer interface (spkv2_set_input / spkv2_get_output copy over PCIe
     # each step): reported beside, never as, the value
-    pcie_steps = max(1, min(args.steps, 5))
-    t0 = time.perf_counter()
-    for _ in range(pcie_steps):
-        m.set_input(0, x)
-        m.run()
-        m.get_output(0)
-    pcie_ips = args.batch * pcie_steps / (time.perf_counter() - t0)
-    m.bind_input(0, xin)
+    pcie_ips = None
+    if not args.no_host_io:
+        pcie_steps = max(1, min(args.steps, 5))
+        t0 = time.perf_counter()
+        for _ in range(pcie_steps):
+            m.set_input(0, x)
+            m.run()
+            m.get_output(0)
+        pcie_ips = args.batch * pcie_steps / (time.perf_counter() - t0)
+        m.bind_input(0, xin)
     conv_ms = 0.0
     node_ms = {}
     for nid in range(len(g.nodes)):

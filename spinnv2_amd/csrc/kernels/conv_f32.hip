@@ -600,6 +600,38 @@ namespace {
 
 std::mutex g_tune_mu;
 std::map<std::string, std::pair<int, int>> g_tuned;  // key -> (cfg, split request)
+bool g_tune_db_loaded = false;
+
+// SPKV2_TUNE_DB names a text file of "key cfg split" lines: read once, and
+// every newly tuned shape is appended, so later processes reuse the
+// choices (same configuration, same results) without timing again.
+const char *tune_db_path() {
+    const char *p = getenv("SPKV2_TUNE_DB");
+    return p && p[0] ? p : nullptr;
+}
+
+void load_tune_db_locked() {
+    if (g_tune_db_loaded) return;
+    g_tune_db_loaded = true;
+    const char *path = tune_db_path();
+    if (!path) return;
+    FILE *f = fopen(path, "r");
+    if (!f) return;
+    char key[512];
+    int cfg = 0, split = 0;
+    while (fscanf(f, "%511s %d %d", key, &cfg, &split) == 3)
+        if (cfg >= 0 && cfg < kNumCfgs && split >= 1 && split <= 64) g_tuned[key] = {cfg, split};
+    fclose(f);
+}
+
+void store_tune_db_locked(const std::string &key, int cfg, int split) {
+    const char *path = tune_db_path();
+    if (!path) return;
+    if (FILE *f = fopen(path, "a")) {
+        fprintf(f, "%s %d %d\n", key.c_str(), cfg, split);
+        fclose(f);
+    }
+}
 
 // Device buffers of one tuning session, freed on scope exit.
 struct TuneBuffers {
@@ -626,6 +658,7 @@ struct TuneBuffers {
 bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
     {
         std::lock_guard<std::mutex> lk(g_tune_mu);
+        load_tune_db_locked();
         auto it = g_tuned.find(gs.key);
         if (it != g_tuned.end()) {
             *cfg_out = it->second.first;
@@ -727,6 +760,7 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     *split_out = keep[0].split;
     std::lock_guard<std::mutex> lk(g_tune_mu);
     g_tuned[gs.key] = {keep[0].cfg, keep[0].split};
+    store_tune_db_locked(gs.key, keep[0].cfg, keep[0].split);
     return true;
 }
 

@@ -20,9 +20,8 @@ from collections import defaultdict
 
 
 def short_name(name: str) -> str:
-    name = re.sub(r"\(.*\)$", "", name)
     name = name.replace("spk::kern::", "").replace("(anonymous namespace)::", "").replace("void ", "")
-    return name
+    return re.sub(r"\(.*\)$", "", name)
 
 
 def stats(path: str, runs: int) -> str:
