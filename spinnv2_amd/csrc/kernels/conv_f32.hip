@@ -350,25 +350,44 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     }
 }
 
-// Sums split-K partials in slice order, then applies the epilogue.
+// Sums split-K partials in slice order, then applies the epilogue.  Each
+// thread owns VEC consecutive columns of one row (VEC = 4 when N is a
+// multiple of 4: 16-byte loads); up to eight slices' loads are in flight
+// before the first add, and the adds stay in slice order.
+template <int VEC>
 __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__ ws, int splitk, int M, int Ntot,
                                                        int OHW, const float *__restrict__ bias,
                                                        const float *__restrict__ res, float *__restrict__ y, int act,
                                                        float alpha) {
+    typedef float vec_t __attribute__((ext_vector_type(VEC)));
     const size_t total = static_cast<size_t>(M) * Ntot;
-    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
-         idx += static_cast<size_t>(gridDim.x) * 256) {
+    const size_t groups = total / VEC;
+    for (size_t gi = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; gi < groups;
+         gi += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t idx = gi * VEC;
         const int m = static_cast<int>(idx / Ntot);
         const int n = static_cast<int>(idx - static_cast<size_t>(m) * Ntot);
-        float v = 0.0f;
-        for (int s = 0; s < splitk; s++) v += ws[s * total + idx];
-        v = alpha * v;
-        if (bias) v += bias[m];
-        const int img = n / OHW;
-        const int sp = n - img * OHW;
-        const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
-        if (res) v += res[yi];
-        y[yi] = apply_act(v, act);
+        vec_t v = 0.0f;
+        int s = 0;
+        for (; s + 8 <= splitk; s += 8) {
+            vec_t p[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
+#pragma unroll
+            for (int t = 0; t < 8; t++) v += p[t];
+        }
+        for (; s < splitk; s++) v += *reinterpret_cast<const vec_t *>(ws + s * total + idx);
+        const float bm = bias ? bias[m] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            float o = alpha * v[e];
+            if (bias) o += bm;
+            const int img = (n + e) / OHW;
+            const int sp = n + e - img * OHW;
+            const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
+            if (res) o += res[yi];
+            y[yi] = apply_act(o, act);
+        }
     }
 }
 
@@ -589,8 +608,12 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.Ntot;
-        hipLaunchKernelGGL(splitk_epilogue, dim3(grid_for(total, 256)), dim3(256), 0, st, ws, tc.splitk, g.M, a.Ntot,
-                           a.OHW, bias, res, y, g.act, alpha);
+        if (a.Ntot % 4 == 0)
+            hipLaunchKernelGGL(splitk_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, ws, tc.splitk,
+                               g.M, a.Ntot, a.OHW, bias, res, y, g.act, alpha);
+        else
+            hipLaunchKernelGGL(splitk_epilogue<1>, dim3(grid_for(total, 256)), dim3(256), 0, st, ws, tc.splitk, g.M,
+                               a.Ntot, a.OHW, bias, res, y, g.act, alpha);
         if (int rc = launch_status("splitk_epilogue")) return rc;
     }
     return 0;

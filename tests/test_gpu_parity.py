@@ -199,3 +199,44 @@ def test_graph_mode_matches_eager(gpu):
             m.set_input(0, xs[0])
             m.run()
             np.testing.assert_array_equal(m.get_output(0), eager)
+
+
+# Every tile configuration, with and without split-K (the last slice of a
+# tile to finish sums the partials in slice order inside the conv kernel),
+# on a ragged residual conv; forced through the tuning overrides.
+SPLIT_CASES = [(cfg, split) for cfg in range(8) for split in (1, 3, 8)]
+
+
+@pytest.mark.parametrize("cfg,split", SPLIT_CASES, ids=[f"cfg{c}_split{s}" for c, s in SPLIT_CASES])
+def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    monkeypatch.setenv("SPKV2_CONV_SPLITK", str(split))
+    g = models.single_conv(2, 72, 11, 13, 150, 3, 1, 1, act="Relu", residual=True)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
+    """Split-K counters re-arm themselves, so replays of a captured graph
+    (no memset nodes) give the eager result every time."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_SPLITK", "6")
+    g = models.single_conv(1, 256, 14, 14, 256, 3, 1, 1, act="Relu")
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        eager = m.get_output(0)
+        assert "splitk=6" in m.kernel_name(0)
+        m.set_graph_mode(True)
+        for i in range(4):
+            m.set_input(0, xs[0])
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0), eager)
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(eager, want) <= FP32_TOL
