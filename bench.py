@@ -35,6 +35,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
+INT8_MFMA_PEAK_TOPS = 5000.0
 
 
 def log(msg: str) -> None:
@@ -134,6 +135,84 @@ def batch1_latency(depth: int, steps: int, lib) -> float:
     return b1_ms
 
 
+def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64) -> dict:
+    """INT8 ResNet-50: per-channel symmetric int8
+    weights, per-tensor activation scales calibrated on 16 seeded single-image
+    batches with the repo's fp32 forward, int32 accumulation, reference
+    dequantization.  Returns images/s at `batch`, batch-1 latency, and the
+    int8 conv throughput (conv node device time: quantize pass + int8 GEMM +
+    epilogue) against the int8 MFMA peak."""
+    from spinnv2_amd.runtime import DeviceBuffer, Model
+    from spinnv2_amd.spk import models, write_spk
+    from spinnv2_amd.spk.quantize import calibrate_activation_scales, quantize_conv_weights
+
+    t0 = time.time()
+    g1 = models.resnet(50, 1)
+    samples = [models.make_input(g1.tensors[g1.inputs[0]].shape, 1000 + i) for i in range(16)]
+    act = calibrate_activation_scales(g1, samples)
+    log(f"int8: calibrated {len(act)} activation scales on 16 batches in {time.time() - t0:.1f}s")
+
+    def build(b):
+        g = models.resnet(50, b)
+        wq = quantize_conv_weights(g)
+        return g, write_spk(g, "mi355x", quant_params=wq + act)
+
+    g, blob = build(batch)
+    ops = {}
+    for n in g.nodes:
+        if n.op_type == "Conv":
+            y = g.shape(n.outputs[0])
+            w = g.tensors[n.inputs[1]].shape
+            ops[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
+    x = models.make_input(g.tensors[g.inputs[0]].shape)
+    m = Model(blob, lib=lib)
+    xin = DeviceBuffer(x.nbytes, lib)
+    xin.upload(x)
+    m.bind_input(0, xin)
+    m.set_profiling(True)
+    for _ in range(warmup):
+        m.run()
+    m.reset_node_times()
+    lib.spkv2_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.run()
+    lib.spkv2_device_synchronize()
+    elapsed = time.perf_counter() - t0
+    conv_ms = 0.0
+    for nid in ops:
+        ms, cnt = m.node_time(nid)
+        conv_ms += ms / max(cnt, 1)
+    names = sorted({m.kernel_name(nid).split("<")[0] for nid in ops})
+    m.close()
+    xin.free()
+    tops = sum(ops.values()) / (conv_ms * 1e-3) / 1e12
+    out = {"workload": "resnet50_int8_224", "batch": batch, "images_per_sec": batch * steps / elapsed,
+           "ms_per_step": elapsed * 1e3 / steps, "conv_ms_per_step": conv_ms,
+           "conv_gop_per_image": sum(ops.values()) / batch / 1e9, "conv_kernels": names,
+           "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                        "frac": tops / INT8_MFMA_PEAK_TOPS}}
+    if b1_steps > 0:
+        g1q, blob1 = build(1)
+        m1 = Model(blob1, lib=lib)
+        x1 = models.make_input(g1q.tensors[g1q.inputs[0]].shape)
+        b1 = DeviceBuffer(x1.nbytes, lib)
+        b1.upload(x1)
+        m1.bind_input(0, b1)
+        m1.set_graph_mode(True)
+        for _ in range(5):
+            m1.run()
+        lib.spkv2_device_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(b1_steps):
+            m1.run()
+        lib.spkv2_device_synchronize()
+        out["b1_ms_per_image"] = (time.perf_counter() - t0) * 1e3 / b1_steps
+        m1.close()
+        b1.free()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -145,6 +224,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
     ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
+    ap.add_argument("--no-int8", action="store_true", help="skip the INT8 ResNet-50 section")
+    ap.add_argument("--int8-only", action="store_true", help="run only the INT8 ResNet-50 section")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
     args = ap.parse_args()
@@ -160,6 +241,9 @@ def main() -> None:
     from spinnv2_amd.spk import models, write_spk
 
     lib = load_library()
+    if args.int8_only:
+        print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps)), flush=True)
+        return
     base = None if args.no_cpu_baseline else cpu_baseline()
 
     # ---------------------------------------------------------- batch B
@@ -236,6 +320,8 @@ def main() -> None:
     # ---------------------------------------------------------- batch 1
     b1_ms = batch1_latency(args.depth, args.b1_steps, lib) if args.b1_steps > 0 else None
 
+    int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps)
+
     result = {
         "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
         "value": args.batch * args.steps / elapsed,
@@ -265,6 +351,7 @@ def main() -> None:
                      "algorithmic_bytes": conv_alg_bytes,
                      "kernel": "conv_igemm_f32 (all conv nodes; HIP events per node on the run stream)"},
         "cpu_baseline": base,
+        "int8": int8,
         "top1_image0": int(logits[0].argmax()),
     }
     print(json.dumps(result), flush=True)

@@ -1,26 +1,39 @@
 // INT8 convolution on MI355X with the reference runtime's semantics
 // (runtime/kernels/optimized/conv/conv_int8.c:22-210):
 //   per image, xq = sat8(round(x * (1/s_x))), rounding half to even for the
-//   first floor(C*H*W/16)*16 elements and half away from zero for the tail;
-//   padded taps are int8 zero;
+//   first floor(C*H*W/16)*16 elements (NCHW order) and half away from zero
+//   for the tail; padded taps are int8 zero;
 //   acc[m][n] = sum_k wq[m][k] * xq[k][n]   (int32, exact);
 //   y = act( fma((float)acc, s_w[m]*s_x, bias[m]) + residual ).
 // Inputs and outputs stay fp32 NCHW; weights are int8 OIHW with per-output-
 // channel scales, the activation scale is per tensor (quantization section).
 //
 // Device plan:
-//   1. quantize_nhwc: one HBM pass reads x (NCHW fp32) and writes xq as
-//      NHWC int8 into the runtime workspace, so the 16 channels of one tap
-//      are one 16-byte load;
-//   2. conv_igemm_i8: implicit GEMM with K ordered (kh, kw, c), weights
-//      repacked at prepare to match, v_mfma_i32_32x32x32_i8 on LDS tiles
-//      stored k-contiguous, dequantize/bias/residual/activation in registers.
-//      Split-K writes int32 partials that a second kernel sums (exactly) and
-//      dequantizes.
+//   1. quantize_pad_nhwc: one HBM pass reads x (NCHW fp32) and writes xq as
+//      zero-padded NHWC int8 ([N][Hp][Wp][Cp], halo and padded channels 0)
+//      into the runtime workspace, so every tap of the convolution is in
+//      bounds and 16 consecutive k are 16 contiguous bytes;
+//   2. conv_igemm_i8<BM,BN,BK>: implicit GEMM.  K is a sequence of 16-byte
+//      groups: with dilation 1 the KW*Cp bytes of one kernel row form one
+//      contiguous run (pixels iw..iw+KW-1), padded to a multiple of 16 with
+//      zero weights; otherwise each (kh, kw) tap is Cp/16 groups.  Group g of
+//      output column n sits at byte col(n) + koff[g] of xq: one
+//      buffer_load_dwordx4 with (voffset, soffset) = (col(n), koff[g]).
+//      Weights are repacked at prepare into [m_tile][k_tile][BM][BK] panels
+//      in the same k order.  v_mfma_i32_32x32x32_i8 on LDS tiles stored
+//      k-contiguous, two-tile register prefetch, dequantize / bias /
+//      residual / activation in registers with buffer stores.
+//   3. split-K (small grids): int32 partials summed by a second kernel.
 // Integer sums are order independent, so the accumulators equal the closed
-// form bit for bit whatever the tiling.
+// form bit for bit whatever the tiling or split.
+#include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
 #include <vector>
 
 #include "conv.hpp"
@@ -30,29 +43,40 @@ namespace spk::kern {
 
 namespace {
 
-constexpr int I8_BM = 128, I8_BN = 128, I8_BK = 64;
-constexpr int I8_LDK = I8_BK + 16;  // bytes per LDS row (80: conflict-free b128 reads)
+// gfx9 buffer resource word 3 (raw, untyped); loads at or beyond num_records
+// return 0, stores there are dropped
+constexpr int kBufWord3 = 0x00020000;
+// byte offset out of range for every buffer (all < 2 GiB)
+constexpr int kOob = 0x7fff0000;
 
-// xq[img][h][w][c] = q(x[img][c][h][w]); 64 pixels x 32 channels per block,
-// transposed through LDS so both sides are coalesced.
-__global__ void __launch_bounds__(256) quantize_nhwc(const float *__restrict__ x, int8_t *__restrict__ xq, int C,
-                                                     int HW, float inv_scale, int split) {
-    __shared__ int8_t tile[32][64 + 4];
+// xq[img][hp][wp][c] = q(x[img][c][hp-pt][wp-pl]) inside the image and for
+// c < C, 0 elsewhere.  A block covers 64 padded pixels x 64 channels,
+// transposed through LDS so reads (along w) and writes (along c) are both
+// contiguous.
+__global__ void __launch_bounds__(256) quantize_pad_nhwc(const float *__restrict__ x, int8_t *__restrict__ xq, int C,
+                                                         int H, int W, int Hp, int Wp, int Cp, int pt, int pl,
+                                                         float inv_scale, int split) {
+    __shared__ int8_t tile[64][64 + 4];
     const int img = blockIdx.z;
     const int p0 = blockIdx.x * 64;
-    const int c0 = blockIdx.y * 32;
+    const int c0 = blockIdx.y * 64;
+    const int HW = H * W;
+    const int HWp = Hp * Wp;
     const float *xi = x + static_cast<size_t>(img) * C * HW;
     const int tp = threadIdx.x & 63;
-    const int tc = threadIdx.x >> 6;  // 0..3
-    for (int cc = tc; cc < 32; cc += 4) {
+    const int pp = p0 + tp;
+    const int hp = pp / Wp;
+    const int h = hp - pt, w = pp - hp * Wp - pl;
+    const bool inside = pp < HWp && static_cast<unsigned>(h) < static_cast<unsigned>(H) &&
+                        static_cast<unsigned>(w) < static_cast<unsigned>(W);
+    for (int cc = threadIdx.x >> 6; cc < 64; cc += 4) {
         const int c = c0 + cc;
-        const int p = p0 + tp;
         int8_t q = 0;
-        if (c < C && p < HW) {
-            const int idx = c * HW + p;
+        if (inside && c < C) {
+            const int idx = c * HW + h * W + w;  // NCHW index inside the image
             const float v = xi[idx] * inv_scale;
             float r;
-            if (v != v) r = 0.0f;
+            if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
             else r = idx < split ? rintf(v) : roundf(v);
             r = fminf(fmaxf(r, -128.0f), 127.0f);
             q = static_cast<int8_t>(static_cast<int>(r));
@@ -60,37 +84,46 @@ __global__ void __launch_bounds__(256) quantize_nhwc(const float *__restrict__ x
         tile[cc][tp] = q;
     }
     __syncthreads();
-    // write: each thread one pixel row segment of 8 channels
-    const int wp = threadIdx.x >> 2;   // pixel 0..63
-    const int wc = (threadIdx.x & 3) * 8;  // channel chunk
-    const int p = p0 + wp;
-    if (p < HW) {
-        int8_t *dst = xq + (static_cast<size_t>(img) * HW + p) * C + c0 + wc;
-        for (int k = 0; k < 8; k++)
-            if (c0 + wc + k < C) dst[k] = tile[wc + k][wp];
+    // each thread writes 16 channels (four dwords) of one pixel
+    const int wpix = threadIdx.x >> 2;
+    const int wc = (threadIdx.x & 3) * 16;
+    const int p = p0 + wpix;
+    if (p >= HWp || c0 + wc >= Cp) return;
+    uint32_t *dst = reinterpret_cast<uint32_t *>(xq + (static_cast<size_t>(img) * HWp + p) * Cp + c0 + wc);
+    const int ndw = min(4, (Cp - c0 - wc) / 4);
+    for (int d = 0; d < ndw; d++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++) word |= static_cast<uint32_t>(static_cast<uint8_t>(tile[wc + 4 * d + b][wpix])) << (8 * b);
+        dst[d] = word;
     }
 }
 
 struct I8Args {
-    const int8_t *__restrict__ xq;      // NHWC int8
+    const int8_t *__restrict__ xq;      // padded NHWC int8
     const int8_t *__restrict__ wp;      // [m_tiles][k_tiles][BM][BK]
-    const int2 *__restrict__ ktab;      // per 16-k group (vec) or per k (bytes)
+    const int *__restrict__ koff;       // byte offset of each 16-byte k group; kOob past K
     const float *__restrict__ scales;   // [M] s_w[m]*s_x
     const float *__restrict__ bias;
     const float *__restrict__ res;
     float *__restrict__ y;
-    int32_t *__restrict__ ws;           // split-K partials or raw accumulator output
-    int H, W, C, M, OW, OHW, Ntot;
-    int sh, sw, ph, pw;
+    int32_t *__restrict__ ws;           // split-K partials [split][M][Ntot], or raw accumulators (NCHW)
+    int x_bytes, y_bytes, ws_bytes;
+    int img_stride;                     // bytes per padded image
+    int Wp, Cp, M, OW, OHW, Ntot;
+    int sh, sw;
     int m_tiles, k_tiles, kt_per_split;
     int act;
     int mode;  // 0: dequant epilogue, 1: int32 partials to ws[split][M][Ntot], 2: raw acc to ws as NCHW
 };
 
-template <bool VEC>
+template <int BM, int BN, int BK>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
-    constexpr int BM = I8_BM, BN = I8_BN, BK = I8_BK, LDK = I8_LDK;
-    constexpr int TM = 2, TN = 2;  // 2x2 waves, 64x64 each
+    constexpr int TM = BM / 64, TN = BN / 64;  // 2x2 waves, each (32*TM) x (32*TN)
+    constexpr int LDK = BK + 16;               // bytes per LDS row
+    constexpr int GPT = BK * BN / 4096;        // 16-byte B groups per thread per k-tile
+    constexpr int APT = BM * BK / 4096;        // 16-byte A chunks per thread per k-tile
+    static_assert(TM >= 1 && TN >= 1 && GPT >= 1 && APT >= 1 && BK % 32 == 0, "tile shape");
     __shared__ __attribute__((aligned(16))) int8_t As[2][BM * LDK];
     __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * LDK];
 
@@ -99,18 +132,22 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
+    // consecutive workgroups land on different XCDs: give each XCD a
+    // contiguous range of tiles, m fastest, so tiles sharing an activation
+    // panel share that XCD's L2
     int bid = blockIdx.x;
     const int nb = gridDim.x;
     if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
     const int mt = bid % a.m_tiles;
     const int nt = bid / a.m_tiles;
-    const int kt_begin = blockIdx.y * a.kt_per_split;
-    const int kt_end = min(kt_begin + a.kt_per_split, a.k_tiles);
+    const int kt0 = blockIdx.y * a.kt_per_split;
+    const int kt1 = min(kt0 + a.kt_per_split, a.k_tiles);
 
-    // B: column bcol, 32 consecutive k of the tile (two 16-byte groups)
-    const int bcol = tid & (BN - 1);
-    const int bhalf = __builtin_amdgcn_readfirstlane(tid >> 7);  // waves 0,1 -> 0; 2,3 -> 1
-    int ih0 = -0x40000000, iw0 = 0, col_off = 0;
+    const int bcol = tid % BN;
+    const int bgrp = __builtin_amdgcn_readfirstlane(tid / BN);  // wave-uniform: BN >= 64
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(a.xq), static_cast<short>(0), a.x_bytes, kBufWord3);
+    int col = kOob;
     {
         const int n = nt * BN + bcol;
         if (n < a.Ntot) {
@@ -118,66 +155,59 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             const int sp = n - img * a.OHW;
             const int oh = sp / a.OW;
             const int ow = sp - oh * a.OW;
-            ih0 = oh * a.sh - a.ph;
-            iw0 = ow * a.sw - a.pw;
-            col_off = ((img * a.H + ih0) * a.W + iw0) * a.C;
+            col = img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
         }
     }
 
-    // native vector types: arrays of HIP's int4 class stay in scratch memory
-    intx4 areg[2];
-    intx4 breg[2];
+    intx4 ar0[APT], ar1[APT], br0[GPT], br1[GPT];
 
-    auto load_tile = [&](int kt) {
-        const intx4 *src = reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt) * (BM * BK));
-        areg[0] = src[tid];
-        areg[1] = src[tid + 256];
-        const int kbase = kt * BK + bhalf * 32;
-        if constexpr (VEC) {
-#pragma unroll
-            for (int g = 0; g < 2; g++) {
-                const int2 e = a.ktab[(kbase >> 4) + g];
-                const int ih = ih0 + (e.y >> 16);
-                const int iw = iw0 + (e.y & 0xffff);
-                const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
-                                static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
-                const intx4 v = *reinterpret_cast<const intx4 *>(a.xq + (ok ? col_off + e.x : 0));
-                breg[g] = ok ? v : intx4{0, 0, 0, 0};
-            }
-        } else {
-            uint32_t words[8];
-#pragma unroll
-            for (int w = 0; w < 8; w++) {
-                uint32_t packed = 0;
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int2 e = a.ktab[kbase + w * 4 + b];
-                    const int ih = ih0 + (e.y >> 16);
-                    const int iw = iw0 + (e.y & 0xffff);
-                    const bool ok = static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
-                                    static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
-                    const int8_t v = a.xq[ok ? col_off + e.x : 0];
-                    packed |= static_cast<uint32_t>(static_cast<uint8_t>(ok ? v : 0)) << (8 * b);
-                }
-                words[w] = packed;
-            }
-            breg[0] = intx4{static_cast<int>(words[0]), static_cast<int>(words[1]), static_cast<int>(words[2]),
-                            static_cast<int>(words[3])};
-            breg[1] = intx4{static_cast<int>(words[4]), static_cast<int>(words[5]), static_cast<int>(words[6]),
-                            static_cast<int>(words[7])};
-        }
-    };
+#define I8_LOAD_TILE(KT, AR, BR)                                                                                     \
+    {                                                                                                                \
+        const int kt_ = min((KT), a.k_tiles - 1);                                                                    \
+        const intx4 *src =                                                                                           \
+            reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt_) * (BM * BK));        \
+        _Pragma("unroll") for (int i = 0; i < APT; i++) AR[i] = src[tid + i * 256];                                  \
+        /* the table has two tiles of out-of-range entries past the last */                                       \
+        const int *ko = a.koff + (KT) * (BK / 16) + bgrp * GPT;                                                      \
+        _Pragma("unroll") for (int g = 0; g < GPT; g++) BR[g] =                                                      \
+            __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, col, ko[g], 0));                    \
+    }
 
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int f = (tid + i * 256) * 16;  // byte index within the BM x BK tile
-            *reinterpret_cast<intx4 *>(&As[buf][(f / BK) * LDK + (f % BK)]) = areg[i];
-        }
-        *reinterpret_cast<intx4 *>(&Bs[buf][bcol * LDK + bhalf * 32]) = breg[0];
-        *reinterpret_cast<intx4 *>(&Bs[buf][bcol * LDK + bhalf * 32 + 16]) = breg[1];
-    };
+#define I8_STORE_TILE(BUF, AR, BR)                                                                                   \
+    {                                                                                                                \
+        _Pragma("unroll") for (int i = 0; i < APT; i++) {                                                            \
+            const int f = (tid + i * 256) * 16;                                                                      \
+            *reinterpret_cast<intx4 *>(&As[BUF][(f / BK) * LDK + (f % BK)]) = AR[i];                                 \
+        }                                                                                                             \
+        _Pragma("unroll") for (int g = 0; g < GPT; g++) * reinterpret_cast<intx4 *>(                                 \
+            &Bs[BUF][bcol * LDK + (bgrp * GPT + g) * 16]) = BR[g];                                                   \
+    }
 
+#define I8_COMPUTE(BUF)                                                                                              \
+    _Pragma("unroll") for (int k32 = 0; k32 < BK / 32; k32++) {                                                      \
+        intx4 af[TM], bf[TN];                                                                                        \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) af[i] =                                                       \
+            *reinterpret_cast<const intx4 *>(&As[BUF][((wm * TM + i) * 32 + row) * LDK + k32 * 32 + khalf]);         \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) bf[j] =                                                       \
+            *reinterpret_cast<const intx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + k32 * 32 + khalf]);         \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =    \
+            __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);                                 \
+    }
+
+    // one pipeline step: tile KT in LDS buffer BUF, tile KT+1 in flight in
+    // (AN, BNX), the free register set (AF, BF) receives tile KT+2
+#define I8_STEP(KT, BUF, AN, BNX, AF, BF)                                                                            \
+    {                                                                                                                \
+        I8_LOAD_TILE((KT) + 2, AF, BF);                                                                              \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8_COMPUTE(BUF);                                                                                             \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8_STORE_TILE((BUF) ^ 1, AN, BNX);                                                                           \
+        __syncthreads();                                                                                             \
+    }
+
+    const int row = lane & 31;
+    const int khalf = 16 * (lane >> 5);  // lanes 32-63 supply bytes 16..31 of each 32-k step
     intx16 acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -186,90 +216,488 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
-    const int row = lane & 31;
-    const int khalf = 16 * (lane >> 5);
-    if (kt_begin < kt_end) {
-        load_tile(kt_begin);
-        store_tile(0);
-        __syncthreads();
-        for (int kt = kt_begin; kt < kt_end; kt++) {
-            const int cur = (kt - kt_begin) & 1;
-            if (kt + 1 < kt_end) load_tile(kt + 1);
-#pragma unroll
-            for (int k32 = 0; k32 < BK / 32; k32++) {
-                intx4 af[TM], bf[TN];
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-                    af[i] = *reinterpret_cast<const intx4 *>(&As[cur][((wm * TM + i) * 32 + row) * LDK + k32 * 32 + khalf]);
-#pragma unroll
-                for (int j = 0; j < TN; j++)
-                    bf[j] = *reinterpret_cast<const intx4 *>(&Bs[cur][((wn * TN + j) * 32 + row) * LDK + k32 * 32 + khalf]);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-            }
-            if (kt + 1 < kt_end) store_tile(cur ^ 1);
-            __syncthreads();
-        }
+    if (kt0 >= kt1) return;  // empty split-K slice
+    I8_LOAD_TILE(kt0, ar0, br0);
+    I8_LOAD_TILE(kt0 + 1, ar1, br1);
+    I8_STORE_TILE(0, ar0, br0);
+    __syncthreads();
+    int kt = kt0;
+    // tiles past kt1 are loaded and ignored: no data-dependent branches
+    for (; kt + 1 < kt1; kt += 2) {
+        I8_STEP(kt, 0, ar1, br1, ar0, br0);
+        I8_STEP(kt + 1, 1, ar0, br0, ar1, br1);
     }
+    if (kt < kt1) {
+        I8_COMPUTE(0);
+    }
+#undef I8_STEP
+#undef I8_COMPUTE
+#undef I8_LOAD_TILE
+#undef I8_STORE_TILE
 
-    const int rsub = 4 * (lane >> 5);
+    // 32x32 accumulator layout: lane holds column (lane & 31) and rows
+    // 8*(r/4) + 4*(lane/32) + (r%4).  Offsets are unsigned bytes; rows past
+    // M and columns past N get out-of-range offsets (stores dropped).
+    const unsigned M = a.M;
+    const unsigned rsub = 4 * (lane >> 5);
+    unsigned mrow[TM];
+#pragma unroll
+    for (int i = 0; i < TM; i++) mrow[i] = mt * BM + (wm * TM + i) * 32 + rsub;
+    if (a.mode == 1) {
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc(a.ws, static_cast<short>(0), a.ws_bytes, kBufWord3);
+        const unsigned nt4 = static_cast<unsigned>(a.Ntot) * 4u;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = nt * BN + (wn * TN + j) * 32 + row;
+            const unsigned wcol = n < a.Ntot ? static_cast<unsigned>(n) * 4u : static_cast<unsigned>(kOob);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                    __builtin_amdgcn_raw_buffer_store_b32(acc[i][j][r], wrs, m < M ? wcol + m * nt4 : kOob,
+                                                          blockIdx.y * M * nt4, 0);
+                }
+        }
+        return;
+    }
+    const unsigned ohw4 = static_cast<unsigned>(a.OHW) * 4u;
+    unsigned obase[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int n = nt * BN + (wn * TN + j) * 32 + row;
-        if (n >= a.Ntot) continue;
         const int img = n / a.OHW;
         const int sp = n - img * a.OHW;
-        const size_t ybase = static_cast<size_t>(img) * a.M * a.OHW + sp;
+        obase[j] = n < a.Ntot
+                       ? (static_cast<unsigned>(img) * M * static_cast<unsigned>(a.OHW) + static_cast<unsigned>(sp)) * 4u
+                       : static_cast<unsigned>(kOob);
+    }
+    if (a.mode == 2) {
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc(a.ws, static_cast<short>(0), a.ws_bytes, kBufWord3);
 #pragma unroll
-        for (int i = 0; i < TM; i++) {
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                    __builtin_amdgcn_raw_buffer_store_b32(acc[i][j][r], wrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
+                }
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t yrs =
+        __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), a.y_bytes, kBufWord3);
+    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.res ? a.res : a.y), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.scales),
+                                                                         static_cast<short>(0), a.M * 4, kBufWord3);
+    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.bias ? a.bias : a.scales), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufWord3);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        // per-row constants of this block, loaded once for all TN blocks
+        floatx16 sc, bi;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const unsigned moff = (mrow[i] + 8 * (r >> 2) + (r & 3)) * 4u;
+            sc[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, moff, 0, 0));
+            bi[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(brs, moff, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            floatx16 v;
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = fmaf(static_cast<float>(acc[i][j][r]), sc[r], bi[r]);
+            if (a.res) {
+                floatx16 rv;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                    rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0));
+                }
+                v += rv;
+            }
+            if (a.act == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+            } else if (a.act == 2) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = mt * BM + (wm * TM + i) * 32 + 8 * (r >> 2) + rsub + (r & 3);
-                if (m >= a.M) continue;
-                const int32_t v = acc[i][j][r];
-                const size_t yi = ybase + static_cast<size_t>(m) * a.OHW;
-                if (a.mode == 1) {
-                    a.ws[(static_cast<size_t>(blockIdx.y) * a.M + m) * a.Ntot + n] = v;
-                } else if (a.mode == 2) {
-                    a.ws[yi] = v;
-                } else {
-                    float f = fmaf(static_cast<float>(v), a.scales[m], a.bias ? a.bias[m] : 0.0f);
-                    if (a.res) f += a.res[yi];
-                    a.y[yi] = apply_act(f, a.act);
-                }
+                const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                // __float_as_uint takes the element by value
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs, m < M ? obase[j] + m * ohw4 : kOob,
+                                                      0, 0);
             }
         }
     }
 }
 
+// Sums the int32 split-K partials (exact in any order), then dequantizes or
+// writes the raw accumulators.  Four consecutive columns per thread when N
+// is a multiple of 4, up to eight slices' loads in flight.
+template <int VEC>
 __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restrict__ ws, int splitk, int M, int Ntot,
                                                           int OHW, const float *__restrict__ scales,
                                                           const float *__restrict__ bias, const float *__restrict__ res,
                                                           float *__restrict__ y, int32_t *__restrict__ raw, int act) {
+    typedef int vec_t __attribute__((ext_vector_type(VEC)));
     const size_t total = static_cast<size_t>(M) * Ntot;
-    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
-         idx += static_cast<size_t>(gridDim.x) * 256) {
+    const size_t groups = total / VEC;
+    for (size_t gi = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; gi < groups;
+         gi += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t idx = gi * VEC;
         const int m = static_cast<int>(idx / Ntot);
         const int n = static_cast<int>(idx - static_cast<size_t>(m) * Ntot);
-        int32_t v = 0;
-        for (int s = 0; s < splitk; s++) v += ws[s * total + idx];
-        const int img = n / OHW;
-        const int sp = n - img * OHW;
-        const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
-        if (raw) {
-            raw[yi] = v;
-            continue;
+        vec_t v = 0;
+        int s = 0;
+        for (; s + 8 <= splitk; s += 8) {
+            vec_t p[8];
+#pragma unroll
+            for (int t = 0; t < 8; t++) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
+#pragma unroll
+            for (int t = 0; t < 8; t++) v += p[t];
         }
-        float f = fmaf(static_cast<float>(v), scales[m], bias ? bias[m] : 0.0f);
-        if (res) f += res[yi];
-        y[yi] = apply_act(f, act);
+        for (; s < splitk; s++) v += *reinterpret_cast<const vec_t *>(ws + s * total + idx);
+        const float sm = scales[m];
+        const float bm = bias ? bias[m] : 0.0f;
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            const int img = (n + e) / OHW;
+            const int sp = n + e - img * OHW;
+            const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
+            if (raw) {
+                raw[yi] = v[e];
+                continue;
+            }
+            float f = fmaf(static_cast<float>(v[e]), sm, bm);
+            if (res) f += res[yi];
+            y[yi] = apply_act(f, act);
+        }
     }
 }
 
+using I8Kernel = void (*)(I8Args);
+
+struct I8Cfg {
+    int BM, BN, BK;
+    const char *name;
+    I8Kernel kernel;
+};
+
+#define I8CFG(BM, BN, BK) {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK>}
+const I8Cfg kI8Cfgs[] = {
+    I8CFG(128, 128, 64), I8CFG(128, 128, 128), I8CFG(128, 64, 64), I8CFG(128, 64, 128),
+    I8CFG(64, 128, 64),  I8CFG(64, 64, 64),    I8CFG(64, 64, 128),
+};
+#undef I8CFG
+constexpr int kNumI8Cfgs = sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]);
+
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// K layout of a layer: 16-byte groups and where each sits in padded NHWC.
+struct I8Layout {
+    int Cp;        // channel stride of xq (bytes per pixel)
+    bool runs;     // dilation-1 kernel rows as contiguous (kw, c) runs
+    int run_groups;  // groups per kernel row (runs) or per tap
+    int groups;    // total 16-byte groups of K
+    int Hp, Wp, pt, pl;
+};
+
+I8Layout i8_layout(const ConvGeom &g) {
+    I8Layout L{};
+    L.runs = g.dw == 1;
+    L.Cp = L.runs ? static_cast<int>(align_up(g.C, 4)) : static_cast<int>(align_up(g.C, 16));
+    L.run_groups = L.runs ? static_cast<int>(align_up(static_cast<size_t>(g.KW) * L.Cp, 16) / 16) : L.Cp / 16;
+    L.groups = L.runs ? g.KH * L.run_groups : g.KH * g.KW * L.run_groups;
+    const int hspan = (g.OH - 1) * g.sh + (g.KH - 1) * g.dh + 1;
+    const int wspan = (g.OW - 1) * g.sw + (g.KW - 1) * g.dw + 1;
+    L.pt = g.ph;
+    L.pl = g.pw;
+    L.Hp = std::max(g.H + g.ph, hspan);
+    L.Wp = std::max(g.W + g.pw, wspan);
+    return L;
+}
+
+// byte offset of group q relative to the window origin in padded NHWC
+int i8_group_offset(const ConvGeom &g, const I8Layout &L, int q) {
+    if (L.runs) {
+        const int kh = q / L.run_groups, r = q % L.run_groups;
+        return kh * g.dh * L.Wp * L.Cp + r * 16;
+    }
+    const int tap = q / L.run_groups, c16 = q % L.run_groups;
+    const int kh = tap / g.KW, kw = tap % g.KW;
+    return (kh * g.dh * L.Wp + kw * g.dw) * L.Cp + c16 * 16;
+}
+
+// weight of packed k byte kb (group kb/16, byte kb%16) for output channel m
+int8_t i8_weight_at(const ConvGeom &g, const I8Layout &L, const int8_t *w, int m, int kb) {
+    const int q = kb / 16, b = kb % 16;
+    int kh, kw, c;
+    if (L.runs) {
+        kh = q / L.run_groups;
+        const int byte = (q % L.run_groups) * 16 + b;
+        kw = byte / L.Cp;
+        c = byte % L.Cp;
+        if (kw >= g.KW) return 0;
+    } else {
+        const int tap = q / L.run_groups;
+        kh = tap / g.KW;
+        kw = tap % g.KW;
+        c = (q % L.run_groups) * 16 + b;
+    }
+    if (kh >= g.KH || c >= g.C) return 0;
+    return w[((static_cast<size_t>(m) * g.C + c) * g.KH + kh) * g.KW + kw];
+}
+
+struct I8Counts {
+    int m_tiles, n_tiles, k_tiles, kt_per_split, splitk;
+};
+
+I8Counts i8_counts(int c, int M, int Ntot, int Kbytes, int split) {
+    const I8Cfg &t = kI8Cfgs[c];
+    I8Counts tc;
+    tc.m_tiles = (M + t.BM - 1) / t.BM;
+    tc.n_tiles = (Ntot + t.BN - 1) / t.BN;
+    tc.k_tiles = (Kbytes + t.BK - 1) / t.BK;
+    tc.kt_per_split = (tc.k_tiles + split - 1) / split;
+    tc.splitk = (tc.k_tiles + tc.kt_per_split - 1) / tc.kt_per_split;
+    return tc;
+}
+
+int cu_count() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        hipDeviceProp_t p;
+        cus = (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess)
+                  ? p.multiProcessorCount
+                  : 256;
+    }
+    return cus;
+}
+
+// Modelled time (us): int8 MFMA work of the busiest CU (two workgroups per
+// CU share it), floored by one workgroup's serial k loop, plus split-K
+// partial traffic.  Prunes what the tuner times.
+double i8_model_us(int c, const I8Counts &tc, int M, int Ntot) {
+    const I8Cfg &t = kI8Cfgs[c];
+    const int cus = cu_count();
+    const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles * tc.splitk;
+    const long rounds = (wgs + 2L * cus - 1) / (2L * cus);
+    const long per_cu = std::min<long>(2, (wgs + cus - 1) / cus);
+    const double tile_us = 2.0 * t.BM * t.BN * t.BK / (8192.0 * 2400.0 * 0.85);
+    const double mfma = static_cast<double>(rounds) * per_cu * tc.kt_per_split * tile_us;
+    const double latency = static_cast<double>(rounds) * tc.kt_per_split * 0.5;
+    double us = std::max(mfma, latency) + 2.0;
+    if (tc.splitk > 1) us += 4.0 * M * static_cast<double>(Ntot) * (tc.splitk + 1) / 4.0e6 + 3.0;
+    return us;
+}
+
+const int kI8Splits[] = {1, 2, 3, 4, 6, 8, 12, 16};
+
+size_t i8_partial_bytes(const I8Counts &tc, int M, int Ntot) {
+    return tc.splitk > 1 ? static_cast<size_t>(tc.splitk) * M * Ntot * sizeof(int32_t) : 0;
+}
+
+void fill_i8_args(I8Args &a, const ConvGeom &g, const I8Layout &L, const I8Counts &tc) {
+    a.x_bytes = static_cast<int>(static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp);
+    a.y_bytes = static_cast<int>(g.y_elems * 4);
+    a.img_stride = L.Hp * L.Wp * L.Cp;
+    a.Wp = L.Wp;
+    a.Cp = L.Cp;
+    a.M = g.M;
+    a.OW = g.OW;
+    a.OHW = g.OH * g.OW;
+    a.Ntot = g.N * a.OHW;
+    a.sh = g.sh;
+    a.sw = g.sw;
+    a.m_tiles = tc.m_tiles;
+    a.k_tiles = tc.k_tiles;
+    a.kt_per_split = tc.kt_per_split;
+    a.act = g.act;
+}
+
+// Launches the GEMM (and the split-K epilogue) of configuration c.
+int launch_i8(hipStream_t st, int c, const I8Counts &tc, I8Args a, int32_t *part, int32_t *raw) {
+    const bool split = tc.splitk > 1;
+    if (split) {
+        a.mode = 1;
+        a.ws = part;
+        a.ws_bytes = static_cast<int>(i8_partial_bytes(tc, a.M, a.Ntot));
+    } else if (raw) {
+        a.mode = 2;
+        a.ws = raw;
+        a.ws_bytes = a.y_bytes;
+    } else {
+        a.mode = 0;
+    }
+    dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
+    kI8Cfgs[c].kernel<<<grid, dim3(256), 0, st>>>(a);
+    if (int rc = launch_status("conv_igemm_i8")) return rc;
+    if (split) {
+        const size_t total = static_cast<size_t>(a.M) * a.Ntot;
+        if (a.Ntot % 4 == 0)
+            hipLaunchKernelGGL(splitk_i8_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, part, tc.splitk,
+                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act);
+        else
+            hipLaunchKernelGGL(splitk_i8_epilogue<1>, dim3(grid_for(total, 256)), dim3(256), 0, st, part, tc.splitk,
+                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act);
+        if (int rc = launch_status("splitk_i8_epilogue")) return rc;
+    }
+    return 0;
+}
+
+std::vector<int> build_i8_koff(const ConvGeom &g, const I8Layout &L, int k_tiles, int BK) {
+    const int per_tile = BK / 16;
+    // two extra tiles of out-of-range entries: the pipeline prefetches up to
+    // two tiles past the last one
+    std::vector<int> koff(static_cast<size_t>((k_tiles + 2) * per_tile), kOob);
+    for (int q = 0; q < L.groups; q++) koff[q] = i8_group_offset(g, L, q);
+    return koff;
+}
+
+std::mutex g_i8_mu;
+std::map<std::string, std::pair<int, int>> g_i8_tuned;
+
+struct DevBufs {
+    std::vector<void *> p;
+    void *get(size_t n) {
+        void *q = nullptr;
+        if (hipMalloc(&q, n ? n : 16) != hipSuccess) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        p.push_back(q);
+        return q;
+    }
+    ~DevBufs() {
+        for (void *q : p) (void)hipFree(q);
+    }
+};
+
+// Times the candidates the model keeps on zero-filled scratch buffers of the
+// layer's shape and returns the fastest (cfg, split); cached per shape.
+bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out, int *split_out) {
+    char key[256];
+    snprintf(key, sizeof(key), "i8|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d", g.N, g.C, g.H, g.W, g.M, g.KH, g.KW,
+             g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, g.has_bias ? 1 : 0, g.has_res ? 1 : 0, g.act);
+    {
+        std::lock_guard<std::mutex> lk(g_i8_mu);
+        auto it = g_i8_tuned.find(key);
+        if (it != g_i8_tuned.end()) {
+            *cfg_out = it->second.first;
+            *split_out = it->second.second;
+            return true;
+        }
+    }
+    const int Ntot = g.N * g.OH * g.OW;
+    const int Kbytes = L.groups * 16;
+    struct Cand {
+        int cfg, split;
+        I8Counts tc;
+        double model, t;
+    };
+    std::vector<Cand> cands;
+    double best = 1e300;
+    for (int c = 0; c < kNumI8Cfgs; c++) {
+        int last = -1;
+        for (int s : kI8Splits) {
+            const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
+            if (tc.splitk == last) continue;
+            if (s > 1 && tc.kt_per_split < 2) break;
+            last = tc.splitk;
+            if (i8_partial_bytes(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
+            const double m = i8_model_us(c, tc, g.M, Ntot);
+            best = std::min(best, m);
+            cands.push_back({c, s, tc, m, 0.0});
+        }
+    }
+    std::vector<Cand> keep;
+    for (const Cand &cd : cands)
+        if (cd.model <= 3.0 * best) keep.push_back(cd);
+    if (keep.empty()) return false;
+    DevBufs db;
+    size_t wbytes = 16, pbytes = 16, kentries = 16;
+    for (const Cand &cd : keep) {
+        const I8Cfg &t = kI8Cfgs[cd.cfg];
+        wbytes = std::max(wbytes, static_cast<size_t>(cd.tc.m_tiles) * cd.tc.k_tiles * t.BM * t.BK);
+        pbytes = std::max(pbytes, i8_partial_bytes(cd.tc, g.M, Ntot));
+        kentries = std::max(kentries, static_cast<size_t>((cd.tc.k_tiles + 2) * t.BK / 16));
+    }
+    const size_t xbytes = static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp;
+    const size_t ybytes = static_cast<size_t>(g.y_elems) * 4;
+    int8_t *xq = static_cast<int8_t *>(db.get(xbytes));
+    int8_t *wp = static_cast<int8_t *>(db.get(wbytes));
+    int *ko = static_cast<int *>(db.get(kentries * sizeof(int)));
+    float *sc = static_cast<float *>(db.get(static_cast<size_t>(g.M) * 4));
+    float *y = static_cast<float *>(db.get(ybytes));
+    float *res = g.has_res ? static_cast<float *>(db.get(ybytes)) : nullptr;
+    int32_t *part = static_cast<int32_t *>(db.get(pbytes));
+    if (!xq || !wp || !ko || !sc || !y || (g.has_res && !res) || !part) return false;
+    (void)hipMemsetAsync(xq, 0, xbytes, st);
+    (void)hipMemsetAsync(wp, 0, wbytes, st);
+    (void)hipMemsetAsync(sc, 0, static_cast<size_t>(g.M) * 4, st);
+    if (res) (void)hipMemsetAsync(res, 0, ybytes, st);
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    std::vector<int> last_kv;
+    int last_bk = -1;
+    bool ok = true;
+    auto time_it = [&](const Cand &cd, int reps) -> double {
+        const I8Cfg &t = kI8Cfgs[cd.cfg];
+        const std::vector<int> kv = build_i8_koff(g, L, cd.tc.k_tiles, t.BK);
+        if (t.BK != last_bk || kv.size() != last_kv.size()) {
+            if (hipMemcpy(ko, kv.data(), kv.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) return 1e300;
+            last_kv = kv;
+            last_bk = t.BK;
+        }
+        I8Args a{};
+        fill_i8_args(a, g, L, cd.tc);
+        a.xq = xq;
+        a.wp = wp;
+        a.koff = ko;
+        a.scales = sc;
+        a.bias = g.has_bias ? sc : nullptr;
+        a.res = res;
+        a.y = y;
+        if (hipEventRecord(e0, st) != hipSuccess) return 1e300;
+        for (int r = 0; r < reps; r++)
+            if (launch_i8(st, cd.cfg, cd.tc, a, part, nullptr) != 0) return 1e300;
+        if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e300;
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e300;
+        return 1e3 * ms / reps;
+    };
+    for (Cand &cd : keep) {
+        (void)time_it(cd, 1);
+        cd.t = time_it(cd, 1);
+        if (cd.t >= 1e300) ok = false;
+    }
+    std::sort(keep.begin(), keep.end(), [](const Cand &x, const Cand &y2) { return x.t < y2.t; });
+    const size_t fin = std::min<size_t>(keep.size(), 3);
+    for (size_t i = 0; i < fin && ok; i++) keep[i].t = std::min(keep[i].t, time_it(keep[i], 3));
+    std::sort(keep.begin(), keep.begin() + fin, [](const Cand &x, const Cand &y2) { return x.t < y2.t; });
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (!ok || hipStreamSynchronize(st) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    *cfg_out = keep[0].cfg;
+    *split_out = keep[0].split;
+    std::lock_guard<std::mutex> lk(g_i8_mu);
+    g_i8_tuned[key] = {keep[0].cfg, keep[0].split};
+    return true;
+}
 
 }  // namespace
 
@@ -285,74 +713,81 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     const int8_t *w = reinterpret_cast<const int8_t *>(host_weight_data(ctx, node->inputs[1]));
     if (!w) return SPKV2_E_UNSUPPORTED;
 
+    const I8Layout L = i8_layout(g);
+    const size_t xq_bytes = static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp;
+    if (xq_bytes >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;  // byte offsets are 31-bit
     plan->path = CONV_IGEMM_I8;
     plan->x_scale = xs[0];
-    const int K = g.C * g.KH * g.KW;
+    plan->Hp = L.Hp;
+    plan->Wp = L.Wp;
+    plan->pt = L.pt;
+    plan->pl = L.pl;
     const int Ntot = g.N * g.OH * g.OW;
-    plan->K = K;
-    plan->BM = I8_BM;
-    plan->BN = I8_BN;
-    plan->BK = I8_BK;
-    plan->m_tiles = (g.M + I8_BM - 1) / I8_BM;
-    plan->n_tiles = (Ntot + I8_BN - 1) / I8_BN;
-    plan->k_tiles = (K + I8_BK - 1) / I8_BK;
-    plan->Kpad = plan->k_tiles * I8_BK;
-    plan->cfg = (g.C % 16 == 0) ? 1 : 0;  // 1: 16-byte channel groups, 0: byte gather
+    const int Kbytes = L.groups * 16;
 
-    // split-K only when the tile grid cannot fill the GPU
-    int split = 1;
-    {
-        int dev = 0, cus = 256;
-        hipDeviceProp_t p;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) cus = p.multiProcessorCount;
-        const int tiles = plan->m_tiles * plan->n_tiles;
-        while (split < 16 && tiles * split * 2 <= cus * 2 && plan->k_tiles / (split * 2) >= 2) split *= 2;
+    int cfg = 0, split = 1;
+    const char *tune_env = getenv("SPKV2_CONV_TUNE");
+    if ((tune_env && tune_env[0] == '0') || !tune_i8(ctx->stream, g, L, &cfg, &split)) {
+        double best = 1e300;
+        for (int c = 0; c < kNumI8Cfgs; c++)
+            for (int s : kI8Splits) {
+                const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
+                if (s > 1 && tc.kt_per_split < 2) break;
+                const double m = i8_model_us(c, tc, g.M, Ntot);
+                if (m < best * 0.999) {
+                    best = m;
+                    cfg = c;
+                    split = s;
+                }
+            }
     }
-    plan->kt_per_split = (plan->k_tiles + split - 1) / split;
-    plan->splitk = (plan->k_tiles + plan->kt_per_split - 1) / plan->kt_per_split;
-    const size_t xq_bytes = align_up(static_cast<size_t>(g.x_elems) + 64, 256);
-    // partials also serve the raw-accumulator hook, which always takes the split path
-    const size_t part_bytes = static_cast<size_t>(plan->splitk) * g.M * Ntot * sizeof(int32_t);
-    plan->workspace = xq_bytes + part_bytes;
+    if (const char *e = getenv("SPKV2_I8_CFG")) {
+        const int c = atoi(e);
+        if (c >= 0 && c < kNumI8Cfgs) cfg = c;
+    }
+    if (const char *e = getenv("SPKV2_I8_SPLITK")) {
+        const int s = atoi(e);
+        if (s >= 1 && s <= 64) split = s;
+    }
+    const I8Cfg &t = kI8Cfgs[cfg];
+    const I8Counts tc = i8_counts(cfg, g.M, Ntot, Kbytes, split);
+    plan->cfg = cfg;
+    plan->K = Kbytes;
+    plan->BM = t.BM;
+    plan->BN = t.BN;
+    plan->BK = t.BK;
+    plan->m_tiles = tc.m_tiles;
+    plan->n_tiles = tc.n_tiles;
+    plan->k_tiles = tc.k_tiles;
+    plan->Kpad = tc.k_tiles * t.BK;
+    plan->kt_per_split = tc.kt_per_split;
+    plan->splitk = tc.splitk;
+    // partials also serve the raw-accumulator hook when the layer splits K
+    const size_t part_bytes = i8_partial_bytes(tc, g.M, Ntot);
+    // partial offsets (slice, row, out-of-range column) must stay below 2^32
+    if (part_bytes >= 0x40000000ULL) return SPKV2_E_UNSUPPORTED;
+    plan->pad_bytes = align_up(xq_bytes + 64, 256);
+    plan->workspace = plan->pad_bytes + part_bytes;
 
     // activation quantization constants (reference conv_int8.c:22-23)
     plan->quant_split = static_cast<int>((static_cast<int64_t>(g.C) * g.H * g.W / 16) * 16);
 
-    // weights: K reordered to (kh, kw, c), packed [m_tiles][k_tiles][BM][BK]
-    std::vector<int8_t> packed(static_cast<size_t>(plan->m_tiles) * plan->k_tiles * I8_BM * I8_BK, 0);
+    // weights packed [m_tiles][k_tiles][BM][BK] in the layer's k order
+    std::vector<int8_t> packed(static_cast<size_t>(tc.m_tiles) * tc.k_tiles * t.BM * t.BK, 0);
     for (int m = 0; m < g.M; m++) {
-        const int mt = m / I8_BM, mi = m % I8_BM;
-        for (int c = 0; c < g.C; c++)
-            for (int kh = 0; kh < g.KH; kh++)
-                for (int kw = 0; kw < g.KW; kw++) {
-                    const int k = (kh * g.KW + kw) * g.C + c;
-                    const int kt = k / I8_BK, kk = k % I8_BK;
-                    packed[((static_cast<size_t>(mt) * plan->k_tiles + kt) * I8_BM + mi) * I8_BK + kk] =
-                        w[((static_cast<size_t>(m) * g.C + c) * g.KH + kh) * g.KW + kw];
-                }
+        const int mt = m / t.BM, mi = m % t.BM;
+        for (int kb = 0; kb < Kbytes; kb++) {
+            const int kt = kb / t.BK, kk = kb % t.BK;
+            packed[((static_cast<size_t>(mt) * tc.k_tiles + kt) * t.BM + mi) * t.BK + kk] = i8_weight_at(g, L, w, m, kb);
+        }
     }
     if (int rc = hip_check(hipMalloc(&plan->wpack, packed.size()), "hipMalloc i8 weights")) return rc;
     if (int rc = hip_check(hipMemcpy(plan->wpack, packed.data(), packed.size(), hipMemcpyHostToDevice), "hipMemcpy"))
         return rc;
-
-    // gather table over NHWC: offset of (kh, kw, c) relative to the window origin
-    const bool vec = plan->cfg == 1;
-    const int entries = vec ? plan->Kpad / 16 : plan->Kpad;
-    std::vector<int2> tab(static_cast<size_t>(entries));
-    for (int e = 0; e < entries; e++) {
-        const int k = vec ? e * 16 : e;
-        if (k < K) {
-            const int tap = k / g.C, c = k % g.C;
-            const int kh = tap / g.KW, kw = tap % g.KW;
-            tab[e].x = (kh * g.dh * g.W + kw * g.dw) * g.C + c;
-            tab[e].y = ((kh * g.dh) << 16) | (kw * g.dw);
-        } else {
-            tab[e].x = 0;
-            tab[e].y = 0x7fff << 16;
-        }
-    }
-    if (int rc = hip_check(hipMalloc(&plan->ktab, tab.size() * sizeof(int2)), "hipMalloc ktab")) return rc;
-    if (int rc = hip_check(hipMemcpy(plan->ktab, tab.data(), tab.size() * sizeof(int2), hipMemcpyHostToDevice), "hipMemcpy"))
+    const std::vector<int> koff = build_i8_koff(g, L, tc.k_tiles, t.BK);
+    if (int rc = hip_check(hipMalloc(&plan->ktab, koff.size() * sizeof(int)), "hipMalloc i8 koff")) return rc;
+    if (int rc = hip_check(hipMemcpy(plan->ktab, koff.data(), koff.size() * sizeof(int), hipMemcpyHostToDevice),
+                           "hipMemcpy"))
         return rc;
 
     std::vector<float> comb(static_cast<size_t>(g.M));
@@ -360,7 +795,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->scales), comb.size() * 4), "hipMalloc")) return rc;
     if (int rc = hip_check(hipMemcpy(plan->scales, comb.data(), comb.size() * 4, hipMemcpyHostToDevice), "hipMemcpy"))
         return rc;
-    set_kernel_name(ctx, node, std::string("conv_igemm_i8<128x128x64,") + (vec ? "vec16" : "bytes") +
+    set_kernel_name(ctx, node, std::string("conv_igemm_i8<") + t.name + (L.runs ? ",runs" : ",taps") +
                                    ",splitk=" + std::to_string(plan->splitk) + ">");
     return 0;
 }
@@ -368,61 +803,28 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
 int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *plan, int32_t *raw_acc_out) {
     const ConvGeom &g = plan->g;
     if (ctx->workspace_size < plan->workspace) return SPKV2_E_UNSUPPORTED;
-    const int HW = g.H * g.W;
+    const I8Layout L = i8_layout(g);
     int8_t *xq = reinterpret_cast<int8_t *>(ctx->workspace);
-    const size_t xq_bytes = align_up(static_cast<size_t>(g.x_elems) + 64, 256);
-    int32_t *part = reinterpret_cast<int32_t *>(ctx->workspace + xq_bytes);
+    int32_t *part = reinterpret_cast<int32_t *>(ctx->workspace + plan->pad_bytes);
     const float inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
 
-    dim3 qgrid((HW + 63) / 64, (g.C + 31) / 32, g.N);
-    hipLaunchKernelGGL(quantize_nhwc, qgrid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]), xq,
-                       g.C, HW, inv_scale, plan->quant_split);
-    if (int rc = launch_status("quantize_nhwc")) return rc;
+    dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
+               static_cast<unsigned>(g.N));
+    hipLaunchKernelGGL(quantize_pad_nhwc, qgrid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]), xq,
+                       g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl, inv_scale, plan->quant_split);
+    if (int rc = launch_status("quantize_pad_nhwc")) return rc;
 
+    const I8Counts tc{plan->m_tiles, plan->n_tiles, plan->k_tiles, plan->kt_per_split, plan->splitk};
     I8Args a{};
+    fill_i8_args(a, g, L, tc);
     a.xq = xq;
     a.wp = static_cast<const int8_t *>(plan->wpack);
-    a.ktab = static_cast<const int2 *>(plan->ktab);
+    a.koff = static_cast<const int *>(plan->ktab);
     a.scales = plan->scales;
     a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
     a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
     a.y = dptr<float>(ctx, node->outputs[0]);
-    a.H = g.H;
-    a.W = g.W;
-    a.C = g.C;
-    a.M = g.M;
-    a.OW = g.OW;
-    a.OHW = g.OH * g.OW;
-    a.Ntot = g.N * a.OHW;
-    a.sh = g.sh;
-    a.sw = g.sw;
-    a.ph = g.ph;
-    a.pw = g.pw;
-    a.m_tiles = plan->m_tiles;
-    a.k_tiles = plan->k_tiles;
-    a.kt_per_split = plan->kt_per_split;
-    a.act = g.act;
-    const bool split = plan->splitk > 1;
-    if (raw_acc_out && !split) {
-        a.mode = 2;
-        a.ws = raw_acc_out;
-    } else if (split) {
-        a.mode = 1;
-        a.ws = part;
-    } else {
-        a.mode = 0;
-    }
-    dim3 grid(static_cast<unsigned>(plan->m_tiles * plan->n_tiles), static_cast<unsigned>(plan->splitk));
-    if (plan->cfg == 1) hipLaunchKernelGGL(conv_igemm_i8<true>, grid, dim3(256), 0, ctx->stream, a);
-    else hipLaunchKernelGGL(conv_igemm_i8<false>, grid, dim3(256), 0, ctx->stream, a);
-    if (int rc = launch_status("conv_igemm_i8")) return rc;
-    if (split) {
-        const size_t total = static_cast<size_t>(g.M) * a.Ntot;
-        hipLaunchKernelGGL(splitk_i8_epilogue, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, part,
-                           plan->splitk, g.M, a.Ntot, a.OHW, plan->scales, a.bias, a.res, a.y, raw_acc_out, g.act);
-        if (int rc = launch_status("splitk_i8_epilogue")) return rc;
-    }
-    return 0;
+    return launch_i8(ctx->stream, plan->cfg, tc, a, part, raw_acc_out);
 }
 
 }  // namespace spk::kern

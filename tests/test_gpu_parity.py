@@ -155,21 +155,21 @@ def test_cpu_generic_package_runs_on_gpu(gpu):
 
 
 INT8_CASES = [
-    (1, 16, 14, 14, 32, 3, 1, 1, "Relu", False),
-    (2, 64, 14, 14, 64, 1, 1, 0, None, True),
-    (1, 3, 32, 32, 64, 7, 2, 3, "Relu", False),     # C % 16 != 0: byte gather
-    (1, 128, 7, 7, 256, 3, 2, 1, "Relu", False),    # split-K
+    dict(n=1, cin=16, h=14, w=14, cout=32, k=3, stride=1, pad=1, act="Relu"),
+    dict(n=2, cin=64, h=14, w=14, cout=64, k=1, stride=1, pad=0, act=None, residual=True),
+    dict(n=1, cin=3, h=32, w=32, cout=64, k=7, stride=2, pad=3, act="Relu"),      # stem: (kw, c) runs, C % 4 != 0
+    dict(n=1, cin=128, h=7, w=7, cout=256, k=3, stride=2, pad=1, act="Relu"),     # small grid
+    dict(n=1, cin=20, h=9, w=9, cout=24, k=3, stride=1, pad=2, dilation=2, act=None),  # per-tap groups, C padded
+    dict(n=2, cin=40, h=10, w=12, cout=30, k=3, stride=1, pad=0, act="Relu", pads=[1, 0, 0, 2]),  # asymmetric pads
+    dict(n=3, cin=256, h=7, w=7, cout=512, k=1, stride=1, pad=0, act="Relu", residual=True),
 ]
 
 
-@pytest.mark.parametrize("case", INT8_CASES, ids=[f"i8_{i}" for i in range(len(INT8_CASES))])
-def test_int8_conv_bit_exact(gpu, case):
+def _int8_check(g, seed=42):
     from spinnv2_amd.runtime import Model
     from oracle.spk_exec import OracleExecutor
 
-    n, cin, h, w, cout, k, s, p, act, res = case
-    g = models.single_conv(n, cin, h, w, cout, k, s, p, act=act, residual=res)
-    xs = rng_inputs(g)
+    xs = rng_inputs(g, seed)
     qp = calibrate_activation_scales(g, [xs]) + quantize_conv_weights(g)
     blob = write_spk(g, "mi355x", quant_params=qp)
     ora = OracleExecutor(blob)
@@ -180,8 +180,28 @@ def test_int8_conv_bit_exact(gpu, case):
         m.run()
         got = m.get_output(0)
         acc = m.int8_accumulators(0, want.nbytes)
+        name = m.kernel_name(0)
     np.testing.assert_array_equal(acc, ora.acc[0].ravel())
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    return name
+
+
+@pytest.mark.parametrize("case", INT8_CASES, ids=[f"i8_{i}" for i in range(len(INT8_CASES))])
+def test_int8_conv_bit_exact(gpu, case):
+    print(f"[int8] {case}", flush=True)
+    _int8_check(models.single_conv(**case))
+
+
+I8_FORCED = [(cfg, split) for cfg in range(7) for split in (1, 3)]
+
+
+@pytest.mark.parametrize("cfg,split", I8_FORCED, ids=[f"i8cfg{c}_split{s}" for c, s in I8_FORCED])
+def test_int8_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
+    monkeypatch.setenv("SPKV2_I8_CFG", str(cfg))
+    monkeypatch.setenv("SPKV2_I8_SPLITK", str(split))
+    name = _int8_check(models.single_conv(2, 48, 11, 13, 70, 3, 1, 1, act="Relu", residual=True))
+    # the effective split is capped by the layer's k-tile count
+    assert ("splitk=1>" in name) == (split == 1), name
 
 
 def test_graph_mode_matches_eager(gpu):
