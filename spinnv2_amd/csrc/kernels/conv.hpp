@@ -44,6 +44,16 @@ struct ConvPlan {
     float x_scale;       // int8 path: activation scale
     int quant_split;     // int8 path: first element index of the per-image tail (round half away)
     size_t workspace;    // bytes of runtime workspace needed per run
+    // int8 requantize handoff.  Producer side: this conv's output is also
+    // quantized in its epilogue, with the consuming int8 conv's scale and
+    // rounding rule, into that conv's zero-padded NHWC buffer (not owned);
+    // y_needed says whether the fp32 output still has other readers.
+    int8_t *q_out;
+    int q_Hp, q_Wp, q_Cp, q_pt, q_pl, q_split;
+    float q_inv_scale;
+    bool y_needed;
+    // Consumer side: the padded NHWC int8 input its producer writes (owned).
+    int8_t *q_in;
 };
 
 void conv_plan_free(void *p);

@@ -87,6 +87,7 @@ void conv_plan_free(void *p) {
     if (plan->wpack) (void)hipFree(plan->wpack);
     if (plan->ktab) (void)hipFree(plan->ktab);
     if (plan->scales) (void)hipFree(plan->scales);
+    if (plan->q_in) (void)hipFree(plan->q_in);
     delete plan;
 }
 

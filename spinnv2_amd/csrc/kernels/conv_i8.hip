@@ -115,7 +115,24 @@ struct I8Args {
     int m_tiles, k_tiles, kt_per_split;
     int act;
     int mode;  // 0: dequant epilogue, 1: int32 partials to ws[split][M][Ntot], 2: raw acc to ws as NCHW
+    // requantize handoff (mode 0): also write q(y) into the consuming conv's
+    // padded NHWC int8 input; y may then be null (no other reader)
+    int8_t *__restrict__ q_out;
+    int q_bytes, q_Hp, q_Wp, q_Cp, q_pt, q_pl, q_split;
+    float q_inv;
 };
+
+// The reference's activation quantization of one value (conv_int8.c:26-55):
+// round half to even below `split` (the 16-wide vector body), half away
+// from zero in the tail, saturate to int8, NaN -> 0.
+__device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even) {
+    const float t = v * inv_scale;
+    float r;
+    if (t != t) r = 0.0f;
+    else r = even ? rintf(t) : roundf(t);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return static_cast<int>(r);
+}
 
 template <int BM, int BN, int BK>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
@@ -287,10 +304,27 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
                 }
         return;
     }
-    const __amdgpu_buffer_rsrc_t yrs =
-        __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), a.y_bytes, kBufWord3);
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(a.y ? a.y : const_cast<float *>(a.scales), static_cast<short>(0),
+                                                                         a.y ? a.y_bytes : 0, kBufWord3);
     const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(a.res ? a.res : a.y), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
+        const_cast<float *>(a.res ? a.res : a.scales), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        a.q_out ? a.q_out : const_cast<int8_t *>(a.xq), static_cast<short>(0), a.q_out ? a.q_bytes : 0, kBufWord3);
+    // handoff: byte offset of this lane's pixel in the consumer's padded NHWC
+    // buffer, and its spatial index (for the NCHW rounding split)
+    unsigned qbase[TN];
+    int qsp[TN];
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = nt * BN + (wn * TN + j) * 32 + row;
+        const int img = n / a.OHW;
+        const int sp = n - img * a.OHW;
+        const int oh = sp / a.OW;
+        const int ow = sp - oh * a.OW;
+        qsp[j] = sp;
+        qbase[j] = n < a.Ntot ? static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp)
+                              : static_cast<unsigned>(kOob);
+    }
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.scales),
                                                                          static_cast<short>(0), a.M * 4, kBufWord3);
     const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
@@ -327,12 +361,31 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
             }
+            if (a.q_out) {
+                // four consecutive channels of the lane -> one dword; channels
+                // past M are written 0 (the padded channels stay zero)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                // __float_as_uint takes the element by value
-                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs, m < M ? obase[j] + m * ohw4 : kOob,
-                                                      0, 0);
+                for (int q4 = 0; q4 < 4; q4++) {
+                    const unsigned m0 = mrow[i] + 8 * q4;
+                    unsigned word = 0;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const unsigned m = m0 + b;
+                        const int idx = static_cast<int>(m) * a.OHW + qsp[j];
+                        const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
+                        word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
+                    }
+                    __builtin_amdgcn_raw_buffer_store_b32(word, qrs, m0 < M ? qbase[j] + m0 : kOob, 0, 0);
+                }
+            }
+            if (a.y) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                    // __float_as_uint takes the element by value
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
+                                                          m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
+                }
             }
         }
     }
@@ -345,7 +398,8 @@ template <int VEC>
 __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restrict__ ws, int splitk, int M, int Ntot,
                                                           int OHW, const float *__restrict__ scales,
                                                           const float *__restrict__ bias, const float *__restrict__ res,
-                                                          float *__restrict__ y, int32_t *__restrict__ raw, int act) {
+                                                          float *__restrict__ y, int32_t *__restrict__ raw, int act,
+                                                          I8Args q) {
     typedef int vec_t __attribute__((ext_vector_type(VEC)));
     const size_t total = static_cast<size_t>(M) * Ntot;
     const size_t groups = total / VEC;
@@ -377,7 +431,13 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
             }
             float f = fmaf(static_cast<float>(v[e]), sm, bm);
             if (res) f += res[yi];
-            y[yi] = apply_act(f, act);
+            f = apply_act(f, act);
+            if (q.q_out) {
+                const int oh = sp / q.OW, ow = sp - (sp / q.OW) * q.OW;
+                q.q_out[(static_cast<size_t>(img * q.q_Hp + oh + q.q_pt) * q.q_Wp + ow + q.q_pl) * q.q_Cp + m] =
+                    static_cast<int8_t>(quantize_one(f, q.q_inv, m * OHW + sp < q.q_split));
+            }
+            if (y) y[yi] = f;
         }
     }
 }
@@ -544,10 +604,10 @@ int launch_i8(hipStream_t st, int c, const I8Counts &tc, I8Args a, int32_t *part
         const size_t total = static_cast<size_t>(a.M) * a.Ntot;
         if (a.Ntot % 4 == 0)
             hipLaunchKernelGGL(splitk_i8_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, part, tc.splitk,
-                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act);
+                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act, a);
         else
             hipLaunchKernelGGL(splitk_i8_epilogue<1>, dim3(grid_for(total, 256)), dim3(256), 0, st, part, tc.splitk,
-                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act);
+                               a.M, a.Ntot, a.OHW, a.scales, a.bias, a.res, a.y, raw, a.act, a);
         if (int rc = launch_status("splitk_i8_epilogue")) return rc;
     }
     return 0;
@@ -701,6 +761,55 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
 
 }  // namespace
 
+// Requantize handoff.  When this int8 conv's input is the only output of an
+// earlier int8 conv, that conv quantizes its result in registers (with this
+// conv's scale and rounding split) straight into a zero-padded NHWC buffer
+// owned by this plan, and this conv skips its quantize pass.  The producer
+// still writes the fp32 tensor when anything else reads it (another
+// consumer, a graph output).  Packages with a protection plan keep every
+// tensor materialized and do not hand off.
+static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan, const I8Layout &L) {
+    if (ctx->protection_count > 0) return 0;
+    if (const char *e = getenv("SPKV2_I8_HANDOFF"))
+        if (e[0] == '0') return 0;
+    const uint32_t t = node->inputs[0];
+    const Spkv2NodeRecord *prod = nullptr;
+    int readers = 0;
+    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *n = &ctx->node_records[i];
+        for (uint16_t k = 0; k < n->input_count; k++)
+            if (n->inputs[k] == t) readers++;
+        if (n->id < node->id)
+            for (uint16_t k = 0; k < n->output_count; k++)
+                if (n->outputs[k] == t) prod = n;
+    }
+    if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
+    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
+    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
+    if (!pp || pp->path != CONV_IGEMM_I8 || pp->q_out) return 0;
+    const ConvGeom &g = plan->g;
+    if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
+    bool is_output = false;
+    for (size_t i = 0; i < ctx->output_count; i++)
+        if (ctx->output_ids[i] == t) is_output = true;
+    const size_t bytes = static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp;
+    if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->q_in), bytes), "hipMalloc int8 handoff"))
+        return rc;
+    // zero once: the producer writes only the interior, so the halo and the
+    // padded channels stay 0
+    if (int rc = hip_check(hipMemset(plan->q_in, 0, bytes), "hipMemset int8 handoff")) return rc;
+    pp->q_out = plan->q_in;
+    pp->q_Hp = L.Hp;
+    pp->q_Wp = L.Wp;
+    pp->q_Cp = L.Cp;
+    pp->q_pt = L.pt;
+    pp->q_pl = L.pl;
+    pp->q_split = plan->quant_split;
+    pp->q_inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
+    pp->y_needed = readers > 1 || is_output;
+    return 0;
+}
+
 int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {
     const ConvGeom &g = plan->g;
     if (g.group != 1 || g.x_dtype != SPKV2_DTYPE_FP32) return SPKV2_E_UNSUPPORTED;
@@ -795,8 +904,9 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->scales), comb.size() * 4), "hipMalloc")) return rc;
     if (int rc = hip_check(hipMemcpy(plan->scales, comb.data(), comb.size() * 4, hipMemcpyHostToDevice), "hipMemcpy"))
         return rc;
+    if (int rc = setup_handoff(ctx, node, plan, L)) return rc;
     set_kernel_name(ctx, node, std::string("conv_igemm_i8<") + t.name + (L.runs ? ",runs" : ",taps") +
-                                   ",splitk=" + std::to_string(plan->splitk) + ">");
+                                   ",splitk=" + std::to_string(plan->splitk) + (plan->q_in ? ",handoff" : "") + ">");
     return 0;
 }
 
@@ -808,11 +918,18 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     int32_t *part = reinterpret_cast<int32_t *>(ctx->workspace + plan->pad_bytes);
     const float inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
 
-    dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
-               static_cast<unsigned>(g.N));
-    hipLaunchKernelGGL(quantize_pad_nhwc, qgrid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]), xq,
-                       g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl, inv_scale, plan->quant_split);
-    if (int rc = launch_status("quantize_pad_nhwc")) return rc;
+    // a fault event may change the fp32 input after its producer ran: then
+    // every tensor is materialized and quantized here
+    const bool handoff = !ctx->fault_event.enabled;
+    if (plan->q_in && handoff) {
+        xq = plan->q_in;  // written by the producer's epilogue
+    } else {
+        dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
+                   static_cast<unsigned>(g.N));
+        hipLaunchKernelGGL(quantize_pad_nhwc, qgrid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]),
+                           xq, g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl, inv_scale, plan->quant_split);
+        if (int rc = launch_status("quantize_pad_nhwc")) return rc;
+    }
 
     const I8Counts tc{plan->m_tiles, plan->n_tiles, plan->k_tiles, plan->kt_per_split, plan->splitk};
     I8Args a{};
@@ -824,6 +941,18 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
     a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
     a.y = dptr<float>(ctx, node->outputs[0]);
+    if (plan->q_out && handoff) {
+        a.q_out = plan->q_out;
+        a.q_bytes = static_cast<int>(static_cast<size_t>(g.N) * plan->q_Hp * plan->q_Wp * plan->q_Cp);
+        a.q_Hp = plan->q_Hp;
+        a.q_Wp = plan->q_Wp;
+        a.q_Cp = plan->q_Cp;
+        a.q_pt = plan->q_pt;
+        a.q_pl = plan->q_pl;
+        a.q_split = plan->q_split;
+        a.q_inv = plan->q_inv_scale;
+        if (!plan->y_needed) a.y = nullptr;
+    }
     return launch_i8(ctx->stream, plan->cfg, tc, a, part, raw_acc_out);
 }
 

@@ -260,3 +260,99 @@ def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
             np.testing.assert_array_equal(m.get_output(0), eager)
     want = run_oracle(blob, xs)[0]
     assert tnorm_err(eager, want) <= FP32_TOL
+
+
+def _int8_network(depth=50, batch=2, image=32):
+    g = models.resnet(depth, batch, image=image, classes=10)
+    xs = rng_inputs(g)
+    cal = models.resnet(depth, 1, image=image, classes=10)
+    samples = [models.make_input(cal.tensors[cal.inputs[0]].shape, 1000 + i) for i in range(4)]
+    qp = calibrate_activation_scales(cal, samples) + quantize_conv_weights(g)
+    return g, xs, write_spk(g, "mi355x", quant_params=qp)
+
+
+def _int8_chain():
+    """Bottleneck-style chain of int8 convs with no fp32 tail: 1x1 -> 3x3 ->
+    1x1 + residual (also a graph output) -> 3x3 stride 2 -> 1x1."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    p = models.Params(3)
+    g = Graph("i8chain")
+    x = g.input("x", [2, 64, 14, 14])
+    h = g.relu(g.conv(x, p.he((32, 64, 1, 1)), p.normal(32, 0.01)))
+    h = g.relu(g.conv(h, p.he((32, 32, 3, 3)), p.normal(32, 0.01), pad=1))
+    h3 = g.relu(g.add(g.conv(h, p.he((64, 32, 1, 1)), p.normal(64, 0.01)), x))
+    h = g.relu(g.conv(h3, p.he((48, 64, 3, 3)), p.normal(48, 0.01), stride=2, pad=1))
+    h = g.conv(h, p.he((40, 48, 1, 1)), None)
+    g.mark_output(h)
+    g.mark_output(h3)
+    run_default_pipeline(g)
+    xs = rng_inputs(g)
+    samples = [[models.make_input([2, 64, 14, 14], 500 + i)] for i in range(3)]
+    qp = calibrate_activation_scales(g, samples) + quantize_conv_weights(g)
+    return g, xs, write_spk(g, "mi355x", quant_params=qp)
+
+
+@pytest.mark.parametrize("handoff", ["1", "0"])
+def test_int8_chain_bit_exact(gpu, monkeypatch, handoff):
+    """Every conv int8; with handoff on, each conv whose only reader is the
+    next int8 conv requantizes in its epilogue (the residual source, also a
+    graph output, still writes fp32).  Outputs bit-exact either way."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_I8_HANDOFF", handoff)
+    g, xs, blob = _int8_chain()
+    want = run_oracle(blob, xs)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = [m.get_output(0), m.get_output(1)]
+        names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+    assert len(names) == 5 and all("conv_igemm_i8" in s for s in names)
+    assert sum(",handoff" in s for s in names) == (4 if handoff == "1" else 0)
+    for a_, b_ in zip(got, want):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
+
+
+@pytest.mark.parametrize("handoff", ["1", "0"])
+def test_int8_resnet50_matches_oracle(gpu, monkeypatch, handoff):
+    """A whole INT8 ResNet-50 (32x32 input), every conv int8: logits within
+    the fp32 tolerance (the fp32 ReduceMean / Gemm tail sums in another
+    order) and the same top-1."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_I8_HANDOFF", handoff)
+    g, xs, blob = _int8_network()
+    want = run_oracle(blob, xs)[0]
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = m.get_output(0)
+    assert tnorm_err(got, want) <= FP32_TOL
+    assert (got.reshape(2, -1).argmax(1) == want.reshape(2, -1).argmax(1)).all()
+
+
+def test_int8_handoff_graph_mode_and_fault_path(gpu):
+    """Graph replays of the handoff network equal eager; with a fault event
+    armed (an injection on a node that never fires), every tensor is
+    materialized and the result is unchanged."""
+    from spinnv2_amd.runtime import FaultEvent, Model
+
+    g, xs, blob = _int8_network(batch=1)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        eager = m.get_output(0)
+        m.set_graph_mode(True)
+        for _ in range(3):
+            m.set_input(0, xs[0])
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0), eager)
+        m.set_graph_mode(False)
+        ev = FaultEvent(node_id=0, tensor_id=g.nodes[0].outputs[0], element_index=0, bit_index=0,
+                        invocation_index=1000, seed=0, enabled=1)
+        m.set_fault_event(ev)
+        m.set_input(0, xs[0])
+        m.run()
+        np.testing.assert_array_equal(m.get_output(0), eager)
