@@ -135,7 +135,7 @@ def batch1_latency(depth: int, steps: int, lib) -> float:
     return b1_ms
 
 
-def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64) -> dict:
+def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, node_report: bool = False) -> dict:
     """INT8 ResNet-50: per-channel symmetric int8
     weights, per-tensor activation scales calibrated on 16 seeded single-image
     batches with the repo's fp32 forward, int32 accumulation, reference
@@ -183,6 +183,11 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64) 
     for nid in ops:
         ms, cnt = m.node_time(nid)
         conv_ms += ms / max(cnt, 1)
+        if node_report:
+            n = g.nodes[nid]
+            xs_, ws_ = g.shape(n.inputs[0]), g.tensors[n.inputs[1]].shape
+            log(f"int8 node {nid:3d} {xs_[1]}x{xs_[2]}->{ws_[0]} k{ws_[2]} s{n.attrs['strides'][0]} "
+                f"{m.kernel_name(nid):52s} {ms / max(cnt, 1) * 1e3:8.1f} us {ops[nid] / (ms / max(cnt, 1)) / 1e9:7.1f} TOP/s")
     names = sorted({m.kernel_name(nid).split("<")[0] for nid in ops})
     m.close()
     xin.free()
@@ -242,7 +247,7 @@ def main() -> None:
 
     lib = load_library()
     if args.int8_only:
-        print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps)), flush=True)
+        print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report)), flush=True)
         return
     base = None if args.no_cpu_baseline else cpu_baseline()
 

@@ -58,6 +58,11 @@ struct ConvPlan {
 
 void conv_plan_free(void *p);
 
+// Per-process table of measured tile choices, keyed by layer shape; with
+// SPKV2_TUNE_DB set it is read from and appended to that file.
+bool tuned_lookup(const std::string &key, int *cfg, int *split);
+void tuned_store(const std::string &key, int cfg, int split);
+
 // int8 path entry points (conv_i8.hip)
 int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan);
 int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *plan, int32_t *raw_acc_out);

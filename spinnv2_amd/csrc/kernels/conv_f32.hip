@@ -623,7 +623,7 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
 namespace {
 
 std::mutex g_tune_mu;
-std::map<std::string, std::pair<int, int>> g_tuned;  // key -> (cfg, split request)
+std::map<std::string, std::pair<int, int>> g_tuned;  // key -> (cfg, split request), fp32 and int8 layers
 bool g_tune_db_loaded = false;
 
 // SPKV2_TUNE_DB names a text file of "key cfg split" lines: read once, and
@@ -644,7 +644,7 @@ void load_tune_db_locked() {
     char key[512];
     int cfg = 0, split = 0;
     while (fscanf(f, "%511s %d %d", key, &cfg, &split) == 3)
-        if (cfg >= 0 && cfg < kNumCfgs && split >= 1 && split <= 64) g_tuned[key] = {cfg, split};
+        if (cfg >= 0 && cfg < 64 && split >= 1 && split <= 64) g_tuned[key] = {cfg, split};
     fclose(f);
 }
 
@@ -656,6 +656,26 @@ void store_tune_db_locked(const std::string &key, int cfg, int split) {
         fclose(f);
     }
 }
+
+}  // namespace
+
+bool tuned_lookup(const std::string &key, int *cfg, int *split) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    load_tune_db_locked();
+    auto it = g_tuned.find(key);
+    if (it == g_tuned.end()) return false;
+    *cfg = it->second.first;
+    *split = it->second.second;
+    return true;
+}
+
+void tuned_store(const std::string &key, int cfg, int split) {
+    std::lock_guard<std::mutex> lk(g_tune_mu);
+    g_tuned[key] = {cfg, split};
+    store_tune_db_locked(key, cfg, split);
+}
+
+namespace {
 
 // Device buffers of one tuning session, freed on scope exit.
 struct TuneBuffers {
@@ -680,16 +700,7 @@ struct TuneBuffers {
 // every context sees the same choice for the same layer.  Returns false
 // when the device could not be used (the caller then trusts the model).
 bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
-    {
-        std::lock_guard<std::mutex> lk(g_tune_mu);
-        load_tune_db_locked();
-        auto it = g_tuned.find(gs.key);
-        if (it != g_tuned.end()) {
-            *cfg_out = it->second.first;
-            *split_out = it->second.second;
-            return true;
-        }
-    }
+    if (tuned_lookup(gs.key, cfg_out, split_out) && *cfg_out < kNumCfgs) return true;
     const int Ntot = g.N * g.OH * g.OW;
     struct Cand {
         int cfg, split;
@@ -782,9 +793,7 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     }
     *cfg_out = keep[0].cfg;
     *split_out = keep[0].split;
-    std::lock_guard<std::mutex> lk(g_tune_mu);
-    g_tuned[gs.key] = {keep[0].cfg, keep[0].split};
-    store_tune_db_locked(gs.key, keep[0].cfg, keep[0].split);
+    tuned_store(gs.key, keep[0].cfg, keep[0].split);
     return true;
 }
 

@@ -622,8 +622,6 @@ std::vector<int> build_i8_koff(const ConvGeom &g, const I8Layout &L, int k_tiles
     return koff;
 }
 
-std::mutex g_i8_mu;
-std::map<std::string, std::pair<int, int>> g_i8_tuned;
 
 struct DevBufs {
     std::vector<void *> p;
@@ -647,15 +645,7 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     char key[256];
     snprintf(key, sizeof(key), "i8|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d", g.N, g.C, g.H, g.W, g.M, g.KH, g.KW,
              g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, g.has_bias ? 1 : 0, g.has_res ? 1 : 0, g.act);
-    {
-        std::lock_guard<std::mutex> lk(g_i8_mu);
-        auto it = g_i8_tuned.find(key);
-        if (it != g_i8_tuned.end()) {
-            *cfg_out = it->second.first;
-            *split_out = it->second.second;
-            return true;
-        }
-    }
+    if (tuned_lookup(key, cfg_out, split_out) && *cfg_out < kNumI8Cfgs) return true;
     const int Ntot = g.N * g.OH * g.OW;
     const int Kbytes = L.groups * 16;
     struct Cand {
@@ -754,8 +744,7 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     }
     *cfg_out = keep[0].cfg;
     *split_out = keep[0].split;
-    std::lock_guard<std::mutex> lk(g_i8_mu);
-    g_i8_tuned[key] = {keep[0].cfg, keep[0].split};
+    tuned_store(key, keep[0].cfg, keep[0].split);
     return true;
 }
 
