@@ -54,6 +54,11 @@ struct ConvPlan {
     bool y_needed;
     // Consumer side: the padded NHWC int8 input its producer writes (owned).
     int8_t *q_in;
+    // fp32 handoff, the same for the zero-padded NCHW input of a padded
+    // conv: producer side (not owned) and consumer side (owned).
+    float *pad_out;
+    int pad_Hp, pad_Wp, pad_pt, pad_pl;
+    float *pad_in;
 };
 
 void conv_plan_free(void *p);

@@ -88,6 +88,7 @@ void conv_plan_free(void *p) {
     if (plan->ktab) (void)hipFree(plan->ktab);
     if (plan->scales) (void)hipFree(plan->scales);
     if (plan->q_in) (void)hipFree(plan->q_in);
+    if (plan->pad_in) (void)hipFree(plan->pad_in);
     delete plan;
 }
 
@@ -118,6 +119,10 @@ struct IgemmArgs {
     int m_tiles, k_tiles, kt_per_split;
     int act;
     float alpha;
+    // handoff: also store the output into the consuming conv's zero-padded
+    // input (NCHW, Hp x Wp planes); y may then be null (no other reader)
+    float *__restrict__ yp;
+    int yp_bytes, yp_Wp, yp_pt, yp_pl, yp_plane;
 };
 
 
@@ -298,12 +303,28 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 const int sp = n - img * a.OHW;
                 obase[j] = n < a.Ntot ? (img * a.M * a.OHW + sp) * 4 : kOobOffset;
             }
+            float *const any = a.y ? a.y : a.yp;
             const __amdgpu_buffer_rsrc_t yrs =
-                __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), a.y_bytes, kBufferWord3);
+                __builtin_amdgcn_make_buffer_rsrc(any, static_cast<short>(0), a.y ? a.y_bytes : 0, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t prs =
+                __builtin_amdgcn_make_buffer_rsrc(any, static_cast<short>(0), a.yp ? a.yp_bytes : 0, kBufferWord3);
             const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float *>(a.res ? a.res : a.y), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufferWord3);
+                const_cast<float *>(a.res ? a.res : any), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufferWord3);
             const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<float *>(a.bias ? a.bias : a.y), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufferWord3);
+                const_cast<float *>(a.bias ? a.bias : any), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufferWord3);
+            // handoff target: this lane's pixel in the padded planes
+            int pbase[TN];
+            const int plane4 = a.yp_plane * 4;
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const int n = nt * BN + (wn * TN + j) * 32 + row;
+                const int img = n / a.OHW;
+                const int sp = n - img * a.OHW;
+                const int oh = sp / a.OW;
+                const int ow = sp - oh * a.OW;
+                pbase[j] = n < a.Ntot ? (img * a.M * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl) * 4
+                                      : kOobOffset;
+            }
             // one 32x32 block at a time: its 16 bias and 16 residual loads are
             // all in flight before the first use
 #pragma unroll
@@ -337,13 +358,23 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 #pragma unroll
                         for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
                     }
+                    if (a.yp) {
 #pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                        // __float_as_uint takes the element by value (a bit
-                        // cast applied to a vector element reads element 0)
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
-                                                              m < a.M ? obase[j] + m * ohw4 : kOobOffset, 0, 0);
+                        for (int r = 0; r < 16; r++) {
+                            const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), prs,
+                                                                  m < a.M ? pbase[j] + m * plane4 : kOobOffset, 0, 0);
+                        }
+                    }
+                    if (a.y) {
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                            // __float_as_uint takes the element by value (a bit
+                            // cast applied to a vector element reads element 0)
+                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
+                                                                  m < a.M ? obase[j] + m * ohw4 : kOobOffset, 0, 0);
+                        }
                     }
                 }
             }
@@ -359,7 +390,7 @@ template <int VEC>
 __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__ ws, int splitk, int M, int Ntot,
                                                        int OHW, const float *__restrict__ bias,
                                                        const float *__restrict__ res, float *__restrict__ y, int act,
-                                                       float alpha) {
+                                                       float alpha, IgemmArgs h) {
     typedef float vec_t __attribute__((ext_vector_type(VEC)));
     const size_t total = static_cast<size_t>(M) * Ntot;
     const size_t groups = total / VEC;
@@ -387,7 +418,12 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             const int sp = n + e - img * OHW;
             const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
             if (res) o += res[yi];
-            y[yi] = apply_act(o, act);
+            o = apply_act(o, act);
+            if (h.yp) {
+                const int oh = sp / h.OW, ow = sp - (sp / h.OW) * h.OW;
+                h.yp[(static_cast<size_t>(img) * M + m) * h.yp_plane + (oh + h.yp_pt) * h.yp_Wp + ow + h.yp_pl] = o;
+            }
+            if (y) y[yi] = o;
         }
     }
 }
@@ -578,7 +614,7 @@ std::vector<int> build_koff(const GatherSpec &gs, int BK) {
 // an already prepared (padded) B source, then the split-K epilogue.
 static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
                         int x_bytes, int x_img_stride, const float *wpack, const int *koff, const float *bias,
-                        const float *res, float *y, float alpha, float *ws) {
+                        const float *res, float *y, float alpha, float *ws, const ConvPlan *handoff = nullptr) {
     const TileCfg &t = kCfgs[cfg];
     IgemmArgs a{};
     a.x = xs;
@@ -602,6 +638,14 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     a.act = g.act;
     a.alpha = alpha;
     a.ws = tc.splitk > 1 ? ws : nullptr;
+    if (handoff) {
+        a.yp = handoff->pad_out;
+        a.yp_plane = handoff->pad_Hp * handoff->pad_Wp;
+        a.yp_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.M * a.yp_plane * 4);
+        a.yp_Wp = handoff->pad_Wp;
+        a.yp_pt = handoff->pad_pt;
+        a.yp_pl = handoff->pad_pl;
+    }
     a.y_bytes = static_cast<int>(g.y_elems * 4);
     a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
     dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
@@ -611,10 +655,10 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
         const size_t total = static_cast<size_t>(g.M) * a.Ntot;
         if (a.Ntot % 4 == 0)
             hipLaunchKernelGGL(splitk_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, ws, tc.splitk,
-                               g.M, a.Ntot, a.OHW, bias, res, y, g.act, alpha);
+                               g.M, a.Ntot, a.OHW, bias, res, y, g.act, alpha, a);
         else
             hipLaunchKernelGGL(splitk_epilogue<1>, dim3(grid_for(total, 256)), dim3(256), 0, st, ws, tc.splitk, g.M,
-                               a.Ntot, a.OHW, bias, res, y, g.act, alpha);
+                               a.Ntot, a.OHW, bias, res, y, g.act, alpha, a);
         if (int rc = launch_status("splitk_epilogue")) return rc;
     }
     return 0;
@@ -971,7 +1015,14 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     if (ctx->workspace_size < p->workspace) return SPKV2_E_UNSUPPORTED;
     const float *xs = x;
     int x_bytes = static_cast<int>(g.x_elems * 4);
-    if (p->padded) {
+    // a fault event may change a tensor after its producer ran: then every
+    // tensor is materialized and padded here
+    const bool handoff = !ctx->fault_event.enabled;
+    if (p->padded && p->pad_in && handoff) {
+        xs = p->pad_in;  // written, zero halo included, by the producer's epilogue
+        x_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.C * p->Hp * p->Wp * 4);
+        x_img_stride = g.C * p->Hp * p->Wp;
+    } else if (p->padded) {
         float *xp = reinterpret_cast<float *>(ctx->workspace);
         const unsigned planes = static_cast<unsigned>(g.N * g.C);
         hipLaunchKernelGGL(pad_nchw, dim3(planes), dim3(256), 0, ctx->stream, x, xp, g.H, g.W, p->Hp, p->Wp, p->pt,
@@ -982,9 +1033,53 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
         x_img_stride = g.C * p->Hp * p->Wp;
     }
     float *ws = reinterpret_cast<float *>(ctx->workspace + p->pad_bytes);
+    const bool give = p->pad_out && handoff;
     return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
-                        static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res, y, alpha,
-                        ws);
+                        static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
+                        give && !p->y_needed ? nullptr : y, alpha, ws, give ? p : nullptr);
+}
+
+// fp32 handoff.  When this padded conv's input is the only output of an
+// earlier fp32 implicit-GEMM conv, that conv stores its result straight into
+// a zero-padded buffer owned by this plan (halo zeroed once here, never
+// written), and this conv skips its padding pass.  The producer still writes
+// the unpadded tensor when anything else reads it.  Packages with a
+// protection plan keep every tensor as written by the reference.
+static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {
+    if (!plan->padded || ctx->protection_count > 0) return 0;
+    if (const char *e = getenv("SPKV2_PAD_HANDOFF"))
+        if (e[0] == '0') return 0;
+    const uint32_t t = node->inputs[0];
+    const Spkv2NodeRecord *prod = nullptr;
+    int readers = 0;
+    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *n = &ctx->node_records[i];
+        for (uint16_t k = 0; k < n->input_count; k++)
+            if (n->inputs[k] == t) readers++;
+        if (n->id < node->id)
+            for (uint16_t k = 0; k < n->output_count; k++)
+                if (n->outputs[k] == t) prod = n;
+    }
+    if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
+    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
+    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
+    if (!pp || pp->path != CONV_IGEMM_F32 || pp->pad_out) return 0;
+    const ConvGeom &g = plan->g;
+    if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
+    bool is_output = false;
+    for (size_t i = 0; i < ctx->output_count; i++)
+        if (ctx->output_ids[i] == t) is_output = true;
+    const size_t bytes = static_cast<size_t>(g.N) * g.C * plan->Hp * plan->Wp * 4;
+    if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->pad_in), bytes), "hipMalloc pad handoff"))
+        return rc;
+    if (int rc = hip_check(hipMemset(plan->pad_in, 0, bytes), "hipMemset pad handoff")) return rc;
+    pp->pad_out = plan->pad_in;
+    pp->pad_Hp = plan->Hp;
+    pp->pad_Wp = plan->Wp;
+    pp->pad_pt = plan->pt;
+    pp->pad_pl = plan->pl;
+    pp->y_needed = readers > 1 || is_output;
+    return 0;
 }
 
 int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res, float *y,
@@ -1052,7 +1147,8 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
             rc = SPKV2_E_UNSUPPORTED;  // weights produced at run time
         } else {
             rc = plan_igemm_f32(ctx->stream, g, w, plan);
-            if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan));
+            if (rc == 0) rc = setup_pad_handoff(ctx, node, plan);
+            if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan) + (plan->pad_in ? "+handoff" : ""));
         }
     } else {
         plan->path = CONV_DIRECT_F32;

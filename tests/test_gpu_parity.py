@@ -356,3 +356,25 @@ def test_int8_handoff_graph_mode_and_fault_path(gpu):
         m.set_input(0, xs[0])
         m.run()
         np.testing.assert_array_equal(m.get_output(0), eager)
+
+
+def test_fp32_pad_handoff_is_bit_identical(gpu, monkeypatch):
+    """A 1x1 conv feeding a padded 3x3 conv stores straight into the 3x3
+    conv's zero-padded input; outputs equal the unfused path bit for bit,
+    and the oracle within tolerance (ResNet-50 at 64x64: every bottleneck)."""
+    from spinnv2_amd.runtime import Model
+
+    g = models.resnet(50, 2, image=64, classes=10)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SPKV2_PAD_HANDOFF", flag)
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            outs[flag] = m.get_output(0)
+            names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+        assert sum("+handoff" in s for s in names) == (16 if flag == "1" else 0)
+    np.testing.assert_array_equal(outs["1"], outs["0"])
+    assert tnorm_err(outs["1"], run_oracle(blob, xs)[0]) <= FP32_TOL
