@@ -28,8 +28,10 @@ _ATTR = struct.Struct("<Iiii4i2i2i2i2i2fii8i3i")
 _QP = struct.Struct("<IHHIQ")
 
 OPS = {1: "Add", 2: "Conv", 3: "Flatten", 4: "Gemm", 5: "MaxPool", 6: "Relu", 7: "Softmax", 8: "Mul", 9: "Sub",
-       10: "Div", 11: "Mod", 12: "Sigmoid", 13: "Reshape", 15: "Concat", 17: "ReduceMean", 18: "ReduceMax",
-       19: "MatMul", 20: "Resize", 22: "Unsqueeze", 25: "Cast", 28: "AveragePool", 29: "GlobalAveragePool"}
+       10: "Div", 11: "Mod", 12: "Sigmoid", 13: "Reshape", 14: "Transpose", 15: "Concat", 16: "Split",
+       17: "ReduceMean", 18: "ReduceMax", 19: "MatMul", 20: "Resize", 21: "Tile", 22: "Unsqueeze",
+       23: "GatherElements", 24: "TopK", 25: "Cast", 26: "Slice", 27: "Gather", 28: "AveragePool",
+       29: "GlobalAveragePool"}
 
 
 @dataclass
@@ -83,7 +85,7 @@ class Package:
             a = _ATTR.unpack_from(blob, aoff + f[17])
             attr = dict(op=a[0], axis=a[1], group=a[2], act=a[3], pads=a[4:8], strides=a[8:10], kernel=a[10:12],
                         dil=a[12:14], trans_a=a[14], trans_b=a[15], alpha=a[16], beta=a[17], extra_count=a[18],
-                        keepdims=a[19], extra=a[20:28])
+                        keepdims=a[19], extra=a[20:28], largest=a[28], sorted=a[29], cast_to=a[30])
             self.nodes.append(NodeInfo(f[0], f[1], list(f[5:5 + nin]), list(f[13:13 + nout]), attr))
         woff = secs[6][0]
         self.weights = {}
@@ -279,6 +281,92 @@ class OracleExecutor:
     def _concat(self, n, vals):
         ax = n.attr["axis"] % len(self._shape(n.outputs[0]))
         vals[n.outputs[0]] = np.concatenate([vals[t] for t in n.inputs], axis=ax)
+
+    # ---- indexing / layout (integer index arithmetic, restated with numpy) ----
+    def _transpose(self, n, vals):
+        # reference shape/transpose.c:14-18: x coord perm[d] = y coord d
+        x = vals[n.inputs[0]]
+        a = n.attr
+        perm = list(a["extra"][:a["extra_count"]]) if a["extra_count"] > 0 else list(range(x.ndim))
+        vals[n.outputs[0]] = np.ascontiguousarray(np.transpose(x, perm))
+
+    def _tile(self, n, vals):
+        # reference shape/tile.c:13-19: x coord = y coord mod x dim
+        x = vals[n.inputs[0]]
+        y_shape = self._shape(n.outputs[0])
+        idx = np.ix_(*[np.arange(ys) % xs for ys, xs in zip(y_shape, x.shape)])
+        vals[n.outputs[0]] = np.ascontiguousarray(x[idx])
+
+    def _split(self, n, vals):
+        # reference tensor/split.c:15-27: consecutive blocks along axis
+        x = vals[n.inputs[0]]
+        ax = n.attr["axis"] % x.ndim
+        start = 0
+        for t in n.outputs:
+            size = self._shape(t)[ax]
+            vals[t] = np.ascontiguousarray(np.take(x, np.arange(start, start + size), axis=ax))
+            start += size
+
+    def _slice(self, n, vals):
+        # reference tensor/slice.c:12-49, first value of each parameter tensor
+        x = vals[n.inputs[0]]
+        start = int(vals[n.inputs[1]].ravel()[0])
+        end = int(vals[n.inputs[2]].ravel()[0])
+        axis = int(vals[n.inputs[3]].ravel()[0]) if len(n.inputs) > 3 else 0
+        step = int(vals[n.inputs[4]].ravel()[0]) if len(n.inputs) > 4 else 1
+        if axis < 0:
+            axis += x.ndim
+        dim = x.shape[axis]
+        if start < 0:
+            start += dim
+        if end < 0:
+            end += dim
+        if end > dim:
+            end = dim
+        if start < 0:
+            start = 0
+        out = (end - start + step - 1) // step
+        vals[n.outputs[0]] = np.ascontiguousarray(np.take(x, start + step * np.arange(out), axis=axis))
+
+    def _gather(self, n, vals):
+        # reference tensor/gather.c:28-36: (int)index, negative + dim
+        data, idx = vals[n.inputs[0]], vals[n.inputs[1]]
+        ax = n.attr["axis"] % data.ndim
+        ix = idx.astype(np.float32).astype(np.int64)  # C float -> int truncates
+        ix = np.where(ix < 0, ix + data.shape[ax], ix)
+        vals[n.outputs[0]] = np.ascontiguousarray(np.take(data, ix, axis=ax)).reshape(self._shape(n.outputs[0]))
+
+    def _gatherelements(self, n, vals):
+        # reference tensor/gather_elements.c:17-25
+        data, idx = vals[n.inputs[0]], vals[n.inputs[1]]
+        ax = n.attr["axis"] % data.ndim
+        ix = idx.astype(np.int64)
+        ix = np.where(ix < 0, ix + data.shape[ax], ix)
+        vals[n.outputs[0]] = np.ascontiguousarray(np.take_along_axis(data, ix, axis=ax))
+
+    def _topk(self, n, vals):
+        # reference tensor/topk.c via oracle_topk_row, one (outer, inner) row at a time
+        x = np.ascontiguousarray(vals[n.inputs[0]], dtype=np.float32)
+        k = int(vals[n.inputs[1]].ravel()[0])
+        ax = n.attr["axis"] % x.ndim
+        dim = x.shape[ax]
+        k = min(k, dim)
+        outer = int(np.prod(x.shape[:ax]))
+        inner = int(np.prod(x.shape[ax + 1:]))
+        values = np.zeros(self._shape(n.outputs[0]), np.float32)
+        indices = np.zeros(self._shape(n.outputs[1]), np.float32)
+        xv, vv, iv = x.reshape(outer, dim, inner), values.reshape(outer, k, inner), indices.reshape(outer, k, inner)
+        fp = ctypes.POINTER(ctypes.c_float)
+        for o in range(outer):
+            for i in range(inner):
+                # the C routine walks the row with stride `inner`
+                self.lib.oracle_topk_row(
+                    ctypes.cast(xv.ctypes.data + 4 * (o * dim * inner + i), fp), ctypes.c_size_t(inner), dim, k,
+                    int(n.attr["largest"] != 0),
+                    ctypes.cast(vv.ctypes.data + 4 * (o * k * inner + i), fp),
+                    ctypes.cast(iv.ctypes.data + 4 * (o * k * inner + i), fp))
+        vals[n.outputs[0]] = values
+        vals[n.outputs[1]] = indices
 
 
 def _setup_signatures() -> None:

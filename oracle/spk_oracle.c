@@ -365,3 +365,70 @@ int oracle_conv2d_int8(const float *x, const int8_t *wq, const float *w_scales, 
     if (!acc_out) free(acc);
     return 0;
 }
+
+/* ------------------------------------------------------------------ TopK */
+
+typedef struct {
+    float v;
+    uint32_t idx;
+} OracleTopkPair;
+
+/* reference tensor/topk.c:7-17 (min-heap) and 19-29 (max-heap) */
+static void topk_sift(OracleTopkPair *h, size_t n, size_t i, int min_heap) {
+    for (;;) {
+        size_t l = 2 * i + 1, r = 2 * i + 2, m = i;
+        if (min_heap) {
+            if (l < n && h[l].v < h[m].v) m = l;
+            if (r < n && h[r].v < h[m].v) m = r;
+        } else {
+            if (l < n && h[l].v > h[m].v) m = l;
+            if (r < n && h[r].v > h[m].v) m = r;
+        }
+        if (m == i) break;
+        OracleTopkPair t = h[i];
+        h[i] = h[m];
+        h[m] = t;
+        i = m;
+    }
+}
+
+/* reference tensor/topk.c:31-48: best first, ties by smaller index */
+static int topk_cmp_desc(const void *a, const void *b) {
+    float av = ((const OracleTopkPair *)a)->v, bv = ((const OracleTopkPair *)b)->v;
+    if (av < bv) return 1;
+    if (av > bv) return -1;
+    return ((const OracleTopkPair *)a)->idx < ((const OracleTopkPair *)b)->idx ? -1 : 1;
+}
+
+static int topk_cmp_asc(const void *a, const void *b) {
+    float av = ((const OracleTopkPair *)a)->v, bv = ((const OracleTopkPair *)b)->v;
+    if (av < bv) return -1;
+    if (av > bv) return 1;
+    return ((const OracleTopkPair *)a)->idx < ((const OracleTopkPair *)b)->idx ? -1 : 1;
+}
+
+void oracle_topk_row(const float *x, size_t inner, int dim, int k, int largest, float *values, float *indices) {
+    if (k <= 0 || dim <= 0) return;
+    if (k > dim) k = dim;
+    OracleTopkPair *h = (OracleTopkPair *)malloc((size_t)k * sizeof(OracleTopkPair));
+    if (!h) return;
+    for (int d = 0; d < k; d++) {
+        h[d].v = x[(size_t)d * inner];
+        h[d].idx = (uint32_t)d;
+    }
+    for (long i = (long)(k / 2) - 1; i >= 0; i--) topk_sift(h, (size_t)k, (size_t)i, largest);
+    for (int d = k; d < dim; d++) {
+        const float v = x[(size_t)d * inner];
+        if (largest ? (v > h[0].v) : (v < h[0].v)) {
+            h[0].v = v;
+            h[0].idx = (uint32_t)d;
+            topk_sift(h, (size_t)k, 0, largest);
+        }
+    }
+    qsort(h, (size_t)k, sizeof(OracleTopkPair), largest ? topk_cmp_desc : topk_cmp_asc);
+    for (int j = 0; j < k; j++) {
+        values[(size_t)j * inner] = h[j].v;
+        indices[(size_t)j * inner] = (float)h[j].idx;
+    }
+    free(h);
+}

@@ -62,6 +62,12 @@ void oracle_reduce_f32(const float *x, const uint32_t *x_shape, int rank, uint32
 /* reference kernels/reference/shape/resize.c:5-31 (nearest, floor) */
 void oracle_resize_nearest_f32(const float *x, float *y, int N, int C, int H, int W, int OH, int OW);
 
+/* reference kernels/reference/tensor/topk.c:56-121 for one row of `dim`
+ * elements at x[d*inner]: heap selection of the k largest (largest=1) or
+ * smallest, then sorted best first, ties by smaller index; values and
+ * indices written at out[j*inner] */
+void oracle_topk_row(const float *x, size_t inner, int dim, int k, int largest, float *values, float *indices);
+
 /* ---- INT8 path (reference kernels/optimized/conv/conv_int8.c) ---- */
 
 /* conv_int8.c:22-56: q = sat8(round(x * (1/scale))), half-to-even for the

@@ -37,6 +37,14 @@ int global_avgpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int softmax_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int reduce_run(Spkv2Context *, const Spkv2NodeRecord *, void *);  // ReduceMean ReduceMax
 int resize_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+// indexing / layout (tensor_ops.hip)
+int transpose_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int tile_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int split_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int slice_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int gather_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int gather_elements_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int topk_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 
 // reliability helpers used by the executor
 int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);

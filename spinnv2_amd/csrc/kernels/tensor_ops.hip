@@ -1,0 +1,464 @@
+// Indexing and layout ops of the YOLO op set: Split, Slice, Transpose, Tile,
+// Gather, GatherElements, TopK.  Reference semantics:
+//   runtime/kernels/reference/tensor/split.c, slice.c, gather.c,
+//   gather_elements.c, topk.c and shape/transpose.c, shape/tile.c.
+// Tensors are float (index tensors hold integral floats, as in the
+// reference).  Every kernel is a grid-stride loop in which consecutive lanes
+// write consecutive output elements; source addresses come from per-node
+// stride tables computed on the host.  Scalar parameters the reference reads
+// from constant input tensors (Slice starts/ends/axes/steps, TopK k) are read
+// from the package on the host; index tensors (Gather, GatherElements) are
+// read on the device, so they may be produced by earlier nodes (TopK).
+// Out-of-range indices, undefined in the reference, read 0 here.
+#include <algorithm>
+#include <cstring>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace spk::kern {
+
+namespace {
+
+constexpr int kRank = 8;
+
+struct StrideMap {
+    int rank;
+    int64_t ydim[kRank];    // output shape
+    int64_t src[kRank];     // source element stride per output dim (Transpose), or source dims (Tile)
+    int64_t sstride[kRank]; // source strides (Tile)
+};
+
+// y[i] = x[sum_d coord_d(i) * src[d]]  (Transpose: src = input stride of
+// the permuted axis)
+__global__ void __launch_bounds__(256) permute_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n,
+                                                      StrideMap m) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        size_t t = i;
+        int64_t off = 0;
+        for (int d = m.rank - 1; d >= 0; d--) {
+            const int64_t c = static_cast<int64_t>(t % m.ydim[d]);
+            t /= m.ydim[d];
+            off += c * m.src[d];
+        }
+        y[i] = x[off];
+    }
+}
+
+// y[i] = x[coords(i) mod xdim]  (reference shape/tile.c:13-19)
+__global__ void __launch_bounds__(256) tile_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n,
+                                                   StrideMap m) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        size_t t = i;
+        int64_t off = 0;
+        for (int d = m.rank - 1; d >= 0; d--) {
+            const int64_t c = static_cast<int64_t>(t % m.ydim[d]);
+            t /= m.ydim[d];
+            off += (c % m.src[d]) * m.sstride[d];
+        }
+        y[i] = x[off];
+    }
+}
+
+// Block copy: y[o * y_stride + j] = x[x_base + o * x_stride + j] for j < block
+// (Split outputs, Slice with step 1).
+__global__ void __launch_bounds__(256) block_copy(const float *__restrict__ x, float *__restrict__ y, size_t outer,
+                                                  size_t block, size_t x_stride, size_t x_base, size_t y_stride) {
+    const size_t n = outer * block;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t o = i / block, j = i - o * block;
+        y[o * y_stride + j] = x[x_base + o * x_stride + j];
+    }
+}
+
+// Slice with a step: y[(o*out + s)*inner + t] = x[(o*dim + start + s*step)*inner + t]
+__global__ void __launch_bounds__(256) slice_kernel(const float *__restrict__ x, float *__restrict__ y, size_t outer,
+                                                    int64_t out, int64_t dim, int64_t start, int64_t step, size_t inner) {
+    const size_t n = outer * static_cast<size_t>(out) * inner;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t t = i % inner;
+        const size_t q = i / inner;
+        const int64_t s = static_cast<int64_t>(q % out);
+        const size_t o = q / out;
+        y[i] = x[(o * dim + start + s * step) * inner + t];
+    }
+}
+
+// Gather (reference tensor/gather.c:28-36):
+// y[(o*J + j)*inner + t] = data[(o*dim + ix_j)*inner + t], ix = (int)idx, +dim if negative
+__global__ void __launch_bounds__(256) gather_kernel(const float *__restrict__ data, const float *__restrict__ idx,
+                                                     float *__restrict__ y, size_t outer, size_t J, int64_t dim,
+                                                     size_t inner) {
+    const size_t n = outer * J * inner;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t t = i % inner;
+        const size_t q = i / inner;
+        const size_t j = q % J;
+        const size_t o = q / J;
+        int ix = static_cast<int>(idx[j]);
+        if (ix < 0) ix += static_cast<int>(dim);
+        y[i] = (ix >= 0 && ix < dim) ? data[(o * dim + ix) * inner + t] : 0.0f;
+    }
+}
+
+// GatherElements (reference tensor/gather_elements.c:17-25): y has the
+// index tensor's shape; coordinate `axis` is replaced by the index value.
+__global__ void __launch_bounds__(256) gather_elements_kernel(const float *__restrict__ data,
+                                                              const float *__restrict__ idx, float *__restrict__ y,
+                                                              size_t n, StrideMap m, int axis, int64_t dim) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
+        size_t t = i;
+        int64_t off = 0;
+        for (int d = m.rank - 1; d >= 0; d--) {
+            const int64_t c = static_cast<int64_t>(t % m.ydim[d]);
+            t /= m.ydim[d];
+            if (d != axis) off += c * m.sstride[d];
+        }
+        int g = static_cast<int>(idx[i]);
+        if (g < 0) g += static_cast<int>(dim);
+        y[i] = (g >= 0 && g < dim) ? data[off + static_cast<int64_t>(g) * m.sstride[axis]] : 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------- TopK
+
+constexpr int kTopkMaxK = 1024;
+
+// order-preserving key of a float: larger float -> larger unsigned
+__device__ __forceinline__ uint32_t fkey(float v) {
+    const uint32_t u = __float_as_uint(v);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+struct HeapPair {
+    float v;
+    uint32_t idx;
+};
+
+// The reference's selection, replayed exactly by one thread (used only when
+// values tie across the k-th place, where the heap's history decides which
+// of the tied elements survive): heap of the first k, sift-down from k/2-1,
+// then every later element replaces the root when strictly better
+// (reference tensor/topk.c:71-101).
+__device__ void topk_heap_replay(const float *__restrict__ x, size_t base, size_t inner, int dim, int k, int largest,
+                                 HeapPair *h) {
+    auto better = [&](float a, float b) { return largest ? (a < b) : (a > b); };  // "a sinks below b"
+    auto sift = [&](int i) {
+        for (;;) {
+            int l = 2 * i + 1, r = 2 * i + 2, m = i;
+            if (l < k && better(h[l].v, h[m].v)) m = l;
+            if (r < k && better(h[r].v, h[m].v)) m = r;
+            if (m == i) break;
+            const HeapPair t = h[i];
+            h[i] = h[m];
+            h[m] = t;
+            i = m;
+        }
+    };
+    for (int d = 0; d < k; d++) h[d] = HeapPair{x[base + static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
+    for (int i = k / 2 - 1; i >= 0; i--) sift(i);
+    for (int d = k; d < dim; d++) {
+        const float v = x[base + static_cast<size_t>(d) * inner];
+        if (largest ? (v > h[0].v) : (v < h[0].v)) {
+            h[0] = HeapPair{v, static_cast<uint32_t>(d)};
+            sift(0);
+        }
+    }
+}
+
+// One workgroup per (outer, inner) row.  Radix select over order-preserving
+// keys finds the k-th best value T; when exactly k elements are at least as
+// good as T (no tie straddles the k-th place, the usual case) they are the
+// reference's selection; otherwise the reference's heap is replayed.  The
+// selection is then sorted by (value, best first; index ascending), the
+// reference's comparator (tensor/topk.c:28-41), with a bitonic sort in LDS.
+__global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, float *__restrict__ values,
+                                                   float *__restrict__ indices, size_t inner, int dim, int k,
+                                                   int largest) {
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_remaining, s_count, s_ambiguous;
+    __shared__ unsigned long long keys[kTopkMaxK];
+    __shared__ HeapPair heap[kTopkMaxK];
+    const size_t row = blockIdx.x;
+    const size_t o = row / inner, in = row % inner;
+    const size_t base = o * static_cast<size_t>(dim) * inner + in;
+    const int tid = threadIdx.x;
+    // -0 and +0 compare equal in the reference: give them one key
+    auto key_of = [&](float v) -> uint32_t {
+        const uint32_t kk = fkey(v == 0.0f ? 0.0f : v);
+        return largest ? kk : ~kk;
+    };
+
+    uint32_t prefix = 0, mask = 0, remaining = static_cast<uint32_t>(k), eq_count = 0;
+    for (int pass = 0; pass < 4; pass++) {
+        const int shift = 24 - 8 * pass;
+        hist[tid] = 0;
+        __syncthreads();
+        for (int d = tid; d < dim; d += 256) {
+            const uint32_t kk = key_of(x[base + static_cast<size_t>(d) * inner]);
+            if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t cum = 0;
+            int digit = 0;
+            for (int b = 255; b >= 0; b--) {
+                if (cum + hist[b] >= remaining) {
+                    digit = b;
+                    break;
+                }
+                cum += hist[b];
+            }
+            s_prefix = prefix | (static_cast<uint32_t>(digit) << shift);
+            s_remaining = remaining - cum;
+            s_count = hist[digit];
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        remaining = s_remaining;
+        eq_count = s_count;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    // T = prefix; `remaining` of the eq_count elements equal to T are needed
+    const bool ambiguous = eq_count != remaining;
+    int kp = 1;
+    while (kp < k) kp <<= 1;
+    for (int i = tid; i < kp; i += 256) keys[i] = 0ull;  // padding sorts last
+    if (tid == 0) s_count = 0;
+    __syncthreads();
+    if (!ambiguous) {
+        for (int d = tid; d < dim; d += 256) {
+            const uint32_t kk = key_of(x[base + static_cast<size_t>(d) * inner]);
+            if (kk >= prefix) {
+                const uint32_t slot = atomicAdd(&s_count, 1u);
+                keys[slot] = (static_cast<unsigned long long>(kk) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(d));
+            }
+        }
+    } else if (tid == 0) {
+        topk_heap_replay(x, base, inner, dim, k, largest, heap);
+        for (int i = 0; i < k; i++)
+            keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
+    }
+    __syncthreads();
+    // bitonic sort, descending
+    for (int size = 2; size <= kp; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < kp; i += 256) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const unsigned long long a = keys[i], b = keys[j];
+                    if (desc ? (a < b) : (a > b)) {
+                        keys[i] = b;
+                        keys[j] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int j = tid; j < k; j += 256) {
+        const uint32_t d = 0xFFFFFFFFu - static_cast<uint32_t>(keys[j] & 0xFFFFFFFFull);
+        const size_t out = (o * static_cast<size_t>(k) + j) * inner + in;
+        values[out] = x[base + static_cast<size_t>(d) * inner];
+        indices[out] = static_cast<float>(d);
+    }
+}
+
+void shape_of(const Spkv2TensorRecord *r, int64_t *dims) {
+    for (int i = 0; i < kRank; i++) dims[i] = i < r->rank ? r->shape[i] : 1;
+}
+
+void strides_of(const Spkv2TensorRecord *r, int64_t *st) {
+    int64_t s = 1;
+    for (int i = r->rank - 1; i >= 0; i--) {
+        st[i] = s;
+        s *= r->shape[i];
+    }
+}
+
+int norm_axis(int axis, int rank) { return axis < 0 ? axis + rank : axis; }
+
+// first value of a constant float tensor (from the package), or `fallback`
+// when the input is absent
+bool const_scalar(Spkv2Context *ctx, const Spkv2NodeRecord *node, int input, float *out) {
+    if (node->input_count <= input || node->inputs[input] == 0xFFFFu) return false;
+    const uint8_t *h = host_weight_data(ctx, node->inputs[input]);
+    if (!h) return false;
+    memcpy(out, h, sizeof(float));
+    return true;
+}
+
+}  // namespace
+
+int transpose_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]), *yr = rec(ctx, node->outputs[0]);
+    if (xr->rank > kRank) return -11;
+    StrideMap m{};
+    m.rank = yr->rank;
+    shape_of(yr, m.ydim);
+    int64_t xs[kRank];
+    strides_of(xr, xs);
+    // reference shape/transpose.c:14-18: x coord perm[d] = y coord d
+    for (int d = 0; d < xr->rank; d++) {
+        const int src_axis = attr.extra_count > 0 ? attr.extra[d] : d;
+        if (src_axis < 0 || src_axis >= xr->rank) return -11;
+        m.src[d] = xs[src_axis];
+    }
+    const size_t n = elem_count(yr);
+    if (n == 0) return 0;
+    set_kernel_name(ctx, node, "transpose");
+    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]), n, m);
+    return launch_status("transpose");
+}
+
+int tile_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]), *yr = rec(ctx, node->outputs[0]);
+    if (xr->rank != yr->rank || xr->rank > kRank) return -11;
+    StrideMap m{};
+    m.rank = yr->rank;
+    shape_of(yr, m.ydim);
+    shape_of(xr, m.src);
+    strides_of(xr, m.sstride);
+    const size_t n = elem_count(yr);
+    if (n == 0) return 0;
+    set_kernel_name(ctx, node, "tile");
+    hipLaunchKernelGGL(tile_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]), n, m);
+    return launch_status("tile");
+}
+
+int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    const int axis = norm_axis(attr.axis, xr->rank);
+    if (axis < 0 || axis >= xr->rank) return -11;
+    size_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= xr->shape[i];
+    for (int i = axis + 1; i < xr->rank; i++) inner *= xr->shape[i];
+    const size_t x_axis = xr->shape[axis];
+    size_t axis_offset = 0;
+    set_kernel_name(ctx, node, "split");
+    for (uint16_t k = 0; k < node->output_count; k++) {
+        const Spkv2TensorRecord *yr = rec(ctx, node->outputs[k]);
+        const size_t block = static_cast<size_t>(yr->shape[axis]) * inner;
+        if (axis_offset + yr->shape[axis] > x_axis) return -11;
+        if (outer * block > 0)
+            hipLaunchKernelGGL(block_copy, dim3(grid_for(outer * block, 256)), dim3(256), 0, ctx->stream,
+                               dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[k]), outer,
+                               block, x_axis * inner, axis_offset * inner, block);
+        if (int rc = launch_status("split")) return rc;
+        axis_offset += yr->shape[axis];
+    }
+    return 0;
+}
+
+int slice_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    // reference tensor/slice.c:12-49: starts/ends (and optional axes, steps)
+    // are float constant inputs; only their first value is used
+    float fs = 0.0f, fe = 0.0f, fa = 0.0f, fst = 1.0f;
+    if (!const_scalar(ctx, node, 1, &fs) || !const_scalar(ctx, node, 2, &fe)) return SPKV2_E_UNSUPPORTED;
+    (void)const_scalar(ctx, node, 3, &fa);
+    (void)const_scalar(ctx, node, 4, &fst);
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    int64_t start = static_cast<int64_t>(fs), end = static_cast<int64_t>(fe);
+    int axis = static_cast<int>(fa);
+    const int64_t step = static_cast<int64_t>(static_cast<int>(fst));
+    if (axis < 0) axis += xr->rank;
+    if (axis < 0 || axis >= xr->rank || step <= 0) return -11;
+    size_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= xr->shape[i];
+    for (int i = axis + 1; i < xr->rank; i++) inner *= xr->shape[i];
+    const int64_t dim = xr->shape[axis];
+    if (start < 0) start += dim;
+    if (end < 0) end += dim;
+    if (end > dim) end = dim;
+    if (start < 0) start = 0;
+    const int64_t out = (end - start + step - 1) / step;
+    if (out <= 0 || outer * inner == 0) return 0;
+    if (start + (out - 1) * step >= dim) return -11;
+    set_kernel_name(ctx, node, "slice");
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    const size_t n = outer * static_cast<size_t>(out) * inner;
+    if (step == 1)
+        hipLaunchKernelGGL(block_copy, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, x, y, outer,
+                           static_cast<size_t>(out) * inner, static_cast<size_t>(dim) * inner,
+                           static_cast<size_t>(start) * inner, static_cast<size_t>(out) * inner);
+    else
+        hipLaunchKernelGGL(slice_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, x, y, outer, out, dim,
+                           start, step, inner);
+    return launch_status("slice");
+}
+
+int gather_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *dr = rec(ctx, node->inputs[0]), *ir = rec(ctx, node->inputs[1]);
+    const int axis = norm_axis(attr.axis, dr->rank);
+    if (axis < 0 || axis >= dr->rank) return -11;
+    size_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= dr->shape[i];
+    for (int i = axis + 1; i < dr->rank; i++) inner *= dr->shape[i];
+    const size_t J = elem_count(ir);
+    const size_t n = outer * J * inner;
+    if (n == 0) return 0;
+    set_kernel_name(ctx, node, "gather");
+    hipLaunchKernelGGL(gather_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<const float>(ctx, node->inputs[1]),
+                       dptr<float>(ctx, node->outputs[0]), outer, J, static_cast<int64_t>(dr->shape[axis]), inner);
+    return launch_status("gather");
+}
+
+int gather_elements_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    const Spkv2TensorRecord *dr = rec(ctx, node->inputs[0]), *ir = rec(ctx, node->inputs[1]);
+    const int axis = norm_axis(attr.axis, dr->rank);
+    if (axis < 0 || axis >= dr->rank || ir->rank != dr->rank || dr->rank > kRank) return -11;
+    StrideMap m{};
+    m.rank = ir->rank;
+    shape_of(ir, m.ydim);
+    strides_of(dr, m.sstride);
+    const size_t n = elem_count(ir);
+    if (n == 0) return 0;
+    set_kernel_name(ctx, node, "gather_elements");
+    hipLaunchKernelGGL(gather_elements_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<const float>(ctx, node->inputs[1]),
+                       dptr<float>(ctx, node->outputs[0]), n, m, axis, static_cast<int64_t>(dr->shape[axis]));
+    return launch_status("gather_elements");
+}
+
+int topk_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    Spkv2AttrRecord attr;
+    if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
+    if (node->output_count < 2) return -11;
+    float fk = 0.0f;
+    if (!const_scalar(ctx, node, 1, &fk)) return SPKV2_E_UNSUPPORTED;  // k computed at run time
+    const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
+    const int axis = norm_axis(attr.axis, xr->rank);
+    if (axis < 0 || axis >= xr->rank) return -11;
+    const int dim = static_cast<int>(xr->shape[axis]);
+    int k = static_cast<int>(fk);
+    if (k <= 0 || dim == 0) return 0;
+    if (k > dim) k = dim;
+    if (k > kTopkMaxK) return SPKV2_E_UNSUPPORTED;
+    size_t outer = 1, inner = 1;
+    for (int i = 0; i < axis; i++) outer *= xr->shape[i];
+    for (int i = axis + 1; i < xr->rank; i++) inner *= xr->shape[i];
+    const size_t rows = outer * inner;
+    if (rows == 0) return 0;
+    if (rows > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+    set_kernel_name(ctx, node, "topk");
+    hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream,
+                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]),
+                       dptr<float>(ctx, node->outputs[1]), inner, dim, k, attr.largest ? 1 : 0);
+    return launch_status("topk");
+}
+
+}  // namespace spk::kern

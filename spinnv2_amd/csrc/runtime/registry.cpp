@@ -93,6 +93,13 @@ const Entry kBuiltins[] = {
     EW(SPKV2_OP_CAST, copy_run),
     EW(SPKV2_OP_UNSQUEEZE, copy_run),
     EW(SPKV2_OP_CONCAT, concat_run),
+    EW(SPKV2_OP_TRANSPOSE, transpose_run),
+    EW(SPKV2_OP_TILE, tile_run),
+    EW(SPKV2_OP_SPLIT, split_run),
+    EW(SPKV2_OP_SLICE, slice_run),
+    EW(SPKV2_OP_GATHER, gather_run),
+    EW(SPKV2_OP_GATHERELEMENTS, gather_elements_run),
+    EW(SPKV2_OP_TOPK, topk_run),
 #undef EW
 };
 // clang-format on

@@ -202,6 +202,68 @@ class Graph:
         shape[axis] = sum(self.shape(t)[axis] for t in xs)
         return self.node("Concat", xs, [shape], {"axis": axis})[0]
 
+    # ---------------------------------------------- indexing / layout ops
+    def _const(self, name: str, values) -> int:
+        return self.weight(f"{name}_{len(self.nodes)}_{len(self.tensors)}", np.asarray(values, np.float32))
+
+    def transpose(self, x: int, perm) -> int:
+        shape = self.shape(x)
+        return self.node("Transpose", [x], [[shape[p] for p in perm]], {"perm": list(perm)})[0]
+
+    def tile(self, x: int, reps) -> int:
+        shape = self.shape(x)
+        out = [d * r for d, r in zip(shape, reps)]
+        return self.node("Tile", [x, self._const("tile_reps", reps)], [out])[0]
+
+    def split(self, x: int, sizes, axis: int = 1) -> list[int]:
+        shape = self.shape(x)
+        ax = axis % len(shape)
+        assert sum(sizes) == shape[ax]
+        outs = [[s if i == ax else d for i, d in enumerate(shape)] for s in sizes]
+        return self.node("Split", [x], outs, {"axis": ax})
+
+    def slice(self, x: int, start: int, end: int, axis: int = 0, step: int = 1) -> int:
+        """ONNX-style Slice with one axis; the parameters are constant inputs
+        (the reference reads the first value of each)."""
+        shape = self.shape(x)
+        ax = axis % len(shape)
+        dim = shape[ax]
+        s, e = start + dim if start < 0 else start, end + dim if end < 0 else end
+        e, s = min(e, dim), max(s, 0)
+        out_dim = max(0, (e - s + step - 1) // step)
+        out = [out_dim if i == ax else d for i, d in enumerate(shape)]
+        ins = [x, self._const("slice_starts", [start]), self._const("slice_ends", [end]),
+               self._const("slice_axes", [axis]), self._const("slice_steps", [step])]
+        return self.node("Slice", ins, [out])[0]
+
+    def gather(self, x: int, indices: int, axis: int = 0) -> int:
+        shape, ishape = self.shape(x), self.shape(indices)
+        ax = axis % len(shape)
+        return self.node("Gather", [x, indices], [shape[:ax] + ishape + shape[ax + 1:]], {"axis": ax})[0]
+
+    def gather_elements(self, x: int, indices: int, axis: int = 0) -> int:
+        return self.node("GatherElements", [x, indices], [self.shape(indices)], {"axis": axis})[0]
+
+    def topk(self, x: int, k: int, axis: int = -1, largest: int = 1) -> tuple[int, int]:
+        shape = self.shape(x)
+        ax = axis % len(shape)
+        out = [min(k, d) if i == ax else d for i, d in enumerate(shape)]
+        v, i = self.node("TopK", [x, self._const("topk_k", [k])], [out, out],
+                         {"axis": ax, "largest": largest, "sorted": 1})
+        return v, i
+
+    def reduce_max(self, x: int, axes, keepdims=1) -> int:
+        shape = self.shape(x)
+        axes = [a % len(shape) for a in axes]
+        out = [1 if i in axes else d for i, d in enumerate(shape)] if keepdims else \
+            [d for i, d in enumerate(shape) if i not in axes]
+        return self.node("ReduceMax", [x], [out], {"axes": axes, "keepdims": keepdims})[0]
+
+    def unsqueeze(self, x: int, axis: int) -> int:
+        shape = list(self.shape(x))
+        shape.insert(axis % (len(shape) + 1), 1)
+        return self.node("Unsqueeze", [x], [shape], {"axes": [axis]})[0]
+
     # ---------------------------------------------------------- compaction
     def compact(self) -> None:
         """Drops tensors no node or graph IO refers to, renumbers ids densely."""

@@ -194,3 +194,34 @@ def single_op(op: str, shape, **kw) -> Graph:
         raise ValueError(op)
     g.mark_output(y)
     return g
+
+
+def index_op(op: str, shape, seed: int = DEFAULT_SEED, **kw) -> Graph:
+    """Graphs of one indexing / layout op (the YOLO op set) on an input of
+    `shape`; index tensors are constants built from `kw`."""
+    g = Graph(op.lower())
+    x = g.input("x", shape)
+    outs: list[int]
+    if op == "Transpose":
+        outs = [g.transpose(x, kw["perm"])]
+    elif op == "Tile":
+        outs = [g.tile(x, kw["reps"])]
+    elif op == "Split":
+        outs = g.split(x, kw["sizes"], kw.get("axis", 1))
+    elif op == "Slice":
+        outs = [g.slice(x, kw["start"], kw["end"], kw.get("axis", 0), kw.get("step", 1))]
+    elif op == "Gather":
+        idx = g.weight("indices", np.asarray(kw["indices"], np.float32))
+        outs = [g.gather(x, idx, kw.get("axis", 0))]
+    elif op == "GatherElements":
+        idx = g.weight("indices", np.asarray(kw["indices"], np.float32))
+        outs = [g.gather_elements(x, idx, kw.get("axis", 0))]
+    elif op == "TopK":
+        outs = list(g.topk(x, kw["k"], kw.get("axis", -1), kw.get("largest", 1)))
+    elif op == "ReduceMax":
+        outs = [g.reduce_max(x, kw["axes"], kw.get("keepdims", 1))]
+    else:
+        raise ValueError(op)
+    for t in outs:
+        g.mark_output(t)
+    return g

@@ -85,6 +85,33 @@ _OPS = [
 for i, (op, shape, kw) in enumerate(_OPS):
     CASES.append((f"op{i}_{op}", "single_op", dict(op=op, shape=shape, **kw), "normal"))
 
+# Indexing / layout ops of the YOLO op set (reference tensor/*.c, shape/tile.c,
+# shape/transpose.c).  Index tensors are constants; "ties" inputs are
+# rounded to a coarse grid so TopK sees values tied across the k-th place.
+_rng = np.random.default_rng(11)
+_IDX = [
+    ("Transpose", [2, 3, 4, 5], dict(perm=[0, 2, 3, 1])),
+    ("Transpose", [6, 7], dict(perm=[1, 0])),
+    ("Transpose", [1, 4, 2, 3, 5], dict(perm=[0, 3, 1, 4, 2])),
+    ("Tile", [2, 3, 4], dict(reps=[1, 2, 3])),
+    ("Split", [2, 10, 3, 3], dict(sizes=[2, 5, 3], axis=1)),
+    ("Split", [4, 6], dict(sizes=[3, 3], axis=-1)),
+    ("Slice", [3, 20, 4], dict(start=2, end=17, axis=1, step=3)),
+    ("Slice", [5, 6], dict(start=-4, end=100, axis=0, step=1)),
+    ("Gather", [5, 4, 3], dict(indices=[[4, 0], [-1, 2]], axis=0)),
+    ("Gather", [2, 7, 3], dict(indices=[6, 1, -2, 0], axis=1)),
+    ("GatherElements", [3, 5], dict(indices=_rng.integers(-5, 5, (3, 4)).tolist(), axis=1)),
+    ("GatherElements", [4, 2, 3], dict(indices=_rng.integers(0, 4, (2, 2, 3)).tolist(), axis=0)),
+    ("TopK", [3, 50], dict(k=7, axis=-1, largest=1)),
+    ("TopK", [2, 40, 3], dict(k=10, axis=1, largest=0)),
+    ("TopK", [1, 8400], dict(k=300, axis=-1, largest=1)),
+    ("ReduceMax", [2, 6, 5, 4], dict(axes=[1, 3], keepdims=1)),
+]
+for i, (op, shape, kw) in enumerate(_IDX):
+    CASES.append((f"idx{i}_{op}", "index_op", dict(op=op, shape=shape, **kw), "normal"))
+CASES.append(("idx_topk_ties", "index_op", dict(op="TopK", shape=[2, 200], k=30, axis=-1, largest=1), "ties"))
+CASES.append(("idx_topk_ties_small", "index_op", dict(op="TopK", shape=[3, 64], k=9, axis=-1, largest=0), "ties"))
+
 # End to end: the LeNet config on U[0,1) input, and a
 # ResNet-18 at 32x32 (every ResNet node kind: stem, pools, basic blocks with
 # projections, ReduceMean, Gemm).
@@ -95,14 +122,17 @@ CASES.append(("resnet50_32px", "resnet", dict(depth=50, batch=1, image=32, class
 
 def build_graph(builder: str, kw: dict):
     kw = dict(kw)
-    if builder == "single_op":
+    if builder in ("single_op", "index_op"):
         op = kw.pop("op")
         shape = kw.pop("shape")
-        return models.single_op(op, shape, **kw)
+        return getattr(models, builder)(op, shape, **kw)
     return getattr(models, builder)(**kw)
 
 
 def case_inputs(g, dist: str, seed: int = 42) -> list[np.ndarray]:
+    if dist == "ties":  # values on a coarse grid: many exact ties
+        return [np.round(models.make_input(g.tensors[t].shape, seed + i, "normal") * 2).astype(np.float32) / 2
+                for i, t in enumerate(g.inputs)]
     return [models.make_input(g.tensors[t].shape, seed + i, dist) for i, t in enumerate(g.inputs)]
 
 
@@ -117,11 +147,13 @@ def main() -> None:
         blob = write_spk(g, "cpu_ref")
         xs = case_inputs(g, dist)
         ref = RefModel(blob)
-        y = ref.run(*xs)
+        ys = [ref.run(*xs, output=o) for o in range(len(g.outputs))]
         ref.close()
+        y = ys[0]
         meta = {"builder": builder, "kwargs": kw, "dist": dist, "seed": 42, "profile": "cpu_ref",
                 "source": "reference runtime (runtime/core + runtime/kernels/reference) built by oracle/Makefile"}
         arrays = {f"x{i}": x for i, x in enumerate(xs)}
+        arrays.update({f"y{o}": v for o, v in enumerate(ys) if o > 0})
         np.savez_compressed(HERE / f"{name}.npz", meta=np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8),
                             y=y, **arrays)
         print(f"{name:24s} inputs {[list(x.shape) for x in xs]} -> {y.size} values")

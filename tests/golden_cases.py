@@ -26,21 +26,27 @@ class GoldenCase:
     builder: str
     kwargs: dict
     inputs: list
-    expected: np.ndarray
+    expected: np.ndarray        # graph output 0
+    more: list | None = None    # graph outputs 1.. (multi-output ops)
+
+    @property
+    def all_expected(self) -> list:
+        return [self.expected] + list(self.more or [])
 
     def graph(self):
         from spinnv2_amd.spk import models
 
         kw = dict(self.kwargs)
-        if self.builder == "single_op":
+        if self.builder in ("single_op", "index_op"):
             op = kw.pop("op")
             shape = kw.pop("shape")
-            return models.single_op(op, shape, **kw)
+            return getattr(models, self.builder)(op, shape, **kw)
         return getattr(models, self.builder)(**kw)
 
     @property
     def exact(self) -> bool:
-        return self.builder == "single_op" and self.kwargs["op"] in EXACT_BUILDER_OPS
+        # index / layout ops move values without arithmetic: bit-exact
+        return self.builder == "index_op" or (self.builder == "single_op" and self.kwargs["op"] in EXACT_BUILDER_OPS)
 
 
 def load_cases() -> list[GoldenCase]:
@@ -49,5 +55,6 @@ def load_cases() -> list[GoldenCase]:
         with np.load(p, allow_pickle=False) as z:
             meta = json.loads(bytes(z["meta"]).decode())
             xs = [z[f"x{i}"] for i in range(len([k for k in z.files if k.startswith("x")]))]
-            cases.append(GoldenCase(p.stem, meta["builder"], meta["kwargs"], xs, z["y"]))
+            more = [z[f"y{o}"] for o in range(1, 1 + len([k for k in z.files if k.startswith("y") and k != "y"]))]
+            cases.append(GoldenCase(p.stem, meta["builder"], meta["kwargs"], xs, z["y"], more))
     return cases

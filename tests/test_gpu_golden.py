@@ -26,12 +26,15 @@ NETWORKS = {"lenet", "resnet18_32px", "resnet50_32px"}
 def test_mi355x_matches_reference_runtime(gpu, case):
     print(f"[golden] {case.name}", flush=True)
     blob = write_spk(case.graph(), "mi355x")
-    got = run_gpu(blob, case.inputs)[0].ravel()
-    assert got.shape == case.expected.shape
-    if case.exact:
-        np.testing.assert_array_equal(got.view(np.uint32), case.expected.view(np.uint32))
-    else:
-        assert tnorm_err(got, case.expected) <= FP32_TOL
+    outs = run_gpu(blob, case.inputs, outputs=len(case.all_expected))
+    for got, want in zip(outs, case.all_expected):
+        got = got.ravel()
+        assert got.shape == want.shape
+        if case.exact:
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+        else:
+            assert tnorm_err(got, want) <= FP32_TOL
+    got = outs[0].ravel()
     if case.name in NETWORKS:
         rows = got.reshape(case.inputs[0].shape[0], -1)
         want = case.expected.reshape(rows.shape)

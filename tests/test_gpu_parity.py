@@ -378,3 +378,41 @@ def test_fp32_pad_handoff_is_bit_identical(gpu, monkeypatch):
         assert sum("+handoff" in s for s in names) == (16 if flag == "1" else 0)
     np.testing.assert_array_equal(outs["1"], outs["0"])
     assert tnorm_err(outs["1"], run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+# Indexing / layout ops at larger sizes than the golden fixtures: bit-exact
+# against the oracle (they move values without arithmetic).
+INDEX_CASES = [
+    ("Transpose", [2, 64, 40, 40], dict(perm=[0, 2, 3, 1])),
+    ("Transpose", [1, 144, 8400], dict(perm=[0, 2, 1])),
+    ("Tile", [1, 8, 1, 50], dict(reps=[2, 1, 30, 1])),
+    ("Split", [1, 128, 40, 40], dict(sizes=[64, 64], axis=1)),
+    ("Split", [1, 64, 8400], dict(sizes=[16, 16, 32], axis=1)),
+    ("Slice", [1, 84, 8400], dict(start=4, end=84, axis=1, step=1)),
+    ("Slice", [2, 33, 17], dict(start=-30, end=-1, axis=1, step=4)),
+    ("Gather", [1, 8400, 4], dict(indices=list(range(8399, 0, -28)), axis=1)),
+    ("GatherElements", [1, 8400, 6], dict(indices=np.random.default_rng(3).integers(0, 8400, (1, 300, 6)).tolist(), axis=1)),
+    ("TopK", [1, 8400], dict(k=300, axis=-1, largest=1)),
+    ("TopK", [4, 24000], dict(k=300, axis=1, largest=1)),
+    ("TopK", [3, 1000, 5], dict(k=17, axis=1, largest=0)),
+    ("ReduceMax", [1, 80, 8400], dict(axes=[1], keepdims=0)),
+]
+
+
+# TopK also on inputs rounded to a coarse grid, so values tie across the
+# k-th place and the reference's heap history decides the selection
+INDEX_RUNS = [(op, shape, kw, "normal") for op, shape, kw in INDEX_CASES] + \
+    [(op, shape, kw, "ties") for op, shape, kw in INDEX_CASES if op == "TopK"]
+
+
+@pytest.mark.parametrize("op,shape,kw,dist", INDEX_RUNS,
+                         ids=[f"{o}{i}_{d}" for i, (o, _, _, d) in enumerate(INDEX_RUNS)])
+def test_index_ops_bitwise(gpu, op, shape, kw, dist):
+    g = models.index_op(op, shape, **kw)
+    xs = rng_inputs(g)
+    if dist == "ties":
+        xs = [np.round(x * 2).astype(np.float32) / 2 for x in xs]
+    got = run_gpu(write_spk(g, "mi355x"), xs, outputs=len(g.outputs))
+    want = run_oracle(write_spk(g, "mi355x"), xs)
+    for a_, b_ in zip(got, want):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))

@@ -22,7 +22,7 @@ CASES = load_cases()
 
 def test_fixture_set_is_complete():
     names = {c.name for c in CASES}
-    assert len(CASES) >= 38
+    assert len(CASES) >= 56
     for required in ("lenet", "resnet18_32px", "resnet50_32px", "conv2", "gemm2", "op0_MaxPool", "op6_Resize",
                      "op7_Softmax", "op2_Add"):
         assert required in names
@@ -31,9 +31,12 @@ def test_fixture_set_is_complete():
 @pytest.mark.parametrize("case", CASES, ids=[c.name for c in CASES])
 def test_oracle_matches_reference_bitwise(case):
     blob = write_spk(case.graph(), "mi355x")
-    got = OracleExecutor(blob).run(*case.inputs)[0].ravel()
-    assert got.shape == case.expected.shape
-    np.testing.assert_array_equal(got.view(np.uint32), case.expected.view(np.uint32))
+    outs = OracleExecutor(blob).run(*case.inputs)
+    assert len(outs) == len(case.all_expected)
+    for got, want in zip(outs, case.all_expected):
+        got = got.ravel()
+        assert got.shape == want.shape
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 def _ref_available() -> bool:
