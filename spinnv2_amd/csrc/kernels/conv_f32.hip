@@ -306,8 +306,8 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
             float *const any = a.y ? a.y : a.yp;
             const __amdgpu_buffer_rsrc_t yrs =
                 __builtin_amdgcn_make_buffer_rsrc(any, static_cast<short>(0), a.y ? a.y_bytes : 0, kBufferWord3);
-            const __amdgpu_buffer_rsrc_t prs =
-                __builtin_amdgcn_make_buffer_rsrc(any, static_cast<short>(0), a.yp ? a.yp_bytes : 0, kBufferWord3);
+            const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+                a.yp ? a.yp : any, static_cast<short>(0), a.yp ? a.yp_bytes : 0, kBufferWord3);
             const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<float *>(a.res ? a.res : any), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufferWord3);
             const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(

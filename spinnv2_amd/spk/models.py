@@ -225,3 +225,94 @@ def index_op(op: str, shape, seed: int = DEFAULT_SEED, **kw) -> Graph:
     for t in outs:
         g.mark_output(t)
     return g
+
+
+# ------------------------------------------------------- YOLOv10n-style graph
+
+def _cbs(g: Graph, p: Params, x: int, cout: int, k: int, stride: int = 1) -> int:
+    """Conv + BN + SiLU (the SiLU as Sigmoid*Mul, fused by the pipeline)."""
+    cin = g.shape(x)[1]
+    h = g.conv(x, p.he((cout, cin, k, k)), None, stride=stride, pad=k // 2)
+    h = g.batchnorm(h, *p.bn(cout))
+    return g.silu(h)
+
+
+def _c2f(g: Graph, p: Params, x: int, c: int, n: int, shortcut: bool = True) -> int:
+    """CSP bottleneck with two convs: 1x1, Split in halves, n residual
+    bottlenecks on the second half (standalone Adds: the convs carry SiLU),
+    Concat of every branch, 1x1."""
+    h = _cbs(g, p, x, c, 1)
+    a, b = g.split(h, [c // 2, c // 2], axis=1)
+    parts = [a, b]
+    for _ in range(n):
+        t = _cbs(g, p, parts[-1], c // 2, 3)
+        t = _cbs(g, p, t, c // 2, 3)
+        parts.append(g.add(parts[-1], t) if shortcut else t)
+    return _cbs(g, p, g.concat(parts, axis=1), c, 1)
+
+
+def _sppf(g: Graph, p: Params, x: int, c: int) -> int:
+    h = _cbs(g, p, x, c // 2, 1)
+    y1 = g.maxpool(h, 5, 1, 2)
+    y2 = g.maxpool(y1, 5, 1, 2)
+    y3 = g.maxpool(y2, 5, 1, 2)
+    return _cbs(g, p, g.concat([h, y1, y2, y3], axis=1), c, 1)
+
+
+def yolo_v10n(batch: int = 1, image: int = 640, seed: int = DEFAULT_SEED, classes: int = 80,
+              topk: int = 300) -> Graph:
+    """YOLOv10n-style detector: CSP backbone of 3x3/2
+    Conv+BN+SiLU downsamples 16->32->64->128->256 with C2f split/concat
+    blocks, SPPF, PAN neck (nearest Resize x2 + Concat), decoupled heads at
+    strides 8/16/32 (4x16 box bins + `classes` scores), and the pre-NMS
+    post-processing: DFL Softmax over the 16 bins, class Sigmoid, per-anchor
+    max, TopK(`topk`), GatherElements of boxes and scores.  Outputs: top
+    scores [B, k], boxes [B, k, 4] (DFL expectations), class scores
+    [B, k, classes], anchor indices [B, k]."""
+    p = Params(seed)
+    g = Graph("yolov10n")
+    x = g.input("images", [batch, 3, image, image])
+    h = _cbs(g, p, x, 16, 3, 2)
+    h = _cbs(g, p, h, 32, 3, 2)
+    h = _c2f(g, p, h, 32, 1)
+    h = _cbs(g, p, h, 64, 3, 2)
+    p3 = _c2f(g, p, h, 64, 2)
+    h = _cbs(g, p, p3, 128, 3, 2)
+    p4 = _c2f(g, p, h, 128, 2)
+    h = _cbs(g, p, p4, 256, 3, 2)
+    h = _c2f(g, p, h, 256, 1)
+    p5 = _sppf(g, p, h, 256)
+    # PAN neck
+    n4 = _c2f(g, p, g.concat([g.resize(p5, 2), p4], axis=1), 128, 1, shortcut=False)
+    n3 = _c2f(g, p, g.concat([g.resize(n4, 2), p3], axis=1), 64, 1, shortcut=False)
+    o4 = _c2f(g, p, g.concat([_cbs(g, p, n3, 64, 3, 2), n4], axis=1), 128, 1, shortcut=False)
+    o5 = _c2f(g, p, g.concat([_cbs(g, p, o4, 128, 3, 2), p5], axis=1), 256, 1, shortcut=False)
+    # decoupled heads
+    bins = 16
+    levels = []
+    for feat in (n3, o4, o5):
+        box = _cbs(g, p, _cbs(g, p, feat, 64, 3), 64, 3)
+        box = g.conv(box, p.he((4 * bins, 64, 1, 1)), p.normal(4 * bins, 0.01))
+        cls = _cbs(g, p, _cbs(g, p, feat, classes, 3), classes, 3)
+        cls = g.conv(cls, p.he((classes, classes, 1, 1)), p.normal(classes, 0.01))
+        hw = g.shape(box)[2] * g.shape(box)[3]
+        levels.append(g.reshape(g.concat([box, cls], axis=1), [batch, 4 * bins + classes, hw]))
+    out = g.concat(levels, axis=2)  # [B, 64 + classes, A]
+    anchors = g.shape(out)[2]
+    box, cls = g.split(out, [4 * bins, classes], axis=1)
+    # DFL: softmax over the 16 bins of each side, expectation by a 1x1 conv
+    box = g.transpose(g.reshape(box, [batch, 4, bins, anchors]), [0, 2, 1, 3])  # [B, 16, 4, A]
+    box = g.softmax(box, axis=1)
+    dfl = g.conv(box, np.arange(bins, dtype=np.float32).reshape(1, bins, 1, 1), None)  # [B, 1, 4, A]
+    dist = g.transpose(g.reshape(dfl, [batch, 4, anchors]), [0, 2, 1])  # [B, A, 4]
+    scores = g.transpose(g.unary("Sigmoid", cls), [0, 2, 1])  # [B, A, classes]
+    best = g.reduce_max(scores, [2], keepdims=0)  # [B, A]
+    k = min(topk, anchors)
+    top_v, top_i = g.topk(best, k, axis=1, largest=1)
+    idx = g.unsqueeze(top_i, 2)  # [B, k, 1]
+    boxes = g.gather_elements(dist, g.tile(idx, [1, 1, 4]), axis=1)
+    cls_k = g.gather_elements(scores, g.tile(idx, [1, 1, classes]), axis=1)
+    for t in (top_v, boxes, cls_k, top_i):
+        g.mark_output(t)
+    run_default_pipeline(g)
+    return g

@@ -118,6 +118,8 @@ CASES.append(("idx_topk_ties_small", "index_op", dict(op="TopK", shape=[3, 64], 
 CASES.append(("lenet", "lenet", {}, "uniform"))
 CASES.append(("resnet18_32px", "resnet", dict(depth=18, batch=2, image=32, classes=10), "normal"))
 CASES.append(("resnet50_32px", "resnet", dict(depth=50, batch=1, image=32, classes=10), "normal"))
+# the YOLOv10n-style detector at 160x160: 525 anchors, TopK(300)
+CASES.append(("yolov10n_160", "yolo_v10n", dict(image=160), "uniform"))
 
 
 def build_graph(builder: str, kw: dict):

@@ -40,3 +40,29 @@ def run_oracle(blob: bytes, inputs: list[np.ndarray]) -> list[np.ndarray]:
     from oracle.spk_exec import OracleExecutor
 
     return [o.ravel() for o in OracleExecutor(blob).run(*inputs)]
+
+
+def check_detections(got: list, want: list, tol: float = FP32_TOL) -> None:
+    """YOLO post-processing outputs [top scores, boxes, class scores,
+    indices]: the sorted top scores agree within the fp32 tolerance; anchors
+    selected by both sides carry the same boxes and class scores (within
+    tolerance); an anchor selected by only one side must sit at a near tie
+    (its score within the tolerance of the selection threshold)."""
+    v, b, s, i = (np.asarray(a).reshape(a.shape) for a in got)
+    wv, wb, ws, wi = (np.asarray(a) for a in want)
+    k = v.size
+    v, wv, i, wi = v.ravel(), wv.ravel(), i.ravel(), wi.ravel()
+    b, wb = b.reshape(k, -1), wb.reshape(k, -1)
+    s, ws = s.reshape(k, -1), ws.reshape(k, -1)
+    assert tnorm_err(v, wv) <= tol
+    scale = float(np.max(np.abs(wv)))
+    pos = {int(a): n for n, a in enumerate(wi)}
+    shared = [(n, pos[int(a)]) for n, a in enumerate(i) if int(a) in pos]
+    for n, m in shared:
+        assert float(np.abs(b[n] - wb[m]).max()) <= tol * max(1.0, float(np.abs(wb).max())), (n, b[n], wb[m])
+        assert float(np.abs(s[n] - ws[m]).max()) <= tol * max(1.0, float(np.abs(ws).max())), n
+    threshold = float(wv[-1])
+    for n, a in enumerate(i):
+        if int(a) not in pos:
+            assert abs(float(v[n]) - threshold) <= tol * scale, (n, a, v[n], threshold)
+    assert len(shared) >= k - 5

@@ -416,3 +416,69 @@ def test_index_ops_bitwise(gpu, op, shape, kw, dist):
     want = run_oracle(write_spk(g, "mi355x"), xs)
     for a_, b_ in zip(got, want):
         np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
+
+
+def test_yolo_v10n_640_e2e(gpu):
+    """The YOLOv10n-style detector at 640x640 (8400 anchors, TopK 300): the
+    whole graph -- C2f Split/Concat blocks, SPPF, PAN Resize/Concat, DFL
+    Softmax, TopK, GatherElements -- on the device against the oracle."""
+    from tests.helpers import check_detections
+
+    g = models.yolo_v10n()
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g, dist="uniform")
+    got = run_gpu(blob, xs, outputs=4)
+    want = [np.asarray(o) for o in __import__("oracle.spk_exec", fromlist=["x"]).OracleExecutor(blob).run(*xs)]
+    check_detections([a.reshape(w.shape) for a, w in zip(got, want)], want)
+
+
+def test_yolo_v10n_graph_mode(gpu):
+    from spinnv2_amd.runtime import Model
+
+    g = models.yolo_v10n(image=320)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g, dist="uniform")
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        eager = [m.get_output(i) for i in range(4)]
+        m.set_graph_mode(True)
+        for _ in range(3):
+            m.set_input(0, xs[0])
+            m.run()
+            for i in range(4):
+                np.testing.assert_array_equal(m.get_output(i), eager[i])
+
+
+def test_fp32_pad_handoff_with_other_readers(gpu, monkeypatch):
+    """A producer whose output feeds a padded conv and is also read elsewhere
+    (here: a graph output and a Concat) writes both the padded copy and the
+    tensor itself; every output matches the unfused path bit for bit."""
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    p = models.Params(5)
+    g = Graph("handoff2")
+    x = g.input("x", [1, 3, 40, 40])
+    a = g.relu(g.conv(x, p.he((16, 3, 3, 3)), p.normal(16, 0.01), stride=2, pad=1))
+    b = g.relu(g.conv(a, p.he((32, 16, 3, 3)), p.normal(32, 0.01), pad=1))
+    c = g.concat([a, g.relu(g.conv(b, p.he((16, 32, 1, 1)), None))], axis=1)
+    g.mark_output(a)
+    g.mark_output(c)
+    run_default_pipeline(g)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SPKV2_PAD_HANDOFF", flag)
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            outs[flag] = [m.get_output(0), m.get_output(1)]
+            if flag == "1":
+                assert "+handoff" in m.kernel_name(1)
+    for u, v in zip(outs["1"], outs["0"]):
+        np.testing.assert_array_equal(u, v)
+    for u, v in zip(outs["1"], run_oracle(blob, xs)):
+        assert tnorm_err(u, v) <= FP32_TOL
