@@ -17,6 +17,24 @@ import numpy as np
 REF_LIB = Path(__file__).resolve().parent / "_ref" / "libspkv2_ref.so"
 
 
+# runtime/include/spkv2_runtime.h:13-38
+class RefFaultEvent(ctypes.Structure):
+    _fields_ = [("node_id", ctypes.c_uint32), ("tensor_id", ctypes.c_uint32), ("element_index", ctypes.c_uint64),
+                ("bit_index", ctypes.c_uint8), ("invocation_index", ctypes.c_uint32), ("seed", ctypes.c_uint64),
+                ("enabled", ctypes.c_int)]
+
+
+class RefReliabilityStats(ctypes.Structure):
+    _fields_ = [("injected_faults", ctypes.c_uint64), ("detected_faults", ctypes.c_uint64),
+                ("recovered_faults", ctypes.c_uint64), ("unrecovered_faults", ctypes.c_uint64),
+                ("rerun_count", ctypes.c_uint64)]
+
+
+class RefRangeObservation(ctypes.Structure):
+    _fields_ = [("node_id", ctypes.c_uint32), ("tensor_id", ctypes.c_uint32), ("observed_min", ctypes.c_float),
+                ("observed_max", ctypes.c_float), ("observations", ctypes.c_uint64)]
+
+
 def available() -> bool:
     return REF_LIB.exists()
 
@@ -36,6 +54,11 @@ class RefModel:
         lib.spkv2_get_output_size.argtypes = [vp, ctypes.c_int, ctypes.POINTER(ctypes.c_size_t)]
         lib.spkv2_get_output.argtypes = [vp, ctypes.c_int, vp, ctypes.c_size_t]
         lib.spkv2_free.argtypes = [vp]
+        lib.spkv2_set_fault_event.argtypes = [vp, ctypes.POINTER(RefFaultEvent)]
+        lib.spkv2_clear_fault_event.argtypes = [vp]
+        lib.spkv2_clear_fault_event.restype = None
+        lib.spkv2_get_reliability_stats.argtypes = [vp, ctypes.POINTER(RefReliabilityStats)]
+        lib.spkv2_get_range_observation.argtypes = [vp, ctypes.c_uint32, ctypes.POINTER(RefRangeObservation)]
         self.lib = lib
         self._blob = ctypes.create_string_buffer(bytes(spk), len(spk))
         self.ctx = vp()
@@ -62,6 +85,44 @@ class RefModel:
         if rc != 0:
             raise RuntimeError(f"reference get_output failed: {rc}")
         return out
+
+    def set_input(self, index: int, a: np.ndarray) -> int:
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        return self.lib.spkv2_set_input(self.ctx, index, a.ctypes.data, a.nbytes)
+
+    def run_rc(self) -> int:
+        return self.lib.spkv2_run(self.ctx)
+
+    def output(self, index: int = 0) -> np.ndarray:
+        size = ctypes.c_size_t()
+        self.lib.spkv2_get_output_size(self.ctx, index, ctypes.byref(size))
+        out = np.empty(size.value // 4, dtype=np.float32)
+        rc = self.lib.spkv2_get_output(self.ctx, index, out.ctypes.data, out.nbytes)
+        if rc != 0:
+            raise RuntimeError(f"reference get_output failed: {rc}")
+        return out
+
+    def set_fault_event(self, event: dict | None) -> int:
+        """`event` holds the Spkv2FaultEvent fields; None clears it."""
+        if event is None:
+            self.lib.spkv2_clear_fault_event(self.ctx)
+            return 0
+        ev = RefFaultEvent(**event)
+        return self.lib.spkv2_set_fault_event(self.ctx, ctypes.byref(ev))
+
+    def reliability_stats(self) -> dict:
+        s = RefReliabilityStats()
+        rc = self.lib.spkv2_get_reliability_stats(self.ctx, ctypes.byref(s))
+        if rc != 0:
+            raise RuntimeError(f"reference stats failed: {rc}")
+        return {name: int(getattr(s, name)) for name, _ in s._fields_}
+
+    def range_observation(self, node_id: int) -> dict:
+        o = RefRangeObservation()
+        rc = self.lib.spkv2_get_range_observation(self.ctx, node_id, ctypes.byref(o))
+        if rc != 0:
+            raise RuntimeError(f"reference range observation failed: {rc}")
+        return {name: getattr(o, name) for name, _ in o._fields_}
 
     def close(self) -> None:
         if self.ctx:

@@ -353,40 +353,61 @@ __global__ void __launch_bounds__(256) resize_nearest(const float *__restrict__ 
 
 __global__ void flip_bit_kernel(uint32_t *p, uint32_t bit) { *p ^= (1u << bit); }
 
+// Range of an fp32 tensor with the reference's fold semantics
+// (runtime/core/executor.c:400-443): min / max start from element 0 and are
+// replaced only on a strict < / >, so NaNs after element 0 never enter, a NaN
+// at element 0 sticks, infinities count, and among equal extrema (+0 / -0)
+// the first by index is kept.  out[2] flags any non-finite element (the
+// in-range test rejects those).  One block: this runs only on protected
+// nodes.
+__device__ inline void minmax_take(float &v, unsigned long long &i, float ov, unsigned long long oi, bool less) {
+    const bool better = less ? (ov < v) : (ov > v);
+    if (better || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
 __global__ void __launch_bounds__(256) minmax_kernel(const float *__restrict__ x, size_t n, float *__restrict__ out) {
-    __shared__ float smin[4], smax[4], snan[4];
+    __shared__ float s_lo[4], s_hi[4], s_bad[4];
+    __shared__ unsigned long long s_li[4], s_hi_i[4];
     float lo = INFINITY, hi = -INFINITY, bad = 0.0f;
+    unsigned long long li = ~0ull, hi_i = ~0ull;
     for (size_t i = threadIdx.x; i < n; i += 256) {
         const float v = x[i];
-        if (!isfinite(v)) bad += 1.0f;
-        else {
-            lo = fminf(lo, v);
-            hi = fmaxf(hi, v);
+        if (!isfinite(v)) bad = 1.0f;
+        if (v == v) {
+            minmax_take(lo, li, v, i, true);
+            minmax_take(hi, hi_i, v, i, false);
         }
     }
     for (int off = 32; off > 0; off >>= 1) {
-        lo = fminf(lo, __shfl_xor(lo, off, 64));
-        hi = fmaxf(hi, __shfl_xor(hi, off, 64));
-        bad += __shfl_xor(bad, off, 64);
+        minmax_take(lo, li, __shfl_xor(lo, off, 64), __shfl_xor(li, off, 64), true);
+        minmax_take(hi, hi_i, __shfl_xor(hi, off, 64), __shfl_xor(hi_i, off, 64), false);
+        bad = fmaxf(bad, __shfl_xor(bad, off, 64));
     }
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
-        smin[w] = lo;
-        smax[w] = hi;
-        snan[w] = bad;
+        s_lo[w] = lo;
+        s_li[w] = li;
+        s_hi[w] = hi;
+        s_hi_i[w] = hi_i;
+        s_bad[w] = bad;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 1; i < 4; i++) {
-            lo = fminf(lo, smin[i]);
-            hi = fmaxf(hi, smax[i]);
-            bad += snan[i];
+        for (int k = 1; k < 4; k++) {
+            minmax_take(lo, li, s_lo[k], s_li[k], true);
+            minmax_take(hi, hi_i, s_hi[k], s_hi_i[k], false);
+            bad = fmaxf(bad, s_bad[k]);
         }
-        lo = fminf(lo, smin[0]);
-        hi = fmaxf(hi, smax[0]);
+        if (n > 0 && x[0] != x[0]) {
+            lo = x[0];
+            hi = x[0];
+        }
         out[0] = lo;
         out[1] = hi;
-        out[2] = snan[0] + snan[1] + snan[2] + snan[3];
+        out[2] = bad;
         out[3] = 0.0f;
     }
 }

@@ -193,6 +193,10 @@ class Model:
     def run(self) -> None:
         _check(self.lib, self.lib.spkv2_run(self.ctx), "run")
 
+    def run_rc(self) -> int:
+        """spkv2_run's return code as is (fault-event errors are negative)."""
+        return self.lib.spkv2_run(self.ctx)
+
     def output_size(self, index: int = 0) -> int:
         size = ctypes.c_size_t()
         _check(self.lib, self.lib.spkv2_get_output_size(self.ctx, index, ctypes.byref(size)), "output size")
@@ -235,16 +239,31 @@ class Model:
                "int8 accumulators")
         return out
 
-    def set_fault_event(self, event: FaultEvent | None) -> int:
+    def set_fault_event(self, event: FaultEvent | dict | None) -> int:
+        """Arms one bit flip (a FaultEvent or a dict of its fields); None
+        clears it.  Returns the entry point's code."""
         if event is None:
             self.lib.spkv2_clear_fault_event(self.ctx)
             return 0
+        if isinstance(event, dict):
+            event = FaultEvent(**event)
         return self.lib.spkv2_set_fault_event(self.ctx, ctypes.byref(event))
 
     def reliability_stats(self) -> dict:
         s = ReliabilityStats()
         _check(self.lib, self.lib.spkv2_get_reliability_stats(self.ctx, ctypes.byref(s)), "stats")
         return {name: int(getattr(s, name)) for name, _ in s._fields_}
+
+    def reset_reliability_stats(self) -> None:
+        self.lib.spkv2_reset_reliability_stats(self.ctx)
+
+    def range_observation(self, node_id: int) -> dict:
+        o = RangeObservation()
+        _check(self.lib, self.lib.spkv2_get_range_observation(self.ctx, node_id, ctypes.byref(o)), "range observation")
+        return {name: getattr(o, name) for name, _ in o._fields_}
+
+    def reset_range_observations(self) -> None:
+        self.lib.spkv2_reset_range_observations(self.ctx)
 
     def close(self) -> None:
         if self.ctx:

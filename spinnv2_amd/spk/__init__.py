@@ -2,4 +2,4 @@
 selection, the package writer, model generators and INT8 quantization."""
 
 from .graph import Graph  # noqa: F401
-from .writer import QuantParam, write_spk  # noqa: F401
+from .writer import Protection, QuantParam, write_spk  # noqa: F401

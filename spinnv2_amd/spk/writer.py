@@ -10,6 +10,7 @@ FNV-1a checksum over everything before the checksum section.
 from __future__ import annotations
 
 import json
+import math
 from dataclasses import dataclass, field
 from pathlib import Path
 
@@ -71,9 +72,48 @@ def _quant_section(params: list[QuantParam]) -> bytes:
     return bytes(recs + data)
 
 
+@dataclass
+class Protection:
+    """One protection-plan entry (reference compiler/reliability/
+    protection_plan.py:15-24): `mode` is "range_guard_rerun" (bounds on the
+    node's single fp32 output) or "dmr_compare_rerun" (run twice, compare
+    bytes, rerun on mismatch; scratch for two copies of the output)."""
+    node_id: int
+    mode: str
+    lower_bound: float = -math.inf
+    upper_bound: float = math.inf
+
+
+PROTECTION_MODES = {"none": 0, "range_guard_rerun": 1, "dmr_compare_rerun": 2}
+
+
+def _protection_section(g: Graph, entries: list[Protection], scratch_offset: int) -> tuple[bytes, int]:
+    """Records in the reference's encoding (protection_plan.py:65-81):
+    infinite bounds as +-FLT_MAX, the DMR scratch right after the kernels'
+    scratch arena.  Returns the records and the extra scratch bytes."""
+    out = bytearray()
+    extra = 0
+    seen = set()
+    for e in entries:
+        n = g.nodes[e.node_id]
+        if e.node_id in seen or len(n.outputs) != 1 or g.tensors[n.outputs[0]].dtype != "fp32":
+            raise ValueError(f"node {e.node_id} cannot be protected")
+        if e.mode == "range_guard_rerun" and e.lower_bound > e.upper_bound:
+            raise ValueError(f"invalid range for node {e.node_id}")
+        seen.add(e.node_id)
+        lower = e.lower_bound if math.isfinite(e.lower_bound) else -3.4028235e38
+        upper = e.upper_bound if math.isfinite(e.upper_bound) else 3.4028235e38
+        dmr = e.mode == "dmr_compare_rerun"
+        if dmr:
+            extra = max(extra, 2 * g.tensors[n.outputs[0]].size_bytes)
+        out += F.PROTECTION.pack(e.node_id, n.outputs[0], PROTECTION_MODES[e.mode], 0, lower, upper,
+                                 scratch_offset if dmr else 0)
+    return bytes(out), extra
+
+
 def write_spk(g: Graph, profile: str = "mi355x", *, quant_params: list[QuantParam] | None = None,
               path: str | Path | None = None, external_inputs: bool = False,
-              external_outputs: bool = False) -> bytes:
+              external_outputs: bool = False, protection: list[Protection] | None = None) -> bytes:
     g.relink()
     bad = sorted({n.op_type for n in g.nodes if n.op_type not in F.OP})
     if bad:
@@ -150,6 +190,10 @@ def write_spk(g: Graph, profile: str = "mi355x", *, quant_params: list[QuantPara
     ]
     if quant_params:
         sections.append((F.SECTION_QUANTIZATION, _quant_section(quant_params), 4))
+    if protection:
+        prot, extra_scratch = _protection_section(g, protection, scratch)
+        sections.append((F.SECTION_PROTECTION_PLAN, prot, 8))
+        scratch += extra_scratch
     sections.append((F.SECTION_STRING_TABLE, bytes(strings), 1))
     sections.append((F.SECTION_CHECKSUM, b"\x00" * 4, 4))
 
