@@ -65,6 +65,12 @@ const char *spkv2_mi355x_last_error(void);
  * (reference runtime/core/loader.c:25-32), exported for package writers. */
 uint32_t spkv2_fnv1a32(const void *data, size_t size);
 
+/* IEEE half -> float widening of `count` values (unaligned buffers allowed):
+ * what the loader applies to FP16 weight tensors, replacing the reference's
+ * per-node promotion in runtime/kernels/optimized/conv/conv.c:961-978 and
+ * mm/gemm.c:150-162 with one pass at load. */
+void spkv2_mi355x_fp16_to_fp32(const void *src, void *dst, size_t count);
+
 /* ---- execution controls --------------------------------------------------- */
 /* 1: after one eager run, capture the node loop into a HIP graph and replay it
  * (re-captured after any bind_*; never used while profiling, fault injection

@@ -92,8 +92,11 @@ class Package:
         for t in self.tensors:
             if t.role == 3:
                 raw = blob[woff + t.offset: woff + t.offset + t.size]
-                dt = np.int8 if t.dtype == 2 else np.float32
-                self.weights[t.id] = np.frombuffer(raw, dtype=dt).reshape(t.shape).copy()
+                # dtype 3: IEEE half weights, widened exactly to fp32 (reference
+                # runtime/kernels/optimized/conv/conv.c:961-978)
+                dt = {2: np.int8, 3: np.dtype("<f2")}.get(t.dtype, np.dtype("<f4"))
+                w = np.frombuffer(raw, dtype=dt).reshape(t.shape)
+                self.weights[t.id] = w.astype(np.float32) if t.dtype == 3 else w.copy()
         self.quant = {}
         if 9 in secs:
             qoff, qsize = secs[9]

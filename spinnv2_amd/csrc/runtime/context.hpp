@@ -23,6 +23,10 @@ struct Spkv2TensorSlot {
 struct Spkv2Context {
     // ---- the package (host memory, zero-copy views into the blob) ----
     uint8_t *owned_model = nullptr;
+    // FP16-weight packages: tensor table copy whose half weights describe the
+    // fp32 copies appended to `promoted_weights` (null when none)
+    Spkv2TensorRecord *promoted_records = nullptr;
+    uint8_t *promoted_weights = nullptr;
     const uint8_t *model = nullptr;
     size_t model_size = 0;
     Spkv2Header header{};

@@ -11,6 +11,7 @@
 #include <cstring>
 
 #include "context.hpp"
+#include "spkv2_mi355x.h"
 #include "spkv2_platform.h"
 
 namespace {
@@ -33,6 +34,65 @@ uint32_t fnv1a32(const uint8_t *p, size_t n) {
 // Finds `"outputs": [id, id, ...]` in the metadata JSON (reference
 // loader.c:46-103).  A malformed or short list leaves output_ids unset, in
 // which case outputs are taken in tensor-table order.
+// IEEE binary16 -> binary32, exact for every input (subnormals normalised,
+// infinities kept, NaN payloads shifted into the high mantissa bits).
+uint32_t half_bits_to_float_bits(uint16_t h) {
+    const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    if (exp == 0x1fu) return sign | 0x7f800000u | (man << 13);
+    if (exp != 0) return sign | ((exp + 112u) << 23) | (man << 13);
+    if (man == 0) return sign;
+    uint32_t e = 113;  // value = man * 2^-24; normalise so bit 10 leads
+    while (!(man & 0x400u)) {
+        man <<= 1;
+        e--;
+    }
+    return sign | (e << 23) | ((man & 0x3ffu) << 13);
+}
+
+// FP16 weights (the reference's --fp16-weights packages,
+// compiler/passes/convert_fp16.py:11-25) are widened to fp32 once at load, as
+// the reference's optimized conv and gemm do per node
+// (runtime/kernels/optimized/conv/conv.c:961-978, mm/gemm.c:150-162).  The
+// context's tensor table becomes a copy whose half weight records describe
+// fp32 copies appended after the package's weight bytes, so every kernel
+// (and every user kernel reading spkv2_ctx_tensor_record) sees fp32 weights.
+int promote_fp16_weights(Spkv2Context *ctx) {
+    const uint32_t nt = ctx->header.num_tensors;
+    size_t extra = 0;
+    const size_t base = (ctx->weights_size + 255) & ~static_cast<size_t>(255);
+    for (uint32_t i = 0; i < nt; i++) {
+        const Spkv2TensorRecord &r = ctx->tensor_records[i];
+        if (r.role != SPKV2_ROLE_WEIGHT || r.dtype != SPKV2_DTYPE_FP16) continue;
+        if (r.data_offset > ctx->weights_size || r.size_bytes > ctx->weights_size - r.data_offset ||
+            r.size_bytes % 2)
+            return -3;
+        extra += ((r.size_bytes * 2) + 255) & ~static_cast<uint64_t>(255);
+    }
+    if (extra == 0) return 0;
+    ctx->promoted_records = static_cast<Spkv2TensorRecord *>(spkv2_platform_malloc(nt * sizeof(Spkv2TensorRecord)));
+    ctx->promoted_weights = static_cast<uint8_t *>(spkv2_platform_calloc(base + extra, 1));
+    if (!ctx->promoted_records || !ctx->promoted_weights) return -1;
+    memcpy(ctx->promoted_records, ctx->tensor_records, nt * sizeof(Spkv2TensorRecord));
+    memcpy(ctx->promoted_weights, ctx->weights_host, ctx->weights_size);
+    size_t off = base;
+    for (uint32_t i = 0; i < nt; i++) {
+        Spkv2TensorRecord &r = ctx->promoted_records[i];
+        if (r.role != SPKV2_ROLE_WEIGHT || r.dtype != SPKV2_DTYPE_FP16) continue;
+        const size_t n = static_cast<size_t>(r.size_bytes / 2);
+        spkv2_mi355x_fp16_to_fp32(ctx->weights_host + r.data_offset, ctx->promoted_weights + off, n);
+        r.dtype = SPKV2_DTYPE_FP32;
+        r.size_bytes = n * 4;
+        r.data_offset = off;
+        off += (n * 4 + 255) & ~static_cast<size_t>(255);
+    }
+    ctx->tensor_records = ctx->promoted_records;
+    ctx->weights_host = ctx->promoted_weights;
+    ctx->weights_size = off;
+    return 0;
+}
+
 int parse_output_order(Spkv2Context *ctx, const Spkv2SectionEntry *meta) {
     if (!meta || meta->size == 0 || ctx->header.num_outputs == 0) return 0;
     const char *p = reinterpret_cast<const char *>(ctx->model + meta->offset);
@@ -114,6 +174,8 @@ void destroy(Spkv2Context *ctx) {
     spkv2_platform_free(ctx->output_ids);
     spkv2_platform_free(ctx->tensors);
     spkv2_platform_free(ctx->owned_model);
+    spkv2_platform_free(ctx->promoted_records);
+    spkv2_platform_free(ctx->promoted_weights);
     ctx->~Spkv2Context();
     spkv2_platform_free(ctx);
 }
@@ -202,6 +264,7 @@ extern "C" int spkv2_load_memory(const void *data, size_t size, Spkv2Context **o
     ctx->attrs_size = attr_sec->size;
     ctx->weights_host = ctx->model + weight_sec->offset;
     ctx->weights_size = weight_sec->size;
+    if (int rc = promote_fp16_weights(ctx)) return fail(rc);
 
     ctx->tensors = static_cast<Spkv2TensorSlot *>(spkv2_platform_calloc(ctx->header.num_tensors ? ctx->header.num_tensors : 1,
                                                                         sizeof(Spkv2TensorSlot)));
@@ -249,6 +312,17 @@ extern "C" int spkv2_load_file(const char *path, Spkv2Context **out_ctx) {
 extern "C" void spkv2_free(Spkv2Context *ctx) { destroy(ctx); }
 
 extern "C" const char *spkv2_runtime_version(void) { return "0.3.0-mi355x"; }
+
+extern "C" void spkv2_mi355x_fp16_to_fp32(const void *src, void *dst, size_t count) {
+    const uint8_t *in = static_cast<const uint8_t *>(src);
+    uint8_t *out = static_cast<uint8_t *>(dst);
+    for (size_t i = 0; i < count; i++) {
+        uint16_t h;
+        memcpy(&h, in + 2 * i, 2);
+        const uint32_t f = half_bits_to_float_bits(h);
+        memcpy(out + 4 * i, &f, 4);
+    }
+}
 
 extern "C" uint32_t spkv2_fnv1a32(const void *data, size_t size) {
     return data ? fnv1a32(static_cast<const uint8_t *>(data), size) : 2166136261u;

@@ -75,6 +75,7 @@ SIGNATURES = {
     "spkv2_get_topology": (VP, []),
     "spkv2_set_affinity": (None, [I]),
     # spkv2_mi355x.h
+    "spkv2_mi355x_fp16_to_fp32": (None, [VP, VP, SZ]),
     "spkv2_ctx_tensor_record": (VP, [VP, U32]),
     "spkv2_ctx_tensor_data": (VP, [VP, U32]),
     "spkv2_ctx_get_attr": (I, [VP, VP, VP]),

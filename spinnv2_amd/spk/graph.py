@@ -18,7 +18,7 @@ class Tensor:
     id: int
     name: str
     shape: list[int]
-    dtype: str = "fp32"  # fp32 | int8
+    dtype: str = "fp32"  # fp32 | int8 | fp16 (weights only)
     role: str = "activation"  # input | output | weight | activation
     data: np.ndarray | None = None
     producer: int | None = None
@@ -29,7 +29,7 @@ class Tensor:
         n = 1
         for d in self.shape:
             n *= int(d)
-        return n * (1 if self.dtype == "int8" else 4)
+        return n * {"int8": 1, "fp16": 2}.get(self.dtype, 4)
 
 
 @dataclass

@@ -183,6 +183,21 @@ def _toposort(g: Graph) -> None:
 DEFAULT_PIPELINE = [fold_batchnorm, fuse_conv_relu, fuse_conv_silu, fuse_add_relu, fuse_conv_add]
 
 
+def convert_weights_fp16(g: Graph) -> int:
+    """Stores every fp32 weight of rank >= 2 as IEEE half (round to nearest
+    even), as the reference's --fp16-weights pass does
+    (compiler/passes/convert_fp16.py:11-25); biases and scalars stay fp32.
+    The runtime widens them back to fp32 once at load.  Returns the number
+    of tensors converted."""
+    count = 0
+    for t in g.tensors:
+        if t.role == "weight" and t.dtype == "fp32" and t.data is not None and len(t.shape) >= 2:
+            t.data = np.asarray(t.data, dtype=np.float32).astype(np.float16)
+            t.dtype = "fp16"
+            count += 1
+    return count
+
+
 def run_default_pipeline(g: Graph, *, conv_add: bool = True) -> dict[str, int]:
     stats = {}
     for p in DEFAULT_PIPELINE:

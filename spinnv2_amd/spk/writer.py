@@ -137,7 +137,7 @@ def write_spk(g: Graph, profile: str = "mi355x", *, quant_params: list[QuantPara
             continue
         weights += b"\x00" * (_align(len(weights), 16) - len(weights))
         w_off[t.id] = len(weights)
-        arr = t.data.astype(np.int8 if t.dtype == "int8" else "<f4", copy=False)
+        arr = t.data.astype({"int8": np.int8, "fp16": "<f2"}.get(t.dtype, "<f4"), copy=False)
         weights += np.ascontiguousarray(arr).tobytes()
 
     # attrs
