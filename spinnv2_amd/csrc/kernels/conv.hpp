@@ -43,7 +43,12 @@ struct ConvPlan {
     float *scales;       // device, int8 path: w_scale[m] * x_scale
     float x_scale;       // int8 path: activation scale
     int quant_split;     // int8 path: first element index of the per-image tail (round half away)
-    size_t workspace;    // bytes of runtime workspace needed per run
+    size_t workspace;    // bytes of device workspace needed per run
+    // the workspace lives in the package's scratch arena at the node's
+    // kernel spec (its scratch_bytes covers it), else in the runtime's own
+    // allocation
+    bool ws_in_scratch;
+    uint32_t spec_id;
     // int8 requantize handoff.  Producer side: this conv's output is also
     // quantized in its epilogue, with the consuming int8 conv's scale and
     // rounding rule, into that conv's zero-padded NHWC buffer (not owned);
@@ -62,6 +67,13 @@ struct ConvPlan {
 };
 
 void conv_plan_free(void *p);
+
+// Places the plan's workspace in the node's kernel-spec scratch when that
+// spec reserves enough; returns the bytes the runtime must allocate for it
+// instead (0 when the scratch arena holds it).
+size_t claim_spec_scratch(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan);
+// Device workspace of a plan for this run, or nullptr when it is missing.
+uint8_t *plan_workspace(const Spkv2Context *ctx, const ConvPlan *plan);
 
 // Per-process table of measured tile choices, keyed by layer shape; with
 // SPKV2_TUNE_DB set it is read from and appended to that file.

@@ -1007,12 +1007,38 @@ std::string igemm_name(const ConvPlan *p) {
            ",splitk=" + std::to_string(p->splitk) + ">";
 }
 
+size_t claim_spec_scratch(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {
+    plan->ws_in_scratch = false;
+    if (plan->workspace == 0) return 0;
+    const Spkv2KernelSpecRecord *s = spec_by_id(ctx, node->kernel_spec_id);
+    if (s && s->node_id == node->id && s->scratch_bytes >= plan->workspace) {
+        plan->ws_in_scratch = true;
+        plan->spec_id = node->kernel_spec_id;
+        return 0;
+    }
+    return plan->workspace;
+}
+
+uint8_t *plan_workspace(const Spkv2Context *ctx, const ConvPlan *p) {
+    if (p->workspace == 0) return ctx->workspace;  // not dereferenced
+    if (p->ws_in_scratch) {
+        // the same bounds the dispatcher checks before handing a kernel its scratch
+        const Spkv2KernelSpecRecord *s = spec_by_id(ctx, p->spec_id);
+        if (!s || !ctx->scratch || s->scratch_bytes < p->workspace || s->scratch_bytes > ctx->scratch_size ||
+            s->scratch_offset > ctx->scratch_size - s->scratch_bytes)
+            return nullptr;
+        return ctx->scratch + s->scratch_offset;
+    }
+    return ctx->workspace_size >= p->workspace ? ctx->workspace : nullptr;
+}
+
 // x_img_stride: elements between consecutive "images" of the B source (a
 // Gemm with trans_a reads A as [K][rows]: stride 1).
 static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res,
                           float *y, float alpha, int x_img_stride) {
     const ConvGeom &g = p->g;
-    if (ctx->workspace_size < p->workspace) return SPKV2_E_UNSUPPORTED;
+    uint8_t *wsb = plan_workspace(ctx, p);
+    if (p->workspace > 0 && !wsb) return SPKV2_E_UNSUPPORTED;
     const float *xs = x;
     int x_bytes = static_cast<int>(g.x_elems * 4);
     // a fault event may change a tensor after its producer ran: then every
@@ -1023,7 +1049,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
         x_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.C * p->Hp * p->Wp * 4);
         x_img_stride = g.C * p->Hp * p->Wp;
     } else if (p->padded) {
-        float *xp = reinterpret_cast<float *>(ctx->workspace);
+        float *xp = reinterpret_cast<float *>(wsb);
         const unsigned planes = static_cast<unsigned>(g.N * g.C);
         hipLaunchKernelGGL(pad_nchw, dim3(planes), dim3(256), 0, ctx->stream, x, xp, g.H, g.W, p->Hp, p->Wp, p->pt,
                            p->pl);
@@ -1032,7 +1058,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
         x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);
         x_img_stride = g.C * p->Hp * p->Wp;
     }
-    float *ws = reinterpret_cast<float *>(ctx->workspace + p->pad_bytes);
+    float *ws = p->workspace > 0 ? reinterpret_cast<float *>(wsb + p->pad_bytes) : nullptr;
     const bool give = p->pad_out && handoff;
     return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
                         static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
@@ -1128,7 +1154,8 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     if (int rc = read_conv_geom(ctx, node, &g)) return rc;
     void **slot = &ctx->node_cache[node->id];
     if (*slot) {
-        *ws = static_cast<ConvPlan *>(*slot)->workspace;
+        const ConvPlan *p = static_cast<ConvPlan *>(*slot);
+        *ws = p->ws_in_scratch ? 0 : p->workspace;
         return 0;
     }
     ConvPlan *plan = new ConvPlan();
@@ -1154,7 +1181,7 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
         plan->path = CONV_DIRECT_F32;
         set_kernel_name(ctx, node, "conv_direct_f32<grouped>");
     }
-    if (rc == 0) *ws = plan->workspace;
+    if (rc == 0) *ws = claim_spec_scratch(ctx, node, plan);
     return rc;
 }
 

@@ -901,10 +901,11 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
 
 int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *plan, int32_t *raw_acc_out) {
     const ConvGeom &g = plan->g;
-    if (ctx->workspace_size < plan->workspace) return SPKV2_E_UNSUPPORTED;
+    uint8_t *wsb = plan_workspace(ctx, plan);
+    if (!wsb) return SPKV2_E_UNSUPPORTED;
     const I8Layout L = i8_layout(g);
-    int8_t *xq = reinterpret_cast<int8_t *>(ctx->workspace);
-    int32_t *part = reinterpret_cast<int32_t *>(ctx->workspace + plan->pad_bytes);
+    int8_t *xq = reinterpret_cast<int8_t *>(wsb);
+    int32_t *part = reinterpret_cast<int32_t *>(wsb + plan->pad_bytes);
     const float inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
 
     // a fault event may change the fp32 input after its producer ran: then

@@ -88,7 +88,8 @@ __global__ void __launch_bounds__(256) matmul_kernel(MatmulArgs p) {
 int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     void **slot = &ctx->node_cache[node->id];
     if (*slot) {
-        *ws = static_cast<GemmPlan *>(*slot)->conv.workspace;
+        const ConvPlan &p = static_cast<GemmPlan *>(*slot)->conv;
+        *ws = p.ws_in_scratch ? 0 : p.workspace;
         return 0;
     }
     Spkv2AttrRecord attr;
@@ -128,7 +129,7 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     gp->conv.g = g;
     if (int rc = plan_igemm_gemm(ctx->stream, g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
     set_kernel_name(ctx, node, "gemm:" + igemm_name(&gp->conv));
-    *ws = gp->conv.workspace;
+    *ws = claim_spec_scratch(ctx, node, &gp->conv);
     return 0;
 }
 

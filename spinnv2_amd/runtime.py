@@ -181,6 +181,12 @@ class Model:
     def prepare(self) -> None:
         _check(self.lib, self.lib.spkv2_prepare(self.ctx, None, 0), "prepare")
 
+    def prepare_with_scratch(self, arena: DeviceBuffer | None = None, scratch: DeviceBuffer | None = None) -> int:
+        """spkv2_prepare_with_scratch with caller-owned device buffers (None:
+        the runtime allocates that one).  Returns the entry point's code."""
+        return self.lib.spkv2_prepare_with_scratch(self.ctx, arena.ptr if arena else None, arena.nbytes if arena else 0,
+                                                   scratch.ptr if scratch else None, scratch.nbytes if scratch else 0)
+
     def set_input(self, index: int, array: np.ndarray) -> None:
         a = np.ascontiguousarray(array, dtype=np.float32)
         _check(self.lib, self.lib.spkv2_set_input(self.ctx, index, a.ctypes.data, a.nbytes), "set input")

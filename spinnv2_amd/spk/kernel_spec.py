@@ -6,25 +6,45 @@ choice of (backend, kind) for those profiles (compiler/planner/kernel_spec.py:
 scratch estimate (kernel_spec.py:240-298), so the reference runtime runs the
 packages as it would run its own compiler's output.
 
-`mi355x` is this backend's target: fp32 Conv -> (mi355x, implicit_gemm_f32)
-with fallback (mi355x, reference) [the direct device conv]; INT8 Conv ->
-(mi355x, implicit_gemm_i8); Gemm / MatMul -> (mi355x, gemm_f32); every other
-op -> (mi355x, device_elementwise).  Fallbacks never name a CPU kind.
+`mi355x` is this backend's target, described by profiles/mi355x.json in the
+reference's profile schema (compiler/target/profiles/cpu_generic.json): each
+op lists `mi355x_<kind>` tokens in preference order, the first that applies
+wins, the next one becomes the fallback spec (reference kernel_spec.py:71-144
+does the same with its simd tokens).  fp32 / fp16-weight Conv ->
+(mi355x, implicit_gemm_f32) with fallback (mi355x, reference) [the direct
+device conv]; INT8 Conv -> (mi355x, implicit_gemm_i8); Gemm / MatMul ->
+(mi355x, gemm_f32); every other op -> (mi355x, device_elementwise).
+Fallbacks never name a CPU kind.
+
+The mi355x kinds carry their device workspace in the spec's scratch_bytes:
+the zero-padded input copy (fp32 NCHW, or quantized int8 NHWC) plus room for
+split-K partial sums, so the runtime runs them out of the package's scratch
+arena (a caller-provided one under spkv2_prepare_with_scratch) instead of
+allocating.
 """
 
 from __future__ import annotations
 
+import json
 from dataclasses import dataclass
+from pathlib import Path
 
-from .graph import Graph, Node
+from .graph import Graph, Node, conv_out
 
 SIMD_TILE_BYTES = 32 * 1024 * 1024
 SIMD_REF_OPS = {"Add", "Mul", "Sub", "Div", "Relu", "Sigmoid", "Transpose", "ReduceMax", "ReduceMean", "Softmax",
                 "MaxPool", "Resize", "AveragePool", "GlobalAveragePool", "Clip", "LeakyRelu"}
 
+MI355X_PROFILE = json.loads((Path(__file__).resolve().parent / "profiles" / "mi355x.json").read_text())
+
+# split-K bound the device workspace estimate allows for: the runtime's
+# largest split, capped per node (a plan that needs more gets a runtime
+# allocation instead)
+MI355X_MAX_SPLITK = 32
+MI355X_SPLITK_CAP = 256 * 1024 * 1024
+
 PROFILES = {
-    "mi355x": {"name": "mi355x", "backends": ["mi355x"], "scratch_arena_max": 1 << 30,
-               "activation_arena_max": 0},
+    "mi355x": MI355X_PROFILE,
     "cpu_generic": {"name": "cpu_generic", "backends": ["ref", "cpu", "simd"], "bnns": True,
                     "scratch_arena_max": 33554432, "activation_arena_max": 0},
     "cpu_generic_nobnns": {"name": "cpu_generic_nobnns", "backends": ["ref", "cpu", "simd"], "bnns": False,
@@ -73,6 +93,67 @@ def _cpu_scratch(g: Graph, n: Node, kind: str, backend: str) -> int:
     return 0
 
 
+def _align256(v: int) -> int:
+    return (v + 255) // 256 * 256
+
+
+def _mi355x_scratch(g: Graph, n: Node, kind: str) -> int:
+    """Device workspace of an mi355x kind: the padded input copy the kernel
+    gathers from (when some tap leaves the input) plus split-K partials."""
+    if kind not in ("implicit_gemm_f32", "implicit_gemm_i8", "gemm_f32"):
+        return 0
+    if kind == "gemm_f32":
+        if n.op_type != "Gemm":
+            return 0
+        a = g.tensors[n.inputs[0]].shape
+        y = g.tensors[n.outputs[0]].shape
+        rows = a[1] if int(n.attrs.get("trans_a", 0)) else a[0]
+        return _align256(min(MI355X_MAX_SPLITK * int(y[-1]) * int(rows) * 4, MI355X_SPLITK_CAP))
+    x, w, y = _conv_geometry(g, n)
+    if int(n.attrs.get("group", 1)) != 1:
+        return 0                                         # grouped: direct conv, no workspace
+    N, C, H, W = (int(v) for v in x)
+    M, KH, KW = int(w[0]), int(w[2]), int(w[3])
+    OH, OW = int(y[2]), int(y[3])
+    sh, sw = (int(v) for v in n.attrs.get("strides", [1, 1]))
+    dh, dw = (int(v) for v in n.attrs.get("dilations", [1, 1]))
+    pt, pl = (int(v) for v in list(n.attrs.get("pads", [0, 0, 0, 0]))[:2])
+    hspan = (OH - 1) * sh + (KH - 1) * dh + 1
+    wspan = (OW - 1) * sw + (KW - 1) * dw + 1
+    Hp, Wp = max(H + pt, hspan), max(W + pl, wspan)
+    partial = min(MI355X_MAX_SPLITK * M * N * OH * OW * 4, MI355X_SPLITK_CAP)
+    if kind == "implicit_gemm_i8":
+        cp = (C + 3) // 4 * 4 if dw == 1 else (C + 15) // 16 * 16
+        return _align256(N * Hp * Wp * cp + 64) + partial
+    padded = pt > 0 or pl > 0 or hspan - pt > H or wspan - pl > W
+    return (_align256(N * C * Hp * Wp * 4) if padded else 0) + partial
+
+
+def _mi355x_specs(g: Graph, n: Node, prof: dict) -> list[Spec]:
+    """The op's applicable mi355x tokens, in the profile's order."""
+    tokens = prof["ops"].get(n.op_type, [])
+    if not tokens:
+        raise ValueError(f"target profile does not support op: {n.op_type}")
+    out = []
+    for tok in tokens:
+        if not tok.startswith("mi355x_"):
+            raise ValueError(f"unknown mi355x profile token {tok}")
+        kind = tok[len("mi355x_"):]
+        dtype = "fp32"
+        if n.op_type == "Conv":
+            int8 = g.tensors[n.inputs[1]].dtype == "int8"
+            if kind == "implicit_gemm_i8":
+                if not int8:
+                    continue
+                dtype = "int8"
+            elif int8:
+                continue                                  # int8 weights need the int8 kernel
+        out.append(Spec(0, n.id, kind, "mi355x", dtype, _mi355x_scratch(g, n, kind)))
+    if not out:
+        raise ValueError(f"no mi355x kernel applies to node {n.id} ({n.op_type})")
+    return out
+
+
 def _cpu_generic_conv_kind(g: Graph, n: Node, bnns: bool) -> str:
     """reference kernel_spec.py:146-224 with the cpu_generic token list."""
     x, w, y = _conv_geometry(g, n)
@@ -102,16 +183,10 @@ def select_kernel_specs(g: Graph, profile: str) -> tuple[list[Spec], dict[int, S
 
     for n in g.nodes:
         if profile == "mi355x":
-            if n.op_type == "Conv":
-                int8 = g.tensors[n.inputs[1]].dtype == "int8"
-                sel = add(Spec(0, n.id, "implicit_gemm_i8" if int8 else "implicit_gemm_f32", "mi355x",
-                               "int8" if int8 else "fp32"))
-                if not int8:
-                    sel.fallback = add(Spec(0, n.id, "reference", "mi355x")).id
-            elif n.op_type in ("Gemm", "MatMul"):
-                sel = add(Spec(0, n.id, "gemm_f32", "mi355x"))
-            else:
-                sel = add(Spec(0, n.id, "device_elementwise", "mi355x"))
+            chain = _mi355x_specs(g, n, prof)
+            sel = add(chain[0])
+            if len(chain) > 1:
+                sel.fallback = add(chain[1]).id
         elif profile == "cpu_ref":
             sel = add(Spec(0, n.id, "reference", "ref"))
         else:
@@ -134,6 +209,7 @@ def select_kernel_specs(g: Graph, profile: str) -> tuple[list[Spec], dict[int, S
                 sel.fallback = add(ref).id
         by_node[n.id] = sel
         scratch = max(scratch, sel.scratch_bytes)
-    if scratch > prof["scratch_arena_max"]:
-        raise MemoryError(f"scratch arena {scratch} exceeds profile limit {prof['scratch_arena_max']}")
+    limit = prof["memory"]["scratch_arena_max"] if "memory" in prof else prof["scratch_arena_max"]
+    if scratch > limit:
+        raise MemoryError(f"scratch arena {scratch} exceeds profile limit {limit}")
     return specs, by_node, scratch
