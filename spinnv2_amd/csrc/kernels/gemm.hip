@@ -42,44 +42,103 @@ void gemm_plan_free(void *p) {
     delete g;
 }
 
+// Batched MatMul y[b] = A[a(b)] x B[b(b)] (reference kernels/reference/mm/
+// matmul.c:3-49: numpy broadcasting of the leading dims, K from A's last
+// dim, no transposes).  One workgroup computes a 64x64 tile of one batch:
+// 4 waves in a 2x2 grid, each a 32x32 block on v_mfma_f32_32x32x2f32.  k
+// tiles of 16 are staged through LDS k-contiguous for both operands (B is
+// transposed on the way in), double-buffered with the next tile's global
+// loads in flight during the MFMAs.
 struct MatmulArgs {
     const float *__restrict__ a;
     const float *__restrict__ b;
     float *__restrict__ y;
-    int64_t M, N, K, batch;
+    int M, N, K;
     int yrank, arank, brank;
-    int64_t yshape[8], ashape[8], bshape[8];
+    int yshape[8], ashape[8], bshape[8];
 };
 
-__global__ void __launch_bounds__(256) matmul_kernel(MatmulArgs p) {
-    const size_t total = static_cast<size_t>(p.batch) * p.M * p.N;
-    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
-         idx += static_cast<size_t>(gridDim.x) * 256) {
-        const int64_t n = idx % p.N;
-        const int64_t m = (idx / p.N) % p.M;
-        int64_t bi = idx / (p.N * p.M);
-        // batch coordinates of y, then broadcast into a and b
-        int64_t coords[8] = {0};
-        for (int d = p.yrank - 3; d >= 0; d--) {
-            coords[d] = bi % p.yshape[d];
-            bi /= p.yshape[d];
+constexpr int kMmTile = 64, kMmBK = 16, kMmLd = kMmBK + 1;
+
+__global__ void __launch_bounds__(256) matmul_mfma(MatmulArgs p) {
+    __shared__ float As[2][kMmTile * kMmLd];
+    __shared__ float Bs[2][kMmTile * kMmLd];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * kMmTile, n0 = blockIdx.x * kMmTile;
+    // batch coordinates of y, broadcast into a and b
+    int coords[8] = {0};
+    int t = blockIdx.z;
+    for (int d = p.yrank - 3; d >= 0; d--) {
+        coords[d] = t % p.yshape[d];
+        t /= p.yshape[d];
+    }
+    size_t ab = 0, bb = 0;
+    for (int d = 0; d + 2 < p.arank; d++) {
+        const int yd = p.yrank - p.arank + d;
+        ab = ab * p.ashape[d] + (p.ashape[d] == 1 || yd < 0 ? 0 : coords[yd]);
+    }
+    for (int d = 0; d + 2 < p.brank; d++) {
+        const int yd = p.yrank - p.brank + d;
+        bb = bb * p.bshape[d] + (p.bshape[d] == 1 || yd < 0 ? 0 : coords[yd]);
+    }
+    const size_t M = p.M, N = p.N, K = p.K;
+    const float *A = p.a + ab * M * K;
+    const float *B = p.b + bb * K * N;
+    float *Y = p.y + static_cast<size_t>(blockIdx.z) * M * N;
+
+    const int ar = tid >> 2, ak = (tid & 3) * 4;   // A tile: row, 4 k's
+    const int bk = tid >> 4, bn = (tid & 15) * 4;  // B tile: k, 4 columns
+    float ra[4], rb[4];
+    auto load = [&](int k0) {
+        const int gm = m0 + ar;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int gk = k0 + ak + i;
+            ra[i] = gm < p.M && gk < p.K ? A[static_cast<size_t>(gm) * K + gk] : 0.0f;
         }
-        int64_t ab = 0, bb = 0;
-        for (int d = 0; d + 2 < p.arank; d++) {
-            const int yd = p.yrank - p.arank + d;
-            const int64_t c = yd >= 0 ? coords[yd] : 0;
-            ab = ab * p.ashape[d] + (p.ashape[d] == 1 ? 0 : c);
+        const int gk = k0 + bk;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int gn = n0 + bn + i;
+            rb[i] = gk < p.K && gn < p.N ? B[static_cast<size_t>(gk) * N + gn] : 0.0f;
         }
-        for (int d = 0; d + 2 < p.brank; d++) {
-            const int yd = p.yrank - p.brank + d;
-            const int64_t c = yd >= 0 ? coords[yd] : 0;
-            bb = bb * p.bshape[d] + (p.bshape[d] == 1 ? 0 : c);
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            As[buf][ar * kMmLd + ak + i] = ra[i];
+            Bs[buf][(bn + i) * kMmLd + bk] = rb[i];
         }
-        const float *ar = p.a + (ab * p.M + m) * p.K;
-        const float *bc = p.b + bb * p.K * p.N + n;
-        float sum = 0.0f;
-        for (int64_t k = 0; k < p.K; k++) sum += ar[k] * bc[k * p.N];
-        p.y[idx] = sum;
+    };
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    const int ktiles = (p.K + kMmBK - 1) / kMmBK;
+    const int row = lane & 31, kh = lane >> 5;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt < ktiles; kt++) {
+        const int buf = kt & 1;
+        if (kt + 1 < ktiles) load((kt + 1) * kMmBK);
+#pragma unroll
+        for (int s = 0; s < kMmBK / 2; s++) {
+            // lanes 0-31 supply k = 2s, lanes 32-63 k = 2s+1, for A and B alike
+            const float av = As[buf][(wm * 32 + row) * kMmLd + 2 * s + kh];
+            const float bv = Bs[buf][(wn * 32 + row) * kMmLd + 2 * s + kh];
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        }
+        if (kt + 1 < ktiles) store(buf ^ 1);  // that buffer was last read before the previous barrier
+        __syncthreads();
+    }
+    // accumulator layout: column lane & 31, rows 8*(r/4) + 4*(lane/32) + r%4
+    const int col = n0 + wn * 32 + row;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (m < p.M && col < p.N) Y[static_cast<size_t>(m) * N + col] = acc[r];
     }
 }
 
@@ -149,27 +208,41 @@ int gemm_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
 int matmul_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const Spkv2TensorRecord *ar = rec(ctx, node->inputs[0]), *br = rec(ctx, node->inputs[1]),
                             *yr = rec(ctx, node->outputs[0]);
-    if (ar->rank < 2 || br->rank < 2 || yr->rank < 2) return -11;
+    if (ar->rank < 2 || br->rank < 2 || yr->rank < 2 || ar->rank > 8 || br->rank > 8 || yr->rank > 8) return -11;
+    if (ar->dtype != SPKV2_DTYPE_FP32 || br->dtype != SPKV2_DTYPE_FP32) return SPKV2_E_UNSUPPORTED;
+    const uint64_t M = yr->shape[yr->rank - 2], N = yr->shape[yr->rank - 1], K = ar->shape[ar->rank - 1];
+    // operands must hold what the loops read (the reference trusts the records)
+    if (ar->shape[ar->rank - 2] != M || br->shape[br->rank - 2] != K || br->shape[br->rank - 1] != N) return -11;
+    const uint64_t total = elem_count(yr);
+    if (total == 0) return 0;
+    const uint64_t batch = total / (M * N);
+    for (int d = 0; d + 2 < yr->rank; d++) {
+        const int da = d - (yr->rank - ar->rank), db = d - (yr->rank - br->rank);
+        if (da >= 0 && ar->shape[da] != 1 && ar->shape[da] != yr->shape[d]) return -11;
+        if (db >= 0 && br->shape[db] != 1 && br->shape[db] != yr->shape[d]) return -11;
+    }
+    if (M > 0x7fffffffULL || N > 0x7fffffffULL || K > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+    const uint64_t mt = (M + kMmTile - 1) / kMmTile, nt = (N + kMmTile - 1) / kMmTile;
+    if (mt > 65535 || batch > 65535 || nt > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
     MatmulArgs p{};
     p.a = dptr<const float>(ctx, node->inputs[0]);
     p.b = dptr<const float>(ctx, node->inputs[1]);
     p.y = dptr<float>(ctx, node->outputs[0]);
-    p.M = yr->shape[yr->rank - 2];
-    p.N = yr->shape[yr->rank - 1];
-    p.K = ar->shape[ar->rank - 1];
-    p.batch = static_cast<int64_t>(elem_count(yr)) / (p.M * p.N == 0 ? 1 : p.M * p.N);
+    p.M = static_cast<int>(M);
+    p.N = static_cast<int>(N);
+    p.K = static_cast<int>(K);
     p.yrank = yr->rank;
     p.arank = ar->rank;
     p.brank = br->rank;
     for (int i = 0; i < 8; i++) {
-        p.yshape[i] = yr->shape[i];
-        p.ashape[i] = ar->shape[i];
-        p.bshape[i] = br->shape[i];
+        p.yshape[i] = static_cast<int>(yr->shape[i]);
+        p.ashape[i] = static_cast<int>(ar->shape[i]);
+        p.bshape[i] = static_cast<int>(br->shape[i]);
     }
-    const size_t total = static_cast<size_t>(elem_count(yr));
-    if (total == 0) return 0;
-    set_kernel_name(ctx, node, "matmul_f32");
-    hipLaunchKernelGGL(matmul_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, p);
+    set_kernel_name(ctx, node, "matmul_mfma_f32<64x64x16>");
+    hipLaunchKernelGGL(matmul_mfma, dim3(static_cast<unsigned>(nt), static_cast<unsigned>(mt),
+                                         static_cast<unsigned>(batch)),
+                       dim3(256), 0, ctx->stream, p);
     return launch_status("matmul");
 }
 

@@ -227,6 +227,19 @@ def index_op(op: str, shape, seed: int = DEFAULT_SEED, **kw) -> Graph:
     return g
 
 
+def matmul_op(a_shape, b_shape, const_b: bool = False, seed: int = DEFAULT_SEED) -> Graph:
+    """One batched MatMul with numpy-style broadcasting of the leading dims;
+    B is a second input, or a constant weight with `const_b`."""
+    g = Graph("matmul")
+    a = g.input("a", list(a_shape))
+    if const_b:
+        b = g.weight("b", Params(seed).normal(tuple(b_shape), 0.5))
+    else:
+        b = g.input("b", list(b_shape))
+    g.mark_output(g.matmul(a, b))
+    return g
+
+
 # ------------------------------------------------------- YOLOv10n-style graph
 
 def _cbs(g: Graph, p: Params, x: int, cout: int, k: int, stride: int = 1) -> int:
@@ -259,11 +272,51 @@ def _sppf(g: Graph, p: Params, x: int, c: int) -> int:
     return _cbs(g, p, g.concat([h, y1, y2, y3], axis=1), c, 1)
 
 
+def _cb(g: Graph, p: Params, x: int, cout: int, k: int = 1, group: int = 1) -> int:
+    """Conv + BN without activation."""
+    cin = g.shape(x)[1]
+    h = g.conv(x, p.he((cout, cin // group, k, k)), None, pad=k // 2, group=group)
+    return g.batchnorm(h, *p.bn(cout))
+
+
+def _attention(g: Graph, p: Params, x: int, heads: int) -> int:
+    """Multi-head self-attention over the H*W positions of a feature map
+    (YOLOv10's PSA attention): 1x1 qkv projection with keys half the head
+    width, softmax((q^T k) / sqrt(key_dim)) over keys, v weighted by the
+    attention, plus a depthwise 3x3 positional term on v, 1x1 output
+    projection."""
+    b, dim, hh, ww = g.shape(x)
+    n = hh * ww
+    head_dim = dim // heads
+    key_dim = head_dim // 2
+    qkv = _cb(g, p, x, dim + 2 * key_dim * heads)
+    qkv = g.reshape(qkv, [b, heads, 2 * key_dim + head_dim, n])
+    q, k, v = g.split(qkv, [key_dim, key_dim, head_dim], axis=2)
+    attn = g.matmul(g.transpose(q, [0, 1, 3, 2]), k)                      # [b, heads, n, n]
+    attn = g.binary("Mul", attn, g._const("attn_scale", [key_dim ** -0.5]))
+    attn = g.softmax(attn, axis=-1)
+    out = g.matmul(v, g.transpose(attn, [0, 1, 3, 2]))                    # [b, heads, head_dim, n]
+    out = g.reshape(out, [b, dim, hh, ww])
+    pe = _cb(g, p, g.reshape(v, [b, dim, hh, ww]), dim, 3, group=dim)
+    return _cb(g, p, g.add(out, pe), dim)
+
+
+def _psa(g: Graph, p: Params, x: int, c: int) -> int:
+    """Partial self-attention block: 1x1, split in halves, attention and a
+    two-conv feed-forward (each residual) on the second half, concat, 1x1."""
+    h = _cbs(g, p, x, c, 1)
+    a, b = g.split(h, [c // 2, c // 2], axis=1)
+    b = g.add(b, _attention(g, p, b, max(1, c // 128)))
+    b = g.add(b, _cb(g, p, _cbs(g, p, b, c, 1), c // 2))
+    return _cbs(g, p, g.concat([a, b], axis=1), c, 1)
+
+
 def yolo_v10n(batch: int = 1, image: int = 640, seed: int = DEFAULT_SEED, classes: int = 80,
               topk: int = 300) -> Graph:
     """YOLOv10n-style detector: CSP backbone of 3x3/2
     Conv+BN+SiLU downsamples 16->32->64->128->256 with C2f split/concat
-    blocks, SPPF, PAN neck (nearest Resize x2 + Concat), decoupled heads at
+    blocks, SPPF, a PSA attention block (2 heads over the stride-32 map:
+    batched MatMul, Softmax), PAN neck (nearest Resize x2 + Concat), decoupled heads at
     strides 8/16/32 (4x16 box bins + `classes` scores), and the pre-NMS
     post-processing: DFL Softmax over the 16 bins, class Sigmoid, per-anchor
     max, TopK(`topk`), GatherElements of boxes and scores.  Outputs: top
@@ -281,7 +334,7 @@ def yolo_v10n(batch: int = 1, image: int = 640, seed: int = DEFAULT_SEED, classe
     p4 = _c2f(g, p, h, 128, 2)
     h = _cbs(g, p, p4, 256, 3, 2)
     h = _c2f(g, p, h, 256, 1)
-    p5 = _sppf(g, p, h, 256)
+    p5 = _psa(g, p, _sppf(g, p, h, 256), 256)
     # PAN neck
     n4 = _c2f(g, p, g.concat([g.resize(p5, 2), p4], axis=1), 128, 1, shortcut=False)
     n3 = _c2f(g, p, g.concat([g.resize(n4, 2), p3], axis=1), 64, 1, shortcut=False)

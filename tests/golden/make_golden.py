@@ -112,6 +112,22 @@ for i, (op, shape, kw) in enumerate(_IDX):
 CASES.append(("idx_topk_ties", "index_op", dict(op="TopK", shape=[2, 200], k=30, axis=-1, largest=1), "ties"))
 CASES.append(("idx_topk_ties_small", "index_op", dict(op="TopK", shape=[3, 64], k=9, axis=-1, largest=0), "ties"))
 
+# Batched MatMul (reference kernels/reference/mm/matmul.c): plain 2-D,
+# batched, leading-dim broadcasting both ways, a constant B, odd sizes that
+# leave partial 64x64 tiles, and the two PSA attention products of the
+# YOLOv10n-style graph at 320 (100 positions, 2 heads).
+_MATMUL = [
+    dict(a_shape=[5, 7], b_shape=[7, 3]),
+    dict(a_shape=[2, 3, 8, 16], b_shape=[2, 3, 16, 5]),
+    dict(a_shape=[2, 1, 4, 6], b_shape=[3, 6, 5]),
+    dict(a_shape=[3, 70, 33], b_shape=[33, 65]),
+    dict(a_shape=[4, 33, 17], b_shape=[17, 9], const_b=True),
+    dict(a_shape=[1, 2, 100, 32], b_shape=[1, 2, 32, 100]),
+    dict(a_shape=[1, 2, 64, 100], b_shape=[1, 2, 100, 100]),
+]
+for i, kw in enumerate(_MATMUL):
+    CASES.append((f"matmul{i}", "matmul_op", kw, "normal"))
+
 # End to end: the LeNet config on U[0,1) input, and a
 # ResNet-18 at 32x32 (every ResNet node kind: stem, pools, basic blocks with
 # projections, ReduceMean, Gemm).
