@@ -428,23 +428,32 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
     }
 }
 
-// Zero-padded copy of an NCHW tensor: xp[p][pt + h][pl + w] = x[p][h][w],
-// every other element of the Hp x Wp planes 0.  One block per plane, 32-bit
-// index math, coalesced on both sides.
-__global__ void __launch_bounds__(256) pad_nchw(const float *__restrict__ x, float *__restrict__ xp, int H, int W,
-                                                int Hp, int Wp, int pt, int pl) {
-    const size_t plane = blockIdx.x;
-    const float *src = x + plane * H * W;
-    float *dst = xp + plane * Hp * Wp;
-    const int total = Hp * Wp;
-    for (int i = threadIdx.x; i < total; i += 256) {
-        const int hq = i / Wp;
-        const int wq = i - hq * Wp;
-        const int h = hq - pt, w = wq - pl;
-        dst[i] = (static_cast<unsigned>(h) < static_cast<unsigned>(H) && static_cast<unsigned>(w) < static_cast<unsigned>(W))
-                     ? src[h * W + w]
-                     : 0.0f;
+// Zero-padded copy of an NCHW tensor: planes of H x W placed at (pt, pl) in
+// planes of Hp x Wp, halo written as zeros.  grid.y strides over planes,
+// grid.x over the elements of a plane (32-bit index math), so small
+// batches still spread over the GPU.
+__global__ void __launch_bounds__(256) pad_nchw(const float *__restrict__ x, float *__restrict__ xp, unsigned planes,
+                                                int H, int W, int Hp, int Wp, int pt, int pl) {
+    const unsigned plane_sz = static_cast<unsigned>(Hp * Wp);
+    for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float *src = x + static_cast<size_t>(plane) * H * W;
+        float *dst = xp + static_cast<size_t>(plane) * plane_sz;
+        for (unsigned r = blockIdx.x * 256 + threadIdx.x; r < plane_sz; r += gridDim.x * 256) {
+            const int hq = static_cast<int>(r / static_cast<unsigned>(Wp));
+            const int h = hq - pt, w = static_cast<int>(r) - hq * Wp - pl;
+            dst[r] = (static_cast<unsigned>(h) < static_cast<unsigned>(H) && static_cast<unsigned>(w) < static_cast<unsigned>(W))
+                         ? src[h * W + w]
+                         : 0.0f;
+        }
     }
+}
+
+// grid of a per-plane kernel: x covers `per_plane` elements with 256-thread
+// blocks, y the planes (capped; the kernels stride over the rest)
+inline dim3 plane_grid(size_t per_plane, size_t planes) {
+    const size_t gx = std::min<size_t>((per_plane + 255) / 256, 1024);
+    const size_t gy = std::min<size_t>(planes, 65535);
+    return dim3(static_cast<unsigned>(gx == 0 ? 1 : gx), static_cast<unsigned>(gy == 0 ? 1 : gy));
 }
 
 
@@ -1051,8 +1060,8 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     } else if (p->padded) {
         float *xp = reinterpret_cast<float *>(wsb);
         const unsigned planes = static_cast<unsigned>(g.N * g.C);
-        hipLaunchKernelGGL(pad_nchw, dim3(planes), dim3(256), 0, ctx->stream, x, xp, g.H, g.W, p->Hp, p->Wp, p->pt,
-                           p->pl);
+        hipLaunchKernelGGL(pad_nchw, plane_grid(static_cast<size_t>(p->Hp) * p->Wp, planes), dim3(256), 0,
+                           ctx->stream, x, xp, planes, g.H, g.W, p->Hp, p->Wp, p->pt, p->pl);
         if (int rc = launch_status("pad_nchw")) return rc;
         xs = xp;
         x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);

@@ -3,6 +3,7 @@
 // wavefront kernels: consecutive lanes touch consecutive addresses of the
 // NCHW output, wide (float4) accesses where shapes allow, one wave per row for
 // row reductions.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 
@@ -170,28 +171,31 @@ struct PoolArgs {
     int N, C, H, W, OH, OW, kh, kw, sh, sw, ph, pw;
 };
 
-// reference pool/maxpool.c:20-40: -inf start, out-of-bounds taps skipped
+// reference pool/maxpool.c:20-40: -inf start, out-of-bounds taps skipped.
+// grid.y strides over the N*C planes, grid.x over the outputs of a plane
+// (32-bit index math).
 __global__ void __launch_bounds__(256) maxpool_kernel(PoolArgs a) {
-    const size_t total = static_cast<size_t>(a.N) * a.C * a.OH * a.OW;
-    for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
-         idx += static_cast<size_t>(gridDim.x) * 256) {
-        const int ow = static_cast<int>(idx % a.OW);
-        const size_t t = idx / a.OW;
-        const int oh = static_cast<int>(t % a.OH);
-        const size_t plane = t / a.OH;
-        const float *xp = a.x + plane * a.H * a.W;
-        float m = -INFINITY;
-        for (int i = 0; i < a.kh; i++) {
-            const int ih = oh * a.sh + i - a.ph;
-            if (ih < 0 || ih >= a.H) continue;
-            for (int j = 0; j < a.kw; j++) {
-                const int iw = ow * a.sw + j - a.pw;
-                if (iw < 0 || iw >= a.W) continue;
-                const float v = xp[ih * a.W + iw];
-                if (v > m) m = v;
+    const unsigned planes = static_cast<unsigned>(a.N * a.C);
+    const unsigned per_plane = static_cast<unsigned>(a.OH * a.OW);
+    for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float *xp = a.x + static_cast<size_t>(plane) * a.H * a.W;
+        float *yp = a.y + static_cast<size_t>(plane) * per_plane;
+        for (unsigned r = blockIdx.x * 256 + threadIdx.x; r < per_plane; r += gridDim.x * 256) {
+            const int oh = static_cast<int>(r / static_cast<unsigned>(a.OW));
+            const int ow = static_cast<int>(r) - oh * a.OW;
+            float m = -INFINITY;
+            for (int i = 0; i < a.kh; i++) {
+                const int ih = oh * a.sh + i - a.ph;
+                if (ih < 0 || ih >= a.H) continue;
+                for (int j = 0; j < a.kw; j++) {
+                    const int iw = ow * a.sw + j - a.pw;
+                    if (iw < 0 || iw >= a.W) continue;
+                    const float v = xp[ih * a.W + iw];
+                    if (v > m) m = v;
+                }
             }
+            yp[r] = m;
         }
-        a.y[idx] = m;
     }
 }
 
@@ -550,7 +554,11 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
     if (total == 0) return 0;
     set_kernel_name(ctx, node, "maxpool");
-    hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, p);
+    const size_t per_plane = static_cast<size_t>(p.OH) * p.OW, planes = static_cast<size_t>(p.N) * p.C;
+    if (per_plane > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>(std::min<size_t>((per_plane + 255) / 256, 1024)),
+                    static_cast<unsigned>(std::min<size_t>(planes, 65535)));
+    hipLaunchKernelGGL(maxpool_kernel, grid, dim3(256), 0, ctx->stream, p);
     return launch_status("maxpool");
 }
 
