@@ -215,16 +215,30 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
             &Bs[BUF][bcol * LDK + bgrp * KPT + j]) = floatx4{BR[j], BR[j + 1], BR[j + 2], BR[j + 3]};                \
     }
 
+    // Operand fragments of one 8-k step: one ds_read_b128 per 32-row block.
+#define IGEMM_FRAG(BUF, K8, AF, BF)                                                                                  \
+    {                                                                                                                \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) AF[i] =                                                       \
+            *reinterpret_cast<const floatx4 *>(&As[BUF][((wm * TM + i) * 32 + row) * LDK + (K8) * 8 + khalf]);       \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) BF[j] =                                                       \
+            *reinterpret_cast<const floatx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + (K8) * 8 + khalf]);       \
+    }
+#define IGEMM_MMA(AF, BF)                                                                                            \
+    _Pragma("unroll") for (int s = 0; s < 4; s++) _Pragma("unroll") for (int i = 0; i < TM; i++)                     \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =                                                   \
+            __builtin_amdgcn_mfma_f32_32x32x2f32(AF[i][s], BF[j][s], acc[i][j], 0, 0, 0);
+    // The fragments of step k8+1 are read while the MFMAs of step k8 run
+    // (two register sets), so LDS latency stays off the MFMA chain.
 #define IGEMM_COMPUTE(BUF)                                                                                           \
-    _Pragma("unroll") for (int k8 = 0; k8 < BK / 8; k8++) {                                                          \
-        floatx4 af[TM], bf[TN];                                                                                      \
-        _Pragma("unroll") for (int i = 0; i < TM; i++) af[i] =                                                       \
-            *reinterpret_cast<const floatx4 *>(&As[BUF][((wm * TM + i) * 32 + row) * LDK + k8 * 8 + khalf]);         \
-        _Pragma("unroll") for (int j = 0; j < TN; j++) bf[j] =                                                       \
-            *reinterpret_cast<const floatx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + k8 * 8 + khalf]);         \
-        _Pragma("unroll") for (int s = 0; s < 4; s++) _Pragma("unroll") for (int i = 0; i < TM; i++)                 \
-            _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =                                               \
-                __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][s], bf[j][s], acc[i][j], 0, 0, 0);                        \
+    {                                                                                                                \
+        floatx4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];                                                                  \
+        IGEMM_FRAG(BUF, 0, fa0, fb0);                                                                                \
+        _Pragma("unroll") for (int k8 = 0; k8 < BK / 8; k8 += 2) {                                                   \
+            if (k8 + 1 < BK / 8) IGEMM_FRAG(BUF, k8 + 1, fa1, fb1);                                                  \
+            IGEMM_MMA(fa0, fb0);                                                                                     \
+            if (k8 + 2 < BK / 8) IGEMM_FRAG(BUF, k8 + 2, fa0, fb0);                                                  \
+            if (k8 + 1 < BK / 8) { IGEMM_MMA(fa1, fb1); }                                                            \
+        }                                                                                                            \
     }
 
     // One pipeline step: tile KT is in LDS buffer BUF, tile KT+1 is in flight
@@ -264,6 +278,8 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
         }
 #undef IGEMM_STEP
 #undef IGEMM_COMPUTE
+#undef IGEMM_MMA
+#undef IGEMM_FRAG
 #undef IGEMM_LOAD_TILE
 #undef IGEMM_STORE_TILE
 
