@@ -36,6 +36,7 @@ sys.path.insert(0, str(ROOT))
 
 FP32_MFMA_PEAK_TFLOPS = 157.3
 INT8_MFMA_PEAK_TOPS = 5000.0
+HBM_PEAK_GBPS = 8000.0
 
 
 def log(msg: str) -> None:
@@ -159,11 +160,17 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
 
     g, blob = build(batch)
     ops = {}
+    hbm = 0  # algorithmic bytes of the INT8 convs under the reference's fp32-in / fp32-out semantics
     for n in g.nodes:
         if n.op_type == "Conv":
+            xsh = g.shape(n.inputs[0])
             y = g.shape(n.outputs[0])
             w = g.tensors[n.inputs[1]].shape
             ops[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
+            y_bytes = 4 * y[0] * y[1] * y[2] * y[3]
+            hbm += 4 * xsh[0] * xsh[1] * xsh[2] * xsh[3] + w[0] * w[1] * w[2] * w[3] + y_bytes
+            hbm += y_bytes if len(n.inputs) > 3 else 0      # fused residual
+            hbm += 4 * y[1] if len(n.inputs) > 2 else 0     # bias
     x = models.make_input(g.tensors[g.inputs[0]].shape)
     m = Model(blob, lib=lib)
     xin = DeviceBuffer(x.nbytes, lib)
@@ -192,11 +199,20 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     m.close()
     xin.free()
     tops = sum(ops.values()) / (conv_ms * 1e-3) / 1e12
+    gbps = hbm / (conv_ms * 1e-3) / 1e9
+    # fp32 activations in and out make these convs HBM-bound: at the int8
+    # MFMA peak the convs would take sum(ops)/5e15 s, far less than moving
+    # their fp32 activations at 8 TB/s; the binding roofline is HBM
     out = {"workload": "resnet50_int8_224", "batch": batch, "images_per_sec": batch * steps / elapsed,
            "ms_per_step": elapsed * 1e3 / steps, "conv_ms_per_step": conv_ms,
            "conv_gop_per_image": sum(ops.values()) / batch / 1e9, "conv_kernels": names,
-           "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
-                        "frac": tops / INT8_MFMA_PEAK_TOPS}}
+           "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": gbps / HBM_PEAK_GBPS, "traffic": None,
+                        "algorithmic_bytes": hbm,
+                        "floor_ms": {"hbm": hbm / HBM_PEAK_GBPS / 1e6,
+                                     "mfma": sum(ops.values()) / INT8_MFMA_PEAK_TOPS / 1e9}},
+           "mfma": {"achieved": tops, "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                    "frac": tops / INT8_MFMA_PEAK_TOPS}}
     if b1_steps > 0:
         g1q, blob1 = build(1)
         m1 = Model(blob1, lib=lib)

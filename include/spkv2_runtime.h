@@ -79,7 +79,11 @@ int spkv2_load_file(const char *path, Spkv2Context **out_ctx);
 int spkv2_load_memory(const void *data, size_t size, Spkv2Context **out_ctx);
 /* reference: runtime/core/executor.c:189 */
 int spkv2_prepare(Spkv2Context *ctx, void *arena, size_t arena_size);
-/* reference: runtime/core/executor.c:193 */
+/* reference: runtime/core/executor.c:193.  The scratch arena (device memory,
+ * at least header.scratch_arena_bytes, else -2) also holds the conv / Gemm
+ * workspaces of mi355x packages (padded input copies, split-K partials): a
+ * plan that fits its kernel spec's scratch_bytes runs there, so the runtime
+ * allocates workspace only for plans that outgrow their spec. */
 int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t arena_size, void *scratch,
                                size_t scratch_size);
 /* reference: runtime/core/executor.c:249 (host -> device copy) */
