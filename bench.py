@@ -234,6 +234,43 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     return out
 
 
+# Memory-bound ops at ResNet / YOLO shapes: (label, single_op args, algorithmic bytes)
+ELEMENTWISE = [
+    ("maxpool_3x3s2_b64_64x112", ("MaxPool", [64, 64, 112, 112]), 4 * (64 * 64 * 112 * 112 + 64 * 64 * 56 * 56)),
+    ("add_b64_256x56", ("Add", [64, 256, 56, 56]), 12 * 64 * 256 * 56 * 56),
+    ("resize2x_b16_128x80", ("Resize", [16, 128, 80, 80]), 20 * 16 * 128 * 80 * 80),
+    ("softmax_4096x1000", ("Softmax", [4096, 1000]), 8 * 4096 * 1000),
+]
+
+
+def elementwise(lib, reps: int = 20) -> dict:
+    """Achieved HBM GB/s of the memory-bound kernels (device time from HIP
+    events around the node), against the 8 TB/s peak; algorithmic bytes are
+    each op's reads + writes, every element once."""
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk import models, write_spk
+
+    out = {}
+    for label, (op, shape), nbytes in ELEMENTWISE:
+        g = models.single_op(op, shape)
+        m = Model(write_spk(g, "mi355x"), lib=lib)
+        for i, t in enumerate(g.inputs):
+            m.set_input(i, models.make_input(g.tensors[t].shape, 7 + i))
+        m.run()
+        m.set_profiling(True)
+        m.reset_node_times()
+        for _ in range(reps):
+            m.run()
+        lib.spkv2_device_synchronize()
+        ms, cnt = m.node_time(g.nodes[0].id)
+        us = ms / max(cnt, 1) * 1e3
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[label] = {"kernel": m.kernel_name(g.nodes[0].id), "us": us, "gbps": gbps,
+                      "frac": gbps / HBM_PEAK_GBPS, "bytes": nbytes}
+        m.close()
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -247,6 +284,8 @@ def main() -> None:
     ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
     ap.add_argument("--no-int8", action="store_true", help="skip the INT8 ResNet-50 section")
     ap.add_argument("--int8-only", action="store_true", help="run only the INT8 ResNet-50 section")
+    ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound op section")
+    ap.add_argument("--elementwise-only", action="store_true", help="run only the memory-bound op section")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
     args = ap.parse_args()
@@ -262,6 +301,9 @@ def main() -> None:
     from spinnv2_amd.spk import models, write_spk
 
     lib = load_library()
+    if args.elementwise_only:
+        print(json.dumps(elementwise(lib)), flush=True)
+        return
     if args.int8_only:
         print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report)), flush=True)
         return
@@ -342,6 +384,7 @@ def main() -> None:
     b1_ms = batch1_latency(args.depth, args.b1_steps, lib) if args.b1_steps > 0 else None
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps)
+    ew = None if args.no_elementwise else elementwise(lib)
 
     result = {
         "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
@@ -373,6 +416,7 @@ def main() -> None:
                      "kernel": "conv_igemm_f32 (all conv nodes; HIP events per node on the run stream)"},
         "cpu_baseline": base,
         "int8": int8,
+        "elementwise": ew,
         "top1_image0": int(logits[0].argmax()),
     }
     print(json.dumps(result), flush=True)

@@ -199,6 +199,49 @@ __global__ void __launch_bounds__(256) maxpool_kernel(PoolArgs a) {
     }
 }
 
+// The ResNet stem's 3x3 / stride 2 / pad 1 MaxPool when W is a multiple of 8
+// and W == 2*OW: each thread makes 4 consecutive outputs of one row from a
+// scalar and two 16-byte loads per input row (the 9 columns its windows
+// touch), visiting each window in the reference's order (rows, then
+// columns, strict >), and stores them as one 16-byte write.
+__global__ void __launch_bounds__(256) maxpool3s2_x4(const float *__restrict__ x, float *__restrict__ y, unsigned planes,
+                                                     int H, int W, int OH, int OW) {
+    const unsigned groups = static_cast<unsigned>(OH * (OW / 4));
+    for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float *xp = x + static_cast<size_t>(plane) * H * W;
+        float *yp = y + static_cast<size_t>(plane) * OH * OW;
+        for (unsigned g = blockIdx.x * 256 + threadIdx.x; g < groups; g += gridDim.x * 256) {
+            const int oh = static_cast<int>(g / static_cast<unsigned>(OW / 4));
+            const int ow0 = 4 * (static_cast<int>(g) - oh * (OW / 4));
+            float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+            for (int i = 0; i < 3; i++) {
+                const int ih = 2 * oh - 1 + i;
+                if (ih < 0 || ih >= H) continue;
+                const float *row = xp + ih * W + 2 * ow0;
+                float c[9];  // input columns 2*ow0-1 .. 2*ow0+7
+                c[0] = ow0 > 0 ? row[-1] : 0.0f;
+                const floatx4 lo = *reinterpret_cast<const floatx4 *>(row);
+                const floatx4 hi = *reinterpret_cast<const floatx4 *>(row + 4);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    c[1 + e] = lo[e];
+                    c[5 + e] = hi[e];
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int j = 0; j < 3; j++) {
+                        if (t == 0 && j == 0 && ow0 == 0) continue;  // column -1: outside the input
+                        const float v = c[2 * t + j];
+                        if (v > m[t]) m[t] = v;
+                    }
+            }
+            *reinterpret_cast<floatx4 *>(yp + oh * OW + ow0) = floatx4{m[0], m[1], m[2], m[3]};
+        }
+    }
+}
+
 // reference pool/avgpool.c:21-45: mean over the in-bounds taps
 __global__ void __launch_bounds__(256) avgpool_kernel(PoolArgs a) {
     const size_t total = static_cast<size_t>(a.N) * a.C * a.OH * a.OW;
@@ -553,6 +596,17 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     if (int rc = pool_args(ctx, node, &p)) return rc;
     const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
     if (total == 0) return 0;
+    if (p.kh == 3 && p.kw == 3 && p.sh == 2 && p.sw == 2 && p.ph == 1 && p.pw == 1 && p.W % 8 == 0 &&
+        p.W == 2 * p.OW && p.H == 2 * p.OH && p.OW % 4 == 0) {
+        set_kernel_name(ctx, node, "maxpool3s2_x4");
+        const size_t groups = static_cast<size_t>(p.OH) * (p.OW / 4), planes = static_cast<size_t>(p.N) * p.C;
+        if (groups > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+        const dim3 grid(static_cast<unsigned>(std::min<size_t>((groups + 255) / 256, 1024)),
+                        static_cast<unsigned>(std::min<size_t>(planes, 65535)));
+        hipLaunchKernelGGL(maxpool3s2_x4, grid, dim3(256), 0, ctx->stream, p.x, p.y, static_cast<unsigned>(planes), p.H,
+                           p.W, p.OH, p.OW);
+        return launch_status("maxpool");
+    }
     set_kernel_name(ctx, node, "maxpool");
     const size_t per_plane = static_cast<size_t>(p.OH) * p.OW, planes = static_cast<size_t>(p.N) * p.C;
     if (per_plane > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
@@ -694,6 +748,27 @@ int reduce_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     return launch_status("reduce");
 }
 
+// Exact 2x nearest upsampling (OH == 2H, OW == 2W, W even; the reference's
+// floor(o / 2) index): each thread reads 2 input columns (8 bytes) and
+// writes them doubled to both output rows (two 16-byte stores).
+__global__ void __launch_bounds__(256) resize2x_x2(const float *__restrict__ x, float *__restrict__ y, unsigned planes,
+                                                   int H, int W) {
+    const unsigned pairs = static_cast<unsigned>(H * (W / 2));
+    const int OW = 2 * W;
+    for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float *xp = x + static_cast<size_t>(plane) * H * W;
+        float *yp = y + static_cast<size_t>(plane) * 4 * H * W;
+        for (unsigned q = blockIdx.x * 256 + threadIdx.x; q < pairs; q += gridDim.x * 256) {
+            const int ih = static_cast<int>(q / static_cast<unsigned>(W / 2));
+            const int iw = 2 * (static_cast<int>(q) - ih * (W / 2));
+            const floatx2 v = *reinterpret_cast<const floatx2 *>(xp + ih * W + iw);
+            const floatx4 o = floatx4{v[0], v[0], v[1], v[1]};
+            *reinterpret_cast<floatx4 *>(yp + (2 * ih) * OW + 2 * iw) = o;
+            *reinterpret_cast<floatx4 *>(yp + (2 * ih + 1) * OW + 2 * iw) = o;
+        }
+    }
+}
+
 int resize_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]), *yr = rec(ctx, node->outputs[0]);
     if (xr->rank != 4 || yr->rank != 4) return -11;
@@ -701,6 +776,17 @@ int resize_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const int H = xr->shape[2], W = xr->shape[3];
     const size_t total = static_cast<size_t>(N) * C * OH * OW;
     if (total == 0) return 0;
+    if (OH == 2 * H && OW == 2 * W && W % 2 == 0 && static_cast<int>(xr->shape[0]) == N &&
+        static_cast<int>(xr->shape[1]) == C) {
+        set_kernel_name(ctx, node, "resize2x_x2");
+        const size_t pairs = static_cast<size_t>(H) * (W / 2), planes = static_cast<size_t>(N) * C;
+        if (pairs > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+        const dim3 grid(static_cast<unsigned>(std::min<size_t>((pairs + 255) / 256, 1024)),
+                        static_cast<unsigned>(std::min<size_t>(planes, 65535)));
+        hipLaunchKernelGGL(resize2x_x2, grid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]),
+                           dptr<float>(ctx, node->outputs[0]), static_cast<unsigned>(planes), H, W);
+        return launch_status("resize");
+    }
     const float scale_h = static_cast<float>(OH) / static_cast<float>(H);
     const float scale_w = static_cast<float>(OW) / static_cast<float>(W);
     set_kernel_name(ctx, node, "resize_nearest");

@@ -90,6 +90,11 @@ EXACT_OPS = [
     ("Add", [1, 8, 5, 5], dict(relu=True)),
     ("Relu", [3, 7, 11], {}),
     ("Resize", [1, 4, 10, 12], dict(scale=2)),
+    # the vectorized 3x3/s2/p1 MaxPool (W % 8 == 0) and 2x Resize (W even) paths, and an odd-W Resize
+    ("MaxPool", [2, 8, 32, 48], dict(k=3, s=2, p=1)),
+    ("MaxPool", [1, 3, 16, 8], dict(k=3, s=2, p=1)),
+    ("Resize", [2, 3, 6, 10], dict(scale=2)),
+    ("Resize", [2, 3, 5, 7], dict(scale=2)),
 ]
 
 
