@@ -357,6 +357,45 @@ __global__ void __launch_bounds__(256) softmax_rows(const float *__restrict__ x,
     for (int i = lane; i < dim; i += 64) yr[i] = yr[i] / s;
 }
 
+// Rows of at most 2048 values that are a multiple of 4 long: one wave per
+// row holds the row in registers (up to 8 float4 per lane), so the row is
+// read once and written once.
+__global__ void __launch_bounds__(256) softmax_rows_reg(const float *__restrict__ x, float *__restrict__ y, size_t rows,
+                                                        int dim) {
+    const int lane = threadIdx.x & 63;
+    const size_t row = static_cast<size_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const floatx4 *xr = reinterpret_cast<const floatx4 *>(x + row * dim);
+    floatx4 *yr = reinterpret_cast<floatx4 *>(y + row * dim);
+    const int quads = dim / 4;
+    floatx4 v[8];
+    float m = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int q = t * 64 + lane;
+        v[t] = q < quads ? xr[q] : floatx4{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        m = fmaxf(m, fmaxf(fmaxf(v[t][0], v[t][1]), fmaxf(v[t][2], v[t][3])));
+    }
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        if (t * 64 + lane < quads) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                v[t][e] = expf(v[t][e] - m);
+                s += v[t][e];
+            }
+        }
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        const int q = t * 64 + lane;
+        if (q < quads) yr[q] = floatx4{v[t][0] / s, v[t][1] / s, v[t][2] / s, v[t][3] / s};
+    }
+}
+
 // Softmax along a strided axis: thread per (outer, inner) column, lanes
 // adjacent in `inner` so every pass over d is coalesced.
 __global__ void __launch_bounds__(256) softmax_strided(const float *__restrict__ x, float *__restrict__ y, size_t outer,
@@ -653,7 +692,9 @@ int softmax_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     float *y = dptr<float>(ctx, node->outputs[0]);
     if (outer * inner == 0 || dim == 0) return 0;
     set_kernel_name(ctx, node, "softmax");
-    if (inner == 1)
+    if (inner == 1 && dim % 4 == 0 && dim <= 2048)
+        hipLaunchKernelGGL(softmax_rows_reg, dim3(blocks_for(outer, 4)), dim3(256), 0, ctx->stream, x, y, outer, dim);
+    else if (inner == 1)
         hipLaunchKernelGGL(softmax_rows, dim3(blocks_for(outer, 4)), dim3(256), 0, ctx->stream, x, y, outer, dim);
     else
         hipLaunchKernelGGL(softmax_strided, dim3(grid_for(outer * inner, 256)), dim3(256), 0, ctx->stream, x, y, outer,

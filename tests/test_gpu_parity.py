@@ -111,6 +111,9 @@ def test_exact_ops_bitwise(gpu, op, shape, kw):
 FLOAT_OPS = [
     ("Softmax", [4, 1000], dict(axis=-1)),
     ("Softmax", [2, 16, 50], dict(axis=1)),
+    ("Softmax", [5, 2048], dict(axis=-1)),     # register-resident rows at their limit
+    ("Softmax", [3, 2052], dict(axis=-1)),     # longer rows: three passes
+    ("Softmax", [3, 6, 7], dict(axis=-1)),     # rows not a multiple of 4
     ("ReduceMean", [4, 2048, 7, 7], dict(axes=[2, 3])),
     ("ReduceMean", [2, 6, 5, 4], dict(axes=[1])),
     ("GlobalAveragePool", [2, 32, 7, 7], {}),
