@@ -153,6 +153,37 @@ def test_resnet18_e2e_b1(gpu):
     assert np.argmax(got) == np.argmax(want)
 
 
+def test_resnet101_e2e_b1(gpu):
+    """The benchmark network at batch 1 against the oracle."""
+    g = models.resnet(101, 1)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+    assert np.argmax(got) == np.argmax(want)
+
+
+def test_resnet101_b64_images_match_batch1(gpu):
+    """The benchmark configuration itself (ResNet-101, 224x224, batch 64):
+    every image is independent through every node, so images 0 and 63 of
+    the batch-64 run must agree with batch-1 runs of the same images (other
+    tiles and split-K choices, so within the fp32 tolerance), and image 0
+    with the oracle."""
+    g64 = models.resnet(101, 64)
+    x = rng_inputs(g64)[0]
+    out64 = run_gpu(write_spk(g64, "mi355x"), [x])[0].reshape(64, -1)
+    g1 = models.resnet(101, 1)
+    blob1 = write_spk(g1, "mi355x")
+    for i in (0, 63):
+        one = run_gpu(blob1, [x[i:i + 1]])[0]
+        assert tnorm_err(out64[i], one) <= FP32_TOL, i
+        assert np.argmax(out64[i]) == np.argmax(one), i
+    want0 = run_oracle(blob1, [x[0:1]])[0]
+    assert tnorm_err(out64[0], want0) <= FP32_TOL
+    assert np.argmax(out64[0]) == np.argmax(want0)
+
+
 def test_cpu_generic_package_runs_on_gpu(gpu):
     """A package compiled for cpu_generic (bnns / simd kinds) runs unchanged."""
     g = models.resnet(18, 1)
