@@ -260,9 +260,9 @@ def test_graph_mode_matches_eager(gpu):
             np.testing.assert_array_equal(m.get_output(0), eager)
 
 
-# Every tile configuration, with and without split-K (the last slice of a
-# tile to finish sums the partials in slice order inside the conv kernel),
-# on a ragged residual conv; forced through the tuning overrides.
+# Every tile configuration, with and without split-K (each slice writes its
+# partial tile; splitk_epilogue sums them in slice order and applies the
+# epilogue), on a ragged residual conv; forced through the tuning overrides.
 SPLIT_CASES = [(cfg, split) for cfg in range(8) for split in (1, 3, 8)]
 
 
@@ -279,8 +279,8 @@ def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
 
 
 def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
-    """Split-K counters re-arm themselves, so replays of a captured graph
-    (no memset nodes) give the eager result every time."""
+    """Split-K partials are fully rewritten by every run (no memset nodes in
+    the captured graph), so its replays give the eager result every time."""
     from spinnv2_amd.runtime import Model
 
     monkeypatch.setenv("SPKV2_CONV_SPLITK", "6")
