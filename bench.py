@@ -163,6 +163,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     g, blob = build(batch)
     ops = {}
     hbm = 0  # algorithmic bytes of the INT8 convs under the reference's fp32-in / fp32-out semantics
+    node_bytes = {}
     for n in g.nodes:
         if n.op_type == "Conv":
             xsh = g.shape(n.inputs[0])
@@ -170,9 +171,11 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
             w = g.tensors[n.inputs[1]].shape
             ops[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
             y_bytes = 4 * y[0] * y[1] * y[2] * y[3]
-            hbm += 4 * xsh[0] * xsh[1] * xsh[2] * xsh[3] + w[0] * w[1] * w[2] * w[3] + y_bytes
-            hbm += y_bytes if len(n.inputs) > 3 else 0      # fused residual
-            hbm += 4 * y[1] if len(n.inputs) > 2 else 0     # bias
+            nb = 4 * xsh[0] * xsh[1] * xsh[2] * xsh[3] + w[0] * w[1] * w[2] * w[3] + y_bytes
+            nb += y_bytes if len(n.inputs) > 3 else 0      # fused residual
+            nb += 4 * y[1] if len(n.inputs) > 2 else 0     # bias
+            node_bytes[n.id] = nb
+            hbm += nb
     x = models.make_input(g.tensors[g.inputs[0]].shape)
     m = Model(blob, lib=lib)
     xin = DeviceBuffer(x.nbytes, lib)
@@ -207,7 +210,8 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
             n = g.nodes[nid]
             xs_, ws_ = g.shape(n.inputs[0]), g.tensors[n.inputs[1]].shape
             log(f"int8 node {nid:3d} {xs_[1]}x{xs_[2]}->{ws_[0]} k{ws_[2]} s{n.attrs['strides'][0]} "
-                f"{m.kernel_name(nid):52s} {ms / max(cnt, 1) * 1e3:8.1f} us {ops[nid] / (ms / max(cnt, 1)) / 1e9:7.1f} TOP/s")
+                f"{m.kernel_name(nid):52s} {ms / max(cnt, 1) * 1e3:8.1f} us {ops[nid] / (ms / max(cnt, 1)) / 1e9:7.1f} TOP/s "
+                f"{node_bytes[nid] / (ms / max(cnt, 1)) / 1e6:7.1f} GB/s")
     names = sorted({m.kernel_name(nid).split("<")[0] for nid in ops})
     m.close()
     xin.free()

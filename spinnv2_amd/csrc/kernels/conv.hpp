@@ -52,13 +52,18 @@ struct ConvPlan {
     // int8 requantize handoff.  Producer side: this conv's output is also
     // quantized in its epilogue, with the consuming int8 conv's scale and
     // rounding rule, into that conv's zero-padded NHWC buffer (not owned);
-    // y_needed says whether the fp32 output still has other readers.
+    // q_readers counts the consumers that read q_out; y_needed says whether
+    // the fp32 output still has other readers.
     int8_t *q_out;
     int q_Hp, q_Wp, q_Cp, q_pt, q_pl, q_split;
     float q_inv_scale;
+    int q_readers;
     bool y_needed;
-    // Consumer side: the padded NHWC int8 input its producer writes (owned).
+    // Consumer side: the padded NHWC int8 input its producer writes (owned),
+    // or, for a later consumer of the same tensor with the same scale and
+    // layout, the first consumer's buffer (q_shared, not owned).
     int8_t *q_in;
+    int8_t *q_shared;
     // fp32 handoff, the same for the zero-padded NCHW input of a padded
     // conv: producer side (not owned) and consumer side (owned).
     float *pad_out;

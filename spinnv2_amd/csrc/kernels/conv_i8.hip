@@ -753,9 +753,12 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
 // Requantize handoff.  When this int8 conv's input is the only output of an
 // earlier int8 conv, that conv quantizes its result in registers (with this
 // conv's scale and rounding split) straight into a zero-padded NHWC buffer
-// owned by this plan, and this conv skips its quantize pass.  The producer
-// still writes the fp32 tensor when anything else reads it (another
-// consumer, a graph output).  Packages with a protection plan keep every
+// owned by this plan, and this conv skips its quantize pass.  A later int8
+// consumer of the same tensor whose quantization is identical (same scale,
+// rounding split and padded layout: e.g. the 1x1 stride-2 projection beside
+// the next block's 1x1 conv) reads that same buffer.  The producer still
+// writes the fp32 tensor when anything else reads it (a consumer served by
+// neither, a graph output).  Packages with a protection plan keep every
 // tensor materialized and do not hand off.
 static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan, const I8Layout &L) {
     if (ctx->protection_count > 0) return 0;
@@ -775,12 +778,24 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
     if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
     if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
     ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
-    if (!pp || pp->path != CONV_IGEMM_I8 || pp->q_out) return 0;
+    if (!pp || pp->path != CONV_IGEMM_I8) return 0;
     const ConvGeom &g = plan->g;
     if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
     bool is_output = false;
     for (size_t i = 0; i < ctx->output_count; i++)
         if (ctx->output_ids[i] == t) is_output = true;
+    const float inv = 1.0f / plan->x_scale;  // reference conv_int8.c:23
+    if (pp->q_out) {
+        // the tensor is already handed off to an earlier consumer: share its
+        // buffer when this conv would quantize to exactly the same bytes
+        if (pp->q_Hp != L.Hp || pp->q_Wp != L.Wp || pp->q_Cp != L.Cp || pp->q_pt != L.pt || pp->q_pl != L.pl ||
+            pp->q_split != plan->quant_split || __builtin_bit_cast(uint32_t, pp->q_inv_scale) != __builtin_bit_cast(uint32_t, inv))
+            return 0;
+        plan->q_shared = pp->q_out;
+        pp->q_readers++;
+        pp->y_needed = readers > pp->q_readers || is_output;
+        return 0;
+    }
     const size_t bytes = static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp;
     if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->q_in), bytes), "hipMalloc int8 handoff"))
         return rc;
@@ -794,8 +809,9 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
     pp->q_pt = L.pt;
     pp->q_pl = L.pl;
     pp->q_split = plan->quant_split;
-    pp->q_inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
-    pp->y_needed = readers > 1 || is_output;
+    pp->q_inv_scale = inv;
+    pp->q_readers = 1;
+    pp->y_needed = readers > pp->q_readers || is_output;
     return 0;
 }
 
@@ -895,7 +911,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
         return rc;
     if (int rc = setup_handoff(ctx, node, plan, L)) return rc;
     set_kernel_name(ctx, node, std::string("conv_igemm_i8<") + t.name + (L.runs ? ",runs" : ",taps") +
-                                   ",splitk=" + std::to_string(plan->splitk) + (plan->q_in ? ",handoff" : "") + ">");
+                                   ",splitk=" + std::to_string(plan->splitk) + (plan->q_in ? ",handoff" : plan->q_shared ? ",shared" : "") + ">");
     return 0;
 }
 
@@ -911,8 +927,8 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     // a fault event may change the fp32 input after its producer ran: then
     // every tensor is materialized and quantized here
     const bool handoff = !ctx->fault_event.enabled;
-    if (plan->q_in && handoff) {
-        xq = plan->q_in;  // written by the producer's epilogue
+    if ((plan->q_in || plan->q_shared) && handoff) {
+        xq = plan->q_in ? plan->q_in : plan->q_shared;  // written by the producer's epilogue
     } else {
         dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
                    static_cast<unsigned>(g.N));

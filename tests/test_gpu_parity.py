@@ -7,6 +7,8 @@ dequantized outputs bit-exact.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -352,6 +354,111 @@ def test_int8_chain_bit_exact(gpu, monkeypatch, handoff):
     assert sum(",handoff" in s for s in names) == (4 if handoff == "1" else 0)
     for a_, b_ in zip(got, want):
         np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
+
+
+def _int8_siblings():
+    """One int8 conv whose output is read by three int8 convs: a 1x1 (takes
+    the handoff), a 1x1 stride 2 (same quantization: shares that buffer) and
+    a 3x3 pad 1 (another padded layout: quantizes for itself)."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    p = models.Params(5)
+    g = Graph("i8siblings")
+    x = g.input("x", [2, 48, 15, 13])
+    h = g.relu(g.conv(x, p.he((64, 48, 1, 1)), p.normal(64, 0.01)))
+    g.mark_output(g.conv(h, p.he((40, 64, 1, 1)), p.normal(40, 0.01)))
+    g.mark_output(g.conv(h, p.he((72, 64, 1, 1)), None, stride=2))
+    g.mark_output(g.conv(h, p.he((24, 64, 3, 3)), p.normal(24, 0.01), pad=1))
+    run_default_pipeline(g)
+    xs = rng_inputs(g)
+    samples = [[models.make_input([2, 48, 15, 13], 600 + i)] for i in range(3)]
+    qp = calibrate_activation_scales(g, samples) + quantize_conv_weights(g)
+    return g, xs, write_spk(g, "mi355x", quant_params=qp)
+
+
+@pytest.mark.parametrize("handoff", ["1", "0"])
+def test_int8_shared_handoff_bit_exact(gpu, monkeypatch, handoff):
+    """Two consumers read one handed-off int8 buffer; the third quantizes the
+    fp32 tensor, which the producer therefore still writes.  Bit-exact
+    against the oracle, and unchanged with a fault event armed (every tensor
+    materialized)."""
+    from spinnv2_amd.runtime import FaultEvent, Model
+
+    monkeypatch.setenv("SPKV2_I8_HANDOFF", handoff)
+    g, xs, blob = _int8_siblings()
+    want = run_oracle(blob, xs)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = [m.get_output(i) for i in range(3)]
+        names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+        ev = FaultEvent(node_id=0, tensor_id=g.nodes[0].outputs[0], element_index=0, bit_index=0,
+                        invocation_index=1000, seed=0, enabled=1)
+        m.set_fault_event(ev)
+        m.set_input(0, xs[0])
+        m.run()
+        armed = [m.get_output(i) for i in range(3)]
+    assert len(names) == 4 and all("conv_igemm_i8" in s for s in names)
+    if handoff == "1":
+        assert [",handoff" in s for s in names] == [False, True, False, False], names
+        assert [",shared" in s for s in names] == [False, False, True, False], names
+    else:
+        assert not any(",handoff" in s or ",shared" in s for s in names), names
+    for a_, b_, c_ in zip(got, want, armed):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
+        np.testing.assert_array_equal(c_.view(np.uint32), b_.view(np.uint32))
+
+
+def test_int8_shared_handoff_skips_unread_fp32(gpu):
+    """With only the two 1x1 consumers, every reader is served in int8: the
+    producer's fp32 output is not written, and the results stay exact."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+    from spinnv2_amd.runtime import Model
+
+    p = models.Params(6)
+    g = Graph("i8pair")
+    x = g.input("x", [1, 32, 9, 11])
+    h = g.relu(g.conv(x, p.he((64, 32, 3, 3)), p.normal(64, 0.01), pad=1))
+    g.mark_output(g.conv(h, p.he((16, 64, 1, 1)), p.normal(16, 0.01)))
+    g.mark_output(g.conv(h, p.he((16, 64, 1, 1)), p.normal(16, 0.01), stride=2))
+    run_default_pipeline(g)
+    xs = rng_inputs(g)
+    qp = calibrate_activation_scales(g, [[models.make_input([1, 32, 9, 11], 700 + i)] for i in range(3)])
+    blob = write_spk(g, "mi355x", quant_params=qp + quantize_conv_weights(g))
+    want = run_oracle(blob, xs)
+    from spinnv2_amd.spk import format as F
+
+    h_id = g.nodes[0].outputs[0]
+    with Model(blob) as m:
+        lib = m.lib
+        names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+
+        def span(tid):
+            rec = F.TENSOR.unpack(ctypes.string_at(lib.spkv2_ctx_tensor_record(m.ctx, tid), F.TENSOR.size))
+            return rec[14], rec[14] + rec[13]
+
+        h0, h1 = span(h_id)
+        others = [span(t) for t in [g.inputs[0]] + [n.outputs[0] for n in g.nodes[1:]]]
+        assert all(e <= h0 or b >= h1 for b, e in others), "the plan places another tensor over h"
+        sentinel = np.full((h1 - h0) // 4, 0x7FC00001, np.uint32)
+        m.set_input(0, xs[0])
+        m.run()
+        got = [m.get_output(i) for i in range(2)]
+        hptr = lib.spkv2_ctx_tensor_data(m.ctx, h_id)
+        assert lib.spkv2_device_memcpy_h2d(hptr, sentinel.ctypes.data, sentinel.nbytes) == 0
+        m.set_input(0, xs[0])
+        m.run()
+        again = [m.get_output(i) for i in range(2)]
+        back = np.empty_like(sentinel)
+        assert lib.spkv2_device_memcpy_d2h(back.ctypes.data, hptr, back.nbytes) == 0
+    assert ",handoff" in names[1] and ",shared" in names[2], names
+    for i, (a_, b_) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}")
+    for i, (a_, b_) in enumerate(zip(again, want)):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}, second run")
+    np.testing.assert_array_equal(back, sentinel)  # the fp32 tensor was not rewritten
 
 
 @pytest.mark.parametrize("handoff", ["1", "0"])
