@@ -103,7 +103,7 @@ constexpr int kOobOffset = 0x7fff0000;
 
 struct IgemmArgs {
     const float *__restrict__ x;     // B-operand source: NCHW input, zero-padded when the conv pads
-    const float *__restrict__ wp;    // [m_tiles][k_tiles][BM][BK] packed weights
+    const float *__restrict__ wp;    // [m_tiles][k_tiles] BM x BK tiles in MFMA fragment order
     const int *__restrict__ koff;    // [Kpad + 2*BK] byte offset of k = (c, kh, kw) in x, kOobOffset past K
     const float *__restrict__ bias;  // [M] or null
     const float *__restrict__ res;   // like y, or null
@@ -139,14 +139,13 @@ template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
 __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     constexpr int TM = BM / (32 * WAVES_M);
     constexpr int TN = BN / (32 * WAVES_N);
+    constexpr int K8 = BK / 8;
     constexpr int LDK = BK + (BK == 16 ? 8 : 4);  // row pitch (floats): keeps b128 LDS traffic conflict-free
     constexpr int KPT = BK * BN / 256;  // B elements per thread per k-tile
-    constexpr int APT = BM * BK / 1024; // A float4 per thread per k-tile
     static_assert(WAVES_M * WAVES_N == 4, "four waves");
-    static_assert(TM >= 1 && TN >= 1 && KPT % 4 == 0 && APT >= 1 && BN >= 64, "tile shape");
+    static_assert(TM >= 1 && TN >= 1 && KPT % 4 == 0 && BN >= 64, "tile shape");
     static_assert(BK % 8 == 0, "BK multiple of 8");
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM * LDK];
     __shared__ __attribute__((aligned(16))) float Bs[2][BN * LDK];
 
     const int tid = threadIdx.x;
@@ -187,69 +186,74 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
             }
         }
 
-        // Two register sets, each holding one k-tile in flight: the loads of
-        // tile t+2 are issued while tile t is multiplied.  Native vector
-        // types: arrays of HIP's float4 class are not promoted to registers.
-        floatx4 ar0[APT], ar1[APT];
+        // The weight operand goes straight from memory (L2: a layer's weights
+        // are shared by all its workgroups) into MFMA fragment registers, one
+        // k-tile ahead, in two register sets; the gathered activation operand
+        // is staged through LDS (shared by the waves of a column), with two
+        // register sets keeping the loads of tile t+2 in flight while tile t
+        // is multiplied.  Native vector types: arrays of HIP's float4 class
+        // are not promoted to registers.
+        floatx4 a0[TM][K8], a1[TM][K8];
         float br0[KPT], br1[KPT];
 
-#define IGEMM_LOAD_TILE(KT, AR, BR)                                                                                  \
+#define IGEMM_LOAD_A(KT, AX)                                                                                         \
     {                                                                                                                \
         const int kt_ = min((KT), a.k_tiles - 1);                                                                    \
         const floatx4 *src =                                                                                         \
             reinterpret_cast<const floatx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt_) * (BM * BK));       \
-        _Pragma("unroll") for (int i = 0; i < APT; i++) AR[i] = src[tid + i * 256];                                   \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int q = 0; q < K8; q++) AX[i][q] =      \
+            src[((wm * TM + i) * K8 + q) * 64 + lane];                                                               \
+    }
+#define IGEMM_LOAD_B(KT, BR)                                                                                         \
+    {                                                                                                                \
         /* the table has two tiles of out-of-range entries past Kpad */                                           \
         const int *ko = a.koff + (KT) * BK + bgrp * KPT;                                                              \
         _Pragma("unroll") for (int j = 0; j < KPT; j++) BR[j] = __builtin_bit_cast(                                  \
             float, __builtin_amdgcn_raw_buffer_load_b32(xrs, col, ko[j], 0));                                        \
     }
-
-#define IGEMM_STORE_TILE(BUF, AR, BR)                                                                                \
+#define IGEMM_STORE_B(BUF, BR)                                                                                       \
     {                                                                                                                \
-        _Pragma("unroll") for (int i = 0; i < APT; i++) {                                                            \
-            const int f = (tid + i * 256) * 4;                                                                       \
-            *reinterpret_cast<floatx4 *>(&As[BUF][(f / BK) * LDK + (f % BK)]) = AR[i];                               \
-        }                                                                                                             \
         _Pragma("unroll") for (int j = 0; j < KPT; j += 4) *reinterpret_cast<floatx4 *>(                             \
             &Bs[BUF][bcol * LDK + bgrp * KPT + j]) = floatx4{BR[j], BR[j + 1], BR[j + 2], BR[j + 3]};                \
     }
 
-    // Operand fragments of one 8-k step: one ds_read_b128 per 32-row block.
-#define IGEMM_FRAG(BUF, K8, AF, BF)                                                                                  \
+    // B fragments of one 8-k step: one ds_read_b128 per 32-column block
+    // (lane: column row, k = 8*q + khalf + 0..3, the same k order as the
+    // packed weights).
+#define IGEMM_FRAG_B(BUF, Q, BF)                                                                                     \
     {                                                                                                                \
-        _Pragma("unroll") for (int i = 0; i < TM; i++) AF[i] =                                                       \
-            *reinterpret_cast<const floatx4 *>(&As[BUF][((wm * TM + i) * 32 + row) * LDK + (K8) * 8 + khalf]);       \
         _Pragma("unroll") for (int j = 0; j < TN; j++) BF[j] =                                                       \
-            *reinterpret_cast<const floatx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + (K8) * 8 + khalf]);       \
+            *reinterpret_cast<const floatx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + (Q) * 8 + khalf]);        \
     }
-#define IGEMM_MMA(AF, BF)                                                                                            \
+#define IGEMM_MMA(AX, Q, BF)                                                                                         \
     _Pragma("unroll") for (int s = 0; s < 4; s++) _Pragma("unroll") for (int i = 0; i < TM; i++)                     \
         _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =                                                   \
-            __builtin_amdgcn_mfma_f32_32x32x2f32(AF[i][s], BF[j][s], acc[i][j], 0, 0, 0);
-    // The fragments of step k8+1 are read while the MFMAs of step k8 run
+            __builtin_amdgcn_mfma_f32_32x32x2f32(AX[i][Q][s], BF[j][s], acc[i][j], 0, 0, 0);
+    // The B fragments of step q+1 are read while the MFMAs of step q run
     // (two register sets), so LDS latency stays off the MFMA chain.
-#define IGEMM_COMPUTE(BUF)                                                                                           \
+#define IGEMM_COMPUTE(BUF, AX)                                                                                       \
     {                                                                                                                \
-        floatx4 fa0[TM], fb0[TN], fa1[TM], fb1[TN];                                                                  \
-        IGEMM_FRAG(BUF, 0, fa0, fb0);                                                                                \
-        _Pragma("unroll") for (int k8 = 0; k8 < BK / 8; k8 += 2) {                                                   \
-            if (k8 + 1 < BK / 8) IGEMM_FRAG(BUF, k8 + 1, fa1, fb1);                                                  \
-            IGEMM_MMA(fa0, fb0);                                                                                     \
-            if (k8 + 2 < BK / 8) IGEMM_FRAG(BUF, k8 + 2, fa0, fb0);                                                  \
-            if (k8 + 1 < BK / 8) { IGEMM_MMA(fa1, fb1); }                                                            \
+        floatx4 fb0[TN], fb1[TN];                                                                                    \
+        IGEMM_FRAG_B(BUF, 0, fb0);                                                                                   \
+        _Pragma("unroll") for (int q = 0; q < K8; q += 2) {                                                          \
+            if (q + 1 < K8) IGEMM_FRAG_B(BUF, q + 1, fb1);                                                           \
+            IGEMM_MMA(AX, q, fb0);                                                                                   \
+            if (q + 2 < K8) IGEMM_FRAG_B(BUF, q + 2, fb0);                                                           \
+            if (q + 1 < K8) { IGEMM_MMA(AX, q + 1, fb1); }                                                           \
         }                                                                                                            \
     }
 
-    // One pipeline step: tile KT is in LDS buffer BUF, tile KT+1 is in flight
-    // in (AN, BNX), the free register set (AF, BF) receives tile KT+2.
-#define IGEMM_STEP(KT, BUF, AN, BNX, AF, BF)                                                                         \
+    // One pipeline step: B of tile KT is in LDS buffer BUF and its A in AC;
+    // B of tile KT+1 is in flight in BNX; B of tile KT+2 is loaded into the
+    // free set BF and A of tile KT+1 into AN.
+#define IGEMM_STEP(KT, BUF, AC, AN, BNX, BF)                                                                         \
     {                                                                                                                \
-        IGEMM_LOAD_TILE((KT) + 2, AF, BF);                                                                           \
+        IGEMM_LOAD_B((KT) + 2, BF);                                                                                  \
+        IGEMM_LOAD_A((KT) + 1, AN);                                                                                  \
         __builtin_amdgcn_sched_barrier(0);                                                                           \
-        IGEMM_COMPUTE(BUF);                                                                                          \
+        IGEMM_COMPUTE(BUF, AC);                                                                                      \
         __builtin_amdgcn_sched_barrier(0);                                                                           \
-        IGEMM_STORE_TILE((BUF) ^ 1, AN, BNX);                                                                        \
+        IGEMM_STORE_B((BUF) ^ 1, BNX);                                                                               \
         __syncthreads();                                                                                             \
     }
 
@@ -262,26 +266,28 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
         if (kt0 >= kt1) return;  // empty split-K slice
-        IGEMM_LOAD_TILE(kt0, ar0, br0);
-        IGEMM_LOAD_TILE(kt0 + 1, ar1, br1);
-        IGEMM_STORE_TILE(0, ar0, br0);
+        IGEMM_LOAD_B(kt0, br0);
+        IGEMM_LOAD_B(kt0 + 1, br1);
+        IGEMM_LOAD_A(kt0, a0);
+        IGEMM_STORE_B(0, br0);
         __syncthreads();
         int kt = kt0;
         // Tiles past kt1 are loaded and ignored, which keeps the loop free of
         // data-dependent branches.
         for (; kt + 1 < kt1; kt += 2) {
-            IGEMM_STEP(kt, 0, ar1, br1, ar0, br0);
-            IGEMM_STEP(kt + 1, 1, ar0, br0, ar1, br1);
+            IGEMM_STEP(kt, 0, a0, a1, br1, br0);
+            IGEMM_STEP(kt + 1, 1, a1, a0, br0, br1);
         }
         if (kt < kt1) {
-            IGEMM_COMPUTE(0);
+            IGEMM_COMPUTE(0, a0);
         }
 #undef IGEMM_STEP
 #undef IGEMM_COMPUTE
 #undef IGEMM_MMA
-#undef IGEMM_FRAG
-#undef IGEMM_LOAD_TILE
-#undef IGEMM_STORE_TILE
+#undef IGEMM_FRAG_B
+#undef IGEMM_LOAD_A
+#undef IGEMM_LOAD_B
+#undef IGEMM_STORE_B
 
         // 32x32 accumulator layout: lane holds column (lane & 31) and rows
         // 8*(r/4) + 4*(lane/32) + (r%4) for r = 0..15.  Output offsets are
@@ -902,10 +908,14 @@ void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *
     *split_out = best_split;
 }
 
-// Packs A[m][k] (row-major, lda = K) into [m_tiles][k_tiles][BM][BK] panels,
-// zero-filling the ragged edges, and uploads it.
+// Packs A[m][k] (row-major, lda = K) into BM x BK tiles [m_tiles][k_tiles],
+// each laid out in MFMA fragment order [BM/32][BK/8][64 lanes][4]: lane l of
+// fragment (b, q) holds row b*32 + (l & 31), k = q*8 + 4*(l >> 5) + 0..3 --
+// the A operand of the four 32x32x2 steps of that 8-k slice, one 16-byte
+// load per lane.  Ragged edges are zero-filled.
 int upload_packed_f32(const float *w, int M, int K, int BM, int BK, int m_tiles, int k_tiles, void **out) {
     std::vector<float> packed(static_cast<size_t>(m_tiles) * k_tiles * BM * BK, 0.0f);
+    const int K8 = BK / 8;
     for (int mt = 0; mt < m_tiles; mt++)
         for (int kt = 0; kt < k_tiles; kt++) {
             float *dst = packed.data() + (static_cast<size_t>(mt) * k_tiles + kt) * BM * BK;
@@ -915,7 +925,9 @@ int upload_packed_f32(const float *w, int M, int K, int BM, int BK, int m_tiles,
                 for (int kk = 0; kk < BK; kk++) {
                     const int k = kt * BK + kk;
                     if (k >= K) break;
-                    dst[i * BK + kk] = w[static_cast<size_t>(m) * K + k];
+                    const int lane = ((kk % 8) / 4) * 32 + i % 32;
+                    dst[((static_cast<size_t>(i / 32) * K8 + kk / 8) * 64 + lane) * 4 + kk % 4] =
+                        w[static_cast<size_t>(m) * K + k];
                 }
             }
         }
