@@ -138,7 +138,8 @@ def batch1_latency(depth: int, steps: int, lib) -> float:
     return b1_ms
 
 
-def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, node_report: bool = False) -> dict:
+def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, node_report: bool = False,
+                  eager: bool = False) -> dict:
     """INT8 ResNet-50: per-channel symmetric int8
     weights, per-tensor activation scales calibrated on 16 seeded single-image
     batches with the repo's fp32 forward, int32 accumulation, reference
@@ -192,7 +193,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
         m.run()
     lib.spkv2_device_synchronize()
     m.set_profiling(False)
-    m.set_graph_mode(True)
+    m.set_graph_mode(not eager)
     for _ in range(warmup):
         m.run()
     lib.spkv2_device_synchronize()
@@ -296,7 +297,8 @@ def main() -> None:
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--depth", type=int, default=101)
     ap.add_argument("--b1-steps", type=int, default=50)
-    ap.add_argument("--eager", action="store_true", help="time the batch-B step without HIP-graph replay")
+    ap.add_argument("--eager", action="store_true",
+                    help="time the batch-B (and INT8) steps without HIP-graph replay (for kernel tracing)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
     ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
@@ -323,7 +325,8 @@ def main() -> None:
         print(json.dumps(elementwise(lib)), flush=True)
         return
     if args.int8_only:
-        print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report)), flush=True)
+        print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
+                                       args.eager)), flush=True)
         return
     base = None if args.no_cpu_baseline else cpu_baseline()
 
@@ -418,7 +421,7 @@ def main() -> None:
     # ---------------------------------------------------------- batch 1
     b1_ms = batch1_latency(args.depth, args.b1_steps, lib) if args.b1_steps > 0 else None
 
-    int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps)
+    int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
     ew = None if args.no_elementwise else elementwise(lib)
 
     result = {

@@ -3,12 +3,21 @@
     python -m spinnv2_amd.rocprof_summary stats   <kernel_stats.csv> --runs N
     python -m spinnv2_amd.rocprof_summary traffic --fetch <pmc.csv> --write <pmc.csv>
            --copy-fetch <pmc.csv> --copy-write <pmc.csv> --copy-bytes B --runs N --match conv_igemm
+    python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
 
 `stats` divides rocprofv3 --kernel-trace --stats totals by the number of
 spkv2_run calls the profiled command made (N), giving per-run kernel time.
 `traffic` sums FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the
 kernels whose name contains --match, per run, and scales each counter by
-bytes / counter of a plain copy kernel of known size profiled the same way.
+bytes / counter of a plain copy kernel of known size profiled the same way;
+per kernel it also gives the HBM GB/s those bytes make over the dispatches'
+own durations (timestamps of the FETCH_SIZE pass).
+`mfma` reads a --pmc pass of SQ_INSTS_VALU_MFMA_MOPS_F32 (fp32 MFMA work in
+units of 512 FLOP), SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: per kernel
+the MFMA FLOP the hardware counted, that work over the dispatches' durations
+against the fp32 MFMA peak, and MFMA busy cycles (per SIMD) over the
+active cycles of all SIMDs: GRBM_GUI_ACTIVE / XCDs x CUs x 4 (on MI355X
+GRBM_GUI_ACTIVE sums the 8 XCDs' counts: about 8 x duration x clock).
 """
 
 from __future__ import annotations
@@ -45,6 +54,19 @@ def _counter_per_kernel(path: str) -> dict[str, list[float]]:
     return agg
 
 
+def _durations_per_kernel(path: str) -> dict[str, float]:
+    """Summed dispatch durations (ns) per kernel, each dispatch once."""
+    seen: dict[str, float] = {}
+    per: dict[str, float] = defaultdict(float)
+    for r in csv.DictReader(open(path)):
+        d = r["Dispatch_Id"]
+        if d in seen:
+            continue
+        seen[d] = 1.0
+        per[r["Kernel_Name"]] += float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+    return per
+
+
 def _copy_scale(path: str, copy_bytes: int) -> float:
     vals = [float(r["Counter_Value"]) for r in csv.DictReader(open(path)) if "copy_kernel" in r["Kernel_Name"]]
     if not vals:
@@ -57,16 +79,19 @@ def traffic(args) -> str:
     ws = _copy_scale(args.copy_write, args.copy_bytes)
     fetch = _counter_per_kernel(args.fetch)
     write = _counter_per_kernel(args.write)
+    dur = _durations_per_kernel(args.fetch)
     out = [f"copy kernel {args.copy_bytes} B: bytes per FETCH_SIZE KiB-unit x{fs:.4f} / 1024, "
            f"per WRITE_SIZE KiB-unit x{ws:.4f} / 1024",
-           f"{'kernel':48s} {'disp/run':>8s} {'read MB/run':>12s} {'write MB/run':>12s}"]
+           f"{'kernel':48s} {'disp/run':>8s} {'read MB/run':>12s} {'write MB/run':>12s} {'HBM GB/s':>9s}"]
     tot_r = tot_w = 0.0
     disp = 0
     for name in sorted(set(fetch) | set(write), key=lambda n: -fetch.get(n, [0, 0])[1]):
         rd = fetch.get(name, [0, 0.0])[1] * 1024 * fs / args.runs
         wr = write.get(name, [0, 0.0])[1] * 1024 * ws / args.runs
+        ns = dur.get(name, 0.0) / args.runs
+        gbps = (rd + wr) / ns if ns > 0 else 0.0
         out.append(f"{short_name(name)[:48]:48s} {fetch.get(name, [0])[0] / args.runs:8.1f} {rd / 1e6:12.1f} "
-                   f"{wr / 1e6:12.1f}")
+                   f"{wr / 1e6:12.1f} {gbps:9.0f}")
         if args.match in name:
             tot_r += rd
             tot_w += wr
@@ -76,6 +101,42 @@ def traffic(args) -> str:
     out.append(f"result {args.match}_write_bytes_per_step = {tot_w:.0f}")
     out.append(f"result conv_hbm_bytes_per_step = {tot_r + tot_w:.0f}")
     out.append(f"result conv_dispatches_per_step = {disp / args.runs:.0f}")
+    return "\n".join(out)
+
+
+def mfma(args) -> str:
+    per: dict[str, dict[str, float]] = defaultdict(lambda: defaultdict(float))
+    seen = set()
+    for r in csv.DictReader(open(args.csv)):
+        k = per[r["Kernel_Name"]]
+        k[r["Counter_Name"]] += float(r["Counter_Value"])
+        if r["Dispatch_Id"] not in seen:
+            seen.add(r["Dispatch_Id"])
+            k["ns"] += float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
+            k["n"] += 1
+    out = [f"{'kernel':48s} {'disp/run':>8s} {'avg us':>8s} {'GFLOP/run':>10s} {'TFLOP/s':>8s} {'% peak':>7s} "
+           f"{'busy %':>7s}"]
+    tot_f = tot_ns = tot_busy = tot_active = 0.0
+    for name, k in sorted(per.items(), key=lambda kv: -kv[1]["ns"]):
+        if args.match not in name:
+            continue
+        flop = k["SQ_INSTS_VALU_MFMA_MOPS_F32"] * 512
+        tf = flop / k["ns"] / 1e3 if k["ns"] else 0.0
+        simd_cycles = k["GRBM_GUI_ACTIVE"] / args.xcds * args.cus * 4
+        busy = k["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_cycles if simd_cycles else 0.0
+        out.append(f"{short_name(name)[:48]:48s} {k['n'] / args.runs:8.1f} {k['ns'] / k['n'] / 1e3:8.2f} "
+                   f"{flop / args.runs / 1e9:10.1f} {tf:8.1f} {100 * tf / args.peak:6.1f}% {100 * busy:6.1f}%")
+        tot_f += flop
+        tot_ns += k["ns"]
+        tot_busy += k["SQ_VALU_MFMA_BUSY_CYCLES"]
+        tot_active += k["GRBM_GUI_ACTIVE"]
+    tf = tot_f / tot_ns / 1e3 if tot_ns else 0.0
+    out.append("")
+    out.append(f"result {args.match}_mfma_flop_per_run = {tot_f / args.runs:.0f}")
+    out.append(f"result {args.match}_mfma_tflops = {tf:.2f}")
+    out.append(f"result {args.match}_mfma_frac_of_peak = {tf / args.peak:.4f}")
+    simd_cycles = tot_active / args.xcds * args.cus * 4
+    out.append(f"result {args.match}_mfma_busy_frac = {tot_busy / simd_cycles if simd_cycles else 0:.4f}")
     return "\n".join(out)
 
 
@@ -91,8 +152,15 @@ def main() -> None:
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--runs", type=int, required=True)
     t.add_argument("--match", default="conv_igemm")
+    m = sub.add_parser("mfma")
+    m.add_argument("csv")
+    m.add_argument("--runs", type=int, required=True)
+    m.add_argument("--match", default="conv_igemm")
+    m.add_argument("--cus", type=int, default=256)
+    m.add_argument("--xcds", type=int, default=8)
+    m.add_argument("--peak", type=float, default=157.3, help="TFLOP/s (fp32 MFMA)")
     a = ap.parse_args()
-    print(stats(a.csv, a.runs) if a.cmd == "stats" else traffic(a))
+    print({"stats": lambda: stats(a.csv, a.runs), "traffic": lambda: traffic(a), "mfma": lambda: mfma(a)}[a.cmd]())
 
 
 if __name__ == "__main__":
