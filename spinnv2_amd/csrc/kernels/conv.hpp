@@ -34,6 +34,7 @@ struct ConvPlan {
     int BM, BN, BK;      // tile shape
     int m_tiles, n_tiles, k_tiles;
     int splitk, kt_per_split;  // split-K factor and k-tiles per slice
+    int dp_tiles, ws_n0;       // hybrid schedule: whole tiles first, partials only from column ws_n0 on
     int K, Kpad;
     void *wpack;         // device: packed weight panels (fp32 or int8)
     void *ktab;          // device: per-k gather table (byte offsets into the B source)

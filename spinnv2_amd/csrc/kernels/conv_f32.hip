@@ -24,6 +24,7 @@
 // k = 8j+s and lanes 32-63 k = 8j+4+s for step s, the same mapping for A and
 // B, so every k is summed exactly once.
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -108,7 +109,9 @@ struct IgemmArgs {
     const float *__restrict__ bias;  // [M] or null
     const float *__restrict__ res;   // like y, or null
     float *__restrict__ y;
-    float *__restrict__ ws;          // split-K partials [splitk][M][Ntot]
+    float *__restrict__ ws;          // split-K partials [splitk][M][ws_ld], column n at n - ws_n0
+    int ws_n0, ws_ld;                // first column with partials, columns per partial row
+    int dp_tiles, rem_split;         // hybrid: whole tiles first, then rem_split slices per remaining tile
     int x_bytes;                     // extent of x for the bounds-checked loads
     int y_bytes;                     // extent of y (and of the residual)
     int ws_bytes;                    // extent of the split-K partials
@@ -157,13 +160,32 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     // Consecutive workgroups land on different XCDs (round robin over 8);
     // remap so each XCD walks a contiguous range of tiles, m fastest, and the
     // tiles sharing one activation panel share that XCD's L2.
+    //
+    // Split-K: blockIdx.y is the k slice and every tile writes partials.
+    // Hybrid (dp_tiles > 0, one grid row): the first dp_tiles workgroups
+    // each compute a whole tile (a multiple of the CU count, so every CU
+    // gets the same number), the remaining tiles are cut into kt_per_split
+    // k-tile slices, one workgroup each, whose partials splitk_epilogue sums.
     int bid = blockIdx.x;
-    const int nb = gridDim.x;
-    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    int slice = blockIdx.y;
+    bool part = a.ws != nullptr;
+    if (a.dp_tiles > 0) {
+        if (bid < a.dp_tiles) {
+            if ((a.dp_tiles & 7) == 0) bid = (bid & 7) * (a.dp_tiles >> 3) + (bid >> 3);
+            part = false;
+        } else {
+            const int r = bid - a.dp_tiles;
+            bid = a.dp_tiles + r / a.rem_split;
+            slice = r - (r / a.rem_split) * a.rem_split;
+        }
+    } else {
+        const int nb = gridDim.x;
+        if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    }
     const int mt = bid % a.m_tiles;
     const int nt = bid / a.m_tiles;
-    const int kt0 = blockIdx.y * a.kt_per_split;
-    const int kt1 = min(kt0 + a.kt_per_split, a.k_tiles);
+    const int kt0 = part ? slice * a.kt_per_split : 0;
+    const int kt1 = part ? min(kt0 + a.kt_per_split, a.k_tiles) : a.k_tiles;
 
     const int bcol = tid % BN;
     const int bgrp = __builtin_amdgcn_readfirstlane(tid / BN);  // wave-uniform: BN >= 64
@@ -297,14 +319,14 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
         int mrow[TM];   // first row of this lane in block i
 #pragma unroll
         for (int i = 0; i < TM; i++) mrow[i] = mt * BM + (wm * TM + i) * 32 + rsub;
-        if (a.ws) {
-            // split-K partials: ws[slice][m][n]
+        if (part) {
+            // split-K partials: ws[slice][m][n - ws_n0], rows of ws_ld columns
             const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
                 a.ws, static_cast<short>(0), a.ws_bytes, kBufferWord3);
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const int n = nt * BN + (wn * TN + j) * 32 + row;
-                obase[j] = n < a.Ntot ? (blockIdx.y * a.M * a.Ntot + n) * 4 : kOobOffset;
+                obase[j] = n < a.Ntot ? (slice * a.M * a.ws_ld + n - a.ws_n0) * 4 : kOobOffset;
             }
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -313,7 +335,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
                         const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                        const int off = m < a.M ? obase[j] + m * a.Ntot * 4 : kOobOffset;
+                        const int off = m < a.M ? obase[j] + m * a.ws_ld * 4 : kOobOffset;
                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), wrs, off, 0, 0);
                     }
         } else {
@@ -405,22 +427,23 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 }
 
 // Sums split-K partials in slice order, then applies the epilogue.  Each
-// thread owns VEC consecutive columns of one row (VEC = 4 when N is a
-// multiple of 4: 16-byte loads); up to eight slices' loads are in flight
+// thread owns VEC consecutive columns of one row (VEC = 4 when the partial
+// columns start and end on multiples of 4: 16-byte loads); up to eight slices' loads are in flight
 // before the first add, and the adds stay in slice order.
 template <int VEC>
-__global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__ ws, int splitk, int M, int Ntot,
+__global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__ ws, int splitk, int M, int ld,
                                                        int OHW, const float *__restrict__ bias,
                                                        const float *__restrict__ res, float *__restrict__ y, int act,
                                                        float alpha, IgemmArgs h) {
     typedef float vec_t __attribute__((ext_vector_type(VEC)));
-    const size_t total = static_cast<size_t>(M) * Ntot;
+    // partial rows hold ld columns starting at column h.ws_n0
+    const size_t total = static_cast<size_t>(M) * ld;
     const size_t groups = total / VEC;
     for (size_t gi = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; gi < groups;
          gi += static_cast<size_t>(gridDim.x) * 256) {
         const size_t idx = gi * VEC;
-        const int m = static_cast<int>(idx / Ntot);
-        const int n = static_cast<int>(idx - static_cast<size_t>(m) * Ntot);
+        const int m = static_cast<int>(idx / ld);
+        const int n = h.ws_n0 + static_cast<int>(idx - static_cast<size_t>(m) * ld);
         vec_t v = 0.0f;
         int s = 0;
         for (; s + 8 <= splitk; s += 8) {
@@ -579,7 +602,14 @@ int resident_wgs(int c) {
 // request `split`, as a plan stores them.
 struct TileCounts {
     int m_tiles, n_tiles, k_tiles, kt_per_split, splitk;
+    // hybrid: dp_tiles whole tiles (n-tile columns below ws_n0), the rest cut
+    // into splitk slices of kt_per_split k-tiles; 0 otherwise
+    int dp_tiles = 0, ws_n0 = 0;
 };
+
+// Split requests at or above kHybrid ask for the hybrid schedule with
+// (split - kHybrid) k slices per remaining tile.
+constexpr int kHybrid = 1000;
 
 TileCounts tile_counts(int c, int M, int Ntot, int K, int split) {
     const TileCfg &t = kCfgs[c];
@@ -587,13 +617,28 @@ TileCounts tile_counts(int c, int M, int Ntot, int K, int split) {
     tc.m_tiles = (M + t.BM - 1) / t.BM;
     tc.n_tiles = (Ntot + t.BN - 1) / t.BN;
     tc.k_tiles = (K + t.BK - 1) / t.BK;
-    tc.kt_per_split = (tc.k_tiles + split - 1) / split;
+    const int req = split >= kHybrid ? split - kHybrid : split;
+    tc.kt_per_split = (tc.k_tiles + req - 1) / req;
     tc.splitk = (tc.k_tiles + tc.kt_per_split - 1) / tc.kt_per_split;
+    if (split >= kHybrid) {
+        // whole tiles: the largest multiple of the CU count that is whole
+        // n-tile columns (so the remaining tiles are the last columns)
+        const int tiles = tc.m_tiles * tc.n_tiles;
+        const int cus = device_cu_count();
+        const int dp_n = (tiles / cus) * cus / tc.m_tiles;
+        if (dp_n <= 0 || dp_n >= tc.n_tiles || tc.splitk <= 1) {
+            tc.kt_per_split = tc.k_tiles;  // no hybrid for this shape: one whole-tile launch
+            tc.splitk = 1;
+        } else {
+            tc.dp_tiles = dp_n * tc.m_tiles;
+            tc.ws_n0 = dp_n * t.BN;
+        }
+    }
     return tc;
 }
 
 size_t partial_bytes_of(const TileCounts &tc, int M, int Ntot) {
-    return tc.splitk > 1 ? static_cast<size_t>(tc.splitk) * M * Ntot * sizeof(float) : 0;
+    return tc.splitk > 1 ? static_cast<size_t>(tc.splitk) * M * (Ntot - tc.ws_n0) * sizeof(float) : 0;
 }
 
 // Modelled time (us) of a candidate: the MFMA work of the busiest CU over
@@ -613,11 +658,20 @@ double model_us(int c, const TileCounts &tc, int M, int Ntot) {
     const double mfma = static_cast<double>(rounds) * per_cu * tc.kt_per_split * tile_us;
     const double latency = static_cast<double>(rounds) * tc.kt_per_split * t.BK * 0.035;
     double us = std::max(mfma, latency) + 2.0;
-    if (tc.splitk > 1) us += 4.0 * M * static_cast<double>(Ntot) * (tc.splitk + 1) / 4.0e6 + 3.0;
+    if (tc.dp_tiles > 0) {
+        // whole tiles spread evenly, then one slice's share of each remaining tile
+        const long rem = static_cast<long>(tc.m_tiles) * tc.n_tiles - tc.dp_tiles;
+        const double units = std::ceil(static_cast<double>(tc.dp_tiles) / cus) +
+                             std::ceil(static_cast<double>(rem) * tc.splitk / cus) * tc.kt_per_split / tc.k_tiles;
+        us = std::max(units * tc.k_tiles * tile_us, static_cast<double>(tc.k_tiles) * t.BK * 0.035) + 2.0;
+    }
+    if (tc.splitk > 1)
+        us += 4.0 * M * static_cast<double>(Ntot - tc.ws_n0) * (tc.splitk + 1) / 4.0e6 + 3.0;
     return us;
 }
 
 const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
+const int kHybridSplits[] = {2, 4, 8, 16};
 
 // What the tuner needs to launch a candidate: the B source geometry and
 // the k -> byte offset rule of the layer.
@@ -669,6 +723,10 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     a.act = g.act;
     a.alpha = alpha;
     a.ws = tc.splitk > 1 ? ws : nullptr;
+    a.ws_n0 = tc.ws_n0;
+    a.ws_ld = a.Ntot - tc.ws_n0;
+    a.dp_tiles = tc.dp_tiles;
+    a.rem_split = tc.splitk;
     if (handoff) {
         a.yp = handoff->pad_out;
         a.yp_plane = handoff->pad_Hp * handoff->pad_Wp;
@@ -679,17 +737,20 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     }
     a.y_bytes = static_cast<int>(g.y_elems * 4);
     a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
-    dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
+    const int tiles = tc.m_tiles * tc.n_tiles;
+    const dim3 grid = tc.dp_tiles > 0
+                          ? dim3(static_cast<unsigned>(tc.dp_tiles + (tiles - tc.dp_tiles) * tc.splitk), 1)
+                          : dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(tc.splitk));
     t.kernel<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
-        const size_t total = static_cast<size_t>(g.M) * a.Ntot;
-        if (a.Ntot % 4 == 0)
+        const size_t total = static_cast<size_t>(g.M) * a.ws_ld;
+        if (a.ws_ld % 4 == 0 && a.ws_n0 % 4 == 0)
             hipLaunchKernelGGL(splitk_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, ws, tc.splitk,
-                               g.M, a.Ntot, a.OHW, bias, res, y, g.act, alpha, a);
+                               g.M, a.ws_ld, a.OHW, bias, res, y, g.act, alpha, a);
         else
             hipLaunchKernelGGL(splitk_epilogue<1>, dim3(grid_for(total, 256)), dim3(256), 0, st, ws, tc.splitk, g.M,
-                               a.Ntot, a.OHW, bias, res, y, g.act, alpha, a);
+                               a.ws_ld, a.OHW, bias, res, y, g.act, alpha, a);
         if (int rc = launch_status("splitk_epilogue")) return rc;
     }
     return 0;
@@ -796,6 +857,14 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
             best_model = std::min(best_model, m);
             cands.push_back({c, split, tc, m, 0.0});
         }
+        for (int rs : kHybridSplits) {
+            const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, kHybrid + rs);
+            if (tc.dp_tiles == 0 || tc.kt_per_split < 2) continue;
+            if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
+            const double m = model_us(c, tc, g.M, Ntot);
+            best_model = std::min(best_model, m);
+            cands.push_back({c, kHybrid + rs, tc, m, 0.0});
+        }
     }
     std::vector<Cand> keep;
     for (const Cand &cd : cands)
@@ -872,9 +941,10 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     return true;
 }
 
-// Picks (cfg, split) for a layer: SPKV2_CONV_CFG / SPKV2_CONV_SPLITK force a
-// choice; otherwise the tuner measures unless SPKV2_CONV_TUNE=0, and the
-// model decides when it does not.
+// Picks (cfg, split) for a layer: SPKV2_CONV_CFG / SPKV2_CONV_SPLITK /
+// SPKV2_CONV_HYBRID (slices per remaining tile) force a choice; otherwise
+// the tuner measures unless SPKV2_CONV_TUNE=0, and the model decides when it
+// does not.
 void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
     const int Ntot = g.N * g.OH * g.OW;
     int best_cfg = 0, best_split = 1;
@@ -903,6 +973,10 @@ void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *
     if (const char *e = getenv("SPKV2_CONV_SPLITK")) {
         const int sk = atoi(e);
         if (sk >= 1 && sk <= 64) best_split = sk;
+    }
+    if (const char *e = getenv("SPKV2_CONV_HYBRID")) {
+        const int rs = atoi(e);
+        if (rs >= 2 && rs <= 64) best_split = kHybrid + rs;
     }
     *cfg_out = best_cfg;
     *split_out = best_split;
@@ -947,7 +1021,7 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 }  // namespace
 
 static TileCounts plan_counts(const ConvPlan *p) {
-    return TileCounts{p->m_tiles, p->n_tiles, p->k_tiles, p->kt_per_split, p->splitk};
+    return TileCounts{p->m_tiles, p->n_tiles, p->k_tiles, p->kt_per_split, p->splitk, p->dp_tiles, p->ws_n0};
 }
 
 static size_t partial_bytes(const ConvPlan *p) {
@@ -975,6 +1049,8 @@ static int plan_tiles_and_weights(hipStream_t st, const ConvGeom &g, const Gathe
     plan->Kpad = tc.k_tiles * t.BK;
     plan->kt_per_split = tc.kt_per_split;
     plan->splitk = tc.splitk;
+    plan->dp_tiles = tc.dp_tiles;
+    plan->ws_n0 = tc.ws_n0;
     if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
     if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack))
         return rc;
@@ -1041,7 +1117,7 @@ int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int 
 
 std::string igemm_name(const ConvPlan *p) {
     return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") +
-           ",splitk=" + std::to_string(p->splitk) + ">";
+           ",splitk=" + std::to_string(p->splitk) + (p->dp_tiles ? ",dp=" + std::to_string(p->dp_tiles) : "") + ">";
 }
 
 size_t claim_spec_scratch(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {

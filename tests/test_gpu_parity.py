@@ -280,6 +280,36 @@ def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
+@pytest.mark.parametrize("cfg", range(8))
+def test_conv_hybrid_schedule(gpu, monkeypatch, cfg):
+    """Hybrid schedule (whole tiles for a multiple of the CU count, the last
+    n-tile columns split over k and summed by splitk_epilogue) on a layer
+    with ragged M and N, bias, residual and Relu: against the oracle, and
+    HIP-graph replays equal to the eager run."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    monkeypatch.setenv("SPKV2_CONV_HYBRID", "4")
+    g = models.single_conv(4, 16, 63, 67, 200, 3, 1, 1, act="Relu", residual=True)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        eager = m.get_output(0)
+        name = m.kernel_name(0)
+        m.set_graph_mode(True)
+        for _ in range(2):
+            for i, x in enumerate(xs):
+                m.set_input(i, x)
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0), eager)
+    assert ",dp=" in name and "splitk=1," not in name, name
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(eager, want) <= FP32_TOL
+
+
 def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
     """Split-K partials are fully rewritten by every run (no memset nodes in
     the captured graph), so its replays give the eager result every time."""
