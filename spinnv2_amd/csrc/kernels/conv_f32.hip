@@ -428,8 +428,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 
 // Sums split-K partials in slice order, then applies the epilogue.  Each
 // thread owns VEC consecutive columns of one row (VEC = 4 when the partial
-// columns start and end on multiples of 4: 16-byte loads); up to eight slices' loads are in flight
-// before the first add, and the adds stay in slice order.
+// columns start and end on multiples of 4: 16-byte loads).
 template <int VEC>
 __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__ ws, int splitk, int M, int ld,
                                                        int OHW, const float *__restrict__ bias,
@@ -444,16 +443,18 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
         const size_t idx = gi * VEC;
         const int m = static_cast<int>(idx / ld);
         const int n = h.ws_n0 + static_cast<int>(idx - static_cast<size_t>(m) * ld);
+        // up to 16 slices' loads in flight before the first add (one round
+        // trip for splitk <= 16); the adds stay in slice order
         vec_t v = 0.0f;
-        int s = 0;
-        for (; s + 8 <= splitk; s += 8) {
-            vec_t p[8];
+        for (int s = 0; s < splitk; s += 16) {
+            vec_t p[16];
 #pragma unroll
-            for (int t = 0; t < 8; t++) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
+            for (int t = 0; t < 16; t++)
+                if (s + t < splitk) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
 #pragma unroll
-            for (int t = 0; t < 8; t++) v += p[t];
+            for (int t = 0; t < 16; t++)
+                if (s + t < splitk) v += p[t];
         }
-        for (; s < splitk; s++) v += *reinterpret_cast<const vec_t *>(ws + s * total + idx);
         const float bm = bias ? bias[m] : 0.0f;
 #pragma unroll
         for (int e = 0; e < VEC; e++) {

@@ -393,7 +393,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 
 // Sums the int32 split-K partials (exact in any order), then dequantizes or
 // writes the raw accumulators.  Four consecutive columns per thread when N
-// is a multiple of 4, up to eight slices' loads in flight.
+// is a multiple of 4.
 template <int VEC>
 __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restrict__ ws, int splitk, int M, int Ntot,
                                                           int OHW, const float *__restrict__ scales,
@@ -408,16 +408,17 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
         const size_t idx = gi * VEC;
         const int m = static_cast<int>(idx / Ntot);
         const int n = static_cast<int>(idx - static_cast<size_t>(m) * Ntot);
+        // up to 16 slices' loads in flight before the first add
         vec_t v = 0;
-        int s = 0;
-        for (; s + 8 <= splitk; s += 8) {
-            vec_t p[8];
+        for (int s = 0; s < splitk; s += 16) {
+            vec_t p[16];
 #pragma unroll
-            for (int t = 0; t < 8; t++) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
+            for (int t = 0; t < 16; t++)
+                if (s + t < splitk) p[t] = *reinterpret_cast<const vec_t *>(ws + (s + t) * total + idx);
 #pragma unroll
-            for (int t = 0; t < 8; t++) v += p[t];
+            for (int t = 0; t < 16; t++)
+                if (s + t < splitk) v += p[t];
         }
-        for (; s < splitk; s++) v += *reinterpret_cast<const vec_t *>(ws + s * total + idx);
         const float sm = scales[m];
         const float bm = bias ? bias[m] : 0.0f;
 #pragma unroll
