@@ -780,8 +780,10 @@ void load_tune_db_locked() {
     if (!f) return;
     char key[512];
     int cfg = 0, split = 0;
+    // split: 1..64, or a hybrid request (1000 + slices per remaining tile)
     while (fscanf(f, "%511s %d %d", key, &cfg, &split) == 3)
-        if (cfg >= 0 && cfg < 64 && split >= 1 && split <= 64) g_tuned[key] = {cfg, split};
+        if (cfg >= 0 && cfg < 64 && ((split >= 1 && split <= 64) || (split >= 1002 && split <= 1064)))
+            g_tuned[key] = {cfg, split};
     fclose(f);
 }
 
