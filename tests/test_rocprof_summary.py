@@ -1,0 +1,77 @@
+"""The rocprofv3 CSV digests behind profiles/: per-run kernel time, copy-kernel
+scaled HBM bytes, and MFMA work / utilisation from counters, on small
+hand-made CSVs whose answers are known."""
+
+from __future__ import annotations
+
+import csv
+from types import SimpleNamespace
+
+import pytest
+
+from spinnv2_amd import rocprof_summary as rs
+
+PMC_COLS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+
+def _write(path, cols, rows):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=cols)
+        w.writeheader()
+        for r in rows:
+            w.writerow(dict(zip(cols, r)))
+    return str(path)
+
+
+def _result(text: str, name: str) -> float:
+    for line in text.splitlines():
+        if line.startswith(f"result {name} ="):
+            return float(line.split("=")[1])
+    raise KeyError(name)
+
+
+def test_stats_per_run(tmp_path):
+    p = _write(tmp_path / "s.csv", ["Name", "Calls", "TotalDurationNs", "AverageNs"],
+               [["void spk::kern::conv_igemm_f32<64, 64, 16, 2, 2>(spk::kern::IgemmArgs)", 20, 2_000_000, 100_000],
+                ["splitk_epilogue<4>", 10, 500_000, 50_000]])
+    out = rs.stats(p, runs=10)
+    line = [ln for ln in out.splitlines() if ln.startswith("conv_igemm_f32<64, 64, 16, 2, 2>")][0].split()
+    # 2 calls per run, 100 us average, 0.2 ms per run, 80% of the total
+    assert line[-4:] == ["2.0", "100.00", "0.200", "80.0%"]
+    assert out.splitlines()[-1].split()[-1] == "0.250"
+
+
+def test_traffic_copy_scaled(tmp_path):
+    mib = 1 << 20
+    # copy kernel of 4 MiB: FETCH_SIZE reads half of it (2048 KiB), WRITE_SIZE all (4096 KiB)
+    cf = _write(tmp_path / "cf.csv", PMC_COLS, [[1, "copy_kernel(float*)", "FETCH_SIZE", 2048, 0, 1000]])
+    cw = _write(tmp_path / "cw.csv", PMC_COLS, [[1, "copy_kernel(float*)", "WRITE_SIZE", 4096, 0, 1000]])
+    # one conv dispatch per run, two runs: 1000 KiB fetched (x2 -> 2000 KiB), 500 KiB written, 1 us each
+    f = _write(tmp_path / "f.csv", PMC_COLS, [[1, "conv_igemm_f32<64>", "FETCH_SIZE", 1000, 0, 1000],
+                                             [2, "conv_igemm_f32<64>", "FETCH_SIZE", 1000, 5000, 6000]])
+    w = _write(tmp_path / "w.csv", PMC_COLS, [[1, "conv_igemm_f32<64>", "WRITE_SIZE", 500, 0, 1000],
+                                             [2, "conv_igemm_f32<64>", "WRITE_SIZE", 500, 5000, 6000]])
+    args = SimpleNamespace(fetch=f, write=w, copy_fetch=cf, copy_write=cw, copy_bytes=4 * mib, runs=2,
+                           match="conv_igemm")
+    out = rs.traffic(args)
+    assert _result(out, "conv_igemm_read_bytes_per_step") == pytest.approx(2000 * 1024)
+    assert _result(out, "conv_igemm_write_bytes_per_step") == pytest.approx(500 * 1024)
+    assert _result(out, "conv_hbm_bytes_per_step") == pytest.approx(2500 * 1024)
+    # 2.56 MB in 1 us per run
+    row = [ln for ln in out.splitlines() if ln.startswith("conv_igemm_f32<64>")][0].split()
+    assert float(row[-1]) == pytest.approx(2500 * 1024 / 1000, rel=1e-3)
+
+
+def test_mfma_work_and_busy(tmp_path):
+    rows = []
+    # two dispatches of 100 us; each counts 1e6 MOPS (x512 FLOP); GUI_ACTIVE sums 8 XCDs
+    for d, t0 in ((1, 0), (2, 1_000_000)):
+        rows += [[d, "conv_igemm_f32<x>", "SQ_INSTS_VALU_MFMA_MOPS_F32", 1e6, t0, t0 + 100_000],
+                 [d, "conv_igemm_f32<x>", "GRBM_GUI_ACTIVE", 8 * 240_000, t0, t0 + 100_000],
+                 [d, "conv_igemm_f32<x>", "SQ_VALU_MFMA_BUSY_CYCLES", 0.5 * 240_000 * 256 * 4, t0, t0 + 100_000]]
+    p = _write(tmp_path / "m.csv", PMC_COLS, rows)
+    out = rs.mfma(SimpleNamespace(csv=p, runs=2, match="conv_igemm", cus=256, xcds=8, peak=157.3))
+    assert _result(out, "conv_igemm_mfma_flop_per_run") == pytest.approx(512e6)
+    # 512e6 FLOP per 100 us = 5.12 TFLOP/s
+    assert _result(out, "conv_igemm_mfma_tflops") == pytest.approx(5.12)
+    assert _result(out, "conv_igemm_mfma_busy_frac") == pytest.approx(0.5)
