@@ -143,7 +143,11 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     constexpr int TM = BM / (32 * WAVES_M);
     constexpr int TN = BN / (32 * WAVES_N);
     constexpr int K8 = BK / 8;
-    constexpr int LDK = BK + (BK == 16 ? 8 : 4);  // row pitch (floats): keeps b128 LDS traffic conflict-free
+    // Row pitch in floats: an odd multiple of 4 (BK + 4), so the 16-byte
+    // accesses of 8 consecutive rows fall on 8 different 4-bank groups of
+    // the LDS's 32 banks and the b128 traffic is conflict-free.
+    constexpr int LDK = BK + 4;
+    static_assert((LDK / 4) % 2 == 1, "row pitch an odd multiple of 16 bytes");
     constexpr int KPT = BK * BN / 256;  // B elements per thread per k-tile
     static_assert(WAVES_M * WAVES_N == 4, "four waves");
     static_assert(TM >= 1 && TN >= 1 && KPT % 4 == 0 && BN >= 64, "tile shape");
