@@ -76,8 +76,9 @@ int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeo
     if (g->C % g->group != 0 || g->M % g->group != 0) return -12;
     if (static_cast<int>(w->shape[1]) * g->group != g->C) return -12;
     if (static_cast<int>(y->shape[0]) != g->N || static_cast<int>(y->shape[1]) != g->M) return -11;
-    // index arithmetic inside the kernels is 32-bit
-    if (g->x_elems >= (int64_t(1) << 31) || g->y_elems >= (int64_t(1) << 31)) return SPKV2_E_UNSUPPORTED;
+    // byte offsets and buffer extents inside the kernels are 32-bit signed:
+    // every fp32 tensor of the node must stay below 2 GiB
+    if (g->x_elems * 4 >= (int64_t(1) << 31) || g->y_elems * 4 >= (int64_t(1) << 31)) return SPKV2_E_UNSUPPORTED;
     if (g->H >= 16384 || g->W >= 16384) return SPKV2_E_UNSUPPORTED;
     return 0;
 }

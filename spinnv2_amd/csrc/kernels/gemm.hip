@@ -185,6 +185,8 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     g.has_bias = node->input_count > 2;
     g.x_elems = static_cast<int64_t>(gp->rows) * gp->K;
     g.y_elems = static_cast<int64_t>(gp->rows) * gp->Nout;
+    // byte offsets inside the kernels are 32-bit signed
+    if (g.x_elems * 4 >= (int64_t(1) << 31) || g.y_elems * 4 >= (int64_t(1) << 31)) return SPKV2_E_UNSUPPORTED;
     gp->conv.g = g;
     if (int rc = plan_igemm_gemm(ctx->stream, g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
     set_kernel_name(ctx, node, "gemm:" + igemm_name(&gp->conv));

@@ -147,3 +147,15 @@ def test_io_size_and_index_codes(gpu):
         finally:
             xb.free()
             yb.free()
+
+
+def test_conv_over_2gib_is_refused(gpu):
+    """A conv whose fp32 input or output reaches 2 GiB is refused at prepare
+    (SPKV2_E_UNSUPPORTED, -32) instead of overflowing 32-bit byte offsets."""
+    from spinnv2_amd.runtime import Model, RuntimeError_
+
+    g = models.single_conv(1, 8, 8192, 8200, 8, 1, 1, 0)  # 537M elements per tensor: 2.1 GB
+    blob = write_spk(g, "mi355x")
+    with pytest.raises(RuntimeError_) as e:
+        Model(blob)
+    assert e.value.code == -32
