@@ -364,6 +364,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             if (a.q_out) {
                 // four consecutive channels of the lane -> one dword; channels
                 // past M are written 0 (the padded channels stay zero)
+                unsigned words[4];
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
                     const unsigned m0 = mrow[i] + 8 * q4;
@@ -375,7 +376,29 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
                         const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
                         word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
                     }
-                    __builtin_amdgcn_raw_buffer_store_b32(word, qrs, m0 < M ? qbase[j] + m0 : kOob, 0, 0);
+                    words[q4] = word;
+                }
+                if (a.q_Cp % 16 == 0) {
+                    // lanes l and l+32 hold one pixel's 32 channels of the
+                    // block, l channels 0-3, 8-11, 16-19, 24-27 and l+32 the
+                    // others: two swaps give lane l channels 0-15 and lane
+                    // l+32 channels 16-31, one 16-byte store each
+                    const bool hi = lane >= 32;
+                    const unsigned r1 = __shfl_xor(hi ? words[0] : words[2], 32);
+                    const unsigned r2 = __shfl_xor(hi ? words[1] : words[3], 32);
+                    const intx4 val = hi ? intx4{static_cast<int>(r1), static_cast<int>(words[2]), static_cast<int>(r2),
+                                                 static_cast<int>(words[3])}
+                                         : intx4{static_cast<int>(words[0]), static_cast<int>(r1),
+                                                 static_cast<int>(words[1]), static_cast<int>(r2)};
+                    const unsigned c16 = mrow[i] - rsub + (hi ? 16u : 0u);
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val),
+                                                           qrs, c16 < M ? qbase[j] + c16 : kOob, 0, 0);
+                } else {
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const unsigned m0 = mrow[i] + 8 * q4;
+                        __builtin_amdgcn_raw_buffer_store_b32(words[q4], qrs, m0 < M ? qbase[j] + m0 : kOob, 0, 0);
+                    }
                 }
             }
             if (a.y) {

@@ -386,6 +386,35 @@ def test_int8_chain_bit_exact(gpu, monkeypatch, handoff):
         np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
 
 
+@pytest.mark.parametrize("mid", [45, 36])
+def test_int8_handoff_odd_channels(gpu, mid):
+    """Handoff into consumers whose padded channel stride is a multiple of
+    16 with channels past M (45 -> 48: 16-byte stores, zero padding) or not
+    (36: dword stores); bit-exact against the oracle."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+    from spinnv2_amd.runtime import Model
+
+    p = models.Params(8)
+    g = Graph("i8odd")
+    x = g.input("x", [2, 24, 13, 11])
+    h = g.relu(g.conv(x, p.he((mid, 24, 1, 1)), p.normal(mid, 0.01)))
+    h = g.relu(g.conv(h, p.he((20, mid, 3, 3)), p.normal(20, 0.01), pad=1))
+    g.mark_output(g.conv(h, p.he((12, 20, 1, 1)), None))
+    run_default_pipeline(g)
+    xs = rng_inputs(g)
+    qp = calibrate_activation_scales(g, [[models.make_input([2, 24, 13, 11], 800 + i)] for i in range(3)])
+    blob = write_spk(g, "mi355x", quant_params=qp + quantize_conv_weights(g))
+    want = run_oracle(blob, xs)[0]
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = m.get_output(0)
+        names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+    assert sum(",handoff" in s for s in names) == 2, names
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 def _int8_siblings():
     """One int8 conv whose output is read by three int8 convs: a 1x1 (takes
     the handoff), a 1x1 stride 2 (same quantization: shares that buffer) and
