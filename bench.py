@@ -16,7 +16,9 @@ Reported:
                  of W + K steps, against the fp32 MFMA peak;
   b1_*           batch-1 latency and images/sec (HIP-graph replay);
   cpu_baseline   the reference runtime (cpu_generic package: naive conv on
-                 x86) on one batch-1 image, timed on the host.
+                 x86) on one batch-1 image, timed on the host;
+  int8, elementwise, yolo   INT8 ResNet-50, the memory-bound ops against
+                 the HBM peak, YOLOv10n 640 images/s (sections of their own).
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--batch 64] [--no-cpu-baseline]
 """
@@ -252,6 +254,57 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     return out
 
 
+def yolo_v10n(lib, steps: int, node_report: bool = False) -> dict:
+    """YOLOv10n-style detector at 640x640, batch 1 and
+    16: images/s from HIP-graph replays of the node loop (the whole YOLO op
+    set on the device: C2f Split/Concat, SPPF, PSA MatMul + Softmax, Resize,
+    DFL Softmax, TopK, GatherElements), plus the node time by op type from an
+    eager pass with per-node events."""
+    from collections import defaultdict
+
+    from spinnv2_amd.runtime import DeviceBuffer, Model
+    from spinnv2_amd.spk import models, write_spk
+
+    out = {"workload": "yolov10n_640"}
+    for batch in (1, 16):
+        g = models.yolo_v10n(batch)
+        m = Model(write_spk(g, "mi355x"), lib=lib)
+        x = models.make_input(g.tensors[g.inputs[0]].shape)
+        xb = DeviceBuffer(x.nbytes, lib)
+        xb.upload(x)
+        m.bind_input(0, xb)
+        m.set_profiling(True)
+        m.run()
+        m.reset_node_times()
+        for _ in range(3):
+            m.run()
+        lib.spkv2_device_synchronize()
+        by_op = defaultdict(float)
+        for n in g.nodes:
+            ms, cnt = m.node_time(n.id)
+            by_op[n.op_type] += ms / max(cnt, 1)
+        m.set_profiling(False)
+        m.set_graph_mode(True)
+        for _ in range(3):
+            m.run()
+        lib.spkv2_device_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            m.run()
+        lib.spkv2_device_synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        out[f"b{batch}_ms_per_step"] = ms
+        out[f"b{batch}_images_per_sec"] = batch * 1e3 / ms
+        if batch == 16:
+            out["node_ms_by_op_b16"] = {k: round(v, 4) for k, v in sorted(by_op.items(), key=lambda kv: -kv[1])}
+        if node_report:
+            for k, v in sorted(by_op.items(), key=lambda kv: -kv[1]):
+                log(f"yolo b={batch} {k:20s} {v:8.3f} ms")
+        m.close()
+        xb.free()
+    return out
+
+
 # Memory-bound ops at ResNet / YOLO shapes: (label, single_op args, algorithmic bytes)
 ELEMENTWISE = [
     ("maxpool_3x3s2_b64_64x112", ("MaxPool", [64, 64, 112, 112]), 4 * (64 * 64 * 112 * 112 + 64 * 64 * 56 * 56)),
@@ -305,6 +358,8 @@ def main() -> None:
     ap.add_argument("--no-int8", action="store_true", help="skip the INT8 ResNet-50 section")
     ap.add_argument("--int8-only", action="store_true", help="run only the INT8 ResNet-50 section")
     ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound op section")
+    ap.add_argument("--no-yolo", action="store_true", help="skip the YOLOv10n section")
+    ap.add_argument("--yolo-only", action="store_true", help="run only the YOLOv10n section")
     ap.add_argument("--elementwise-only", action="store_true", help="run only the memory-bound op section")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
@@ -323,6 +378,9 @@ def main() -> None:
     lib = load_library()
     if args.elementwise_only:
         print(json.dumps(elementwise(lib)), flush=True)
+        return
+    if args.yolo_only:
+        print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report)), flush=True)
         return
     if args.int8_only:
         print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
@@ -423,6 +481,7 @@ def main() -> None:
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
     ew = None if args.no_elementwise else elementwise(lib)
+    yolo = None if args.no_yolo else yolo_v10n(lib, max(args.steps, 10))
 
     result = {
         "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
@@ -457,6 +516,7 @@ def main() -> None:
         "cpu_baseline": base,
         "int8": int8,
         "elementwise": ew,
+        "yolo": yolo,
         "top1_image0": int(logits[0].argmax()),
     }
     print(json.dumps(result), flush=True)
