@@ -154,17 +154,6 @@ int launch_copy(hipStream_t s, const void *src, void *dst, size_t bytes) {
     return launch_status("copy");
 }
 
-// Strided block copy for Concat: `outer` blocks of `block` floats from src
-// (contiguous) into dst with row pitch `dst_pitch`.
-__global__ void __launch_bounds__(256) concat_copy(const float *__restrict__ src, float *__restrict__ dst, size_t outer,
-                                                   size_t block, size_t dst_pitch) {
-    const size_t total = outer * block;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += static_cast<size_t>(gridDim.x) * 256) {
-        const size_t o = i / block, r = i - o * block;
-        dst[o * dst_pitch + r] = src[i];
-    }
-}
-
 struct PoolArgs {
     const float *__restrict__ x;
     float *__restrict__ y;
@@ -598,11 +587,8 @@ int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         const float *x = dptr<const float>(ctx, node->inputs[i]);
         const size_t block = static_cast<size_t>(xr->shape[axis]) * inner;
         float *dst = y + axis_off * inner;
-        if (!(outer == 1 && dst == x) && outer * block > 0) {
-            hipLaunchKernelGGL(concat_copy, dim3(grid_for(outer * block, 256)), dim3(256), 0, ctx->stream, x, dst,
-                               outer, block, y_axis * inner);
-            if (int rc = launch_status("concat")) return rc;
-        }
+        if (!(outer == 1 && dst == x) && outer * block > 0)
+            if (int rc = strided_block_copy(ctx->stream, x, dst, outer, block, block, 0, y_axis * inner)) return rc;
         axis_off += xr->shape[axis];
     }
     return 0;

@@ -46,6 +46,11 @@ int gather_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int gather_elements_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int topk_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 
+// y[o * y_stride + j] = x[x_base + o * x_stride + j], o < outer, j < block
+// (float elements; Concat, Split, Slice)
+int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, size_t block, size_t x_stride,
+                       size_t x_base, size_t y_stride);
+
 // reliability helpers used by the executor
 int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);
 int minmax(hipStream_t s, const float *x, size_t n, float *dev_out4);

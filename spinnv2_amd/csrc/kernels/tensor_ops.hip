@@ -71,6 +71,16 @@ __global__ void __launch_bounds__(256) block_copy(const float *__restrict__ x, f
     }
 }
 
+// The same copy in 16-byte units: grid.y walks the blocks, grid.x the
+// float4s of a block, so no division per element.
+__global__ void __launch_bounds__(256) block_copy4(const floatx4 *__restrict__ x, floatx4 *__restrict__ y, size_t outer,
+                                                   size_t block4, size_t x_stride4, size_t y_stride4) {
+    for (size_t o = blockIdx.y; o < outer; o += gridDim.y)
+        for (size_t j = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; j < block4;
+             j += static_cast<size_t>(gridDim.x) * 256)
+            y[o * y_stride4 + j] = x[o * x_stride4 + j];
+}
+
 // Slice with a step: y[(o*out + s)*inner + t] = x[(o*dim + start + s*step)*inner + t]
 __global__ void __launch_bounds__(256) slice_kernel(const float *__restrict__ x, float *__restrict__ y, size_t outer,
                                                     int64_t out, int64_t dim, int64_t start, int64_t step, size_t inner) {
@@ -332,6 +342,26 @@ int tile_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     return launch_status("tile");
 }
 
+// y[o * y_stride + j] = x[x_base + o * x_stride + j] for o < outer, j < block
+// (elements): 16-byte copies when every offset and both pointers allow it.
+int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, size_t block, size_t x_stride,
+                       size_t x_base, size_t y_stride) {
+    if (outer * block == 0) return 0;
+    const bool vec = block % 4 == 0 && x_stride % 4 == 0 && x_base % 4 == 0 && y_stride % 4 == 0 &&
+                     reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
+    if (vec) {
+        const size_t block4 = block / 4;
+        const unsigned gx = static_cast<unsigned>(std::min<size_t>((block4 + 255) / 256, 1024));
+        const unsigned gy = static_cast<unsigned>(std::min<size_t>(outer, 65535));
+        hipLaunchKernelGGL(block_copy4, dim3(gx, gy), dim3(256), 0, s, reinterpret_cast<const floatx4 *>(x + x_base),
+                           reinterpret_cast<floatx4 *>(y), outer, block4, x_stride / 4, y_stride / 4);
+    } else {
+        hipLaunchKernelGGL(block_copy, dim3(grid_for(outer * block, 256)), dim3(256), 0, s, x, y, outer, block,
+                           x_stride, x_base, y_stride);
+    }
+    return launch_status("block_copy");
+}
+
 int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     Spkv2AttrRecord attr;
     if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
@@ -348,11 +378,10 @@ int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         const Spkv2TensorRecord *yr = rec(ctx, node->outputs[k]);
         const size_t block = static_cast<size_t>(yr->shape[axis]) * inner;
         if (axis_offset + yr->shape[axis] > x_axis) return -11;
-        if (outer * block > 0)
-            hipLaunchKernelGGL(block_copy, dim3(grid_for(outer * block, 256)), dim3(256), 0, ctx->stream,
-                               dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[k]), outer,
-                               block, x_axis * inner, axis_offset * inner, block);
-        if (int rc = launch_status("split")) return rc;
+        if (int rc = strided_block_copy(ctx->stream, dptr<const float>(ctx, node->inputs[0]),
+                                        dptr<float>(ctx, node->outputs[k]), outer, block, x_axis * inner,
+                                        axis_offset * inner, block))
+            return rc;
         axis_offset += yr->shape[axis];
     }
     return 0;
@@ -387,9 +416,9 @@ int slice_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     float *y = dptr<float>(ctx, node->outputs[0]);
     const size_t n = outer * static_cast<size_t>(out) * inner;
     if (step == 1)
-        hipLaunchKernelGGL(block_copy, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, x, y, outer,
-                           static_cast<size_t>(out) * inner, static_cast<size_t>(dim) * inner,
-                           static_cast<size_t>(start) * inner, static_cast<size_t>(out) * inner);
+        return strided_block_copy(ctx->stream, x, y, outer, static_cast<size_t>(out) * inner,
+                                  static_cast<size_t>(dim) * inner, static_cast<size_t>(start) * inner,
+                                  static_cast<size_t>(out) * inner);
     else
         hipLaunchKernelGGL(slice_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, x, y, outer, out, dim,
                            start, step, inner);

@@ -595,6 +595,11 @@ INDEX_CASES = [
     ("Split", [1, 64, 8400], dict(sizes=[16, 16, 32], axis=1)),
     ("Slice", [1, 84, 8400], dict(start=4, end=84, axis=1, step=1)),
     ("Slice", [2, 33, 17], dict(start=-30, end=-1, axis=1, step=4)),
+    # strided block copies: 16-byte path with several blocks, and odd widths (scalar path)
+    ("Split", [4, 8, 6, 4], dict(sizes=[4, 4], axis=1)),
+    ("Split", [2, 6, 5, 3], dict(sizes=[1, 5], axis=1)),
+    ("Slice", [3, 10, 7], dict(start=2, end=9, axis=1, step=1)),
+    ("Slice", [3, 16, 8], dict(start=4, end=12, axis=1, step=1)),
     ("Gather", [1, 8400, 4], dict(indices=list(range(8399, 0, -28)), axis=1)),
     ("GatherElements", [1, 8400, 6], dict(indices=np.random.default_rng(3).integers(0, 8400, (1, 300, 6)).tolist(), axis=1)),
     ("TopK", [1, 8400], dict(k=300, axis=-1, largest=1)),
@@ -602,6 +607,24 @@ INDEX_CASES = [
     ("TopK", [3, 1000, 5], dict(k=17, axis=1, largest=0)),
     ("ReduceMax", [1, 80, 8400], dict(axes=[1], keepdims=0)),
 ]
+
+
+@pytest.mark.parametrize("batch,chans", [(3, (8, 16)), (2, (3, 5))])
+def test_concat_strided_bitwise(gpu, batch, chans):
+    """Channel Concat of batch > 1 inputs (one strided block copy per input:
+    16-byte path for widths that allow it, scalar otherwise) against the
+    oracle."""
+    from spinnv2_amd.spk.graph import Graph
+
+    g = Graph("concat")
+    a = g.input("a", [batch, chans[0], 6, 10])
+    b = g.input("b", [batch, chans[1], 6, 10])
+    g.mark_output(g.concat([g.relu(a), g.relu(b)], axis=1))
+    xs = rng_inputs(g)
+    blob = write_spk(g, "mi355x")
+    got = run_gpu(blob, xs)[0]
+    want = run_oracle(blob, xs)[0]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 # TopK also on inputs rounded to a coarse grid, so values tie across the
