@@ -133,6 +133,7 @@ __global__ void __launch_bounds__(256) gather_elements_kernel(const float *__res
 // ---------------------------------------------------------------- TopK
 
 constexpr int kTopkMaxK = 1024;
+constexpr int kTopkRowLds = 16384;  // rows up to this length are staged in LDS for the heap replay
 
 // order-preserving key of a float: larger float -> larger unsigned
 __device__ __forceinline__ uint32_t fkey(float v) {
@@ -150,7 +151,9 @@ struct HeapPair {
 // of the tied elements survive): heap of the first k, sift-down from k/2-1,
 // then every later element replaces the root when strictly better
 // (reference tensor/topk.c:71-101).
-__device__ void topk_heap_replay(const float *__restrict__ x, size_t base, size_t inner, int dim, int k, int largest,
+// `row` holds the row's values (LDS when it fits, else the input itself with
+// stride `inner`); the root's value is kept in a register.
+__device__ void topk_heap_replay(const float *__restrict__ row, size_t inner, int dim, int k, int largest,
                                  HeapPair *h) {
     auto better = [&](float a, float b) { return largest ? (a < b) : (a > b); };  // "a sinks below b"
     auto sift = [&](int i) {
@@ -165,13 +168,29 @@ __device__ void topk_heap_replay(const float *__restrict__ x, size_t base, size_
             i = m;
         }
     };
-    for (int d = 0; d < k; d++) h[d] = HeapPair{x[base + static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
+    for (int d = 0; d < k; d++) h[d] = HeapPair{row[static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
     for (int i = k / 2 - 1; i >= 0; i--) sift(i);
-    for (int d = k; d < dim; d++) {
-        const float v = x[base + static_cast<size_t>(d) * inner];
-        if (largest ? (v > h[0].v) : (v < h[0].v)) {
+    float root = h[0].v;
+    int d = k;
+    // four values ahead: their loads do not wait for the heap
+    for (; d + 4 <= dim; d += 4) {
+        float v4[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v4[u] = row[static_cast<size_t>(d + u) * inner];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (largest ? (v4[u] > root) : (v4[u] < root)) {
+                h[0] = HeapPair{v4[u], static_cast<uint32_t>(d + u)};
+                sift(0);
+                root = h[0].v;
+            }
+    }
+    for (; d < dim; d++) {
+        const float v = row[static_cast<size_t>(d) * inner];
+        if (largest ? (v > root) : (v < root)) {
             h[0] = HeapPair{v, static_cast<uint32_t>(d)};
             sift(0);
+            root = h[0].v;
         }
     }
 }
@@ -189,6 +208,7 @@ __global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, 
     __shared__ uint32_t s_prefix, s_remaining, s_count, s_ambiguous;
     __shared__ unsigned long long keys[kTopkMaxK];
     __shared__ HeapPair heap[kTopkMaxK];
+    __shared__ float rowbuf[kTopkRowLds];
     const size_t row = blockIdx.x;
     const size_t o = row / inner, in = row % inner;
     const size_t base = o * static_cast<size_t>(dim) * inner + in;
@@ -245,10 +265,21 @@ __global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, 
                 keys[slot] = (static_cast<unsigned long long>(kk) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(d));
             }
         }
-    } else if (tid == 0) {
-        topk_heap_replay(x, base, inner, dim, k, largest, heap);
-        for (int i = 0; i < k; i++)
-            keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
+    } else {
+        // the replay is one thread's sequential scan: stage the row in LDS
+        // first (all threads), so its reads cost LDS latency, not memory's
+        const bool staged = dim <= kTopkRowLds;
+        if (staged)
+            for (int d = tid; d < dim; d += 256) rowbuf[d] = x[base + static_cast<size_t>(d) * inner];
+        __syncthreads();
+        if (tid == 0) {
+            if (staged)
+                topk_heap_replay(rowbuf, 1, dim, k, largest, heap);
+            else
+                topk_heap_replay(x + base, inner, dim, k, largest, heap);
+            for (int i = 0; i < k; i++)
+                keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
+        }
     }
     __syncthreads();
     // bitonic sort, descending
