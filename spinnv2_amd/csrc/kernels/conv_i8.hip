@@ -99,6 +99,47 @@ __global__ void __launch_bounds__(256) quantize_pad_nhwc(const float *__restrict
     }
 }
 
+// The same quantization for inputs with few channels (Cp <= 16, e.g. an RGB
+// stem): one thread per padded pixel reads its C values and writes its Cp
+// bytes as dwords, instead of 64-channel tiles that would sit mostly idle.
+__global__ void __launch_bounds__(256) quantize_pad_nhwc_narrow(const float *__restrict__ x, int8_t *__restrict__ xq,
+                                                                int C, int H, int W, int Hp, int Wp, int Cp, int pt,
+                                                                int pl, float inv_scale, int split, int images) {
+    const int HW = H * W;
+    const int HWp = Hp * Wp;
+    const size_t total = static_cast<size_t>(images) * HWp;
+    for (size_t t = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * 256) {
+        const int img = static_cast<int>(t / HWp);
+        const int pp = static_cast<int>(t - static_cast<size_t>(img) * HWp);
+        const int hp = pp / Wp;
+        const int h = hp - pt, w = pp - hp * Wp - pl;
+        const bool inside = static_cast<unsigned>(h) < static_cast<unsigned>(H) &&
+                            static_cast<unsigned>(w) < static_cast<unsigned>(W);
+        const float *xi = x + static_cast<size_t>(img) * C * HW;
+        uint32_t *dst = reinterpret_cast<uint32_t *>(xq + t * Cp);
+        for (int c0 = 0; c0 < Cp; c0 += 4) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int c = c0 + b;
+                int8_t q = 0;
+                if (inside && c < C) {
+                    const int idx = c * HW + h * W + w;  // NCHW index inside the image
+                    const float v = xi[idx] * inv_scale;
+                    float r;
+                    if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
+                    else r = idx < split ? rintf(v) : roundf(v);
+                    r = fminf(fmaxf(r, -128.0f), 127.0f);
+                    q = static_cast<int8_t>(static_cast<int>(r));
+                }
+                word |= static_cast<uint32_t>(static_cast<uint8_t>(q)) << (8 * b);
+            }
+            dst[c0 / 4] = word;
+        }
+    }
+}
+
 struct I8Args {
     const int8_t *__restrict__ xq;      // padded NHWC int8
     const int8_t *__restrict__ wp;      // [m_tiles][k_tiles][BM][BK]
@@ -953,6 +994,12 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     const bool handoff = !ctx->fault_event.enabled;
     if ((plan->q_in || plan->q_shared) && handoff) {
         xq = plan->q_in ? plan->q_in : plan->q_shared;  // written by the producer's epilogue
+    } else if (L.Cp <= 16) {
+        const size_t pixels = static_cast<size_t>(g.N) * L.Hp * L.Wp;
+        hipLaunchKernelGGL(quantize_pad_nhwc_narrow, dim3(grid_for(pixels, 256)), dim3(256), 0, ctx->stream,
+                           dptr<const float>(ctx, node->inputs[0]), xq, g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl,
+                           inv_scale, plan->quant_split, g.N);
+        if (int rc = launch_status("quantize_pad_nhwc_narrow")) return rc;
     } else {
         dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
                    static_cast<unsigned>(g.N));
