@@ -99,11 +99,11 @@ def copy_calibration(mib: int, reps: int) -> None:
     buf.free()
 
 
-def pmc_traffic() -> dict | None:
-    """HBM bytes of the conv kernels per step, from the committed rocprofv3
+def pmc_traffic(name: str = "conv_igemm_f32_resnet101_b64_traffic.txt") -> dict | None:
+    """HBM bytes of the conv kernels per step, from a committed rocprofv3
     --pmc summary (FETCH_SIZE and WRITE_SIZE passes scaled by the copy
     kernel's reading).  None when no summary is committed."""
-    p = ROOT / "profiles" / "conv_igemm_f32_resnet101_b64_traffic.txt"
+    p = ROOT / "profiles" / name
     if not p.exists():
         return None
     vals = {}
@@ -220,6 +220,8 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     xin.free()
     tops = sum(ops.values()) / (conv_ms * 1e-3) / 1e12
     gbps = hbm / (conv_ms * 1e-3) / 1e9
+    t8 = pmc_traffic("conv_igemm_i8_resnet50_b64_traffic.txt")
+    i8_traffic = t8.get("conv_hbm_bytes_per_step") if t8 else None
     # fp32 activations in and out make these convs HBM-bound: at the int8
     # MFMA peak the convs would take sum(ops)/5e15 s, far less than moving
     # their fp32 activations at 8 TB/s; the binding roofline is HBM
@@ -227,7 +229,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
            "ms_per_step": elapsed * 1e3 / steps, "conv_ms_per_step": conv_ms,
            "conv_gop_per_image": sum(ops.values()) / batch / 1e9, "conv_kernels": names,
            "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                        "frac": gbps / HBM_PEAK_GBPS, "traffic": None,
+                        "frac": gbps / HBM_PEAK_GBPS, "traffic": i8_traffic,
                         "algorithmic_bytes": hbm,
                         "floor_ms": {"hbm": hbm / HBM_PEAK_GBPS / 1e6,
                                      "mfma": sum(ops.values()) / INT8_MFMA_PEAK_TOPS / 1e9}},
@@ -254,7 +256,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     return out
 
 
-def yolo_v10n(lib, steps: int, node_report: bool = False) -> dict:
+def yolo_v10n(lib, steps: int, node_report: bool = False, eager: bool = False) -> dict:
     """YOLOv10n-style detector at 640x640, batch 1 and
     16: images/s from HIP-graph replays of the node loop (the whole YOLO op
     set on the device: C2f Split/Concat, SPPF, PSA MatMul + Softmax, Resize,
@@ -284,7 +286,7 @@ def yolo_v10n(lib, steps: int, node_report: bool = False) -> dict:
             ms, cnt = m.node_time(n.id)
             by_op[n.op_type] += ms / max(cnt, 1)
         m.set_profiling(False)
-        m.set_graph_mode(True)
+        m.set_graph_mode(not eager)
         for _ in range(3):
             m.run()
         lib.spkv2_device_synchronize()
@@ -293,6 +295,7 @@ def yolo_v10n(lib, steps: int, node_report: bool = False) -> dict:
             m.run()
         lib.spkv2_device_synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / steps
+        m.set_graph_mode(False)
         out[f"b{batch}_ms_per_step"] = ms
         out[f"b{batch}_images_per_sec"] = batch * 1e3 / ms
         if batch == 16:
@@ -351,7 +354,7 @@ def main() -> None:
     ap.add_argument("--depth", type=int, default=101)
     ap.add_argument("--b1-steps", type=int, default=50)
     ap.add_argument("--eager", action="store_true",
-                    help="time the batch-B (and INT8) steps without HIP-graph replay (for kernel tracing)")
+                    help="time every section without HIP-graph replay (for kernel tracing)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--node-report", action="store_true", help="print per-node device times to stderr")
     ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
@@ -380,7 +383,7 @@ def main() -> None:
         print(json.dumps(elementwise(lib)), flush=True)
         return
     if args.yolo_only:
-        print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report)), flush=True)
+        print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report, args.eager)), flush=True)
         return
     if args.int8_only:
         print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
@@ -481,7 +484,7 @@ def main() -> None:
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
     ew = None if args.no_elementwise else elementwise(lib)
-    yolo = None if args.no_yolo else yolo_v10n(lib, max(args.steps, 10))
+    yolo = None if args.no_yolo else yolo_v10n(lib, max(args.steps, 10), eager=args.eager)
 
     result = {
         "metric": "ResNet-101 224^2 images/sec (b=64); conv TFLOP/s as % of fp32 MFMA peak",
