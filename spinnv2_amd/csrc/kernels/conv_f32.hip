@@ -168,9 +168,10 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     //
     // Split-K: blockIdx.y is the k slice and every tile writes partials.
     // Hybrid (dp_tiles > 0, one grid row): the first dp_tiles workgroups
-    // each compute a whole tile (a multiple of the CU count, so every CU
-    // gets the same number), the remaining tiles are cut into kt_per_split
-    // k-tile slices, one workgroup each, whose partials splitk_epilogue sums.
+    // each compute a whole tile (the largest multiple of the CU count that is
+    // whole n-tile columns, rounded down to such columns, so the CUs get
+    // equal shares), the remaining tiles are cut into kt_per_split k-tile
+    // slices, one workgroup each, whose partials splitk_epilogue sums.
     int bid = blockIdx.x;
     int slice = blockIdx.y;
     bool part = a.ws != nullptr;
