@@ -351,7 +351,7 @@ int oracle_conv2d_int8(const float *x, const int8_t *wq, const float *w_scales, 
                        const float *res, float *y, int32_t *acc_out, int N, int C, int H, int W, int M, int KH,
                        int KW, int OH, int OW, int sh, int sw, int ph, int pw, int dh, int dw, int act) {
     const size_t chw = (size_t)C * H * W;
-    int8_t *xq = (int8_t *)malloc(chw * N + 1);
+    int8_t *xq = (int8_t *)calloc(chw * N + 1, 1);
     int32_t *acc = acc_out ? acc_out : (int32_t *)malloc((size_t)N * M * OH * OW * sizeof(int32_t) + 4);
     if (!xq || !acc) {
         free(xq);
