@@ -152,9 +152,13 @@ struct HeapPair {
 // then every later element replaces the root when strictly better
 // (reference tensor/topk.c:71-101).
 // `row` holds the row's values (LDS when it fits, else the input itself with
-// stride `inner`); the root's value is kept in a register.
+// stride `inner`).  Run by one wave: lane 0 builds and sifts the heap, and
+// the wave scans 64 elements at a time for the next one that enters (strictly
+// better than the current root), so runs of elements that cannot enter cost
+// one ballot; after each insertion the rest of the 64 are checked against
+// the new root, which keeps the reference's element-by-element order.
 __device__ void topk_heap_replay(const float *__restrict__ row, size_t inner, int dim, int k, int largest,
-                                 HeapPair *h) {
+                                 HeapPair *h, int lane) {
     auto better = [&](float a, float b) { return largest ? (a < b) : (a > b); };  // "a sinks below b"
     auto sift = [&](int i) {
         for (;;) {
@@ -168,29 +172,27 @@ __device__ void topk_heap_replay(const float *__restrict__ row, size_t inner, in
             i = m;
         }
     };
-    for (int d = 0; d < k; d++) h[d] = HeapPair{row[static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
-    for (int i = k / 2 - 1; i >= 0; i--) sift(i);
-    float root = h[0].v;
-    int d = k;
-    // four values ahead: their loads do not wait for the heap
-    for (; d + 4 <= dim; d += 4) {
-        float v4[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) v4[u] = row[static_cast<size_t>(d + u) * inner];
-#pragma unroll
-        for (int u = 0; u < 4; u++)
-            if (largest ? (v4[u] > root) : (v4[u] < root)) {
-                h[0] = HeapPair{v4[u], static_cast<uint32_t>(d + u)};
-                sift(0);
-                root = h[0].v;
-            }
+    if (lane == 0) {
+        for (int d = 0; d < k; d++) h[d] = HeapPair{row[static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
+        for (int i = k / 2 - 1; i >= 0; i--) sift(i);
     }
-    for (; d < dim; d++) {
-        const float v = row[static_cast<size_t>(d) * inner];
-        if (largest ? (v > root) : (v < root)) {
-            h[0] = HeapPair{v, static_cast<uint32_t>(d)};
-            sift(0);
+    __builtin_amdgcn_wave_barrier();
+    float root = h[0].v;
+    for (int d0 = k; d0 < dim; d0 += 64) {
+        const int d = d0 + lane;
+        const bool live = d < dim;
+        const float v = live ? row[static_cast<size_t>(d) * inner] : 0.0f;
+        unsigned long long m = __ballot(live && (largest ? (v > root) : (v < root)));
+        while (m) {
+            const int j = __ffsll(static_cast<long long>(m)) - 1;
+            const float vj = __shfl(v, j);
+            if (lane == 0) {
+                h[0] = HeapPair{vj, static_cast<uint32_t>(d0 + j)};
+                sift(0);
+            }
+            __builtin_amdgcn_wave_barrier();
             root = h[0].v;
+            m = __ballot(live && lane > j && (largest ? (v > root) : (v < root)));
         }
     }
 }
@@ -272,12 +274,12 @@ __global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, 
         if (staged)
             for (int d = tid; d < dim; d += 256) rowbuf[d] = x[base + static_cast<size_t>(d) * inner];
         __syncthreads();
-        if (tid == 0) {
+        if (tid < 64) {
             if (staged)
-                topk_heap_replay(rowbuf, 1, dim, k, largest, heap);
+                topk_heap_replay(rowbuf, 1, dim, k, largest, heap, tid);
             else
-                topk_heap_replay(x + base, inner, dim, k, largest, heap);
-            for (int i = 0; i < k; i++)
+                topk_heap_replay(x + base, inner, dim, k, largest, heap, tid);
+            for (int i = tid; i < k; i += 64)
                 keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
         }
     }
