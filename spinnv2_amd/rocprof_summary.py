@@ -4,6 +4,7 @@
     python -m spinnv2_amd.rocprof_summary traffic --fetch <pmc.csv> --write <pmc.csv>
            --copy-fetch <pmc.csv> --copy-write <pmc.csv> --copy-bytes B --runs N --match conv_igemm
     python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
+           [--mops SQ_INSTS_VALU_MFMA_MOPS_I8 --peak 5000]
 
 `stats` divides rocprofv3 --kernel-trace --stats totals by the number of
 spkv2_run calls the profiled command made (N), giving per-run kernel time.
@@ -12,10 +13,12 @@ kernels whose name contains --match, per run, and scales each counter by
 bytes / counter of a plain copy kernel of known size profiled the same way;
 per kernel it also gives the HBM GB/s those bytes make over the dispatches'
 own durations (timestamps of the FETCH_SIZE pass).
-`mfma` reads a --pmc pass of SQ_INSTS_VALU_MFMA_MOPS_F32 (fp32 MFMA work in
-units of 512 FLOP), SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: per kernel
-the MFMA FLOP the hardware counted, that work over the dispatches' durations
-against the fp32 MFMA peak, and MFMA busy cycles (per SIMD) over the
+`mfma` reads a --pmc pass of an MFMA work counter (--mops, default
+SQ_INSTS_VALU_MFMA_MOPS_F32; every SQ_INSTS_VALU_MFMA_MOPS_* counts in units
+of 512 operations), SQ_VALU_MFMA_BUSY_CYCLES and GRBM_GUI_ACTIVE: per kernel
+the MFMA operations the hardware counted, that work over the dispatches'
+durations against --peak (T ops/s of the counted type; 157.3 for fp32, 5000
+for int8), and MFMA busy cycles (per SIMD) over the
 active cycles of all SIMDs: GRBM_GUI_ACTIVE / XCDs x CUs x 4 (on MI355X
 GRBM_GUI_ACTIVE sums the 8 XCDs' counts: about 8 x duration x clock).
 """
@@ -114,13 +117,14 @@ def mfma(args) -> str:
             seen.add(r["Dispatch_Id"])
             k["ns"] += float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
             k["n"] += 1
-    out = [f"{'kernel':48s} {'disp/run':>8s} {'avg us':>8s} {'GFLOP/run':>10s} {'TFLOP/s':>8s} {'% peak':>7s} "
-           f"{'busy %':>7s}"]
+    op = "OP" if args.mops.endswith("I8") else "FLOP"  # integer MFMA work is counted in operations
+    out = [f"{'kernel':48s} {'disp/run':>8s} {'avg us':>8s} {'G' + op + '/run':>10s} {'T' + op + '/s':>8s} "
+           f"{'% peak':>7s} {'busy %':>7s}"]
     tot_f = tot_ns = tot_busy = tot_active = 0.0
     for name, k in sorted(per.items(), key=lambda kv: -kv[1]["ns"]):
         if args.match not in name:
             continue
-        flop = k["SQ_INSTS_VALU_MFMA_MOPS_F32"] * 512
+        flop = k[args.mops] * 512
         tf = flop / k["ns"] / 1e3 if k["ns"] else 0.0
         simd_cycles = k["GRBM_GUI_ACTIVE"] / args.xcds * args.cus * 4
         busy = k["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_cycles if simd_cycles else 0.0
@@ -158,7 +162,8 @@ def main() -> None:
     m.add_argument("--match", default="conv_igemm")
     m.add_argument("--cus", type=int, default=256)
     m.add_argument("--xcds", type=int, default=8)
-    m.add_argument("--peak", type=float, default=157.3, help="TFLOP/s (fp32 MFMA)")
+    m.add_argument("--peak", type=float, default=157.3, help="T ops/s of the counted MFMA type (fp32: 157.3)")
+    m.add_argument("--mops", default="SQ_INSTS_VALU_MFMA_MOPS_F32", help="MFMA work counter (units of 512 ops)")
     a = ap.parse_args()
     print({"stats": lambda: stats(a.csv, a.runs), "traffic": lambda: traffic(a), "mfma": lambda: mfma(a)}[a.cmd]())
 

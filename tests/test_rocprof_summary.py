@@ -70,8 +70,24 @@ def test_mfma_work_and_busy(tmp_path):
                  [d, "conv_igemm_f32<x>", "GRBM_GUI_ACTIVE", 8 * 240_000, t0, t0 + 100_000],
                  [d, "conv_igemm_f32<x>", "SQ_VALU_MFMA_BUSY_CYCLES", 0.5 * 240_000 * 256 * 4, t0, t0 + 100_000]]
     p = _write(tmp_path / "m.csv", PMC_COLS, rows)
-    out = rs.mfma(SimpleNamespace(csv=p, runs=2, match="conv_igemm", cus=256, xcds=8, peak=157.3))
+    out = rs.mfma(SimpleNamespace(csv=p, runs=2, match="conv_igemm", cus=256, xcds=8, peak=157.3,
+                                  mops="SQ_INSTS_VALU_MFMA_MOPS_F32"))
     assert _result(out, "conv_igemm_mfma_flop_per_run") == pytest.approx(512e6)
     # 512e6 FLOP per 100 us = 5.12 TFLOP/s
     assert _result(out, "conv_igemm_mfma_tflops") == pytest.approx(5.12)
     assert _result(out, "conv_igemm_mfma_busy_frac") == pytest.approx(0.5)
+
+
+def test_mfma_int8_counter(tmp_path):
+    # int8 work: 2e6 units of 512 ops in one 200 us dispatch = 5.12 TOP/s of a 5000 TOP/s peak
+    rows = [[1, "conv_igemm_i8<128>", "SQ_INSTS_VALU_MFMA_MOPS_I8", 2e6, 0, 200_000],
+            [1, "conv_igemm_i8<128>", "GRBM_GUI_ACTIVE", 8 * 480_000, 0, 200_000],
+            [1, "conv_igemm_i8<128>", "SQ_VALU_MFMA_BUSY_CYCLES", 0.25 * 480_000 * 256 * 4, 0, 200_000],
+            [2, "quantize_pad_nhwc", "SQ_INSTS_VALU_MFMA_MOPS_I8", 0, 300_000, 310_000]]
+    p = _write(tmp_path / "m8.csv", PMC_COLS, rows)
+    out = rs.mfma(SimpleNamespace(csv=p, runs=1, match="conv_igemm_i8", cus=256, xcds=8, peak=5000.0,
+                                  mops="SQ_INSTS_VALU_MFMA_MOPS_I8"))
+    assert _result(out, "conv_igemm_i8_mfma_flop_per_run") == pytest.approx(1.024e9)
+    assert _result(out, "conv_igemm_i8_mfma_tflops") == pytest.approx(5.12)
+    assert _result(out, "conv_igemm_i8_mfma_frac_of_peak") == pytest.approx(5.12 / 5000, abs=1e-4)
+    assert _result(out, "conv_igemm_i8_mfma_busy_frac") == pytest.approx(0.25)
