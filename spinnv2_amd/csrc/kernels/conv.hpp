@@ -74,6 +74,22 @@ struct ConvPlan {
 
 void conv_plan_free(void *p);
 
+// Node cache of a MaxPool (3x3 / stride 2 / pad 1 over fp32 NCHW, channels a
+// multiple of 64) whose output int8 convs may take as an int8 handoff: the
+// pooling kernel then also quantizes its output, with the consumers' scale
+// and rounding rule, into their zero-padded NHWC buffer.  The q_* fields and
+// y_needed mean what ConvPlan's producer-side fields mean; q_out stays null
+// when no consumer takes the handoff.
+struct PoolPlan {
+    int8_t *q_out;
+    int q_Hp, q_Wp, q_Cp, q_pt, q_pl, q_split;
+    float q_inv_scale;
+    int q_readers;
+    bool y_needed;
+};
+
+void pool_plan_free(void *p);
+
 // Places the plan's workspace in the node's kernel-spec scratch when that
 // spec reserves enough; returns the bytes the runtime must allocate for it
 // instead (0 when the scratch arena holds it).

@@ -825,30 +825,13 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
 // writes the fp32 tensor when anything else reads it (a consumer served by
 // neither, a graph output).  Packages with a protection plan keep every
 // tensor materialized and do not hand off.
-static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan, const I8Layout &L) {
-    if (ctx->protection_count > 0) return 0;
-    if (const char *e = getenv("SPKV2_I8_HANDOFF"))
-        if (e[0] == '0') return 0;
-    const uint32_t t = node->inputs[0];
-    const Spkv2NodeRecord *prod = nullptr;
-    int readers = 0;
-    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
-        const Spkv2NodeRecord *n = &ctx->node_records[i];
-        for (uint16_t k = 0; k < n->input_count; k++)
-            if (n->inputs[k] == t) readers++;
-        if (n->id < node->id)
-            for (uint16_t k = 0; k < n->output_count; k++)
-                if (n->outputs[k] == t) prod = n;
-    }
-    if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
-    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
-    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
-    if (!pp || pp->path != CONV_IGEMM_I8) return 0;
+// Joins this conv to its producer's int8 handoff: the producer (an int8 conv
+// or a MaxPool, plan type P, both with the q_* fields) writes the quantized
+// input straight into this conv's padded NHWC buffer.  The first consumer
+// owns the buffer; a later one with identical quantization shares it.
+template <class P>
+static int join_handoff(P *pp, ConvPlan *plan, const I8Layout &L, int readers, bool is_output) {
     const ConvGeom &g = plan->g;
-    if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
-    bool is_output = false;
-    for (size_t i = 0; i < ctx->output_count; i++)
-        if (ctx->output_ids[i] == t) is_output = true;
     const float inv = 1.0f / plan->x_scale;  // reference conv_int8.c:23
     if (pp->q_out) {
         // the tensor is already handed off to an earlier consumer: share its
@@ -878,6 +861,42 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
     pp->q_readers = 1;
     pp->y_needed = readers > pp->q_readers || is_output;
     return 0;
+}
+
+static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan, const I8Layout &L) {
+    if (ctx->protection_count > 0) return 0;
+    if (const char *e = getenv("SPKV2_I8_HANDOFF"))
+        if (e[0] == '0') return 0;
+    const uint32_t t = node->inputs[0];
+    const Spkv2NodeRecord *prod = nullptr;
+    int readers = 0;
+    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *n = &ctx->node_records[i];
+        for (uint16_t k = 0; k < n->input_count; k++)
+            if (n->inputs[k] == t) readers++;
+        if (n->id < node->id)
+            for (uint16_t k = 0; k < n->output_count; k++)
+                if (n->outputs[k] == t) prod = n;
+    }
+    if (!prod || prod->output_count != 1) return 0;
+    bool is_output = false;
+    for (size_t i = 0; i < ctx->output_count; i++)
+        if (ctx->output_ids[i] == t) is_output = true;
+    const ConvGeom &g = plan->g;
+    if (prod->op_type == SPKV2_OP_MAXPOOL) {
+        // prepared by the built-in MaxPool as a fused pooling + quantization
+        // candidate: 64-channel blocks, 16-byte pixel stores
+        if (ctx->node_cache_dtors[prod->id] != pool_plan_free) return 0;
+        PoolPlan *pp = static_cast<PoolPlan *>(ctx->node_cache[prod->id]);
+        if (!pp || L.Cp != g.C || g.C % 64 != 0) return 0;
+        return join_handoff(pp, plan, L, readers, is_output);
+    }
+    if (prod->op_type != SPKV2_OP_CONV) return 0;
+    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
+    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
+    if (!pp || pp->path != CONV_IGEMM_I8) return 0;
+    if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
+    return join_handoff(pp, plan, L, readers, is_output);
 }
 
 int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {

@@ -8,6 +8,7 @@
 #include <cstring>
 
 #include "common.hpp"
+#include "conv.hpp"
 #include "kernels.hpp"
 
 namespace spk::kern {
@@ -189,10 +190,39 @@ __global__ void __launch_bounds__(256) maxpool_kernel(PoolArgs a) {
 }
 
 // The ResNet stem's 3x3 / stride 2 / pad 1 MaxPool when W is a multiple of 8
-// and W == 2*OW: each thread makes 4 consecutive outputs of one row from a
+// and W == 2*OW: 4 consecutive outputs (oh, ow0..ow0+3) of one plane from a
 // scalar and two 16-byte loads per input row (the 9 columns its windows
 // touch), visiting each window in the reference's order (rows, then
-// columns, strict >), and stores them as one 16-byte write.
+// columns, strict >).
+__device__ __forceinline__ void pool3s2_x4(const float *__restrict__ xp, int H, int W, int oh, int ow0, float m[4]) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) m[t] = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int ih = 2 * oh - 1 + i;
+        if (ih < 0 || ih >= H) continue;
+        const float *row = xp + ih * W + 2 * ow0;
+        float c[9];  // input columns 2*ow0-1 .. 2*ow0+7
+        c[0] = ow0 > 0 ? row[-1] : 0.0f;
+        const floatx4 lo = *reinterpret_cast<const floatx4 *>(row);
+        const floatx4 hi = *reinterpret_cast<const floatx4 *>(row + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            c[1 + e] = lo[e];
+            c[5 + e] = hi[e];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                if (t == 0 && j == 0 && ow0 == 0) continue;  // column -1: outside the input
+                const float v = c[2 * t + j];
+                if (v > m[t]) m[t] = v;
+            }
+    }
+}
+
+// Each thread makes 4 outputs of one row and stores them as one 16-byte write.
 __global__ void __launch_bounds__(256) maxpool3s2_x4(const float *__restrict__ x, float *__restrict__ y, unsigned planes,
                                                      int H, int W, int OH, int OW) {
     const unsigned groups = static_cast<unsigned>(OH * (OW / 4));
@@ -202,33 +232,78 @@ __global__ void __launch_bounds__(256) maxpool3s2_x4(const float *__restrict__ x
         for (unsigned g = blockIdx.x * 256 + threadIdx.x; g < groups; g += gridDim.x * 256) {
             const int oh = static_cast<int>(g / static_cast<unsigned>(OW / 4));
             const int ow0 = 4 * (static_cast<int>(g) - oh * (OW / 4));
-            float m[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
-#pragma unroll
-            for (int i = 0; i < 3; i++) {
-                const int ih = 2 * oh - 1 + i;
-                if (ih < 0 || ih >= H) continue;
-                const float *row = xp + ih * W + 2 * ow0;
-                float c[9];  // input columns 2*ow0-1 .. 2*ow0+7
-                c[0] = ow0 > 0 ? row[-1] : 0.0f;
-                const floatx4 lo = *reinterpret_cast<const floatx4 *>(row);
-                const floatx4 hi = *reinterpret_cast<const floatx4 *>(row + 4);
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    c[1 + e] = lo[e];
-                    c[5 + e] = hi[e];
-                }
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int j = 0; j < 3; j++) {
-                        if (t == 0 && j == 0 && ow0 == 0) continue;  // column -1: outside the input
-                        const float v = c[2 * t + j];
-                        if (v > m[t]) m[t] = v;
-                    }
-            }
+            float m[4];
+            pool3s2_x4(xp, H, W, oh, ow0, m);
             *reinterpret_cast<floatx4 *>(yp + oh * OW + ow0) = floatx4{m[0], m[1], m[2], m[3]};
         }
     }
+}
+
+// The same pooling with the output handed to int8 convs: each pooled value
+// is quantized as those convs quantize their input (v * inv_scale; NaN to 0;
+// element index < split: round half to even, else half away from zero;
+// clamp to [-128, 127]; the index is the NCHW index inside one image of the
+// pooled tensor) and written into their zero-padded NHWC int8 buffer
+// [N][Hp][Wp][Cp] at pixel (oh + pt, ow + pl); the fp32 output is written
+// too when y is non-null.  Block (x, y, z) = (64 consecutive outputs of a
+// plane, 64 channels, image): each thread pools four (channel, 4-output
+// group) items, 16 groups of one channel per 16 lanes so a wave reads 512
+// contiguous bytes per input row, the bytes are transposed through LDS, and
+// each thread stores 16 channels of one pixel (one 16-byte store).  Needs
+// C % 64 == 0 and Cp a multiple of 16; the halo and channels C..Cp-1 of xq
+// are never written (they stay zero).
+__global__ void __launch_bounds__(256) maxpool3s2_q8(const float *__restrict__ x, float *__restrict__ y,
+                                                     int8_t *__restrict__ xq, int C, int H, int W, int OH, int OW,
+                                                     int Hp, int Wp, int Cp, int pt, int pl, float inv_scale,
+                                                     int split) {
+    __shared__ uint32_t tile[64][16 + 1];  // [channel][4-output group]: 4 bytes, one per output
+    const int img = blockIdx.z;
+    const int OHW = OH * OW;
+    const int gl = threadIdx.x & 15;
+    const int g = blockIdx.x * 16 + gl;  // 4-output group of the plane
+    if (4 * g < OHW) {
+        const int oh = g / (OW / 4);
+        const int ow0 = 4 * (g - oh * (OW / 4));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int cl = (threadIdx.x >> 4) + 16 * i;
+            const int c = blockIdx.y * 64 + cl;
+            const size_t plane = static_cast<size_t>(img) * C + c;
+            float m[4];
+            pool3s2_x4(x + plane * H * W, H, W, oh, ow0, m);
+            if (y) *reinterpret_cast<floatx4 *>(y + plane * OHW + oh * OW + ow0) = floatx4{m[0], m[1], m[2], m[3]};
+            uint32_t word = 0;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int idx = c * OHW + oh * OW + ow0 + t;  // NCHW index inside the image
+                const float v = m[t] * inv_scale;
+                float r;
+                if (v != v) r = 0.0f;
+                else r = idx < split ? rintf(v) : roundf(v);
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                word |= static_cast<uint32_t>(static_cast<uint8_t>(static_cast<int8_t>(static_cast<int>(r)))) << (8 * t);
+            }
+            tile[cl][gl] = word;
+        }
+    }
+    __syncthreads();
+    const int px = threadIdx.x >> 2;        // output 0..63 of the block
+    const int ch = (threadIdx.x & 3) * 16;  // first of the 16 channels this thread stores
+    const int p = blockIdx.x * 64 + px;
+    if (p >= OHW) return;
+    const int oh = p / OW;
+    const int ow = p - oh * OW;
+    uint32_t w[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int b = 0; b < 4; b++)
+            word |= ((tile[ch + 4 * d + b][px >> 2] >> (8 * (px & 3))) & 0xffu) << (8 * b);
+        w[d] = word;
+    }
+    int8_t *dst = xq + ((static_cast<size_t>(img) * Hp + oh + pt) * Wp + ow + pl) * Cp + blockIdx.y * 64 + ch;
+    *reinterpret_cast<uintx4 *>(dst) = uintx4{w[0], w[1], w[2], w[3]};
 }
 
 // reference pool/avgpool.c:21-45: mean over the in-bounds taps
@@ -616,13 +691,55 @@ static int pool_args(Spkv2Context *ctx, const Spkv2NodeRecord *node, PoolArgs *p
     return 0;
 }
 
+static bool is_pool3s2_x4(const PoolArgs &p) {
+    return p.kh == 3 && p.kw == 3 && p.sh == 2 && p.sw == 2 && p.ph == 1 && p.pw == 1 && p.W % 8 == 0 &&
+           p.W == 2 * p.OW && p.H == 2 * p.OH && p.OW % 4 == 0;
+}
+
+void pool_plan_free(void *p) {
+    // q_out belongs to the first consuming conv
+    delete static_cast<PoolPlan *>(p);
+}
+
+// A MaxPool that the fused pooling + int8 quantization kernel can run gets a
+// PoolPlan, which an int8 conv reading its output fills in at its own
+// prepare (the conv nodes come later in the node table).
+int maxpool_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
+    *ws = 0;
+    void **slot = &ctx->node_cache[node->id];
+    if (*slot) return 0;
+    PoolArgs p;
+    if (pool_args(ctx, node, &p) != 0) return 0;  // the run reports it
+    if (rec(ctx, node->inputs[0])->dtype != SPKV2_DTYPE_FP32 || !is_pool3s2_x4(p) || p.C % 64 != 0 || p.N < 1 || p.N > 65535 ||
+        static_cast<int64_t>(p.N) * p.C * p.H * p.W * 4 >= (int64_t(1) << 31))
+        return 0;
+    PoolPlan *plan = new PoolPlan();
+    memset(plan, 0, sizeof(*plan));
+    *slot = plan;
+    ctx->node_cache_dtors[node->id] = pool_plan_free;
+    return 0;
+}
+
 int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     PoolArgs p;
     if (int rc = pool_args(ctx, node, &p)) return rc;
     const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
     if (total == 0) return 0;
-    if (p.kh == 3 && p.kw == 3 && p.sh == 2 && p.sw == 2 && p.ph == 1 && p.pw == 1 && p.W % 8 == 0 &&
-        p.W == 2 * p.OW && p.H == 2 * p.OH && p.OW % 4 == 0) {
+    // int8 handoff, unless a fault event may change the fp32 output after
+    // this node ran (then the consumers quantize it themselves)
+    const PoolPlan *q = ctx->node_cache_dtors[node->id] == pool_plan_free
+                            ? static_cast<const PoolPlan *>(ctx->node_cache[node->id])
+                            : nullptr;
+    if (q && q->q_out && !ctx->fault_event.enabled && is_pool3s2_x4(p) && p.C % 64 == 0) {
+        set_kernel_name(ctx, node, q->y_needed ? "maxpool3s2_q8+y" : "maxpool3s2_q8");
+        const dim3 grid(static_cast<unsigned>((p.OH * p.OW + 63) / 64), static_cast<unsigned>(p.C / 64),
+                        static_cast<unsigned>(p.N));
+        hipLaunchKernelGGL(maxpool3s2_q8, grid, dim3(256), 0, ctx->stream, p.x, q->y_needed ? p.y : nullptr, q->q_out,
+                           p.C, p.H, p.W, p.OH, p.OW, q->q_Hp, q->q_Wp, q->q_Cp, q->q_pt, q->q_pl, q->q_inv_scale,
+                           q->q_split);
+        return launch_status("maxpool");
+    }
+    if (is_pool3s2_x4(p)) {
         set_kernel_name(ctx, node, "maxpool3s2_x4");
         const size_t groups = static_cast<size_t>(p.OH) * (p.OW / 4), planes = static_cast<size_t>(p.N) * p.C;
         if (groups > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;

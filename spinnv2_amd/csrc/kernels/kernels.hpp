@@ -32,6 +32,7 @@ int unary_run(Spkv2Context *, const Spkv2NodeRecord *, void *);   // Relu Sigmoi
 int copy_run(Spkv2Context *, const Spkv2NodeRecord *, void *);    // Flatten Reshape Cast Unsqueeze
 int concat_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int maxpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
+int maxpool_prepare(Spkv2Context *, const Spkv2NodeRecord *, size_t *);
 int avgpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int global_avgpool_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int softmax_run(Spkv2Context *, const Spkv2NodeRecord *, void *);

@@ -81,7 +81,9 @@ const Entry kBuiltins[] = {
     EW(SPKV2_OP_SIGMOID, unary_run),
     EW(SPKV2_OP_CLIP, unary_run),
     EW(SPKV2_OP_LEAKYRELU, unary_run),
-    EW(SPKV2_OP_MAXPOOL, maxpool_run),
+    E(SPKV2_OP_MAXPOOL, SPKV2_BACKEND_MI355X, SPKV2_KERNEL_DEVICE_ELEMENTWISE, maxpool_run, maxpool_prepare),
+    E(SPKV2_OP_MAXPOOL, SPKV2_BACKEND_SIMD, SPKV2_KERNEL_REFERENCE, maxpool_run, maxpool_prepare),
+    E(SPKV2_OP_MAXPOOL, SPKV2_BACKEND_REF, SPKV2_KERNEL_REFERENCE, maxpool_run, maxpool_prepare),
     EW(SPKV2_OP_AVERAGEPOOL, avgpool_run),
     EW(SPKV2_OP_GLOBALAVGPOOL, global_avgpool_run),
     EW(SPKV2_OP_SOFTMAX, softmax_run),

@@ -520,6 +520,78 @@ def test_int8_shared_handoff_skips_unread_fp32(gpu):
     np.testing.assert_array_equal(back, sentinel)  # the fp32 tensor was not rewritten
 
 
+def _int8_pool_consumers(shape, cout, third, pool_out):
+    """int8 conv + Relu -> MaxPool 3x3/2 pad 1 -> a 1x1 int8 conv and a 1x1
+    stride-2 int8 conv (the same quantization), plus `third`: None, or a 3x3
+    pad-1 int8 conv (another padded layout, so it reads the fp32 tensor);
+    pool_out also makes the pooled tensor a graph output."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    p = models.Params(9)
+    g = Graph("i8pool")
+    x = g.input("x", shape)
+    h = g.relu(g.conv(x, p.he((cout, shape[1], 3, 3)), p.normal(cout, 0.01), pad=1))
+    q = g.maxpool(h, 3, 2, 1)
+    g.mark_output(g.conv(q, p.he((40, cout, 1, 1)), p.normal(40, 0.01)))
+    g.mark_output(g.conv(q, p.he((24, cout, 1, 1)), None, stride=2))
+    if third:
+        g.mark_output(g.conv(q, p.he((16, cout, 3, 3)), p.normal(16, 0.01), pad=1))
+    if pool_out:
+        g.mark_output(q)
+    run_default_pipeline(g)
+    xs = rng_inputs(g)
+    qp = calibrate_activation_scales(g, [[models.make_input(shape, 800 + i)] for i in range(3)])
+    return g, xs, write_spk(g, "mi355x", quant_params=qp + quantize_conv_weights(g))
+
+
+# (input shape, pooled channels, 3x3 reader, pooled tensor is an output):
+# planes of 192 outputs (3 blocks of 64), 120 (a partial last block) and 32
+# (less than one block); one and two 64-channel blocks
+POOL_CASES = [([2, 16, 24, 32], 64, False, False), ([1, 16, 20, 24], 128, True, False),
+              ([2, 8, 24, 32], 64, False, True), ([1, 8, 8, 16], 64, False, False)]
+
+
+@pytest.mark.parametrize("handoff", ["1", "0"])
+@pytest.mark.parametrize("case", range(len(POOL_CASES)))
+def test_int8_maxpool_handoff_bit_exact(gpu, monkeypatch, case, handoff):
+    """A MaxPool read by int8 convs quantizes its output for them in the
+    pooling kernel (fp32 written only where something else reads it):
+    every output bit-exact against the oracle, eager and with a fault event
+    armed (then the pool writes fp32 and each conv quantizes)."""
+    from spinnv2_amd.runtime import FaultEvent, Model
+
+    monkeypatch.setenv("SPKV2_I8_HANDOFF", handoff)
+    shape, cout, third, pool_out = POOL_CASES[case]
+    g, xs, blob = _int8_pool_consumers(shape, cout, third, pool_out)
+    want = run_oracle(blob, xs)
+    n_out = len(g.outputs)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = [m.get_output(i) for i in range(n_out)]
+        pool_name = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "MaxPool"][0]
+        names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+        m.set_input(0, xs[0])
+        m.run()
+        again = [m.get_output(i) for i in range(n_out)]
+        ev = FaultEvent(node_id=0, tensor_id=g.nodes[0].outputs[0], element_index=0, bit_index=0,
+                        invocation_index=1000, seed=0, enabled=1)
+        m.set_fault_event(ev)
+        m.set_input(0, xs[0])
+        m.run()
+        armed = [m.get_output(i) for i in range(n_out)]
+    if handoff == "1":
+        assert pool_name == ("maxpool3s2_q8+y" if third or pool_out else "maxpool3s2_q8"), pool_name
+        assert ",handoff" in names[1] and ",shared" in names[2], names
+    else:
+        assert pool_name == "maxpool3s2_x4", pool_name
+    for i, (a_, b_, c_, d_) in enumerate(zip(got, want, again, armed)):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}")
+        np.testing.assert_array_equal(c_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}, second run")
+        np.testing.assert_array_equal(d_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}, fault armed")
+
+
 @pytest.mark.parametrize("handoff", ["1", "0"])
 def test_int8_resnet50_matches_oracle(gpu, monkeypatch, handoff):
     """A whole INT8 ResNet-50 (32x32 input), every conv int8: logits within
