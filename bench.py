@@ -256,7 +256,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     return out
 
 
-def yolo_v10n(lib, steps: int, node_report: bool = False, eager: bool = False) -> dict:
+def yolo_v10n(lib, steps: int, node_report: bool = False, eager: bool = False, batches=(1, 16)) -> dict:
     """YOLOv10n-style detector at 640x640, batch 1 and
     16: images/s from HIP-graph replays of the node loop (the whole YOLO op
     set on the device: C2f Split/Concat, SPPF, PSA MatMul + Softmax, Resize,
@@ -268,7 +268,7 @@ def yolo_v10n(lib, steps: int, node_report: bool = False, eager: bool = False) -
     from spinnv2_amd.spk import models, write_spk
 
     out = {"workload": "yolov10n_640"}
-    for batch in (1, 16):
+    for batch in batches:
         g = models.yolo_v10n(batch)
         m = Model(write_spk(g, "mi355x"), lib=lib)
         x = models.make_input(g.tensors[g.inputs[0]].shape)
@@ -363,6 +363,8 @@ def main() -> None:
     ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound op section")
     ap.add_argument("--no-yolo", action="store_true", help="skip the YOLOv10n section")
     ap.add_argument("--yolo-only", action="store_true", help="run only the YOLOv10n section")
+    ap.add_argument("--yolo-batch", type=int, choices=(1, 16), default=None,
+                    help="with --yolo-only: only this batch (a profile of one shape)")
     ap.add_argument("--elementwise-only", action="store_true", help="run only the memory-bound op section")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
@@ -383,7 +385,8 @@ def main() -> None:
         print(json.dumps(elementwise(lib)), flush=True)
         return
     if args.yolo_only:
-        print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report, args.eager)), flush=True)
+        batches = (args.yolo_batch,) if args.yolo_batch else (1, 16)
+        print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report, args.eager, batches)), flush=True)
         return
     if args.int8_only:
         print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
