@@ -1163,9 +1163,9 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     if (p->workspace > 0 && !wsb) return SPKV2_E_UNSUPPORTED;
     const float *xs = x;
     int x_bytes = static_cast<int>(g.x_elems * 4);
-    // a fault event may change a tensor after its producer ran: then every
-    // tensor is materialized and padded here
-    const bool handoff = !ctx->fault_event.enabled;
+    // with the handoffs not live (a fault event armed, or the kernel registry
+    // changed since prepare) every tensor is materialized and padded here
+    const bool handoff = handoffs_live(ctx);
     if (p->padded && p->pad_in && handoff) {
         xs = p->pad_in;  // written, zero halo included, by the producer's epilogue
         x_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.C * p->Hp * p->Wp * 4);

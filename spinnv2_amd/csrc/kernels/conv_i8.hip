@@ -1008,9 +1008,9 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     int32_t *part = reinterpret_cast<int32_t *>(wsb + plan->pad_bytes);
     const float inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
 
-    // a fault event may change the fp32 input after its producer ran: then
-    // every tensor is materialized and quantized here
-    const bool handoff = !ctx->fault_event.enabled;
+    // with the handoffs not live (a fault event armed, or the kernel registry
+    // changed since prepare) every tensor is materialized and quantized here
+    const bool handoff = handoffs_live(ctx);
     if ((plan->q_in || plan->q_shared) && handoff) {
         xq = plan->q_in ? plan->q_in : plan->q_shared;  // written by the producer's epilogue
     } else if (L.Cp <= 16) {

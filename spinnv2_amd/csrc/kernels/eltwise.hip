@@ -725,12 +725,13 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     if (int rc = pool_args(ctx, node, &p)) return rc;
     const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
     if (total == 0) return 0;
-    // int8 handoff, unless a fault event may change the fp32 output after
-    // this node ran (then the consumers quantize it themselves)
+    // int8 handoff while the handoffs are live (no fault event armed, the
+    // kernel registry as at prepare); otherwise the consumers quantize the
+    // fp32 output themselves
     const PoolPlan *q = ctx->node_cache_dtors[node->id] == pool_plan_free
                             ? static_cast<const PoolPlan *>(ctx->node_cache[node->id])
                             : nullptr;
-    if (q && q->q_out && !ctx->fault_event.enabled && is_pool3s2_x4(p) && p.C % 64 == 0) {
+    if (q && q->q_out && handoffs_live(ctx) && is_pool3s2_x4(p) && p.C % 64 == 0) {
         set_kernel_name(ctx, node, q->y_needed ? "maxpool3s2_q8+y" : "maxpool3s2_q8");
         const dim3 grid(static_cast<unsigned>((p.OH * p.OW + 63) / 64), static_cast<unsigned>(p.C / 64),
                         static_cast<unsigned>(p.N));

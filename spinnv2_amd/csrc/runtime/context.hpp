@@ -84,6 +84,9 @@ struct Spkv2Context {
     hipGraphExec_t graph_exec = nullptr;
     uint64_t binding_epoch = 1;  // bumped by every bind_*
     uint64_t graph_epoch = 0;    // binding_epoch the graph was captured at
+    // registry_generation() when the nodes were prepared: the handoffs set up
+    // then assume the built-in kernels run every producer and consumer
+    uint32_t prepared_generation = 0;
     bool profiling = false;
     std::vector<hipEvent_t> ev_begin, ev_end;
     std::vector<double> node_ms;
@@ -96,6 +99,19 @@ namespace spk {
 int execute_node(Spkv2Context *ctx, const Spkv2NodeRecord *node);
 int prepare_node(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *workspace_bytes);
 const Spkv2KernelSpecRecord *spec_by_id(const Spkv2Context *ctx, uint32_t id);
+// Bumped by every spkv2_register_kernel / spkv2_clear_user_kernels.
+uint32_t registry_generation();
+
+// Whether the prepare-time handoffs (a producer writing its consumer's padded
+// or int8 input) are in force for this run: not while a fault event is armed
+// (a fault may change a tensor after its producer ran), nor once the kernel
+// registry has changed since prepare (a user kernel may now run a producer or
+// consumer in place of the built-in that the handoff relies on).  When they
+// are not, every producer writes its output and every consumer reads it, as
+// the reference does.
+inline bool handoffs_live(const Spkv2Context *ctx) {
+    return !ctx->fault_event.enabled && ctx->prepared_generation == registry_generation();
+}
 void set_last_error(const char *what, hipError_t err);
 void set_last_error_text(const std::string &text);
 int hip_check(hipError_t err, const char *what);

@@ -418,6 +418,7 @@ extern "C" int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t
         if (int rc = alloc_zeroed(reinterpret_cast<uint8_t **>(&ctx->dev_flag), 4 * sizeof(uint32_t), ctx->stream))
             return rc;
         size_t workspace = 0;
+        ctx->prepared_generation = spk::registry_generation();
         for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
             size_t ws = 0;
             int rc = spk::prepare_node(ctx, &ctx->node_records[i], &ws);
@@ -509,7 +510,7 @@ extern "C" int spkv2_run(Spkv2Context *ctx) {
     for (uint32_t i = 0; i < ctx->header.num_tensors; i++)
         if (ctx->tensor_records[i].role != SPKV2_ROLE_WEIGHT && !ctx->tensors[i].data) return -5;
     const bool can_graph =
-        ctx->graph_mode && !ctx->profiling && !ctx->fault_event.enabled && ctx->protection_count == 0;
+        ctx->graph_mode && !ctx->profiling && spk::handoffs_live(ctx) && ctx->protection_count == 0;
     if (can_graph) return run_graph(ctx);
     return run_eager(ctx);
 }

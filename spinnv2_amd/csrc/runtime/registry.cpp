@@ -13,6 +13,7 @@
 // (backend, kind) triple, so packages compiled for cpu_ref / cpu_generic /
 // cpu_arm_neon run on the GPU unchanged, and the final (ref, reference)
 // fallback is a device kernel too.  No node ever runs on the CPU.
+#include <atomic>
 #include <cstring>
 
 #include "../kernels/kernels.hpp"
@@ -39,6 +40,7 @@ struct UserEntry {
 };
 UserEntry g_user[kUserMax];
 int g_user_count = 0;
+std::atomic<uint32_t> g_generation{0};
 
 #define E(op, be, kind, run, prep) {op, be, kind, 0, run, prep}
 using namespace spk::kern;
@@ -182,6 +184,8 @@ int prepare_with_spec(Spkv2Context *ctx, const Spkv2NodeRecord *node, const Spkv
 
 namespace spk {
 
+uint32_t registry_generation() { return g_generation.load(std::memory_order_relaxed); }
+
 const Spkv2KernelSpecRecord *spec_by_id(const Spkv2Context *ctx, uint32_t id) {
     if (id == 0xFFFFFFFFu || id >= ctx->spec_count) return nullptr;
     return &ctx->spec_records[id];
@@ -227,7 +231,11 @@ extern "C" int spkv2_register_kernel(uint16_t op_type, uint16_t backend, uint16_
     if (!fn) return -1;
     if (g_user_count >= kUserMax) return -2;
     g_user[g_user_count++] = UserEntry{op_type, backend, kernel_kind, priority, fn};
+    g_generation.fetch_add(1, std::memory_order_relaxed);
     return 0;
 }
 
-extern "C" void spkv2_clear_user_kernels(void) { g_user_count = 0; }
+extern "C" void spkv2_clear_user_kernels(void) {
+    g_user_count = 0;
+    g_generation.fetch_add(1, std::memory_order_relaxed);
+}

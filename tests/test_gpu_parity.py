@@ -592,6 +592,56 @@ def test_int8_maxpool_handoff_bit_exact(gpu, monkeypatch, case, handoff):
         np.testing.assert_array_equal(d_.view(np.uint32), b_.view(np.uint32), err_msg=f"output {i}, fault armed")
 
 
+def test_int8_handoffs_off_after_registry_change(gpu):
+    """A MaxPool kernel registered after prepare runs in place of the built-in
+    pooling kernel, which alone writes the int8 handoff: the consumers then
+    quantize the fp32 tensor the user kernel wrote (not a stale handoff
+    buffer), and every output stays exact; after the registry is cleared the
+    built-ins run without handoffs, still exact."""
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk import format as F
+
+    lib = gpu
+    shape = [2, 8, 24, 32]
+    g, xs, blob = _int8_pool_consumers(shape, 64, False, True)  # the pooled tensor is the last output
+    xb = [models.make_input(shape, 4242)]
+    want_a, want_b = run_oracle(blob, xs), run_oracle(blob, xb)
+    pooled_b = np.ascontiguousarray(want_b[-1], np.float32)
+    calls = []
+    kernel_fn = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)
+    node_outputs = 4 + 2 * 4 + 8 * 4  # byte offset of outputs[0] in Spkv2NodeRecord
+
+    def pool_b(ctx, node, scratch):
+        calls.append(1)
+        out = lib.spkv2_ctx_tensor_data(ctx, ctypes.c_uint32.from_address(node + node_outputs).value)
+        return lib.spkv2_device_memcpy_h2d(out, pooled_b.ctypes.data, pooled_b.nbytes)
+
+    k = kernel_fn(pool_b)
+    n_out = len(g.outputs)
+    try:
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            got_a = [m.get_output(i) for i in range(n_out)]
+            assert m.kernel_name([n.id for n in g.nodes if n.op_type == "MaxPool"][0]) == "maxpool3s2_q8+y"
+            assert lib.spkv2_register_kernel(F.OP["MaxPool"], F.BACKEND["mi355x"], F.KIND["device_elementwise"],
+                                             ctypes.cast(k, ctypes.c_void_p), 0) == 0
+            m.set_input(0, xb[0])
+            m.run()
+            got_b = [m.get_output(i) for i in range(n_out)]
+            lib.spkv2_clear_user_kernels()
+            m.set_input(0, xs[0])
+            m.run()
+            got_a2 = [m.get_output(i) for i in range(n_out)]
+    finally:
+        lib.spkv2_clear_user_kernels()
+    assert len(calls) == 1
+    for i in range(n_out):
+        np.testing.assert_array_equal(got_a[i].view(np.uint32), want_a[i].view(np.uint32), err_msg=f"A {i}")
+        np.testing.assert_array_equal(got_b[i].view(np.uint32), want_b[i].view(np.uint32), err_msg=f"B {i}")
+        np.testing.assert_array_equal(got_a2[i].view(np.uint32), want_a[i].view(np.uint32), err_msg=f"A2 {i}")
+
+
 @pytest.mark.parametrize("handoff", ["1", "0"])
 def test_int8_resnet50_matches_oracle(gpu, monkeypatch, handoff):
     """A whole INT8 ResNet-50 (32x32 input), every conv int8: logits within
