@@ -114,9 +114,9 @@ def pmc_traffic(name: str = "conv_igemm_f32_resnet101_b64_traffic.txt") -> dict 
     return vals or None
 
 
-def batch1_latency(depth: int, steps: int, lib) -> float:
-    """Batch-1 latency: ms per spkv2_run of a HIP-graph-captured node loop,
-    input already resident on the device."""
+def batch1_latency(depth: int, steps: int, lib, eager: bool = False) -> float:
+    """Batch-1 latency: ms per spkv2_run of a HIP-graph-captured node loop
+    (the plain node loop with eager), input already resident on the device."""
     from spinnv2_amd.runtime import DeviceBuffer, Model
     from spinnv2_amd.spk import models, write_spk
 
@@ -126,7 +126,7 @@ def batch1_latency(depth: int, steps: int, lib) -> float:
     x1buf = DeviceBuffer(x1.nbytes, lib)
     x1buf.upload(x1)
     m1.bind_input(0, x1buf)
-    m1.set_graph_mode(True)
+    m1.set_graph_mode(not eager)
     for _ in range(5):
         m1.run()
     lib.spkv2_device_synchronize()
@@ -242,7 +242,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
         b1 = DeviceBuffer(x1.nbytes, lib)
         b1.upload(x1)
         m1.bind_input(0, b1)
-        m1.set_graph_mode(True)
+        m1.set_graph_mode(not eager)
         for _ in range(5):
             m1.run()
         lib.spkv2_device_synchronize()
@@ -483,7 +483,7 @@ def main() -> None:
     conv_tflops = conv_flops / (conv_ms * 1e-3) / 1e12
 
     # ---------------------------------------------------------- batch 1
-    b1_ms = batch1_latency(args.depth, args.b1_steps, lib) if args.b1_steps > 0 else None
+    b1_ms = batch1_latency(args.depth, args.b1_steps, lib, args.eager) if args.b1_steps > 0 else None
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
     ew = None if args.no_elementwise else elementwise(lib)

@@ -93,6 +93,13 @@ int spkv2_mi355x_node_kernel_name(Spkv2Context *ctx, uint32_t node_id, char *buf
  * accumulators, laid out [N][Cout][OH][OW], to host memory `out`.
  * Call after spkv2_run.  size must be N*Cout*OH*OW*4. */
 int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t node_id, int32_t *out, size_t size);
+/* 1: from the next spkv2_run on, every INT8 convolution node also stores its
+ * raw int32 accumulators (from the very input the run quantized, handed-off
+ * or not) into a device buffer of its own, which
+ * spkv2_mi355x_conv_int8_accumulators then returns instead of re-running the
+ * node; 0 frees the buffers.  Allocates one N*Cout*OH*OW*4-byte buffer per
+ * INT8 conv node when enabled. */
+int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable);
 
 #ifdef __cplusplus
 }

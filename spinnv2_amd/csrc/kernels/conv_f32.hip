@@ -1209,8 +1209,9 @@ static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, Con
                 if (n->outputs[k] == t) prod = n;
     }
     if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
-    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
-    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
+    if (!builtin_runs(ctx, prod->id) || !builtin_runs(ctx, node->id)) return 0;  // a user kernel runs one end
+    if (ctx->plan_dtors[prod->id] != conv_plan_free) return 0;
+    ConvPlan *pp = static_cast<ConvPlan *>(ctx->plans[prod->id]);
     if (!pp || pp->path != CONV_IGEMM_F32 || pp->pad_out) return 0;
     const ConvGeom &g = plan->g;
     if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
@@ -1274,7 +1275,7 @@ static int run_direct(Spkv2Context *ctx, const Spkv2NodeRecord *node, const Conv
 int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     ConvGeom g;
     if (int rc = read_conv_geom(ctx, node, &g)) return rc;
-    void **slot = &ctx->node_cache[node->id];
+    void **slot = &ctx->plans[node->id];
     if (*slot) {
         const ConvPlan *p = static_cast<ConvPlan *>(*slot);
         *ws = p->ws_in_scratch ? 0 : p->workspace;
@@ -1284,7 +1285,7 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     memset(plan, 0, sizeof(*plan));
     plan->g = g;
     *slot = plan;
-    ctx->node_cache_dtors[node->id] = conv_plan_free;
+    ctx->plan_dtors[node->id] = conv_plan_free;
     int rc = 0;
     if (g.w_dtype == SPKV2_DTYPE_INT8) {
         rc = conv_i8_prepare(ctx, node, plan);
@@ -1309,7 +1310,8 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
 
 int conv_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratch) {
     (void)scratch;
-    ConvPlan *plan = static_cast<ConvPlan *>(ctx->node_cache[node->id]);
+    if (ctx->plan_dtors[node->id] != conv_plan_free) return SPKV2_E_UNSUPPORTED;  // not prepared as a conv
+    ConvPlan *plan = static_cast<ConvPlan *>(ctx->plans[node->id]);
     if (!plan) return SPKV2_E_UNSUPPORTED;  // prepare did not run for this node
     switch (plan->path) {
     case CONV_IGEMM_F32:
@@ -1333,7 +1335,8 @@ int conv_direct_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratc
 }
 
 int conv_int8_accumulators(Spkv2Context *ctx, const Spkv2NodeRecord *node, int32_t *dev_out) {
-    ConvPlan *plan = static_cast<ConvPlan *>(ctx->node_cache[node->id]);
+    if (ctx->plan_dtors[node->id] != conv_plan_free) return SPKV2_E_UNSUPPORTED;
+    ConvPlan *plan = static_cast<ConvPlan *>(ctx->plans[node->id]);
     if (!plan || plan->path != CONV_IGEMM_I8) return SPKV2_E_UNSUPPORTED;
     return conv_i8_run(ctx, node, plan, dev_out);
 }

@@ -879,6 +879,7 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
                 if (n->outputs[k] == t) prod = n;
     }
     if (!prod || prod->output_count != 1) return 0;
+    if (!builtin_runs(ctx, prod->id) || !builtin_runs(ctx, node->id)) return 0;  // a user kernel runs one end
     bool is_output = false;
     for (size_t i = 0; i < ctx->output_count; i++)
         if (ctx->output_ids[i] == t) is_output = true;
@@ -886,14 +887,14 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
     if (prod->op_type == SPKV2_OP_MAXPOOL) {
         // prepared by the built-in MaxPool as a fused pooling + quantization
         // candidate: 64-channel blocks, 16-byte pixel stores
-        if (ctx->node_cache_dtors[prod->id] != pool_plan_free) return 0;
-        PoolPlan *pp = static_cast<PoolPlan *>(ctx->node_cache[prod->id]);
+        if (ctx->plan_dtors[prod->id] != pool_plan_free) return 0;
+        PoolPlan *pp = static_cast<PoolPlan *>(ctx->plans[prod->id]);
         if (!pp || L.Cp != g.C || g.C % 64 != 0) return 0;
         return join_handoff(pp, plan, L, readers, is_output);
     }
     if (prod->op_type != SPKV2_OP_CONV) return 0;
-    if (ctx->node_cache_dtors[prod->id] != conv_plan_free) return 0;
-    ConvPlan *pp = static_cast<ConvPlan *>(ctx->node_cache[prod->id]);
+    if (ctx->plan_dtors[prod->id] != conv_plan_free) return 0;
+    ConvPlan *pp = static_cast<ConvPlan *>(ctx->plans[prod->id]);
     if (!pp || pp->path != CONV_IGEMM_I8) return 0;
     if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
     return join_handoff(pp, plan, L, readers, is_output);
@@ -1049,7 +1050,12 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
         a.q_inv = plan->q_inv_scale;
         if (!plan->y_needed) a.y = nullptr;
     }
-    return launch_i8(ctx->stream, plan->cfg, tc, a, part, raw_acc_out);
+    if (int rc = launch_i8(ctx->stream, plan->cfg, tc, a, part, raw_acc_out)) return rc;
+    // accumulator capture: the same GEMM again on the same quantized input,
+    // storing the raw int32 sums (the outputs above are already written)
+    if (!raw_acc_out && node->id < ctx->acc_capture.size() && ctx->acc_capture[node->id])
+        return launch_i8(ctx->stream, plan->cfg, tc, a, part, ctx->acc_capture[node->id]);
+    return 0;
 }
 
 }  // namespace spk::kern

@@ -706,7 +706,7 @@ void pool_plan_free(void *p) {
 // prepare (the conv nodes come later in the node table).
 int maxpool_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     *ws = 0;
-    void **slot = &ctx->node_cache[node->id];
+    void **slot = &ctx->plans[node->id];
     if (*slot) return 0;
     PoolArgs p;
     if (pool_args(ctx, node, &p) != 0) return 0;  // the run reports it
@@ -716,7 +716,7 @@ int maxpool_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) 
     PoolPlan *plan = new PoolPlan();
     memset(plan, 0, sizeof(*plan));
     *slot = plan;
-    ctx->node_cache_dtors[node->id] = pool_plan_free;
+    ctx->plan_dtors[node->id] = pool_plan_free;
     return 0;
 }
 
@@ -728,8 +728,8 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     // int8 handoff while the handoffs are live (no fault event armed, the
     // kernel registry as at prepare); otherwise the consumers quantize the
     // fp32 output themselves
-    const PoolPlan *q = ctx->node_cache_dtors[node->id] == pool_plan_free
-                            ? static_cast<const PoolPlan *>(ctx->node_cache[node->id])
+    const PoolPlan *q = ctx->plan_dtors[node->id] == pool_plan_free
+                            ? static_cast<const PoolPlan *>(ctx->plans[node->id])
                             : nullptr;
     if (q && q->q_out && handoffs_live(ctx) && is_pool3s2_x4(p) && p.C % 64 == 0) {
         set_kernel_name(ctx, node, q->y_needed ? "maxpool3s2_q8+y" : "maxpool3s2_q8");

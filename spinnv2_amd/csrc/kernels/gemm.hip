@@ -145,7 +145,7 @@ __global__ void __launch_bounds__(256) matmul_mfma(MatmulArgs p) {
 }  // namespace
 
 int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
-    void **slot = &ctx->node_cache[node->id];
+    void **slot = &ctx->plans[node->id];
     if (*slot) {
         const ConvPlan &p = static_cast<GemmPlan *>(*slot)->conv;
         *ws = p.ws_in_scratch ? 0 : p.workspace;
@@ -162,7 +162,7 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     GemmPlan *gp = new GemmPlan();
     memset(gp, 0, sizeof(*gp));
     *slot = gp;
-    ctx->node_cache_dtors[node->id] = gemm_plan_free;
+    ctx->plan_dtors[node->id] = gemm_plan_free;
     gp->rows = attr.trans_a ? ar->shape[1] : ar->shape[0];
     gp->K = attr.trans_a ? ar->shape[0] : ar->shape[1];
     gp->Nout = attr.trans_b ? br->shape[0] : br->shape[1];
@@ -198,7 +198,8 @@ int run_igemm_f32_strided(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
                           float alpha, int x_img_stride);
 
 int gemm_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
-    GemmPlan *gp = static_cast<GemmPlan *>(ctx->node_cache[node->id]);
+    if (ctx->plan_dtors[node->id] != gemm_plan_free) return SPKV2_E_UNSUPPORTED;  // not prepared as a Gemm
+    GemmPlan *gp = static_cast<GemmPlan *>(ctx->plans[node->id]);
     if (!gp) return SPKV2_E_UNSUPPORTED;
     const float *a = dptr<const float>(ctx, node->inputs[0]);
     const float *c = node->input_count > 2 ? dptr<const float>(ctx, node->inputs[2]) : nullptr;

@@ -67,8 +67,17 @@ struct Spkv2Context {
 
     // per-node state
     size_t node_count = 0;
+    // the per-node cache slots of the kernel ABI (reference context.h:46-48),
+    // owned by whatever kernel runs the node: third-party kernels reach them
+    // through spkv2_ctx_node_cache
     void **node_cache = nullptr;
     void (**node_cache_dtors)(void *) = nullptr;
+    // the built-in device kernels' per-node plans (packed weights, tile and
+    // split choice, handoff buffers), kept apart from node_cache so that a
+    // user kernel winning a node at run time, or answering -99, never meets a
+    // foreign object, and a built-in fallback always finds its plan
+    std::vector<void *> plans;
+    std::vector<void (*)(void *)> plan_dtors;
     std::vector<std::string> node_kernel_names;
 
     // ---- reliability (reference executor.c:335-498) ----
@@ -84,13 +93,22 @@ struct Spkv2Context {
     hipGraphExec_t graph_exec = nullptr;
     uint64_t binding_epoch = 1;  // bumped by every bind_*
     uint64_t graph_epoch = 0;    // binding_epoch the graph was captured at
-    // registry_generation() when the nodes were prepared: the handoffs set up
-    // then assume the built-in kernels run every producer and consumer
-    uint32_t prepared_generation = 0;
+    // the kernel that runs each node (the first spec of its chain with a
+    // registered kernel), as resolved at prepare; builtin_winner marks the
+    // nodes a built-in device kernel runs.  Handoffs are set up only between
+    // such nodes, and stay in force only while every node still resolves to
+    // the kernel it had at prepare (re-checked when the registry changes).
+    std::vector<Spkv2NodeKernelFn> winners;
+    std::vector<uint8_t> builtin_winner;
+    uint32_t checked_generation = 0;  // registry_generation() winners_match was computed at
+    bool winners_match = true;
     bool profiling = false;
     std::vector<hipEvent_t> ev_begin, ev_end;
     std::vector<double> node_ms;
     std::vector<uint32_t> node_runs;
+    // INT8 accumulator capture (test hook): per node, a device buffer that
+    // each run of an int8 conv fills with its raw int32 accumulators
+    std::vector<int32_t *> acc_capture;
 };
 
 // ---- internal helpers shared by the runtime translation units ----
@@ -101,17 +119,24 @@ int prepare_node(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *workspa
 const Spkv2KernelSpecRecord *spec_by_id(const Spkv2Context *ctx, uint32_t id);
 // Bumped by every spkv2_register_kernel / spkv2_clear_user_kernels.
 uint32_t registry_generation();
+// Re-resolves every node's kernel when the registry changed since the last
+// check, and sets ctx->winners_match to whether each node still resolves to
+// the kernel it had at prepare.
+void refresh_winners(Spkv2Context *ctx);
+
+// Whether a built-in device kernel was resolved to run this node at prepare.
+inline bool builtin_runs(const Spkv2Context *ctx, uint32_t node_id) {
+    return node_id < ctx->builtin_winner.size() && ctx->builtin_winner[node_id] != 0;
+}
 
 // Whether the prepare-time handoffs (a producer writing its consumer's padded
 // or int8 input) are in force for this run: not while a fault event is armed
-// (a fault may change a tensor after its producer ran), nor once the kernel
-// registry has changed since prepare (a user kernel may now run a producer or
-// consumer in place of the built-in that the handoff relies on).  When they
-// are not, every producer writes its output and every consumer reads it, as
-// the reference does.
-inline bool handoffs_live(const Spkv2Context *ctx) {
-    return !ctx->fault_event.enabled && ctx->prepared_generation == registry_generation();
-}
+// (a fault may change a tensor after its producer ran), nor while any node
+// resolves to another kernel than at prepare (a user kernel registered or
+// cleared since may now run a producer or consumer in place of the built-in
+// the handoff relies on).  When they are not, every producer writes its
+// output and every consumer reads it, as the reference does.
+inline bool handoffs_live(const Spkv2Context *ctx) { return !ctx->fault_event.enabled && ctx->winners_match; }
 void set_last_error(const char *what, hipError_t err);
 void set_last_error_text(const std::string &text);
 int hip_check(hipError_t err, const char *what);

@@ -418,7 +418,6 @@ extern "C" int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t
         if (int rc = alloc_zeroed(reinterpret_cast<uint8_t **>(&ctx->dev_flag), 4 * sizeof(uint32_t), ctx->stream))
             return rc;
         size_t workspace = 0;
-        ctx->prepared_generation = spk::registry_generation();
         for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
             size_t ws = 0;
             int rc = spk::prepare_node(ctx, &ctx->node_records[i], &ws);
@@ -509,6 +508,7 @@ extern "C" int spkv2_run(Spkv2Context *ctx) {
     if (ctx->invocations) memset(ctx->invocations, 0, ctx->node_count * sizeof(uint32_t));
     for (uint32_t i = 0; i < ctx->header.num_tensors; i++)
         if (ctx->tensor_records[i].role != SPKV2_ROLE_WEIGHT && !ctx->tensors[i].data) return -5;
+    spk::refresh_winners(ctx);
     const bool can_graph =
         ctx->graph_mode && !ctx->profiling && spk::handoffs_live(ctx) && ctx->protection_count == 0;
     if (can_graph) return run_graph(ctx);
@@ -720,6 +720,31 @@ extern "C" int spkv2_mi355x_node_kernel_name(Spkv2Context *ctx, uint32_t node_id
     return 0;
 }
 
+extern "C" int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable) {
+    if (!ctx) return -1;
+    if (!ctx->prepared) return SPKV2_E_NO_DEVICE;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    for (int32_t *&p : ctx->acc_capture) {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+    }
+    ctx->acc_capture.assign(ctx->node_count, nullptr);
+    ctx->binding_epoch++;  // a captured HIP graph holds the launches of the old setting
+    if (!enable) return 0;
+    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *node = &ctx->node_records[i];
+        if (node->op_type != SPKV2_OP_CONV || node->input_count < 2) continue;
+        if (ctx->tensor_records[node->inputs[1]].dtype != SPKV2_DTYPE_INT8) continue;
+        const size_t bytes = ctx->tensor_records[node->outputs[0]].size_bytes;
+        if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&ctx->acc_capture[node->id]), bytes),
+                               "hipMalloc accumulator capture"))
+            return rc;
+        if (int rc = hip_check(hipMemset(ctx->acc_capture[node->id], 0, bytes), "hipMemset")) return rc;
+    }
+    return 0;
+}
+
 extern "C" int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t node_id, int32_t *out, size_t size) {
     if (!ctx || !out || node_id >= ctx->node_count) return -1;
     if (!ctx->prepared) return SPKV2_E_NO_DEVICE;
@@ -727,6 +752,11 @@ extern "C" int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t n
     if (node->op_type != SPKV2_OP_CONV) return -1;
     const Spkv2TensorRecord *y = &ctx->tensor_records[node->outputs[0]];
     if (size != y->size_bytes) return -2;
+    if (node_id < ctx->acc_capture.size() && ctx->acc_capture[node_id]) {
+        // captured during the last spkv2_run
+        if (int rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return rc;
+        return hip_check(hipMemcpy(out, ctx->acc_capture[node_id], size, hipMemcpyDeviceToHost), "hipMemcpy");
+    }
     int32_t *dev = nullptr;
     if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&dev), size), "hipMalloc")) return rc;
     int rc = spk::kern::conv_int8_accumulators(ctx, node, dev);

@@ -153,6 +153,8 @@ void destroy(Spkv2Context *ctx) {
             else spkv2_platform_free(ctx->node_cache[i]);
         }
     }
+    for (size_t i = 0; i < ctx->plans.size(); i++)
+        if (ctx->plans[i] && ctx->plan_dtors[i]) ctx->plan_dtors[i](ctx->plans[i]);
     if (ctx->prepared || ctx->stream) {
         (void)hipSetDevice(ctx->device);
         if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
@@ -165,6 +167,8 @@ void destroy(Spkv2Context *ctx) {
         if (ctx->weights_dev) (void)hipFree(ctx->weights_dev);
         if (ctx->dev_minmax) (void)hipFree(ctx->dev_minmax);
         if (ctx->dev_flag) (void)hipFree(ctx->dev_flag);
+        for (int32_t *p : ctx->acc_capture)
+            if (p) (void)hipFree(p);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     }
     spkv2_platform_free(ctx->node_cache);
@@ -283,6 +287,8 @@ extern "C" int spkv2_load_memory(const void *data, size_t size, Spkv2Context **o
             static_cast<Spkv2RangeObservation *>(spkv2_platform_calloc(ctx->node_count, sizeof(Spkv2RangeObservation)));
         if (!ctx->node_cache || !ctx->node_cache_dtors || !ctx->invocations || !ctx->ranges) return fail(-1);
         ctx->node_kernel_names.resize(ctx->node_count);
+        ctx->plans.assign(ctx->node_count, nullptr);
+        ctx->plan_dtors.assign(ctx->node_count, nullptr);
         ctx->node_ms.assign(ctx->node_count, 0.0);
         ctx->node_runs.assign(ctx->node_count, 0);
     }

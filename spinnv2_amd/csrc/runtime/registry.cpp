@@ -170,14 +170,37 @@ int execute_with_spec(Spkv2Context *ctx, const Spkv2NodeRecord *node, const Spkv
     return f.fn(ctx, node, scratch);
 }
 
-// Prepare mirrors execute: the first spec in the chain whose kernel exists
-// and whose prepare step accepts the node is the one prepared.
+const Entry *find_builtin(uint16_t op, const Spkv2KernelSpecRecord *spec) {
+    for (const Entry &e : kBuiltins)
+        if (e.op == op && e.backend == spec->backend && e.kind == spec->kernel_kind) return &e;
+    return nullptr;
+}
+
+// Prepare walks the chain over the built-in table only: the first spec with a
+// built-in kernel whose prepare step accepts the node is prepared, whether or
+// not a user kernel wins that spec.  A user kernel that answers -99, or is
+// cleared after prepare, then hands the node to a built-in that has its plan
+// and its workspace.
 int prepare_with_spec(Spkv2Context *ctx, const Spkv2NodeRecord *node, const Spkv2KernelSpecRecord *spec,
                       size_t *ws) {
+    const Entry *b = find_builtin(node->op_type, spec);
+    if (!b) return -99;
+    return b->prepare ? b->prepare(ctx, node, ws) : 0;
+}
+
+// The kernel execute_node would call first for this node: the winner of the
+// first spec in the chain that has one.
+Found resolve(const Spkv2Context *ctx, const Spkv2NodeRecord *node) {
+    Spkv2KernelSpecRecord ref_storage;
+    const Spkv2KernelSpecRecord *spec = selected_spec(ctx, node, &ref_storage);
     Found f = find_kernel(node->op_type, spec);
-    if (!f.fn) return -99;
-    if (f.builtin && f.builtin->prepare) return f.builtin->prepare(ctx, node, ws);
-    return 0;
+    if (f.fn) return f;
+    if (const Spkv2KernelSpecRecord *fb = spk::spec_by_id(ctx, spec->fallback_kernel_spec_id)) {
+        f = find_kernel(node->op_type, fb);
+        if (f.fn) return f;
+    }
+    Spkv2KernelSpecRecord ref = ref_spec_for(node->id);
+    return find_kernel(node->op_type, &ref);
 }
 
 }  // namespace
@@ -209,7 +232,28 @@ int execute_node(Spkv2Context *ctx, const Spkv2NodeRecord *node) {
     return execute_with_spec(ctx, node, &ref);
 }
 
+void refresh_winners(Spkv2Context *ctx) {
+    const uint32_t gen = registry_generation();
+    if (gen == ctx->checked_generation) return;
+    bool match = true;
+    for (uint32_t i = 0; i < ctx->header.num_nodes && match; i++)
+        match = i < ctx->winners.size() && resolve(ctx, &ctx->node_records[i]).fn == ctx->winners[i];
+    ctx->winners_match = match;
+    ctx->checked_generation = gen;
+}
+
 int prepare_node(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
+    if (ctx->winners.size() != ctx->node_count) {
+        ctx->winners.assign(ctx->node_count, nullptr);
+        ctx->builtin_winner.assign(ctx->node_count, 0);
+        ctx->checked_generation = registry_generation();
+        ctx->winners_match = true;
+    }
+    // recorded before the node's prepare step, which may set up a handoff
+    // with an earlier node when the built-ins run both
+    const Found w = resolve(ctx, node);
+    ctx->winners[node->id] = w.fn;
+    ctx->builtin_winner[node->id] = w.builtin != nullptr;
     Spkv2KernelSpecRecord ref_storage;
     const Spkv2KernelSpecRecord *spec = selected_spec(ctx, node, &ref_storage);
     int rc = prepare_with_spec(ctx, node, spec, ws);

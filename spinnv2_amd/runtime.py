@@ -98,6 +98,7 @@ SIGNATURES = {
     "spkv2_mi355x_reset_node_times": (None, [VP]),
     "spkv2_mi355x_node_kernel_name": (I, [VP, U32, ctypes.c_char_p, SZ]),
     "spkv2_mi355x_conv_int8_accumulators": (I, [VP, U32, VP, SZ]),
+    "spkv2_mi355x_set_int8_capture": (I, [VP, I]),
 }
 
 _LIB = None
@@ -239,6 +240,11 @@ class Model:
         buf = ctypes.create_string_buffer(128)
         _check(self.lib, self.lib.spkv2_mi355x_node_kernel_name(self.ctx, node_id, buf, 128), "kernel name")
         return buf.value.decode()
+
+    def set_int8_capture(self, on: bool) -> None:
+        """Every later run also keeps each INT8 conv's raw int32 accumulators
+        (read back with int8_accumulators)."""
+        _check(self.lib, self.lib.spkv2_mi355x_set_int8_capture(self.ctx, 1 if on else 0), "int8 capture")
 
     def int8_accumulators(self, node_id: int, nbytes: int) -> np.ndarray:
         out = np.empty(nbytes // 4, dtype=np.int32)

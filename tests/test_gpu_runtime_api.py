@@ -159,3 +159,105 @@ def test_conv_over_2gib_is_refused(gpu):
     with pytest.raises(RuntimeError_) as e:
         Model(blob)
     assert e.value.code == -32
+
+
+def test_user_conv_kernel_before_prepare_then_cleared(gpu):
+    """A user Conv kernel registered before prepare wins the conv nodes; the
+    built-in plans are prepared anyway (apart from the user's node_cache
+    slot), so when the user kernel answers -99 the built-in runs the node,
+    and after the registry is cleared the built-ins run every node: both
+    equal the oracle.  No handoff is set up with a node a user kernel runs."""
+    from spinnv2_amd.runtime import Model
+    from tests.helpers import FP32_TOL, rng_inputs, run_oracle, tnorm_err
+
+    lib = gpu
+    g = models.resnet(50, 1, image=64, classes=10)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    want = run_oracle(blob, xs)[0]
+    calls = []
+    objects = {}
+
+    def refuse(ctx, node, scratch):
+        calls.append(1)
+        # the user owns the ABI node_cache slot: keep an object of its own
+        # there (freed by the runtime with spkv2_platform_free, no destructor)
+        slot = ctypes.c_void_p()
+        nid = ctypes.c_uint32.from_address(node).value
+        assert lib.spkv2_ctx_node_cache(ctx, nid, ctypes.addressof(slot), None) == 0
+        if not ctypes.c_void_p.from_address(slot.value).value:
+            obj = lib.spkv2_platform_malloc(64)
+            ctypes.memset(obj, 0x5A, 64)
+            ctypes.c_void_p.from_address(slot.value).value = obj
+            objects[nid] = obj
+        return -99
+
+    k = KERNEL_FN(refuse)
+    try:
+        lib.spkv2_clear_user_kernels()
+        assert lib.spkv2_register_kernel(F.OP["Conv"], F.BACKEND["mi355x"], F.KIND["implicit_gemm_f32"],
+                                         ctypes.cast(k, ctypes.c_void_p), 5) == 0
+        with Model(blob) as m:
+            names = [m.kernel_name(n.id) for n in g.nodes if n.op_type == "Conv"]
+            assert not any("+handoff" in s for s in names), names
+            for mode in (False, True):
+                m.set_graph_mode(mode)
+                m.set_input(0, xs[0])
+                m.run()
+                assert tnorm_err(m.get_output(0), want) <= FP32_TOL
+            assert len(calls) == 2 * len(names)
+            lib.spkv2_clear_user_kernels()
+            for mode in (False, True):
+                m.set_graph_mode(mode)
+                m.set_input(0, xs[0])
+                m.run()
+                assert tnorm_err(m.get_output(0), want) <= FP32_TOL
+            assert len(calls) == 2 * len(names)
+            # the slots still hold the user's objects, untouched by the built-ins
+            assert len(objects) == len(names)
+            for nid, obj in objects.items():
+                slot = ctypes.c_void_p()
+                assert lib.spkv2_ctx_node_cache(m.ctx, nid, ctypes.addressof(slot), None) == 0
+                assert ctypes.c_void_p.from_address(slot.value).value == obj
+                assert ctypes.string_at(obj, 64) == b"\x5a" * 64
+    finally:
+        lib.spkv2_clear_user_kernels()
+
+
+def test_register_then_clear_restores_handoffs_and_graph(gpu):
+    """Registering a kernel for an op no node uses leaves every node's kernel
+    as at prepare: handoffs and HIP-graph replay stay on, bit-identical to
+    before; a MaxPool kernel that does take a node turns them off until the
+    registry is cleared again."""
+    from spinnv2_amd.runtime import Model
+    from tests.helpers import rng_inputs
+
+    lib = gpu
+    g = models.resnet(50, 2, image=64, classes=10)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    k = _fill_kernel(lib, 7.0)
+    try:
+        lib.spkv2_clear_user_kernels()
+        with Model(blob) as m:
+            m.set_graph_mode(True)
+            m.set_input(0, xs[0])
+            m.run()
+            base = m.get_output(0)
+            assert lib.spkv2_register_kernel(F.OP["TopK"], F.BACKEND["mi355x"], F.KIND["device_elementwise"],
+                                             ctypes.cast(k, ctypes.c_void_p), 0) == 0
+            m.set_input(0, xs[0])
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0), base)
+            assert lib.spkv2_register_kernel(F.OP["MaxPool"], F.BACKEND["mi355x"], F.KIND["device_elementwise"],
+                                             ctypes.cast(k, ctypes.c_void_p), 0) == 0
+            m.set_input(0, xs[0])
+            m.run()
+            assert not np.array_equal(m.get_output(0), base)  # the pooled tensor is all 7.0 now
+            lib.spkv2_clear_user_kernels()
+            for _ in range(2):
+                m.set_input(0, xs[0])
+                m.run()
+                np.testing.assert_array_equal(m.get_output(0), base)
+    finally:
+        lib.spkv2_clear_user_kernels()
