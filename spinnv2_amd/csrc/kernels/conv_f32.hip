@@ -23,6 +23,8 @@
 // ds_read_b128 per operand row feeds four MFMA k-steps: lanes 0-31 supply
 // k = 8j+s and lanes 32-63 k = 8j+4+s for step s, the same mapping for A and
 // B, so every k is summed exactly once.
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -769,19 +771,19 @@ std::mutex g_tune_mu;
 std::map<std::string, std::pair<int, int>> g_tuned;  // key -> (cfg, split request), fp32 and int8 layers
 bool g_tune_db_loaded = false;
 
-// SPKV2_TUNE_DB names a text file of "key cfg split" lines: read once, and
-// every newly tuned shape is appended, so later processes reuse the
-// choices (same configuration, same results) without timing again.
+// Tune tables are text files of "key cfg split" lines.  mi355x.tune beside
+// the library holds the choices for the benchmark networks' layer shapes
+// (read-only), so every process picks the same tiles and split-K for them
+// and their fp32 results are bit-reproducible across processes.
+// SPKV2_TUNE_DB names a file of the caller's: read after it (its entries
+// win), and every newly tuned shape is appended, so later processes reuse
+// those choices without timing again.
 const char *tune_db_path() {
     const char *p = getenv("SPKV2_TUNE_DB");
     return p && p[0] ? p : nullptr;
 }
 
-void load_tune_db_locked() {
-    if (g_tune_db_loaded) return;
-    g_tune_db_loaded = true;
-    const char *path = tune_db_path();
-    if (!path) return;
+void load_tune_file_locked(const char *path) {
     FILE *f = fopen(path, "r");
     if (!f) return;
     char key[512];
@@ -791,6 +793,21 @@ void load_tune_db_locked() {
         if (cfg >= 0 && cfg < 64 && ((split >= 1 && split <= 64) || (split >= 1002 && split <= 1064)))
             g_tuned[key] = {cfg, split};
     fclose(f);
+}
+
+void load_tune_db_locked() {
+    if (g_tune_db_loaded) return;
+    g_tune_db_loaded = true;
+    const char *use_table = getenv("SPKV2_TUNE_TABLE");  // "0": ignore the built-in table (to regenerate it)
+    Dl_info info;
+    if (!(use_table && use_table[0] == '0') && dladdr(reinterpret_cast<void *>(&load_tune_file_locked), &info) &&
+        info.dli_fname) {
+        std::string dir(info.dli_fname);
+        const size_t slash = dir.rfind('/');
+        dir = slash == std::string::npos ? std::string(".") : dir.substr(0, slash);
+        load_tune_file_locked((dir + "/mi355x.tune").c_str());
+    }
+    if (const char *path = tune_db_path()) load_tune_file_locked(path);
 }
 
 void store_tune_db_locked(const std::string &key, int cfg, int split) {
@@ -944,9 +961,18 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
         (void)hipGetLastError();
         return false;
     }
-    *cfg_out = keep[0].cfg;
-    *split_out = keep[0].split;
-    tuned_store(gs.key, keep[0].cfg, keep[0].split);
+    // timings within 2% of the fastest are a tie, broken by the model (then
+    // the candidate order), not by the noise of this process's measurement
+    size_t pick = 0;
+    for (size_t i = 1; i < finalists; i++)
+        if (keep[i].t <= keep[0].t * 1.02 &&
+            (keep[i].model < keep[pick].model ||
+             (keep[i].model == keep[pick].model &&
+              std::make_pair(keep[i].cfg, keep[i].split) < std::make_pair(keep[pick].cfg, keep[pick].split))))
+            pick = i;
+    *cfg_out = keep[pick].cfg;
+    *split_out = keep[pick].split;
+    tuned_store(gs.key, keep[pick].cfg, keep[pick].split);
     return true;
 }
 

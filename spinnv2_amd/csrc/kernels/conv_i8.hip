@@ -175,13 +175,14 @@ __device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even)
     return static_cast<int>(r);
 }
 
-template <int BM, int BN, int BK>
+template <int BM, int BN, int BK, int BMAP>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int TM = BM / 64, TN = BN / 64;  // 2x2 waves, each (32*TM) x (32*TN)
     constexpr int LDK = BK + 16;               // bytes per LDS row
     constexpr int GPT = BK * BN / 4096;        // 16-byte B groups per thread per k-tile
     constexpr int APT = BM * BK / 4096;        // 16-byte A chunks per thread per k-tile
     static_assert(TM >= 1 && TN >= 1 && GPT >= 1 && APT >= 1 && BK % 32 == 0, "tile shape");
+    static_assert(BMAP == 0 || BN % (4096 / BK) == 0, "BMAP 1: whole pixel passes");
     __shared__ __attribute__((aligned(16))) int8_t As[2][BM * LDK];
     __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * LDK];
 
@@ -201,20 +202,35 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     const int kt0 = blockIdx.y * a.kt_per_split;
     const int kt1 = min(kt0 + a.kt_per_split, a.k_tiles);
 
-    const int bcol = tid % BN;
-    const int bgrp = __builtin_amdgcn_readfirstlane(tid / BN);  // wave-uniform: BN >= 64
     const __amdgpu_buffer_rsrc_t xrs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(a.xq), static_cast<short>(0), a.x_bytes, kBufWord3);
-    int col = kOob;
-    {
-        const int n = nt * BN + bcol;
-        if (n < a.Ntot) {
-            const int img = n / a.OHW;
-            const int sp = n - img * a.OHW;
-            const int oh = sp / a.OW;
-            const int ow = sp - oh * a.OW;
-            col = img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
-        }
+    // byte offset of output column n's receptive-field origin in xq
+    auto col_of = [&](int n) -> int {
+        if (n >= a.Ntot) return kOob;
+        const int img = n / a.OHW;
+        const int sp = n - img * a.OHW;
+        const int oh = sp / a.OW;
+        const int ow = sp - oh * a.OW;
+        return img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
+    };
+    // B gather, two lane maps:
+    //  BMAP 0: lane = column n, one wave-uniform k group per load (koff[g] in
+    //          the scalar offset) -- any K layout, but the 64 lanes of a load
+    //          touch 64 pixels Cp bytes apart;
+    //  BMAP 1: lane = (pixel, k group), groups fastest, so 8 lanes read 128
+    //          contiguous bytes of one pixel -- for layers whose BK/16 groups
+    //          of a k-tile are contiguous in xq (the tile's base offset in the
+    //          scalar offset, the group's 16-byte step in the lane offset).
+    constexpr int G = BK / 16;       // 16-byte k groups per tile
+    constexpr int PPP = 256 / G;     // pixels per pass of the whole workgroup (BMAP 1)
+    const int bcol = BMAP ? (tid / G) : (tid % BN);
+    const int bgrp = BMAP ? (tid % G) : __builtin_amdgcn_readfirstlane(tid / BN);  // wave-uniform for BMAP 0
+    int colp[BMAP ? GPT : 1];
+    if constexpr (BMAP) {
+#pragma unroll
+        for (int p = 0; p < GPT; p++) colp[p] = col_of(nt * BN + p * PPP + bcol) + bgrp * 16;
+    } else {
+        colp[0] = col_of(nt * BN + bcol);
     }
 
     intx4 ar0[APT], ar1[APT], br0[GPT], br1[GPT];
@@ -226,9 +242,15 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt_) * (BM * BK));        \
         _Pragma("unroll") for (int i = 0; i < APT; i++) AR[i] = src[tid + i * 256];                                  \
         /* the table has two tiles of out-of-range entries past the last */                                       \
-        const int *ko = a.koff + (KT) * (BK / 16) + bgrp * GPT;                                                      \
-        _Pragma("unroll") for (int g = 0; g < GPT; g++) BR[g] =                                                      \
-            __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, col, ko[g], 0));                    \
+        if constexpr (BMAP) {                                                                                        \
+            const int kbase = a.koff[(KT) * G];                                                                      \
+            _Pragma("unroll") for (int p = 0; p < GPT; p++) BR[p] =                                                  \
+                __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, colp[p], kbase, 0));            \
+        } else {                                                                                                     \
+            const int *ko = a.koff + (KT) * G + bgrp * GPT;                                                          \
+            _Pragma("unroll") for (int g = 0; g < GPT; g++) BR[g] =                                                  \
+                __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, colp[0], ko[g], 0));            \
+        }                                                                                                            \
     }
 
 #define I8_STORE_TILE(BUF, AR, BR)                                                                                   \
@@ -237,8 +259,13 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             const int f = (tid + i * 256) * 16;                                                                      \
             *reinterpret_cast<intx4 *>(&As[BUF][(f / BK) * LDK + (f % BK)]) = AR[i];                                 \
         }                                                                                                             \
-        _Pragma("unroll") for (int g = 0; g < GPT; g++) * reinterpret_cast<intx4 *>(                                 \
-            &Bs[BUF][bcol * LDK + (bgrp * GPT + g) * 16]) = BR[g];                                                   \
+        if constexpr (BMAP) {                                                                                        \
+            _Pragma("unroll") for (int p = 0; p < GPT; p++) * reinterpret_cast<intx4 *>(                             \
+                &Bs[BUF][(p * PPP + bcol) * LDK + bgrp * 16]) = BR[p];                                               \
+        } else {                                                                                                     \
+            _Pragma("unroll") for (int g = 0; g < GPT; g++) * reinterpret_cast<intx4 *>(                             \
+                &Bs[BUF][bcol * LDK + (bgrp * GPT + g) * 16]) = BR[g];                                               \
+        }                                                                                                            \
     }
 
 #define I8_COMPUTE(BUF)                                                                                              \
@@ -511,16 +538,21 @@ using I8Kernel = void (*)(I8Args);
 
 struct I8Cfg {
     int BM, BN, BK;
+    int bmap;  // B gather lane map (see conv_igemm_i8)
     const char *name;
     I8Kernel kernel;
 };
 
-#define I8CFG(BM, BN, BK) {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK>}
+#define I8CFG(BM, BN, BK) {BM, BN, BK, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0>}
+#define I8CFGP(BM, BN, BK) {BM, BN, BK, 1, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1>}
 const I8Cfg kI8Cfgs[] = {
-    I8CFG(128, 128, 64), I8CFG(128, 128, 128), I8CFG(128, 64, 64), I8CFG(128, 64, 128),
-    I8CFG(64, 128, 64),  I8CFG(64, 64, 64),    I8CFG(64, 64, 128),
+    I8CFG(128, 128, 64),  I8CFG(128, 128, 128),  I8CFG(128, 64, 64),  I8CFG(128, 64, 128),
+    I8CFG(64, 128, 64),   I8CFG(64, 64, 64),     I8CFG(64, 64, 128),
+    I8CFGP(128, 128, 64), I8CFGP(128, 128, 128), I8CFGP(128, 64, 64), I8CFGP(128, 64, 128),
+    I8CFGP(64, 128, 64),  I8CFGP(64, 64, 64),    I8CFGP(64, 64, 128),
 };
 #undef I8CFG
+#undef I8CFGP
 constexpr int kNumI8Cfgs = sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]);
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -547,6 +579,17 @@ I8Layout i8_layout(const ConvGeom &g) {
     L.Hp = std::max(g.H + g.ph, hspan);
     L.Wp = std::max(g.W + g.pw, wspan);
     return L;
+}
+
+// Whether configuration c can run a layer: the BMAP 1 gather needs the
+// BK/16 groups of every k-tile contiguous in xq, i.e. no tile crosses from
+// one kernel row (or tap) to the next.  A tile past the last group reads
+// memory beyond the layer's K, which meets zero weights.
+bool i8_cfg_fits(const I8Layout &L, int c) {
+    const I8Cfg &t = kI8Cfgs[c];
+    if (!t.bmap) return true;
+    const int G = t.BK / 16;
+    return L.run_groups % G == 0 || L.groups == L.run_groups;
 }
 
 // byte offset of group q relative to the window origin in padded NHWC
@@ -721,6 +764,7 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     std::vector<Cand> cands;
     double best = 1e300;
     for (int c = 0; c < kNumI8Cfgs; c++) {
+        if (!i8_cfg_fits(L, c)) continue;
         int last = -1;
         for (int s : kI8Splits) {
             const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
@@ -930,6 +974,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
         double best = 1e300;
         for (int c = 0; c < kNumI8Cfgs; c++)
             for (int s : kI8Splits) {
+                if (!i8_cfg_fits(L, c)) break;
                 const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
                 if (s > 1 && tc.kt_per_split < 2) break;
                 const double m = i8_model_us(c, tc, g.M, Ntot);
@@ -942,7 +987,13 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     }
     if (const char *e = getenv("SPKV2_I8_CFG")) {
         const int c = atoi(e);
-        if (c >= 0 && c < kNumI8Cfgs) cfg = c;
+        if (c >= 0 && c < kNumI8Cfgs) {
+            if (!i8_cfg_fits(L, c)) {
+                set_last_error_text("SPKV2_I8_CFG names a configuration whose gather this layer's K layout does not allow");
+                return SPKV2_E_UNSUPPORTED;
+            }
+            cfg = c;
+        }
     }
     if (const char *e = getenv("SPKV2_I8_SPLITK")) {
         const int s = atoi(e);

@@ -1,6 +1,6 @@
 """Digests rocprofv3 CSV output into the short text summaries kept in profiles/.
 
-    python -m spinnv2_amd.rocprof_summary stats   <kernel_stats.csv> --runs N
+    python -m spinnv2_amd.rocprof_summary stats   <kernel_stats.csv> --runs N [--match conv_igemm_i8]
     python -m spinnv2_amd.rocprof_summary traffic --fetch <pmc.csv> --write <pmc.csv>
            --copy-fetch <pmc.csv> --copy-write <pmc.csv> --copy-bytes B --runs N --match conv_igemm
     python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
@@ -36,7 +36,7 @@ def short_name(name: str) -> str:
     return re.sub(r"\(.*\)$", "", name)
 
 
-def stats(path: str, runs: int) -> str:
+def stats(path: str, runs: int, match: str | None = None) -> str:
     rows = list(csv.DictReader(open(path)))
     total = sum(float(r["TotalDurationNs"]) for r in rows)
     out = [f"{'kernel':48s} {'calls/run':>9s} {'avg us':>9s} {'ms/run':>9s} {'share':>7s}"]
@@ -45,6 +45,13 @@ def stats(path: str, runs: int) -> str:
         out.append(f"{short_name(r['Name'])[:48]:48s} {int(r['Calls']) / runs:9.1f} {float(r['AverageNs']) / 1e3:9.2f} "
                    f"{t / runs / 1e6:9.3f} {100 * t / total:6.1f}%")
     out.append(f"{'all kernels':48s} {'':9s} {'':9s} {total / runs / 1e6:9.3f}")
+    if match:
+        sel = [r for r in rows if match in r["Name"]]
+        ms = sum(float(r["TotalDurationNs"]) for r in sel) / runs / 1e6
+        calls = sum(int(r["Calls"]) for r in sel) / runs
+        out.append("")
+        out.append(f"result {match}_ms_per_run = {ms:.6f}")
+        out.append(f"result {match}_calls_per_run = {calls:.1f}")
     return "\n".join(out)
 
 
@@ -150,6 +157,7 @@ def main() -> None:
     s = sub.add_parser("stats")
     s.add_argument("csv")
     s.add_argument("--runs", type=int, required=True)
+    s.add_argument("--match", default=None, help="also total the kernels whose name contains this")
     t = sub.add_parser("traffic")
     for k in ("fetch", "write", "copy_fetch", "copy_write"):
         t.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
@@ -165,7 +173,8 @@ def main() -> None:
     m.add_argument("--peak", type=float, default=157.3, help="T ops/s of the counted MFMA type (fp32: 157.3)")
     m.add_argument("--mops", default="SQ_INSTS_VALU_MFMA_MOPS_F32", help="MFMA work counter (units of 512 ops)")
     a = ap.parse_args()
-    print({"stats": lambda: stats(a.csv, a.runs), "traffic": lambda: traffic(a), "mfma": lambda: mfma(a)}[a.cmd]())
+    print({"stats": lambda: stats(a.csv, a.runs, a.match), "traffic": lambda: traffic(a),
+           "mfma": lambda: mfma(a)}[a.cmd]())
 
 
 if __name__ == "__main__":

@@ -171,14 +171,14 @@ class Graph:
     def reshape(self, x: int, shape) -> int:
         return self.node("Reshape", [x], [list(shape)])[0]
 
-    def gemm(self, a: int, b: np.ndarray, c: np.ndarray | None = None, *, alpha=1.0, beta=1.0, trans_b=0,
-             name=None) -> int:
-        rows = self.shape(a)[0]
+    def gemm(self, a: int, b: np.ndarray, c: np.ndarray | None = None, *, alpha=1.0, beta=1.0, trans_a=0,
+             trans_b=0, name=None) -> int:
+        rows = self.shape(a)[1] if trans_a else self.shape(a)[0]
         nout = b.shape[0] if trans_b else b.shape[1]
         ins = [a, self.weight(f"{name or 'fc'}_w{len(self.nodes)}", b)]
         if c is not None:
             ins.append(self.weight(f"{name or 'fc'}_b{len(self.nodes)}", c))
-        attrs = {"alpha": alpha, "beta": beta, "transB": trans_b}
+        attrs = {"alpha": alpha, "beta": beta, "transA": trans_a, "transB": trans_b}
         return self.node("Gemm", ins, [[rows, nout]], attrs, name)[0]
 
     def matmul(self, a: int, b: int) -> int:

@@ -1,10 +1,13 @@
 """KernelSpec selection per target profile.
 
-`cpu_generic` / `cpu_generic_nobnns` / `cpu_ref` reproduce the reference's
-choice of (backend, kind) for those profiles (compiler/planner/kernel_spec.py:
-71-224, compiler/target/profiles/cpu_generic.json), including its per-node
-scratch estimate (kernel_spec.py:240-298), so the reference runtime runs the
-packages as it would run its own compiler's output.
+`cpu_generic` / `cpu_generic_nobnns` / `cpu_ref` / `cpu_arm_neon` reproduce
+the reference's choice of (backend, kind) for those profiles
+(compiler/planner/kernel_spec.py:71-224, compiler/target/profiles/*.json),
+including its per-node scratch estimate (kernel_spec.py:240-298), so the
+reference runtime runs the packages as it would run its own compiler's
+output.  `cpu_arm_neon_exp` selects the two conv kinds the reference runtime
+dispatches but no reference profile emits (Winograd F(2,3), 3x3/s2 direct),
+so that packages carrying every conv kind code can be produced.
 
 `mi355x` is this backend's target, described by profiles/mi355x.json in the
 reference's profile schema (compiler/target/profiles/cpu_generic.json): each
@@ -50,6 +53,18 @@ PROFILES = {
     "cpu_generic_nobnns": {"name": "cpu_generic_nobnns", "backends": ["ref", "cpu", "simd"], "bnns": False,
                            "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
     "cpu_ref": {"name": "cpu_ref", "backends": ["ref"], "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
+    # the reference's ARM profile (compiler/target/profiles/cpu_arm_neon.json):
+    # Conv tokens int8, pointwise, depthwise, Winograd F(4,3), im2col
+    "cpu_arm_neon": {"name": "cpu_arm_neon", "backends": ["ref", "cpu", "simd"], "bnns": False,
+                     "conv_kinds": ["pointwise_1x1", "depthwise_direct", "winograd_f43"],
+                     "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
+    # the two conv kinds the reference runtime keeps (spkv2_format.h:130-131,
+    # kernels.c:75-77) but no reference profile selects: Winograd F(2,3) for
+    # 3x3/s1/p1 and the 3x3/s2/p1 direct conv; packages carrying them must
+    # still run unchanged
+    "cpu_arm_neon_exp": {"name": "cpu_arm_neon_exp", "backends": ["ref", "cpu", "simd"], "bnns": False,
+                         "conv_kinds": ["pointwise_1x1", "depthwise_direct", "winograd_3x3s1", "conv3x3s2_direct"],
+                         "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
 }
 
 
@@ -85,6 +100,11 @@ def _cpu_scratch(g: Graph, n: Node, kind: str, backend: str) -> int:
         k = x[1] * w[2] * w[3]
         spatial = y[2] * y[3]
         return _align(x[1] * x[2] * x[3] + k * spatial + w[0] * spatial * 4)
+    if kind in ("winograd_3x3s1", "winograd_f43"):
+        # transformed input and output tiles (reference kernel_spec.py:244-263)
+        side, alpha = (2, 16) if kind == "winograd_3x3s1" else (4, 36)
+        tiles = ((y[2] + side - 1) // side) * ((y[3] + side - 1) // side)
+        return _align(min(alpha * (x[1] + w[0]) * tiles * 4, SIMD_TILE_BYTES))
     if kind == "im2col_gemm":
         k = x[1] * w[2] * w[3]
         if backend == "simd":
@@ -107,7 +127,7 @@ def _mi355x_scratch(g: Graph, n: Node, kind: str) -> int:
             return 0
         a = g.tensors[n.inputs[0]].shape
         y = g.tensors[n.outputs[0]].shape
-        rows = a[1] if int(n.attrs.get("trans_a", 0)) else a[0]
+        rows = a[1] if int(n.attrs.get("transA", 0)) else a[0]
         return _align256(min(MI355X_MAX_SPLITK * int(y[-1]) * int(rows) * 4, MI355X_SPLITK_CAP))
     x, w, y = _conv_geometry(g, n)
     if int(n.attrs.get("group", 1)) != 1:
@@ -154,19 +174,41 @@ def _mi355x_specs(g: Graph, n: Node, prof: dict) -> list[Spec]:
     return out
 
 
-def _cpu_generic_conv_kind(g: Graph, n: Node, bnns: bool) -> str:
-    """reference kernel_spec.py:146-224 with the cpu_generic token list."""
+def _cpu_conv_kind(g: Graph, n: Node, prof: dict) -> str:
+    """reference kernel_spec.py:146-224: the first conv kind of the profile's
+    token list whose shape conditions the node meets (cpu_generic: bnns,
+    pointwise, depthwise; cpu_arm_neon: pointwise, depthwise, Winograd
+    F(4,3); the experimental list: F(2,3) and the 3x3/s2 direct conv),
+    else im2col."""
     x, w, y = _conv_geometry(g, n)
     group = int(n.attrs.get("group", 1))
     strides = list(n.attrs.get("strides", [1, 1]))
     pads = list(n.attrs.get("pads", [0, 0, 0, 0]))
     dil = list(n.attrs.get("dilations", [1, 1]))
-    if bnns and group == 1:
-        return "bnns_fp32"
-    if group == 1 and w[2] == 1 and w[3] == 1 and strides == [1, 1] and pads == [0, 0, 0, 0] and dil == [1, 1]:
-        return "pointwise_1x1"
-    if group == x[1] and group == w[0] and w[2] == 3 and w[3] == 3 and dil == [1, 1]:
-        return "depthwise_direct"
+    k3 = w[2] == 3 and w[3] == 3 and dil == [1, 1] and group == 1 and pads == [1, 1, 1, 1]
+    kinds = prof.get("conv_kinds", ["bnns_fp32", "pointwise_1x1", "depthwise_direct"])
+    for kind in kinds:
+        if kind == "bnns_fp32" and prof.get("bnns", True) and group == 1:
+            return kind
+        if (kind == "pointwise_1x1" and group == 1 and w[2] == 1 and w[3] == 1 and strides == [1, 1]
+                and pads == [0, 0, 0, 0] and dil == [1, 1]):
+            return kind
+        if kind == "depthwise_direct" and group == x[1] and group == w[0] and w[2] == 3 and w[3] == 3 and dil == [1, 1]:
+            return kind
+        if kind == "winograd_f43" and k3 and strides == [1, 1]:
+            oh, ow = y[2], y[3]
+            tiles = ((oh + 3) // 4) * ((ow + 3) // 4)
+            if (oh >= 8 and ow >= 8 and (x[1] >= 8 or w[0] >= 8) and tiles >= 4
+                    and 36 * (x[1] + w[0]) * tiles * 4 <= SIMD_TILE_BYTES):
+                return kind
+        # the reference's x86 kernels of these two kinds take no residual
+        # operand (optimized/conv/conv.c:1021-1048 pass none), so a conv with
+        # a fused residual keeps im2col
+        plain = len(n.inputs) < 4
+        if kind == "winograd_3x3s1" and k3 and plain and strides == [1, 1] and y[2] == x[2] and y[3] == x[3]:
+            return kind
+        if kind == "conv3x3s2_direct" and k3 and plain and strides == [2, 2]:
+            return kind
     return "im2col_gemm"
 
 
@@ -196,7 +238,7 @@ def select_kernel_specs(g: Graph, profile: str) -> tuple[list[Spec], dict[int, S
                 if int8 and int(n.attrs.get("group", 1)) == 1:
                     sel = Spec(0, n.id, "int8_im2col_gemm", "simd", "int8")
                 else:
-                    sel = Spec(0, n.id, _cpu_generic_conv_kind(g, n, prof.get("bnns", True)), "simd")
+                    sel = Spec(0, n.id, _cpu_conv_kind(g, n, prof), "simd")
             elif n.op_type in ("Gemm", "MatMul"):
                 sel = Spec(0, n.id, "direct", "simd")
             elif n.op_type in SIMD_REF_OPS:

@@ -151,12 +151,13 @@ def single_conv(n: int, cin: int, h: int, w: int, cout: int, k: int, stride: int
     return g
 
 
-def single_gemm(rows: int, k: int, nout: int, *, alpha=1.0, trans_b=0, bias=True, seed=DEFAULT_SEED) -> Graph:
+def single_gemm(rows: int, k: int, nout: int, *, alpha=1.0, trans_a=0, trans_b=0, bias=True,
+                seed=DEFAULT_SEED) -> Graph:
     p = Params(seed)
     g = Graph("gemm")
-    a = g.input("a", [rows, k])
+    a = g.input("a", [k, rows] if trans_a else [rows, k])
     b = p.he((nout, k)) if trans_b else p.he((nout, k)).T.copy()
-    y = g.gemm(a, b, p.normal(nout, 0.01) if bias else None, alpha=alpha, trans_b=trans_b)
+    y = g.gemm(a, b, p.normal(nout, 0.01) if bias else None, alpha=alpha, trans_a=trans_a, trans_b=trans_b)
     g.mark_output(y)
     return g
 
@@ -179,7 +180,7 @@ def single_op(op: str, shape, **kw) -> Graph:
             run_default_pipeline(g)
             g.mark_output(g.nodes[-1].outputs[0])
             return g
-    elif op in ("Mul", "Sub", "Div"):
+    elif op in ("Mul", "Sub", "Div", "Mod"):
         b = g.input("b", kw.get("b_shape", shape))
         y = g.binary(op, x, b)
     elif op == "Resize":

@@ -89,7 +89,8 @@ def forward_fp32(g: Graph, inputs: list[np.ndarray], want: set[int]) -> dict[int
                 y = x.reshape(g.shape(n.outputs[0]))
             elif n.op_type == "Gemm":
                 w = vals[n.inputs[1]]
-                y = a.get("alpha", 1.0) * (x @ (w.T if a.get("transB") else w))
+                xa = x.T if a.get("transA") else x
+                y = a.get("alpha", 1.0) * (xa @ (w.T if a.get("transB") else w))
                 if len(n.inputs) > 2:
                     y = y + vals[n.inputs[2]]
             elif n.op_type == "Softmax":

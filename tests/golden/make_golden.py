@@ -4,8 +4,10 @@ The reference runtime is compiled from its own sources under
 /root/reference/runtime into oracle/_ref/libspkv2_ref.so (`make -C oracle
 ref`); this script runs it on packages written by this repo's SPK writer with
 the `cpu_ref` profile (every node on the reference kernels,
-runtime/kernels/reference/*) and stores, per case, the builder call, the
-inputs and the reference runtime's output.  The fixtures are data only: the
+runtime/kernels/reference/*) -- or, for the `arm_*` cases, with the ARM
+profiles whose conv kinds its optimized x86 kernels run -- and stores, per
+case, the builder call, the profile, the inputs and the reference runtime's
+output.  The fixtures are data only: the
 tests re-create each package with the same builder call and compare the CPU
 oracle (and, on the GPU box, the MI355X runtime) against the stored output.
 
@@ -59,6 +61,9 @@ _GEMM = [
     dict(rows=4, k=33, nout=9, trans_b=1),
     dict(rows=3, k=7, nout=5, trans_b=1, alpha=2.0),
     dict(rows=2, k=3, nout=4, trans_b=1),
+    # transA (reference mm/gemm.c:17-31: A read as [K][rows])
+    dict(rows=5, k=33, nout=9, trans_a=1),
+    dict(rows=4, k=20, nout=7, trans_a=1, trans_b=1, alpha=0.5),
 ]
 for i, kw in enumerate(_GEMM):
     CASES.append((f"gemm{i}", "single_gemm", kw, "normal"))
@@ -81,9 +86,31 @@ _OPS = [
     ("Mul", [2, 8, 4, 4], dict(b_shape=[8, 1, 1])),
     ("Sub", [2, 3, 4], dict(b_shape=[4])),
     ("Div", [2, 3, 4], dict(b_shape=[3, 1])),
+    # Mod (reference math/binary.c:25-26: C remainder of the truncated
+    # operands); divisors kept at |b| >= 1 so the reference's int % never
+    # divides by zero
+    ("Mod", [2, 3, 4], dict(b_shape=[3, 1])),
 ]
 for i, (op, shape, kw) in enumerate(_OPS):
-    CASES.append((f"op{i}_{op}", "single_op", dict(op=op, shape=shape, **kw), "normal"))
+    CASES.append((f"op{i}_{op}", "single_op", dict(op=op, shape=shape, **kw), "mod" if op == "Mod" else "normal"))
+
+# Packages with the reference's optimized conv kinds, run by its x86 (AVX2)
+# kernels: the cpu_arm_neon profile's Winograd F(4,3) (kind 9) with a fused
+# residual, and the two kinds no reference profile selects but its runtime
+# dispatches (kernels.c:75-77): Winograd F(2,3) (kind 7) and the 3x3/s2
+# direct conv (kind 8); plus ResNet-18 at 64x64 under both ARM profiles.
+# Their outputs carry the Winograd / AVX2 rounding, so they pin within the
+# fp32 tolerance, not bit for bit.
+CASES.append(("arm_f43_conv", "single_conv",
+              dict(n=1, cin=32, h=12, w=12, cout=32, k=3, stride=1, pad=1, act="Relu", residual=True), "normal",
+              "cpu_arm_neon"))
+CASES.append(("arm_f23_conv", "single_conv", dict(n=2, cin=24, h=13, w=11, cout=40, k=3, stride=1, pad=1, act="Relu"),
+              "normal", "cpu_arm_neon_exp"))
+CASES.append(("arm_s2_conv", "single_conv", dict(n=2, cin=16, h=15, w=17, cout=24, k=3, stride=2, pad=1, act="Relu"),
+              "normal", "cpu_arm_neon_exp"))
+CASES.append(("arm_resnet18_64px", "resnet", dict(depth=18, batch=1, image=64, classes=10), "normal", "cpu_arm_neon"))
+CASES.append(("arm_exp_resnet18_64px", "resnet", dict(depth=18, batch=1, image=64, classes=10), "normal",
+              "cpu_arm_neon_exp"))
 
 # Indexing / layout ops of the YOLO op set (reference tensor/*.c, shape/tile.c,
 # shape/transpose.c).  Index tensors are constants; "ties" inputs are
@@ -151,6 +178,11 @@ def case_inputs(g, dist: str, seed: int = 42) -> list[np.ndarray]:
     if dist == "ties":  # values on a coarse grid: many exact ties
         return [np.round(models.make_input(g.tensors[t].shape, seed + i, "normal") * 2).astype(np.float32) / 2
                 for i, t in enumerate(g.inputs)]
+    if dist == "mod":  # dividend N(0, 20^2); divisor of magnitude in [1, 7.9), either sign
+        a = models.make_input(g.tensors[g.inputs[0]].shape, seed, "normal") * np.float32(20)
+        u = models.make_input(g.tensors[g.inputs[1]].shape, seed + 1, "uniform")
+        b = (np.floor(u * 7) + 1 + 0.9 * np.abs(np.sin(u * 97))) * np.where(u < 0.5, -1, 1)
+        return [a.astype(np.float32), b.astype(np.float32)]
     return [models.make_input(g.tensors[t].shape, seed + i, dist) for i, t in enumerate(g.inputs)]
 
 
@@ -158,18 +190,30 @@ def main() -> None:
     if not available():
         sys.exit("oracle/_ref/libspkv2_ref.so is not built: make -C oracle ref (needs /root/reference)")
     only = set(sys.argv[1:])
-    for name, builder, kw, dist in CASES:
+    for case in CASES:
+        name, builder, kw, dist = case[:4]
+        profile = case[4] if len(case) > 4 else "cpu_ref"
         if only and name not in only:
             continue
         g = build_graph(builder, kw)
-        blob = write_spk(g, "cpu_ref")
+        blob = write_spk(g, profile)
         xs = case_inputs(g, dist)
         ref = RefModel(blob)
         ys = [ref.run(*xs, output=o) for o in range(len(g.outputs))]
         ref.close()
         y = ys[0]
-        meta = {"builder": builder, "kwargs": kw, "dist": dist, "seed": 42, "profile": "cpu_ref",
-                "source": "reference runtime (runtime/core + runtime/kernels/reference) built by oracle/Makefile"}
+        if profile != "cpu_ref" and name != "arm_s2_conv":
+            # a Winograd kernel, not the naive reference conv, ran: the bits
+            # differ (the 3x3/s2 direct kernel sums in the naive conv's order
+            # and matches it bit for bit)
+            naive = RefModel(write_spk(build_graph(builder, kw), "cpu_ref"))
+            y0 = naive.run(*xs)
+            naive.close()
+            assert not np.array_equal(y.view(np.uint32), y0.view(np.uint32)), name
+        meta = {"builder": builder, "kwargs": kw, "dist": dist, "seed": 42, "profile": profile,
+                "source": "reference runtime (runtime/core + runtime/kernels/reference"
+                          + (" + runtime/kernels/optimized, x86 AVX2" if profile != "cpu_ref" else "")
+                          + ") built by oracle/Makefile"}
         arrays = {f"x{i}": x for i, x in enumerate(xs)}
         arrays.update({f"y{o}": v for o, v in enumerate(ys) if o > 0})
         np.savez_compressed(HERE / f"{name}.npz", meta=np.frombuffer(json.dumps(meta).encode(), dtype=np.uint8),

@@ -17,7 +17,7 @@ GOLDEN = Path(__file__).resolve().parent / "golden"
 
 # ops whose reference kernels are a pure selection, copy or one IEEE add per
 # element: any correct restatement is bit-exact
-EXACT_BUILDER_OPS = {"MaxPool", "Add", "Relu", "Resize", "Sub", "Mul", "Div"}
+EXACT_BUILDER_OPS = {"MaxPool", "Add", "Relu", "Resize", "Sub", "Mul", "Div", "Mod"}
 
 
 @dataclass
@@ -28,6 +28,14 @@ class GoldenCase:
     inputs: list
     expected: np.ndarray        # graph output 0
     more: list | None = None    # graph outputs 1.. (multi-output ops)
+    profile: str = "cpu_ref"    # the profile of the package the reference ran
+
+    @property
+    def optimized(self) -> bool:
+        """The reference ran its optimized x86 kernels (Winograd, AVX2
+        im2col), whose rounding a restatement of the naive kernels matches
+        within the fp32 tolerance only."""
+        return self.profile != "cpu_ref"
 
     @property
     def all_expected(self) -> list:
@@ -56,5 +64,6 @@ def load_cases() -> list[GoldenCase]:
             meta = json.loads(bytes(z["meta"]).decode())
             xs = [z[f"x{i}"] for i in range(len([k for k in z.files if k.startswith("x")]))]
             more = [z[f"y{o}"] for o in range(1, 1 + len([k for k in z.files if k.startswith("y") and k != "y"]))]
-            cases.append(GoldenCase(p.stem, meta["builder"], meta["kwargs"], xs, z["y"], more))
+            cases.append(GoldenCase(p.stem, meta["builder"], meta["kwargs"], xs, z["y"], more,
+                                    meta.get("profile", "cpu_ref")))
     return cases

@@ -25,9 +25,18 @@ DETECTORS = {"yolov10n_160"}
 @pytest.mark.gpu
 @pytest.mark.parametrize("case", CASES, ids=[c.name for c in CASES])
 def test_mi355x_matches_reference_runtime(gpu, case):
+    """The mi355x package of every fixture; for the ARM-profile fixtures also
+    the very package the reference ran (conv kinds 7/8/9 and SIMD im2col
+    dispatched to the device kernels unchanged)."""
     print(f"[golden] {case.name}", flush=True)
-    blob = write_spk(case.graph(), "mi355x")
-    outs = run_gpu(blob, case.inputs, outputs=len(case.all_expected))
+    blobs = [write_spk(case.graph(), "mi355x")]
+    if case.optimized:
+        blobs.append(write_spk(case.graph(), case.profile))
+    for blob in blobs:
+        _check(case, run_gpu(blob, case.inputs, outputs=len(case.all_expected)))
+
+
+def _check(case, outs):
     if case.name in DETECTORS:
         check_detections(outs, case.all_expected)
         return
@@ -39,7 +48,7 @@ def test_mi355x_matches_reference_runtime(gpu, case):
         else:
             assert tnorm_err(got, want) <= FP32_TOL
     got = outs[0].ravel()
-    if case.name in NETWORKS:
+    if case.name in NETWORKS or case.builder == "resnet":
         rows = got.reshape(case.inputs[0].shape[0], -1)
         want = case.expected.reshape(rows.shape)
         assert (rows.argmax(axis=1) == want.argmax(axis=1)).all()

@@ -245,6 +245,33 @@ def test_int8_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert ("splitk=1>" in name) == (split == 1), name
 
 
+# Pixel-major gather configurations (7-13): every one on a 1x1 conv (one
+# kernel row: always eligible) and on a 3x3 conv with 64 channels (12 groups
+# per kernel row: eligible for BK = 64 only), with split-K, ragged M and N,
+# residual and Relu; ineligible forcings are refused.
+I8_PX = [(cfg, shape, split) for cfg in range(7, 14) for shape in ("1x1", "3x3") for split in (1, 3)]
+
+
+@pytest.mark.parametrize("cfg,shape,split", I8_PX, ids=[f"i8px{c}_{s}_split{k}" for c, s, k in I8_PX])
+def test_int8_pixel_gather_configs(gpu, monkeypatch, cfg, shape, split):
+    from spinnv2_amd.runtime import RuntimeError_
+
+    monkeypatch.setenv("SPKV2_I8_CFG", str(cfg))
+    monkeypatch.setenv("SPKV2_I8_SPLITK", str(split))
+    if shape == "1x1":
+        g = models.single_conv(3, 96, 9, 11, 70, 1, 1, 0, act="Relu", residual=True)
+    else:
+        g = models.single_conv(2, 64, 11, 13, 70, 3, 1, 1, act="Relu", residual=True)
+    bk = [64, 128, 64, 128, 64, 64, 128][cfg - 7]
+    if shape == "3x3" and bk == 128:
+        with pytest.raises(RuntimeError_) as e:
+            _int8_check(g)
+        assert e.value.code == -32
+        return
+    name = _int8_check(g)
+    assert ",px," in name, name
+
+
 def test_graph_mode_matches_eager(gpu):
     from spinnv2_amd.runtime import Model
 
@@ -333,13 +360,54 @@ def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
     assert tnorm_err(eager, want) <= FP32_TOL
 
 
-def _int8_network(depth=50, batch=2, image=32):
+def _int8_network(depth=50, batch=2, image=32, profile="mi355x"):
     g = models.resnet(depth, batch, image=image, classes=10)
     xs = rng_inputs(g)
     cal = models.resnet(depth, 1, image=image, classes=10)
     samples = [models.make_input(cal.tensors[cal.inputs[0]].shape, 1000 + i) for i in range(4)]
     qp = calibrate_activation_scales(cal, samples) + quantize_conv_weights(g)
-    return g, xs, write_spk(g, "mi355x", quant_params=qp)
+    return g, xs, write_spk(g, profile, quant_params=qp)
+
+
+def test_int8_cpu_generic_package_runs_on_gpu(gpu):
+    """An INT8 package as the reference compiler writes it for a CPU target:
+    every conv under (simd, int8_im2col_gemm) with a (ref, reference)
+    fallback (reference compiler/planner/kernel_spec.py:120-126) and the
+    CPU scratch estimate.  It runs unchanged on the device int8 kernels:
+    every conv's accumulators equal the oracle's, and the logits equal the
+    mi355x package's bit for bit."""
+    from oracle.spk_exec import OracleExecutor
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk import format as F
+    from spinnv2_amd.spk.kernel_spec import select_kernel_specs
+
+    g, xs, blob = _int8_network(profile="cpu_generic")
+    _, by_node, _ = select_kernel_specs(g, "cpu_generic")
+    convs = [n for n in g.nodes if n.op_type == "Conv"]
+    assert {(by_node[n.id].backend, F.KIND[by_node[n.id].kind]) for n in convs} == {("simd", 10)}
+    _, _, blob_mi = _int8_network()
+    ora = OracleExecutor(blob)
+    want = ora.run(xs[0])[0].ravel()
+    with Model(blob) as m:
+        m.set_int8_capture(True)
+        m.set_input(0, xs[0])
+        m.run()
+        got = m.get_output(0)
+        for n in convs:
+            np.testing.assert_array_equal(m.int8_accumulators(n.id, ora.acc[n.id].nbytes), ora.acc[n.id].ravel())
+            assert m.kernel_name(n.id).startswith("conv_igemm_i8"), m.kernel_name(n.id)
+    np.testing.assert_array_equal(got, run_gpu(blob_mi, xs)[0])
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+def test_gemm_trans_a_shapes(gpu):
+    """Gemm with transA (A read as [K][rows], reference mm/gemm.c:17-31) at
+    the FC shapes, alone and with transB and alpha."""
+    for rows, k, nout, tb, alpha in [(1, 2048, 1000, 0, 1.0), (64, 2048, 1000, 1, 1.0), (7, 130, 33, 1, 0.5)]:
+        g = models.single_gemm(rows, k, nout, trans_a=1, trans_b=tb, alpha=alpha)
+        blob = write_spk(g, "mi355x")
+        xs = rng_inputs(g)
+        assert tnorm_err(run_gpu(blob, xs)[0], run_oracle(blob, xs)[0]) <= FP32_TOL, (rows, k, nout, tb)
 
 
 def _int8_chain():

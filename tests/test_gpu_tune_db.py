@@ -43,6 +43,42 @@ def _child(db: Path) -> dict:
     return json.loads(out.stdout.strip().splitlines()[-1])
 
 
+NETWORK_CHILD = r"""
+import hashlib, json, sys
+sys.path.insert(0, %r)
+from spinnv2_amd.runtime import Model
+from spinnv2_amd.spk import models, write_spk
+g = models.resnet(101, 1)
+x = models.make_input(g.tensors[g.inputs[0]].shape, 5)
+with Model(write_spk(g, "mi355x")) as m:
+    m.set_input(0, x)
+    m.run()
+    y = m.get_output(0)
+    names = [m.kernel_name(n.id) for n in g.nodes if n.op_type in ("Conv", "Gemm")]
+print(json.dumps({"sha": hashlib.sha256(y.tobytes()).hexdigest(), "names": names}))
+""" % str(ROOT)
+
+
+def test_benchmark_network_is_bit_reproducible_across_processes(gpu):
+    """The committed tune table (spinnv2_amd/lib/mi355x.tune) fixes the tile
+    and split-K choice of every ResNet-101 layer, so two fresh processes
+    without a tune DB of their own pick the same kernels and produce the
+    same logits bit for bit."""
+    assert (ROOT / "spinnv2_amd" / "lib" / "mi355x.tune").stat().st_size > 0
+    env = dict(os.environ)
+    for k in ("SPKV2_TUNE_DB", "SPKV2_TUNE_TABLE", "SPKV2_CONV_CFG", "SPKV2_CONV_SPLITK", "SPKV2_CONV_HYBRID",
+              "SPKV2_CONV_TUNE"):
+        env.pop(k, None)
+    runs = []
+    for _ in range(2):
+        out = subprocess.run([sys.executable, "-c", NETWORK_CHILD], env=env, capture_output=True, text=True,
+                             timeout=100)
+        assert out.returncode == 0, out.stderr[-2000:]
+        runs.append(json.loads(out.stdout.strip().splitlines()[-1]))
+    assert runs[0]["names"] == runs[1]["names"]
+    assert runs[0]["sha"] == runs[1]["sha"]
+
+
 def test_tune_db_reuses_hybrid_choice(gpu, tmp_path):
     db = tmp_path / "tune.db"
     first = _child(db)

@@ -157,6 +157,40 @@ def test_kernel_specs_per_profile(resnet18):
     assert all(s.backend == "ref" for s in by_node.values())
 
 
+def test_arm_profiles_conv_kinds_and_scratch():
+    """cpu_arm_neon picks Winograd F(4,3) for 3x3/s1/p1 convs of at least
+    8x8 outputs and 4 tiles (reference kernel_spec.py:188-206), with scratch
+    36*(C+M)*tiles*4 (kernel_spec.py:255-263); the experimental profile
+    picks F(2,3) (scratch 16*(C+M)*tiles*4 with 2x2 tiles, :244-254) and the
+    3x3/s2 direct conv (no scratch) for convs without a fused residual."""
+    g = models.resnet(18, 1, image=64, classes=10)
+    _, arm, _ = select_kernel_specs(g, "cpu_arm_neon")
+    _, exp, _ = select_kernel_specs(g, "cpu_arm_neon_exp")
+    seen = set()
+    for n in g.nodes:
+        if n.op_type != "Conv":
+            continue
+        x, w, y = (g.tensors[t].shape for t in (n.inputs[0], n.inputs[1], n.outputs[0]))
+        s1p1 = w[2] == 3 and n.attrs["strides"] == [1, 1] and n.attrs["pads"] == [1, 1, 1, 1]
+        s2p1 = w[2] == 3 and n.attrs["strides"] == [2, 2] and n.attrs["pads"] == [1, 1, 1, 1]
+        t4 = ((y[2] + 3) // 4) * ((y[3] + 3) // 4)
+        if s1p1 and y[2] >= 8 and t4 >= 4:
+            assert arm[n.id].kind == "winograd_f43"
+            assert arm[n.id].scratch_bytes == 36 * (x[1] + w[0]) * t4 * 4
+        else:
+            assert arm[n.id].kind in ("im2col_gemm", "pointwise_1x1"), arm[n.id].kind
+        plain = len(n.inputs) < 4
+        t2 = ((y[2] + 1) // 2) * ((y[3] + 1) // 2)
+        if s1p1 and plain:
+            assert exp[n.id].kind == "winograd_3x3s1"
+            assert exp[n.id].scratch_bytes == 16 * (x[1] + w[0]) * t2 * 4
+        elif s2p1 and plain:
+            assert exp[n.id].kind == "conv3x3s2_direct" and exp[n.id].scratch_bytes == 0
+        seen |= {arm[n.id].kind, exp[n.id].kind}
+        assert arm[n.id].backend == exp[n.id].backend == "simd"
+    assert {"winograd_f43", "winograd_3x3s1", "conv3x3s2_direct", "im2col_gemm"} <= seen
+
+
 def test_spk_round_trips_through_the_runtime_loader(resnet18):
     import ctypes
 
