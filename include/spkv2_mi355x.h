@@ -100,6 +100,15 @@ int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t node_id, int
  * node; 0 frees the buffers.  Allocates one N*Cout*OH*OW*4-byte buffer per
  * INT8 conv node when enabled. */
 int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable);
+/* No counterpart in the reference.  The same as
+ * spkv2_mi355x_conv_int8_accumulators, for callers that cannot allocate
+ * device memory (HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc): the accumulators are staged through a fixed 16 MiB device
+ * array the library holds on each GPU for the life of the process, and the
+ * call makes no hipMalloc / hipFree.  size above 16 MiB is refused with
+ * SPKV2_E_UNSUPPORTED (spkv2_mi355x_last_error says why).  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU race. */
+int spkv2_mi355x_conv_int8_accumulators_noalloc(Spkv2Context *ctx, uint32_t node_id, int32_t *out, size_t size);
 
 #ifdef __cplusplus
 }

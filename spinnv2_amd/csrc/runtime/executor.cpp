@@ -16,6 +16,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../kernels/kernels.hpp"
@@ -763,5 +764,63 @@ extern "C" int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t n
     if (rc == 0) rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     if (rc == 0) rc = hip_check(hipMemcpy(out, dev, size, hipMemcpyDeviceToHost), "hipMemcpy");
     (void)hipFree(dev);
+    return rc;
+}
+
+// ---------------------------------------------- allocation-free accumulators
+//
+// The raw accumulators staged through a fixed device array instead of a
+// per-call hipMalloc.  Each GPU holds its own copy of `scratch` for the life
+// of the process; host code uses only the per-device address from
+// hipGetSymbolAddress (the array's name is a host-side stand-in, not a
+// device address).  Every call on one GPU shares that GPU's array: calls
+// that overlap on one GPU (other threads, other contexts' streams) race.
+// Nothing in it must start at zero: the accumulator kernels write every
+// element of the first `size` bytes, and only those are copied out.
+
+constexpr size_t kAccScratchBytes = size_t(16) << 20;  // 16 MiB per GPU
+static __device__ __align__(256) int32_t scratch[kAccScratchBytes / sizeof(int32_t)];
+
+namespace {
+
+std::mutex g_scratch_mu;
+int32_t *g_scratch_ptr[64] = {};  // per device ordinal, resolved once with the device current
+
+int32_t *scratch_for_device(int dev) {
+    if (dev < 0 || dev >= 64) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            spk::set_last_error_text("hipGetSymbolAddress(scratch) failed");
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<int32_t *>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int spkv2_mi355x_conv_int8_accumulators_noalloc(Spkv2Context *ctx, uint32_t node_id, int32_t *out,
+                                                           size_t size) {
+    if (!ctx || !out || node_id >= ctx->node_count) return -1;
+    if (!ctx->prepared) return SPKV2_E_NO_DEVICE;
+    const Spkv2NodeRecord *node = &ctx->node_records[node_id];
+    if (node->op_type != SPKV2_OP_CONV) return -1;
+    const Spkv2TensorRecord *y = &ctx->tensor_records[node->outputs[0]];
+    if (size != y->size_bytes) return -2;
+    if (size > kAccScratchBytes) {
+        spk::set_last_error_text("int8 accumulators of " + std::to_string(size) +
+                                 " bytes exceed the 16 MiB allocation-free staging array");
+        return SPKV2_E_UNSUPPORTED;
+    }
+    if (int rc = hip_check(hipSetDevice(ctx->device), "hipSetDevice")) return rc;
+    int32_t *dev = scratch_for_device(ctx->device);
+    if (!dev) return SPKV2_E_HIP;
+    int rc = spk::kern::conv_int8_accumulators(ctx, node, dev);
+    if (rc == 0) rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    if (rc == 0) rc = hip_check(hipMemcpy(out, dev, size, hipMemcpyDeviceToHost), "hipMemcpy");
     return rc;
 }

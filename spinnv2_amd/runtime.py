@@ -99,6 +99,7 @@ SIGNATURES = {
     "spkv2_mi355x_node_kernel_name": (I, [VP, U32, ctypes.c_char_p, SZ]),
     "spkv2_mi355x_conv_int8_accumulators": (I, [VP, U32, VP, SZ]),
     "spkv2_mi355x_set_int8_capture": (I, [VP, I]),
+    "spkv2_mi355x_conv_int8_accumulators_noalloc": (I, [VP, U32, VP, SZ]),
 }
 
 _LIB = None
