@@ -451,6 +451,15 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
         const size_t idx = gi * VEC;
         const int m = static_cast<int>(idx / ld);
         const int n = h.ws_n0 + static_cast<int>(idx - static_cast<size_t>(m) * ld);
+        // bias and residual loads issued first: their latency overlaps the
+        // partials'
+        const float bm = bias ? bias[m] : 0.0f;
+        float rv[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; e++) {
+            const int img = (n + e) / OHW;
+            rv[e] = res ? res[(static_cast<size_t>(img) * M + m) * OHW + (n + e - img * OHW)] : 0.0f;
+        }
         // up to 16 slices' loads in flight before the first add (one round
         // trip for splitk <= 16); the adds stay in slice order
         vec_t v = 0.0f;
@@ -463,7 +472,6 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             for (int t = 0; t < 16; t++)
                 if (s + t < splitk) v += p[t];
         }
-        const float bm = bias ? bias[m] : 0.0f;
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
             float o = alpha * v[e];
@@ -471,7 +479,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             const int img = (n + e) / OHW;
             const int sp = n + e - img * OHW;
             const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
-            if (res) o += res[yi];
+            if (res) o += rv[e];
             o = apply_act(o, act);
             if (h.yp) {
                 const int oh = sp / h.OW, ow = sp - (sp / h.OW) * h.OW;
@@ -754,7 +762,10 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.ws_ld;
-        if (a.ws_ld % 4 == 0 && a.ws_n0 % 4 == 0)
+        // four columns per thread where that still gives every CU a
+        // workgroup; small (batch-1) outputs take one column per thread, so
+        // the partial loads spread over more CUs
+        if (a.ws_ld % 4 == 0 && a.ws_n0 % 4 == 0 && total / 4 >= 256u * 256u)
             hipLaunchKernelGGL(splitk_epilogue<4>, dim3(grid_for(total / 4, 256)), dim3(256), 0, st, ws, tc.splitk,
                                g.M, a.ws_ld, a.OHW, bias, res, y, g.act, alpha, a);
         else

@@ -175,6 +175,13 @@ __device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even)
     return static_cast<int>(r);
 }
 
+constexpr int i8_stage_bytes(int BM, int BN);
+template <int BM>
+__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_sc, float *s_bi);
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
+                                            int lane, const float *s_sc, const float *s_bi, int8_t *s_q);
+
 template <int BM, int BN, int BK, int BMAP>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int TM = BM / 64, TN = BN / 64;  // 2x2 waves, each (32*TM) x (32*TN)
@@ -183,8 +190,13 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int APT = BM * BK / 4096;        // 16-byte A chunks per thread per k-tile
     static_assert(TM >= 1 && TN >= 1 && GPT >= 1 && APT >= 1 && BK % 32 == 0, "tile shape");
     static_assert(BMAP == 0 || BN % (4096 / BK) == 0, "BMAP 1: whole pixel passes");
-    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * LDK];
-    __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * LDK];
+    // the operand buffers, reused by the epilogue's staging area
+    constexpr int OPS = 2 * (BM + BN) * LDK;
+    constexpr int SMEM = OPS > i8_stage_bytes(BM, BN) ? OPS : i8_stage_bytes(BM, BN);
+    __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
+    __shared__ float s_par[2 * BM];
+    int8_t(*As)[BM * LDK] = reinterpret_cast<int8_t(*)[BM * LDK]>(smem);
+    int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem + 2 * BM * LDK);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -302,6 +314,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     if (kt0 >= kt1) return;  // empty split-K slice
+    i8_load_row_params<BM>(a, mt * BM, s_par, s_par + BM);  // read after the loop's barriers
     I8_LOAD_TILE(kt0, ar0, br0);
     I8_LOAD_TILE(kt0 + 1, ar1, br1);
     I8_STORE_TILE(0, ar0, br0);
@@ -319,7 +332,37 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #undef I8_COMPUTE
 #undef I8_LOAD_TILE
 #undef I8_STORE_TILE
+    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, s_par + BM, smem);
+}
 
+// Workgroup-shared memory of the int8 GEMM kernels' epilogue: the tile's
+// per-row combined scales and biases (BM each, loaded in the prologue), and
+// a [BN pixels][BM + 16 bytes] staging area for the handoff's int8 values
+// that aliases the k-loop's operand buffers (free once the loop is done).
+constexpr int i8_stage_bytes(int BM, int BN) { return BN * (BM + 16); }
+
+template <int BM>
+__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_sc, float *s_bi) {
+    for (int i = threadIdx.x; i < BM; i += 256) {
+        const int m = mt0 + i;
+        s_sc[i] = m < a.M ? a.scales[m] : 0.0f;
+        s_bi[i] = a.bias && m < a.M ? a.bias[m] : 0.0f;
+    }
+}
+
+// The epilogue of the int8 GEMM kernels: one wave's TM x TN blocks of 32x32
+// accumulators, at rows wmo.. and columns wno.. of the workgroup's BM x BN
+// tile at (mt0, nt0) (blockIdx.y is the split-K slice).  mode 1 stores int32
+// partials, mode 2 the raw accumulators as NCHW, mode 0 dequantizes (+ bias,
+// residual, activation) into y and/or requantizes into the consumer's padded
+// NHWC int8 buffer: through the LDS staging area when its channel pitch is a
+// multiple of 16, so each pixel's channels of the tile leave as contiguous
+// 16-byte pieces (the other waves' channels of the same pixel beside them).
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
+                                            int lane, const float *s_sc, const float *s_bi, int8_t *s_q) {
+    const int m0 = mt0 + wmo, n0 = nt0 + wno;
+    const int row = lane & 31;
     // 32x32 accumulator layout: lane holds column (lane & 31) and rows
     // 8*(r/4) + 4*(lane/32) + (r%4).  Offsets are unsigned bytes; rows past
     // M and columns past N get out-of-range offsets (stores dropped).
@@ -327,14 +370,14 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     const unsigned rsub = 4 * (lane >> 5);
     unsigned mrow[TM];
 #pragma unroll
-    for (int i = 0; i < TM; i++) mrow[i] = mt * BM + (wm * TM + i) * 32 + rsub;
+    for (int i = 0; i < TM; i++) mrow[i] = m0 + i * 32 + rsub;
     if (a.mode == 1) {
         const __amdgpu_buffer_rsrc_t wrs =
             __builtin_amdgcn_make_buffer_rsrc(a.ws, static_cast<short>(0), a.ws_bytes, kBufWord3);
         const unsigned nt4 = static_cast<unsigned>(a.Ntot) * 4u;
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int n = nt * BN + (wn * TN + j) * 32 + row;
+            const int n = n0 + j * 32 + row;
             const unsigned wcol = n < a.Ntot ? static_cast<unsigned>(n) * 4u : static_cast<unsigned>(kOob);
 #pragma unroll
             for (int i = 0; i < TM; i++)
@@ -351,7 +394,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     unsigned obase[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-        const int n = nt * BN + (wn * TN + j) * 32 + row;
+        const int n = n0 + j * 32 + row;
         const int img = n / a.OHW;
         const int sp = n - img * a.OHW;
         obase[j] = n < a.Ntot
@@ -384,7 +427,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     int qsp[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
-        const int n = nt * BN + (wn * TN + j) * 32 + row;
+        const int n = n0 + j * 32 + row;
         const int img = n / a.OHW;
         const int sp = n - img * a.OHW;
         const int oh = sp / a.OW;
@@ -393,19 +436,20 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
         qbase[j] = n < a.Ntot ? static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp)
                               : static_cast<unsigned>(kOob);
     }
-    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.scales),
-                                                                         static_cast<short>(0), a.M * 4, kBufWord3);
-    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(a.bias ? a.bias : a.scales), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufWord3);
+    // staged handoff (workgroup-uniform): the staging area aliases the
+    // k-loop's LDS operands, so every wave must be past its last read
+    const bool stage = a.q_out && a.q_Cp % 16 == 0;
+    constexpr int SQ = BM + 16;  // staging row pitch: an odd multiple of 16 bytes
+    if (stage) __syncthreads();
 #pragma unroll
     for (int i = 0; i < TM; i++) {
-        // per-row constants of this block, loaded once for all TN blocks
+        // per-row constants of this block (LDS), for all TN blocks
         floatx16 sc, bi;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-            const unsigned moff = (mrow[i] + 8 * (r >> 2) + (r & 3)) * 4u;
-            sc[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(srs, moff, 0, 0));
-            bi[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(brs, moff, 0, 0));
+            const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * (r >> 2) + (r & 3);
+            sc[r] = s_sc[ml];
+            bi[r] = s_bi[ml];
         }
 #pragma unroll
         for (int j = 0; j < TN; j++) {
@@ -446,21 +490,14 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
                     }
                     words[q4] = word;
                 }
-                if (a.q_Cp % 16 == 0) {
-                    // lanes l and l+32 hold one pixel's 32 channels of the
-                    // block, l channels 0-3, 8-11, 16-19, 24-27 and l+32 the
-                    // others: two swaps give lane l channels 0-15 and lane
-                    // l+32 channels 16-31, one 16-byte store each
-                    const bool hi = lane >= 32;
-                    const unsigned r1 = __shfl_xor(hi ? words[0] : words[2], 32);
-                    const unsigned r2 = __shfl_xor(hi ? words[1] : words[3], 32);
-                    const intx4 val = hi ? intx4{static_cast<int>(r1), static_cast<int>(words[2]), static_cast<int>(r2),
-                                                 static_cast<int>(words[3])}
-                                         : intx4{static_cast<int>(words[0]), static_cast<int>(r1),
-                                                 static_cast<int>(words[1]), static_cast<int>(r2)};
-                    const unsigned c16 = mrow[i] - rsub + (hi ? 16u : 0u);
-                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val),
-                                                           qrs, c16 < M ? qbase[j] + c16 : kOob, 0, 0);
+                if (stage) {
+                    // the tile's pixel row in LDS: 4 channels per dword
+                    const int pl = wno + j * 32 + row;
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const int cl = wmo + i * 32 + static_cast<int>(rsub) + 8 * q4;
+                        *reinterpret_cast<unsigned *>(&s_q[pl * SQ + cl]) = words[q4];
+                    }
                 } else {
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
@@ -480,6 +517,174 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             }
         }
     }
+    if (!stage) return;
+    __syncthreads();
+    // 16-byte pieces of the staged tile, the BM/16 pieces of one pixel on
+    // consecutive threads; a piece is stored when its first channel is below
+    // M (channels from M to the padded pitch hold 0)
+    constexpr int PPX = BM / 16;
+    for (int t = threadIdx.x; t < BN * PPX; t += 256) {
+        const int pl = t / PPX;
+        const int c16 = (t - pl * PPX) * 16;
+        const int n = nt0 + pl;
+        if (n >= a.Ntot || mt0 + c16 >= a.M) continue;
+        const int img = n / a.OHW;
+        const int sp = n - img * a.OHW;
+        const int oh = sp / a.OW;
+        const int ow = sp - oh * a.OW;
+        const unsigned off =
+            static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp + mt0 + c16);
+        const uintx4 val = *reinterpret_cast<const uintx4 *>(&s_q[pl * SQ + c16]);
+        __builtin_amdgcn_raw_buffer_store_b128(val, qrs, off, 0, 0);
+    }
+}
+
+// Implicit GEMM with the weight operand straight from memory: the packed
+// weights of a k-tile are stored in MFMA fragment order ([BM/32 row blocks]
+// [BK/32 k steps][64 lanes][16 bytes]: lane l holds row l%32 and bytes
+// 16*(l/32)..+15 of the 32-byte k step), so each wave loads its A fragments
+// with one 16-byte load per fragment from L2 (a layer's weights are shared
+// by all its workgroups) into registers, two k-tiles ahead, and only the
+// gathered activations go through LDS (pixel-major gather, as BMAP 1 of
+// conv_igemm_i8).  WAVES_M x WAVES_N waves, each (32*TM) x (32*TN).
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+__global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
+    constexpr int TM = BM / (32 * WAVES_M), TN = BN / (32 * WAVES_N);
+    constexpr int K32 = BK / 32;       // 32-byte k steps per tile
+    constexpr int LDK = BK + 16;       // bytes per LDS row: an odd multiple of 16
+    constexpr int G = BK / 16;         // 16-byte k groups per tile
+    constexpr int PPP = 256 / G;       // pixels per pass of the workgroup
+    constexpr int GPT = BN / PPP;      // 16-byte B loads per thread per tile
+    static_assert(WAVES_M * WAVES_N == 4 && TM >= 1 && TN >= 1 && BK % 32 == 0, "tile shape");
+    static_assert(GPT >= 1 && BN % PPP == 0 && (LDK / 16) % 2 == 1, "B gather shape");
+    // the operand buffers, reused by the epilogue's staging area
+    constexpr int SMEM = 2 * BN * LDK > i8_stage_bytes(BM, BN) ? 2 * BN * LDK : i8_stage_bytes(BM, BN);
+    __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
+    __shared__ float s_par[2 * BM];
+    int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    // each XCD walks a contiguous range of tiles, m fastest (see conv_igemm_i8)
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int mt = bid % a.m_tiles;
+    const int nt = bid / a.m_tiles;
+    const int kt0 = blockIdx.y * a.kt_per_split;
+    const int kt1 = min(kt0 + a.kt_per_split, a.k_tiles);
+
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(a.xq), static_cast<short>(0), a.x_bytes, kBufWord3);
+    const int bpix = tid / G, bgrp = tid % G;
+    int colp[GPT];
+#pragma unroll
+    for (int p = 0; p < GPT; p++) {
+        const int n = nt * BN + p * PPP + bpix;
+        int c = kOob;
+        if (n < a.Ntot) {
+            const int img = n / a.OHW;
+            const int sp = n - img * a.OHW;
+            const int oh = sp / a.OW;
+            const int ow = sp - oh * a.OW;
+            c = img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
+        }
+        colp[p] = c + bgrp * 16;
+    }
+    const int row = lane & 31;
+    const int khalf = 16 * (lane >> 5);
+
+    intx4 a0[TM][K32], a1[TM][K32], br0[GPT], br1[GPT];
+
+#define I8X_LOAD_A(KT, AX)                                                                                           \
+    {                                                                                                                \
+        const int kt_ = min((KT), a.k_tiles - 1);                                                                    \
+        const intx4 *src =                                                                                           \
+            reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(mt) * a.k_tiles + kt_) * (BM * BK));        \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int q = 0; q < K32; q++) AX[i][q] =     \
+            src[((wm * TM + i) * K32 + q) * 64 + lane];                                                              \
+    }
+    // the table has two tiles of out-of-range entries past the last
+#define I8X_LOAD_B(KT, BR)                                                                                           \
+    {                                                                                                                \
+        const int kbase = a.koff[(KT) * G];                                                                          \
+        _Pragma("unroll") for (int p = 0; p < GPT; p++) BR[p] =                                                      \
+            __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, colp[p], kbase, 0));                \
+    }
+#define I8X_STORE_B(BUF, BR)                                                                                         \
+    {                                                                                                                \
+        _Pragma("unroll") for (int p = 0; p < GPT; p++) * reinterpret_cast<intx4 *>(                                 \
+            &Bs[BUF][(p * PPP + bpix) * LDK + bgrp * 16]) = BR[p];                                                   \
+    }
+#define I8X_FRAG_B(BUF, Q, BF)                                                                                       \
+    {                                                                                                                \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) BF[j] =                                                       \
+            *reinterpret_cast<const intx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + (Q) * 32 + khalf]);        \
+    }
+#define I8X_MMA(AX, Q, BF)                                                                                           \
+    _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =        \
+        __builtin_amdgcn_mfma_i32_32x32x32_i8(AX[i][Q], BF[j], acc[i][j], 0, 0, 0);
+    // the B fragments of step q+1 are read while the MFMAs of step q run
+#define I8X_COMPUTE(BUF, AX)                                                                                         \
+    {                                                                                                                \
+        intx4 fb0[TN], fb1[TN];                                                                                      \
+        I8X_FRAG_B(BUF, 0, fb0);                                                                                     \
+        _Pragma("unroll") for (int q = 0; q < K32; q += 2) {                                                         \
+            if (q + 1 < K32) I8X_FRAG_B(BUF, q + 1, fb1);                                                            \
+            I8X_MMA(AX, q, fb0);                                                                                     \
+            if (q + 2 < K32) I8X_FRAG_B(BUF, q + 2, fb0);                                                            \
+            if (q + 1 < K32) { I8X_MMA(AX, q + 1, fb1); }                                                            \
+        }                                                                                                            \
+    }
+    // one pipeline step: B of tile KT in LDS buffer BUF, its A in AC; B of
+    // tile KT+1 in flight in BNX; B of tile KT+2 into the free set BF and A
+    // of tile KT+1 into AN
+#define I8X_STEP(KT, BUF, AC, AN, BNX, BF)                                                                           \
+    {                                                                                                                \
+        I8X_LOAD_B((KT) + 2, BF);                                                                                    \
+        I8X_LOAD_A((KT) + 1, AN);                                                                                    \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8X_COMPUTE(BUF, AC);                                                                                        \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8X_STORE_B((BUF) ^ 1, BNX);                                                                                 \
+        __syncthreads();                                                                                             \
+    }
+
+    intx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+
+    if (kt0 >= kt1) return;  // empty split-K slice
+    i8_load_row_params<BM>(a, mt * BM, s_par, s_par + BM);  // read after the loop's barriers
+    I8X_LOAD_B(kt0, br0);
+    I8X_LOAD_B(kt0 + 1, br1);
+    I8X_LOAD_A(kt0, a0);
+    I8X_STORE_B(0, br0);
+    __syncthreads();
+    int kt = kt0;
+    // tiles past kt1 are loaded and ignored: no data-dependent branches
+    for (; kt + 1 < kt1; kt += 2) {
+        I8X_STEP(kt, 0, a0, a1, br1, br0);
+        I8X_STEP(kt + 1, 1, a1, a0, br0, br1);
+    }
+    if (kt < kt1) {
+        I8X_COMPUTE(0, a0);
+    }
+#undef I8X_STEP
+#undef I8X_COMPUTE
+#undef I8X_MMA
+#undef I8X_FRAG_B
+#undef I8X_STORE_B
+#undef I8X_LOAD_B
+#undef I8X_LOAD_A
+    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, s_par + BM, smem);
 }
 
 // Sums the int32 split-K partials (exact in any order), then dequantizes or
@@ -538,21 +743,29 @@ using I8Kernel = void (*)(I8Args);
 
 struct I8Cfg {
     int BM, BN, BK;
-    int bmap;  // B gather lane map (see conv_igemm_i8)
+    int bmap;     // B gather lane map (see conv_igemm_i8)
+    int adirect;  // 1: conv_igemm_i8x, weights packed in MFMA fragment order and loaded straight to registers
     const char *name;
     I8Kernel kernel;
 };
 
-#define I8CFG(BM, BN, BK) {BM, BN, BK, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0>}
-#define I8CFGP(BM, BN, BK) {BM, BN, BK, 1, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1>}
+// New configurations go at the end: the tune tables store indices.
+#define I8CFG(BM, BN, BK) {BM, BN, BK, 0, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0>}
+#define I8CFGP(BM, BN, BK) {BM, BN, BK, 1, 0, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1>}
+#define I8CFGX(BM, BN, BK, WM, WN) \
+    {BM, BN, BK, 1, 1, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN, conv_igemm_i8x<BM, BN, BK, WM, WN>}
 const I8Cfg kI8Cfgs[] = {
     I8CFG(128, 128, 64),  I8CFG(128, 128, 128),  I8CFG(128, 64, 64),  I8CFG(128, 64, 128),
     I8CFG(64, 128, 64),   I8CFG(64, 64, 64),     I8CFG(64, 64, 128),
     I8CFGP(128, 128, 64), I8CFGP(128, 128, 128), I8CFGP(128, 64, 64), I8CFGP(128, 64, 128),
     I8CFGP(64, 128, 64),  I8CFGP(64, 64, 64),    I8CFGP(64, 64, 128),
+    I8CFGX(128, 128, 128, 2, 2), I8CFGX(128, 64, 128, 2, 2), I8CFGX(64, 128, 128, 2, 2),
+    I8CFGX(64, 64, 128, 2, 2),   I8CFGX(128, 128, 64, 2, 2),  I8CFGX(128, 64, 64, 2, 2),
+    I8CFGX(64, 64, 64, 2, 2),    I8CFGX(256, 64, 64, 4, 1),   I8CFGX(256, 64, 128, 4, 1),
 };
 #undef I8CFG
 #undef I8CFGP
+#undef I8CFGX
 constexpr int kNumI8Cfgs = sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]);
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -1022,13 +1235,21 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     // activation quantization constants (reference conv_int8.c:22-23)
     plan->quant_split = static_cast<int>((static_cast<int64_t>(g.C) * g.H * g.W / 16) * 16);
 
-    // weights packed [m_tiles][k_tiles][BM][BK] in the layer's k order
+    // weights packed per (m_tile, k_tile) in the layer's k order: [BM][BK]
+    // rows, or for conv_igemm_i8x in MFMA fragment order [BM/32][BK/32][64
+    // lanes][16 bytes], lane = 32 * (16-byte half of the k step) + row % 32
     std::vector<int8_t> packed(static_cast<size_t>(tc.m_tiles) * tc.k_tiles * t.BM * t.BK, 0);
     for (int m = 0; m < g.M; m++) {
         const int mt = m / t.BM, mi = m % t.BM;
         for (int kb = 0; kb < Kbytes; kb++) {
             const int kt = kb / t.BK, kk = kb % t.BK;
-            packed[((static_cast<size_t>(mt) * tc.k_tiles + kt) * t.BM + mi) * t.BK + kk] = i8_weight_at(g, L, w, m, kb);
+            const size_t tile = (static_cast<size_t>(mt) * tc.k_tiles + kt) * t.BM * t.BK;
+            size_t at = static_cast<size_t>(mi) * t.BK + kk;
+            if (t.adirect) {
+                const int q = kk / 32, h = (kk % 32) / 16, b = kk % 16;
+                at = ((static_cast<size_t>(mi / 32) * (t.BK / 32) + q) * 64 + h * 32 + mi % 32) * 16 + b;
+            }
+            packed[tile + at] = i8_weight_at(g, L, w, m, kb);
         }
     }
     if (int rc = hip_check(hipMalloc(&plan->wpack, packed.size()), "hipMalloc i8 weights")) return rc;

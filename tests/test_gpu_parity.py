@@ -245,11 +245,14 @@ def test_int8_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert ("splitk=1>" in name) == (split == 1), name
 
 
-# Pixel-major gather configurations (7-13): every one on a 1x1 conv (one
-# kernel row: always eligible) and on a 3x3 conv with 64 channels (12 groups
-# per kernel row: eligible for BK = 64 only), with split-K, ragged M and N,
-# residual and Relu; ineligible forcings are refused.
-I8_PX = [(cfg, shape, split) for cfg in range(7, 14) for shape in ("1x1", "3x3") for split in (1, 3)]
+# Pixel-major gather configurations (7-13, and the direct-weight kernel
+# conv_igemm_i8x: 14-22): every one on a 1x1 conv (one kernel row: always
+# eligible) and on a 3x3 conv with 64 channels (12 groups per kernel row:
+# eligible for BK = 64 only), with split-K, ragged M and N, residual and
+# Relu; ineligible forcings are refused.
+I8_PX_BK = {7: 64, 8: 128, 9: 64, 10: 128, 11: 64, 12: 64, 13: 128,
+            14: 128, 15: 128, 16: 128, 17: 128, 18: 64, 19: 64, 20: 64, 21: 64, 22: 128}
+I8_PX = [(cfg, shape, split) for cfg in I8_PX_BK for shape in ("1x1", "3x3") for split in (1, 3)]
 
 
 @pytest.mark.parametrize("cfg,shape,split", I8_PX, ids=[f"i8px{c}_{s}_split{k}" for c, s, k in I8_PX])
@@ -262,14 +265,13 @@ def test_int8_pixel_gather_configs(gpu, monkeypatch, cfg, shape, split):
         g = models.single_conv(3, 96, 9, 11, 70, 1, 1, 0, act="Relu", residual=True)
     else:
         g = models.single_conv(2, 64, 11, 13, 70, 3, 1, 1, act="Relu", residual=True)
-    bk = [64, 128, 64, 128, 64, 64, 128][cfg - 7]
-    if shape == "3x3" and bk == 128:
+    if shape == "3x3" and I8_PX_BK[cfg] == 128:
         with pytest.raises(RuntimeError_) as e:
             _int8_check(g)
         assert e.value.code == -32
         return
     name = _int8_check(g)
-    assert ",px," in name, name
+    assert (",ax" in name) if cfg >= 14 else (",px," in name), name
 
 
 def test_graph_mode_matches_eager(gpu):
