@@ -114,7 +114,7 @@ struct IgemmArgs {
     float *__restrict__ y;
     float *__restrict__ ws;          // split-K partials [splitk][M][ws_ld], column n at n - ws_n0
     int ws_n0, ws_ld;                // first column with partials, columns per partial row
-    int dp_tiles, rem_split;         // hybrid: whole tiles first, then rem_split slices per remaining tile
+    int dp_tiles, rem_split;         // hybrid: whole tiles first; rem_split slices per split tile
     int x_bytes;                     // extent of x for the bounds-checked loads
     int y_bytes;                     // extent of y (and of the residual)
     int ws_bytes;                    // extent of the split-K partials
@@ -129,6 +129,11 @@ struct IgemmArgs {
     // input (NCHW, Hp x Wp planes); y may then be null (no other reader)
     float *__restrict__ yp;
     int yp_bytes, yp_Wp, yp_pt, yp_pl, yp_plane;
+    // skinny kernel: k = tap * sk_C + c (a tap's channels consecutive);
+    // channel c of a tap is c * sk_cstride elements past channel 0, tap
+    // (kh, kw) = (tap / sk_KW, tap % sk_KW) kh * sk_tap_h + kw * sk_tap_w
+    // elements past tap 0
+    int sk_C, sk_cstride, sk_KW, sk_tap_h, sk_tap_w;
 };
 
 
@@ -346,7 +351,9 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                         const int off = m < a.M ? obase[j] + m * a.ws_ld * 4 : kOobOffset;
                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][r]), wrs, off, 0, 0);
                     }
-        } else {
+            return;  // splitk_epilogue sums the partials
+        }
+        {
             const int ohw4 = a.OHW * 4;
 #pragma unroll
             for (int j = 0; j < TN; j++) {
@@ -431,6 +438,127 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 }
             }
         }
+    }
+}
+
+// Skinny implicit GEMM, for layers whose output is too small to fill the GPU
+// with 64-wide tiles (batch 1): one 16 x 16 output tile per workgroup, its
+// k range cut into chunks of 64 dealt round robin to the W waves (chunk c to
+// wave c % W), each wave accumulating the whole tile over its chunks on
+// v_mfma_f32_16x16x4f32; the W partial tiles are summed through LDS in wave
+// order, then the epilogue runs.  Many workgroups without split-K partials
+// in memory and without a second kernel.
+//
+// k order: k = tap * C + c with C a multiple of 64, so a chunk is 64
+// consecutive channels of one tap.  MFMA t (0..15) of a chunk takes its k
+// slot g (lanes 16g..16g+15) from k = 64 * chunk + 16g + t: a lane's 16 A
+// values (its row m) are one 64-byte run of the packed weights, and its 16 B
+// values are channels 16g..16g+15 of the chunk at its column n, loaded with
+// voffset = col(n) + chunk base and soffset = t * channel stride.  Columns
+// past N use an out-of-range voffset and load 0.
+template <int W>
+__global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
+    constexpr int P = 4;  // chunks in flight per wave: 4 x 20 loads, within the 63 vmcnt allows
+    __shared__ float red[W][256];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int mt = bid % a.m_tiles;
+    const int nt = bid / a.m_tiles;
+    const int KC = a.k_tiles;  // chunks of 64 k
+
+    int col = kOobOffset;
+    {
+        const int n = nt * 16 + l16;
+        if (n < a.Ntot) {
+            const int img = n / a.OHW;
+            const int sp = n - img * a.OHW;
+            const int oh = sp / a.OW;
+            const int ow = sp - oh * a.OW;
+            col = (img * a.x_img_stride + oh * a.sh * a.Wp + ow * a.sw) * 4;
+        }
+    }
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
+    const int cs4 = a.sk_cstride * 4;
+    // packed weights [m_tiles][KC][4 slots][16 rows][16 k]
+    const floatx4 *wsrc = reinterpret_cast<const floatx4 *>(a.wp) +
+                          (static_cast<size_t>(mt) * KC * 1024 + (g * 16 + l16) * 16) / 4;
+    const int nch = wave < KC ? (KC - wave + W - 1) / W : 0;
+
+    // the epilogue's element of this thread (tid < 256): its bias and
+    // residual are loaded now, so their latency hides under the k loop
+    const int em = mt * 16 + (tid >> 4);
+    const int en = nt * 16 + (tid & 15);
+    const bool eown = tid < 256 && em < a.M && en < a.Ntot;
+    const int eimg = eown ? en / a.OHW : 0;
+    const int esp = en - eimg * a.OHW;
+    const size_t eyi = (static_cast<size_t>(eimg) * a.M + em) * a.OHW + esp;
+    const float ebias = eown && a.bias ? a.bias[em] : 0.0f;
+    const float eres = eown && a.res ? a.res[eyi] : 0.0f;
+
+    floatx4 av[P][4];
+    float bv[P][16];
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+
+    // loads chunk I of this wave into register set S; past the wave's last
+    // chunk it loads a valid chunk that is never used
+#define SK_LOAD(I, S)                                                                                             \
+    {                                                                                                             \
+        const int kc_ = min(wave + W * (I), KC - 1);                                                              \
+        const floatx4 *src_ = wsrc + static_cast<size_t>(kc_) * 256;                                              \
+        _Pragma("unroll") for (int q = 0; q < 4; q++) av[S][q] = src_[q];                                         \
+        const int k0_ = kc_ * 64;                                                                                 \
+        const int tap_ = k0_ / a.sk_C;                                                                            \
+        const int c0_ = k0_ - tap_ * a.sk_C + 16 * g;                                                             \
+        const int kh_ = tap_ / a.sk_KW;                                                                           \
+        const int kw_ = tap_ - kh_ * a.sk_KW;                                                                     \
+        const int vo_ =                                                                                           \
+            col == kOobOffset ? kOobOffset : col + (kh_ * a.sk_tap_h + kw_ * a.sk_tap_w + c0_ * a.sk_cstride) * 4; \
+        _Pragma("unroll") for (int t = 0; t < 16; t++) bv[S][t] =                                                 \
+            __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, vo_, t * cs4, 0));                \
+    }
+#define SK_MMA(S)                                                                                                 \
+    _Pragma("unroll") for (int t = 0; t < 16; t++) acc =                                                          \
+        __builtin_amdgcn_mfma_f32_16x16x4f32(av[S][t >> 2][t & 3], bv[S][t], acc, 0, 0, 0);
+
+    if (nch > 0) {
+#pragma unroll
+        for (int p = 0; p < P - 1; p++) SK_LOAD(p, p);
+        for (int i0 = 0; i0 < nch; i0 += P) {
+#pragma unroll
+            for (int p = 0; p < P; p++) {
+                SK_LOAD(i0 + p + P - 1, (p + P - 1) % P);
+                if (i0 + p < nch) { SK_MMA(p); }
+            }
+        }
+    }
+#undef SK_LOAD
+#undef SK_MMA
+
+    // 16x16 accumulator layout: lane (g, l16) holds rows 4g..4g+3 of column l16
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave][(4 * g + i) * 16 + l16] = acc[i];
+    __syncthreads();
+    if (eown) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) v += red[w][tid];
+        if (a.alpha != 1.0f) v *= a.alpha;
+        if (a.bias) v += ebias;
+        if (a.res) v += eres;
+        v = apply_act(v, a.act);
+        if (a.yp) {
+            const int oh = esp / a.OW;
+            const int ow = esp - oh * a.OW;
+            a.yp[(static_cast<size_t>(eimg) * a.M + em) * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl] = v;
+        }
+        if (a.y) a.y[eyi] = v;
     }
 }
 
@@ -572,19 +700,30 @@ namespace {
 using IgemmKernel = void (*)(IgemmArgs);
 
 struct TileCfg {
-    int BM, BN, BK;
+    int BM, BN, BK;  // skinny kernel: 16, 16 and the 64-k chunk
     const char *name;
     IgemmKernel kernel;
     double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
+    int skinny_waves = 0;  // > 0: conv_skinny_f32 with this many waves (no split-K)
 };
 
 #define CFG(BM, BN, BK, EFF) {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, 2, 2>, EFF}
 const TileCfg kCfgs[] = {
     CFG(128, 128, 16, 0.85), CFG(128, 128, 32, 0.85), CFG(64, 128, 16, 0.90), CFG(64, 128, 32, 0.88),
     CFG(128, 64, 16, 1.00),  CFG(128, 64, 32, 0.95),  CFG(64, 64, 16, 0.96),  CFG(64, 64, 32, 0.98),
+    // deep k-tiles: a short split-K slice (batch 1) is one or two of them,
+    // so its operand loads are in flight together instead of one k-tile of
+    // latency per 16 k
+    CFG(64, 64, 64, 0.95),   CFG(64, 64, 128, 0.95), CFG(128, 64, 64, 0.95),  CFG(64, 128, 64, 0.90),
+    // 16 x 16 tiles, k over 4 or 8 waves: small outputs without split-K
+    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, 1.0, 4},
+    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, 1.0, 8},
 };
 #undef CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+// threads per workgroup of configuration c
+int cfg_threads(int c) { return kCfgs[c].skinny_waves > 0 ? 64 * kCfgs[c].skinny_waves : 256; }
 
 int device_cu_count() {
     static int cus = 0;
@@ -599,18 +738,22 @@ int device_cu_count() {
     return cus;
 }
 
-// Workgroups of configuration c one CU holds at once.
+// Workgroups of configuration c one CU holds at once; 0 when its kernels
+// cannot launch on this device (e.g. more LDS than a workgroup may have),
+// which takes the configuration out of every choice.
 int resident_wgs(int c) {
     static int cache[kNumCfgs] = {0};
-    if (cache[c] == 0) {
+    static bool known[kNumCfgs] = {false};
+    if (!known[c]) {
         int n = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(kCfgs[c].kernel), 256, 0) !=
-                hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void *>(kCfgs[c].kernel),
+                                                         cfg_threads(c), 0) != hipSuccess ||
             n < 1) {
             (void)hipGetLastError();
-            n = 1;
+            n = 0;
         }
         cache[c] = n;
+        known[c] = true;
     }
     return cache[c];
 }
@@ -634,10 +777,10 @@ TileCounts tile_counts(int c, int M, int Ntot, int K, int split) {
     tc.m_tiles = (M + t.BM - 1) / t.BM;
     tc.n_tiles = (Ntot + t.BN - 1) / t.BN;
     tc.k_tiles = (K + t.BK - 1) / t.BK;
-    const int req = split >= kHybrid ? split - kHybrid : split;
+    const int req = t.skinny_waves > 0 ? 1 : split >= kHybrid ? split - kHybrid : split;  // skinny: no split-K
     tc.kt_per_split = (tc.k_tiles + req - 1) / req;
     tc.splitk = (tc.k_tiles + tc.kt_per_split - 1) / tc.kt_per_split;
-    if (split >= kHybrid) {
+    if (split >= kHybrid && t.skinny_waves == 0) {
         // whole tiles: the largest multiple of the CU count that is whole
         // n-tile columns (so the remaining tiles are the last columns)
         const int tiles = tc.m_tiles * tc.n_tiles;
@@ -667,6 +810,15 @@ size_t partial_bytes_of(const TileCounts &tc, int M, int Ntot) {
 double model_us(int c, const TileCounts &tc, int M, int Ntot) {
     const TileCfg &t = kCfgs[c];
     const int cus = device_cu_count();
+    if (t.skinny_waves > 0) {
+        // a wave's chunks are 16 MFMAs of 32 cycles each; rounds of resident
+        // workgroups; ~1 us of load latency per round
+        const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles;
+        const long slots = static_cast<long>(cus) * resident_wgs(c);
+        const long rounds = (wgs + slots - 1) / slots;
+        const int chunks = (tc.k_tiles + t.skinny_waves - 1) / t.skinny_waves;
+        return static_cast<double>(rounds) * (chunks * 16 * 32 / 2400.0 + 1.0) + 2.0;
+    }
     const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles * tc.splitk;
     const long slots = static_cast<long>(cus) * resident_wgs(c);
     const long rounds = (wgs + slots - 1) / slots;
@@ -688,6 +840,10 @@ double model_us(int c, const TileCounts &tc, int M, int Ntot) {
 }
 
 const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32};
+
+// Fewest k-tiles a split-K slice may hold: two for the shallow tiles (a
+// slice of one 16- or 32-k tile is all pipeline fill), one for the deep ones.
+int min_slice_tiles(int c) { return kCfgs[c].BK >= 64 ? 1 : 2; }
 const int kHybridSplits[] = {2, 4, 8, 16};
 
 // What the tuner needs to launch a candidate: the B source geometry and
@@ -699,7 +855,17 @@ struct GatherSpec {
     int x_img_stride;  // elements between images of the B source
     std::function<int(int)> koff;  // byte offset of k < K
     std::string key;   // everything the timing depends on
+    SkinnyGeom sk;     // the same rule per tap (skinny kernel)
 };
+
+// The skinny kernel takes a layer whose channels per tap are a multiple of
+// its 64-k chunk (so a chunk never straddles two taps).
+bool skinny_fits(const GatherSpec &gs) { return gs.sk.C > 0 && gs.sk.C % 64 == 0; }
+
+// Configuration c can run the layer.
+bool cfg_fits(int c, const GatherSpec &gs) {
+    return resident_wgs(c) > 0 && (kCfgs[c].skinny_waves == 0 || skinny_fits(gs));
+}
 
 std::vector<int> build_koff(const GatherSpec &gs, int BK) {
     const int kpad = (gs.K + BK - 1) / BK * BK;
@@ -716,7 +882,8 @@ std::vector<int> build_koff(const GatherSpec &gs, int BK) {
 // an already prepared (padded) B source, then the split-K epilogue.
 static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
                         int x_bytes, int x_img_stride, const float *wpack, const int *koff, const float *bias,
-                        const float *res, float *y, float alpha, float *ws, const ConvPlan *handoff = nullptr) {
+                        const float *res, float *y, float alpha, float *ws, const SkinnyGeom &sk,
+                        const ConvPlan *handoff = nullptr) {
     const TileCfg &t = kCfgs[cfg];
     IgemmArgs a{};
     a.x = xs;
@@ -755,6 +922,22 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     a.y_bytes = static_cast<int>(g.y_elems * 4);
     a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
     const int tiles = tc.m_tiles * tc.n_tiles;
+    if (t.skinny_waves > 0) {
+        // the kernel's chunks never straddle taps: checked here as well as
+        // at planning, since a chunk past its tap would read other channels
+        if (sk.C <= 0 || sk.C % 64 != 0 || tc.k_tiles * 64 != sk.C * (g.KH * g.KW)) {
+            set_last_error_text("conv_skinny_f32: layer without whole 64-channel chunks per tap");
+            return SPKV2_E_UNSUPPORTED;
+        }
+        a.sk_C = sk.C;
+        a.sk_cstride = sk.cstride;
+        a.sk_KW = sk.KW;
+        a.sk_tap_h = sk.tap_h;
+        a.sk_tap_w = sk.tap_w;
+        a.ws = nullptr;
+        t.kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0, st>>>(a);
+        return launch_status("conv_skinny_f32");
+    }
     const dim3 grid = tc.dp_tiles > 0
                           ? dim3(static_cast<unsigned>(tc.dp_tiles + (tiles - tc.dp_tiles) * tc.splitk), 1)
                           : dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(tc.splitk));
@@ -873,7 +1056,8 @@ struct TuneBuffers {
 // every context sees the same choice for the same layer.  Returns false
 // when the device could not be used (the caller then trusts the model).
 bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cfg_out, int *split_out) {
-    if (tuned_lookup(gs.key, cfg_out, split_out) && *cfg_out < kNumCfgs) return true;
+    if (tuned_lookup(gs.key, cfg_out, split_out) && *cfg_out >= 0 && *cfg_out < kNumCfgs && cfg_fits(*cfg_out, gs))
+        return true;
     const int Ntot = g.N * g.OH * g.OW;
     struct Cand {
         int cfg, split;
@@ -883,11 +1067,12 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     std::vector<Cand> cands;
     double best_model = 1e300;
     for (int c = 0; c < kNumCfgs; c++) {
+        if (!cfg_fits(c, gs)) continue;
         int last_splitk = -1;
         for (int split : kSplits) {
             const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, split);
             if (tc.splitk == last_splitk) continue;
-            if (split > 1 && tc.kt_per_split < 2) break;
+            if (split > 1 && tc.kt_per_split < min_slice_tiles(c)) break;
             last_splitk = tc.splitk;
             if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
             const double m = model_us(c, tc, g.M, Ntot);
@@ -896,7 +1081,7 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
         }
         for (int rs : kHybridSplits) {
             const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, kHybrid + rs);
-            if (tc.dp_tiles == 0 || tc.kt_per_split < 2) continue;
+            if (tc.dp_tiles == 0 || tc.kt_per_split < min_slice_tiles(c)) continue;
             if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
             const double m = model_us(c, tc, g.M, Ntot);
             best_model = std::min(best_model, m);
@@ -922,14 +1107,15 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     float *ws = static_cast<float *>(tb.alloc(ws_bytes));
     float *bias = g.has_bias ? static_cast<float *>(tb.alloc(static_cast<size_t>(g.M) * 4)) : nullptr;
     float *res = g.has_res ? static_cast<float *>(tb.alloc(y_bytes)) : nullptr;
-    int *koff[2] = {nullptr, nullptr};  // BK 16, BK 32
-    for (int i = 0; i < 2; i++) {
+    int *koff[4] = {nullptr, nullptr, nullptr, nullptr};  // BK 16, 32, 64, 128
+    for (int i = 0; i < 4; i++) {
         const std::vector<int> kv = build_koff(gs, 16 << i);
         koff[i] = static_cast<int *>(tb.alloc(kv.size() * sizeof(int)));
         if (koff[i] && hipMemcpy(koff[i], kv.data(), kv.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
             koff[i] = nullptr;
     }
-    if (!xs || !wp || !y || !ws || (g.has_bias && !bias) || (g.has_res && !res) || !koff[0] || !koff[1]) return false;
+    if (!xs || !wp || !y || !ws || (g.has_bias && !bias) || (g.has_res && !res) || !koff[0] || !koff[1] || !koff[2] || !koff[3])
+        return false;
     // operands of zeros: the timing does not depend on the values
     (void)hipMemsetAsync(xs, 0, gs.x_bytes, st);
     (void)hipMemsetAsync(wp, 0, wpack_bytes, st);
@@ -942,11 +1128,12 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
         return false;
     }
     auto time_it = [&](const Cand &cd, int reps) -> double {
-        const int *ko = koff[kCfgs[cd.cfg].BK == 16 ? 0 : 1];
+        const int bk = kCfgs[cd.cfg].BK;
+        const int *ko = koff[bk == 16 ? 0 : bk == 32 ? 1 : bk == 64 ? 2 : 3];
         if (hipEventRecord(e0, st) != hipSuccess) return 1e300;
         for (int r = 0; r < reps; r++)
             if (launch_igemm(st, cd.cfg, cd.tc, g, gs.Wp, xs, gs.x_bytes, gs.x_img_stride, wp, ko, bias, res, y, 1.0f,
-                             ws) != 0)
+                             ws, gs.sk) != 0)
                 return 1e300;
         if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e300;
         float ms = 0.0f;
@@ -984,6 +1171,15 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
     *cfg_out = keep[pick].cfg;
     *split_out = keep[pick].split;
     tuned_store(gs.key, keep[pick].cfg, keep[pick].split);
+    if (const char *e = getenv("SPKV2_TUNE_LOG"))
+        if (e[0] == '1') {
+            // every timed candidate, fastest first: config, split request,
+            // model estimate and measured time (us)
+            fprintf(stderr, "[tune] %s -> cfg %d split %d\n", gs.key.c_str(), keep[pick].cfg, keep[pick].split);
+            for (const Cand &cd : keep)
+                fprintf(stderr, "[tune]   %-10s split %4d splitk %2d  model %7.2f  time %7.2f\n", kCfgs[cd.cfg].name,
+                        cd.split, cd.tc.splitk, cd.model, cd.t);
+        }
     return true;
 }
 
@@ -999,9 +1195,10 @@ void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *
     if (!(tune && tune_tiles(st, g, gs, &best_cfg, &best_split))) {
         double best = 1e300;
         for (int c = 0; c < kNumCfgs; c++) {
+            if (!cfg_fits(c, gs)) continue;
             for (int split : kSplits) {
                 const TileCounts tc = tile_counts(c, g.M, Ntot, gs.K, split);
-                if (split > 1 && tc.kt_per_split < 2) break;
+                if (split > 1 && tc.kt_per_split < min_slice_tiles(c)) break;
                 if (partial_bytes_of(tc, g.M, Ntot) > (size_t(1) << 29)) continue;
                 const double m = model_us(c, tc, g.M, Ntot);
                 if (m < best * 0.999) {
@@ -1014,7 +1211,7 @@ void choose_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *
     }
     if (const char *e = getenv("SPKV2_CONV_CFG")) {
         const int c = atoi(e);
-        if (c >= 0 && c < kNumCfgs) best_cfg = c;
+        if (c >= 0 && c < kNumCfgs && cfg_fits(c, gs)) best_cfg = c;
     }
     if (const char *e = getenv("SPKV2_CONV_SPLITK")) {
         const int sk = atoi(e);
@@ -1051,6 +1248,26 @@ int upload_packed_f32(const float *w, int M, int K, int BM, int BK, int m_tiles,
                 }
             }
         }
+    const size_t bytes = packed.size() * sizeof(float);
+    if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc packed weights")) return rc;
+    return hip_check(hipMemcpy(*out, packed.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy packed weights");
+}
+
+// Packs w[m][c][tap] (k = c * taps + tap, the reference's order) for the
+// skinny kernel: k' = tap * C + c in chunks of 64, tile [m_tiles][KC][4 slots
+// g][16 rows][16 t] holding row m, k' = 64 * chunk + 16g + t -- lane (g, row)
+// of MFMA t reads element t of its 64-byte run.  Rows past M are zero.
+int upload_packed_skinny(const float *w, int M, int C, int taps, int m_tiles, int KC, void **out) {
+    std::vector<float> packed(static_cast<size_t>(m_tiles) * KC * 1024, 0.0f);
+    for (int m = 0; m < M; m++) {
+        const int mt = m / 16, ml = m % 16;
+        for (int kp = 0; kp < KC * 64; kp++) {
+            const int tap = kp / C, c = kp % C;
+            const int kc = kp / 64, g = (kp % 64) / 16, t = kp % 16;
+            packed[(static_cast<size_t>(mt) * KC + kc) * 1024 + (g * 16 + ml) * 16 + t] =
+                w[(static_cast<size_t>(m) * C + c) * taps + tap];
+        }
+    }
     const size_t bytes = packed.size() * sizeof(float);
     if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc packed weights")) return rc;
     return hip_check(hipMemcpy(*out, packed.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy packed weights");
@@ -1098,8 +1315,14 @@ static int plan_tiles_and_weights(hipStream_t st, const ConvGeom &g, const Gathe
     plan->dp_tiles = tc.dp_tiles;
     plan->ws_n0 = tc.ws_n0;
     if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
-    if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack))
+    plan->sk = gs.sk;
+    if (t.skinny_waves > 0) {
+        if (int rc = upload_packed_skinny(w_host, g.M, gs.sk.C, gs.K / gs.sk.C, plan->m_tiles, plan->k_tiles,
+                                          &plan->wpack))
+            return rc;
+    } else if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack)) {
         return rc;
+    }
     return upload_koff(build_koff(gs, t.BK), &plan->ktab);
 }
 
@@ -1138,6 +1361,11 @@ int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvP
         return ((c * Hp + kh * g.dh) * Wp + kw * g.dw) * 4;
     };
     gs.key = shape_key("conv", g, plan, gs.x_img_stride);
+    gs.sk.C = g.C;
+    gs.sk.cstride = Hp * Wp;
+    gs.sk.KW = g.KW;
+    gs.sk.tap_h = g.dh * Wp;
+    gs.sk.tap_w = g.dw;
     if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = plan->pad_bytes + partial_bytes(plan);
     return 0;
@@ -1156,12 +1384,17 @@ int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int 
     gs.x_img_stride = k_stride == 1 ? g.C : 1;
     gs.koff = [k_stride](int k) { return k * k_stride * 4; };
     gs.key = shape_key(k_stride == 1 ? "gemm" : "gemm_ta", g, plan, gs.x_img_stride);
+    gs.sk.C = g.C;  // one tap
+    gs.sk.cstride = k_stride;
     if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = partial_bytes(plan);
     return 0;
 }
 
 std::string igemm_name(const ConvPlan *p) {
+    if (kCfgs[p->cfg].skinny_waves > 0)
+        return std::string("conv_skinny_f32<16x16,w") + std::to_string(kCfgs[p->cfg].skinny_waves) +
+               (p->padded ? ",pad" : "") + ">";
     return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") +
            ",splitk=" + std::to_string(p->splitk) + (p->dp_tiles ? ",dp=" + std::to_string(p->dp_tiles) : "") + ">";
 }
@@ -1221,7 +1454,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     const bool give = p->pad_out && handoff;
     return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
                         static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
-                        give && !p->y_needed ? nullptr : y, alpha, ws, give ? p : nullptr);
+                        give && !p->y_needed ? nullptr : y, alpha, ws, p->sk, give ? p : nullptr);
 }
 
 // fp32 handoff.  When this padded conv's input is the only output of an

@@ -291,10 +291,12 @@ def test_graph_mode_matches_eager(gpu):
             np.testing.assert_array_equal(m.get_output(0), eager)
 
 
-# Every tile configuration, with and without split-K (each slice writes its
+# Every tile configuration (the fp32 table of conv_f32.hip: 8 shallow-k
+# tiles, then 4 deep-k ones), with and without split-K (each slice writes its
 # partial tile; splitk_epilogue sums them in slice order and applies the
 # epilogue), on a ragged residual conv; forced through the tuning overrides.
-SPLIT_CASES = [(cfg, split) for cfg in range(8) for split in (1, 3, 8)]
+F32_CFGS = 12
+SPLIT_CASES = [(cfg, split) for cfg in range(F32_CFGS) for split in (1, 3, 8)]
 
 
 @pytest.mark.parametrize("cfg,split", SPLIT_CASES, ids=[f"cfg{c}_split{s}" for c, s in SPLIT_CASES])
@@ -309,7 +311,57 @@ def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
-@pytest.mark.parametrize("cfg", range(8))
+# The skinny configurations (16 x 16 tiles, k over 4 or 8 waves summed in
+# LDS; entries 12 and 13 of the fp32 table) on layers whose channels per tap
+# are multiples of 64: ragged M and N, padding, stride, dilation, residual,
+# and Gemm with alpha and with transA.
+SKINNY_CASES = [
+    ("conv3x3_res", lambda: models.single_conv(2, 128, 11, 13, 150, 3, 1, 1, act="Relu", residual=True)),
+    ("conv1x1_s2", lambda: models.single_conv(1, 256, 14, 14, 72, 1, 2, 0, act=None)),
+    ("conv3x3_s2_dil2", lambda: models.single_conv(1, 64, 15, 15, 40, 3, 2, 2, dilation=2, act="Relu")),
+    ("gemm_alpha", lambda: models.single_gemm(3, 192, 70, alpha=0.5)),
+    ("gemm_trans_a", lambda: models.single_gemm(5, 128, 33, trans_a=1)),
+]
+
+
+@pytest.mark.parametrize("cfg", [F32_CFGS, F32_CFGS + 1])
+@pytest.mark.parametrize("name,build", SKINNY_CASES, ids=[c[0] for c in SKINNY_CASES])
+def test_skinny_configs(gpu, monkeypatch, cfg, name, build):
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    g = build()
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        got = m.get_output(0)
+        name = m.kernel_name(0)
+    assert f"conv_skinny_f32<16x16,w{4 if cfg == F32_CFGS else 8}" in name, name
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
+    """A layer whose channels per tap are not a multiple of 64 does not take
+    a forced skinny configuration (its chunks would straddle taps)."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_CFGS))
+    g = models.single_conv(1, 72, 11, 13, 40, 3, 1, 1)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = m.get_output(0)
+        assert "skinny" not in m.kernel_name(0)
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+@pytest.mark.parametrize("cfg", range(F32_CFGS))
 def test_conv_hybrid_schedule(gpu, monkeypatch, cfg):
     """Hybrid schedule (whole tiles for a multiple of the CU count, the last
     n-tile columns split over k and summed by splitk_epilogue) on a layer
