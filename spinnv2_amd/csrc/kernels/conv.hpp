@@ -25,7 +25,7 @@ struct ConvGeom {
 
 int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeom *g);
 
-enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2 };
+enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV_DW_F32 = 3 };
 
 // The k -> offset rule of an fp32 implicit-GEMM B source per tap, for the
 // skinny kernel: k = c * taps + tap sits at c * cstride + (tap / KW) * tap_h

@@ -693,6 +693,71 @@ __global__ void __launch_bounds__(256) conv_direct_f32(DirectArgs a) {
     }
 }
 
+// ---------------------------------------------------------- depthwise kernel
+
+// Depthwise conv (one input channel per group, any channel multiplier), K x K
+// taps known at compile time: each thread computes kDwVO outputs of one
+// column, in consecutive rows, and lanes take consecutive columns, so each
+// load instruction of a wave reads a contiguous run of an input row.  All of
+// a thread's tap loads, its bias and its residuals are issued before the
+// first multiply-add (one memory round trip); each output is then summed in
+// the reference's order (from the bias, kh then kw, out-of-bounds taps
+// skipped, one fused multiply-add per tap), the residual added and the
+// activation applied.  The host keeps the thread count below 2^31, so the
+// index math is 32-bit.
+constexpr int kDwVO = 4;
+
+template <int K>
+__global__ void __launch_bounds__(256) conv_dw_f32(DirectArgs a, int row_groups, unsigned total) {
+    const unsigned t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= total) return;
+    const int ow = static_cast<int>(t % static_cast<unsigned>(a.OW));
+    unsigned r = t / static_cast<unsigned>(a.OW);
+    const int oh0 = static_cast<int>(r % static_cast<unsigned>(row_groups)) * kDwVO;
+    r /= static_cast<unsigned>(row_groups);
+    const int m = static_cast<int>(r % static_cast<unsigned>(a.M));
+    const int n = static_cast<int>(r / static_cast<unsigned>(a.M));
+    const int c = m / a.Mg;
+    const float *xc = a.x + (static_cast<size_t>(n) * a.C + c) * a.H * a.W;
+    const float *wm = a.w + static_cast<size_t>(m) * K * K;
+    const size_t ybase = (static_cast<size_t>(n) * a.M + m) * a.OH * a.OW + ow;
+    float wv[K * K];
+#pragma unroll
+    for (int i = 0; i < K * K; i++) wv[i] = wm[i];
+    float xv[kDwVO][K][K];
+    bool ok[kDwVO][K][K];
+#pragma unroll
+    for (int v = 0; v < kDwVO; v++)
+#pragma unroll
+        for (int kh = 0; kh < K; kh++) {
+            const int ih = (oh0 + v) * a.sh + kh * a.dh - a.ph;
+            const bool hin = oh0 + v < a.OH && static_cast<unsigned>(ih) < static_cast<unsigned>(a.H);
+#pragma unroll
+            for (int kw = 0; kw < K; kw++) {
+                const int iw = ow * a.sw + kw * a.dw - a.pw;
+                ok[v][kh][kw] = hin && static_cast<unsigned>(iw) < static_cast<unsigned>(a.W);
+                xv[v][kh][kw] = ok[v][kh][kw] ? xc[ih * a.W + iw] : 0.0f;
+            }
+        }
+    const float b0 = a.bias ? a.bias[m] : 0.0f;
+    float rv[kDwVO];
+#pragma unroll
+    for (int v = 0; v < kDwVO; v++)
+        rv[v] = a.res && oh0 + v < a.OH ? a.res[ybase + static_cast<size_t>(oh0 + v) * a.OW] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < kDwVO; v++) {
+        if (oh0 + v >= a.OH) break;
+        float sum = b0;
+#pragma unroll
+        for (int kh = 0; kh < K; kh++)
+#pragma unroll
+            for (int kw = 0; kw < K; kw++)
+                if (ok[v][kh][kw]) sum = fmaf(xv[v][kh][kw], wv[kh * K + kw], sum);
+        if (a.res) sum += rv[v];
+        a.y[ybase + static_cast<size_t>(oh0 + v) * a.OW] = apply_act(sum, a.act);
+    }
+}
+
 // ------------------------------------------------------------- host side
 
 namespace {
@@ -718,6 +783,12 @@ const TileCfg kCfgs[] = {
     // 16 x 16 tiles, k over 4 or 8 waves: small outputs without split-K
     {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, 1.0, 4},
     {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, 1.0, 8},
+    // 32-row tiles, the four waves side by side along n: layers with 16-48
+    // output channels (YOLO) fill half or more of the MFMA rows instead of
+    // a quarter to three quarters of a 64-row tile
+    {32, 128, 16, "32x128x16", conv_igemm_f32<32, 128, 16, 1, 4>, 0.90},
+    {32, 128, 32, "32x128x32", conv_igemm_f32<32, 128, 32, 1, 4>, 0.90},
+    {32, 256, 16, "32x256x16", conv_igemm_f32<32, 256, 16, 1, 4>, 0.90},
 };
 #undef CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -1512,6 +1583,54 @@ int run_igemm_f32_strided(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     return run_igemm_impl(ctx, p, x, bias, nullptr, y, alpha, x_img_stride);
 }
 
+// The depthwise kernel takes group convs with one input channel per group and
+// square 3x3, 5x5 or 7x7 taps.
+static bool dw_fits(const ConvGeom &g) {
+    return g.group > 1 && g.C == g.group && g.M % g.group == 0 && g.KH == g.KW &&
+           (g.KH == 3 || g.KH == 5 || g.KH == 7);
+}
+
+static int run_direct(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom &g);
+
+static int run_dw(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom &g) {
+    DirectArgs a{};
+    a.x = dptr<const float>(ctx, node->inputs[0]);
+    a.w = dptr<const float>(ctx, node->inputs[1]);
+    a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
+    a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
+    a.y = dptr<float>(ctx, node->outputs[0]);
+    a.N = g.N;
+    a.C = g.C;
+    a.H = g.H;
+    a.W = g.W;
+    a.M = g.M;
+    a.KH = g.KH;
+    a.KW = g.KW;
+    a.OH = g.OH;
+    a.OW = g.OW;
+    a.sh = g.sh;
+    a.sw = g.sw;
+    a.ph = g.ph;
+    a.pw = g.pw;
+    a.dh = g.dh;
+    a.dw = g.dw;
+    a.Cg = 1;
+    a.Mg = g.M / g.group;
+    a.act = g.act;
+    const int row_groups = (g.OH + kDwVO - 1) / kDwVO;
+    const size_t threads = static_cast<size_t>(g.N) * g.M * row_groups * g.OW;
+    if (threads >= (size_t(1) << 31)) return run_direct(ctx, node, g);
+    const unsigned total = static_cast<unsigned>(threads);
+    const dim3 grid((total + 255) / 256);
+    if (g.KH == 3)
+        hipLaunchKernelGGL(conv_dw_f32<3>, grid, dim3(256), 0, ctx->stream, a, row_groups, total);
+    else if (g.KH == 5)
+        hipLaunchKernelGGL(conv_dw_f32<5>, grid, dim3(256), 0, ctx->stream, a, row_groups, total);
+    else
+        hipLaunchKernelGGL(conv_dw_f32<7>, grid, dim3(256), 0, ctx->stream, a, row_groups, total);
+    return launch_status("conv_dw_f32");
+}
+
 static int run_direct(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom &g) {
     DirectArgs a{};
     a.x = dptr<const float>(ctx, node->inputs[0]);
@@ -1570,6 +1689,9 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
             if (rc == 0) rc = setup_pad_handoff(ctx, node, plan);
             if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan) + (plan->pad_in ? "+handoff" : ""));
         }
+    } else if (dw_fits(g)) {
+        plan->path = CONV_DW_F32;
+        set_kernel_name(ctx, node, "conv_dw_f32");
     } else {
         plan->path = CONV_DIRECT_F32;
         set_kernel_name(ctx, node, "conv_direct_f32<grouped>");
@@ -1590,6 +1712,7 @@ int conv_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratch) {
                              plan->g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr,
                              dptr<float>(ctx, node->outputs[0]), 1.0f);
     case CONV_DIRECT_F32: return run_direct(ctx, node, plan->g);
+    case CONV_DW_F32: return run_dw(ctx, node, plan->g);
     case CONV_IGEMM_I8: return conv_i8_run(ctx, node, plan, nullptr);
     }
     return SPKV2_E_UNSUPPORTED;

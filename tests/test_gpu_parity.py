@@ -46,6 +46,39 @@ def test_conv_f32_vs_oracle(gpu, case):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
+# Depthwise convs (one input channel per group) run conv_dw_f32, which sums
+# each output in the reference's order with one fused multiply-add per
+# in-bounds tap, as the oracle does: bit-exact without SiLU.
+# (N, C, H, W, multiplier, k, stride, pads [t, l, b, r], dilation, act, residual)
+DW_CASES = [
+    (1, 16, 10, 10, 1, 3, 1, [1, 1, 1, 1], 1, "Relu", False),
+    (2, 32, 50, 70, 1, 3, 1, [1, 1, 1, 1], 1, None, True),     # several 16x16 tiles, residual
+    (1, 24, 33, 31, 2, 5, 2, [2, 2, 2, 2], 1, "Relu", False),  # channel multiplier 2, stride 2
+    (1, 8, 29, 23, 1, 7, 1, [3, 3, 3, 3], 1, None, False),      # 7x7
+    (1, 8, 20, 20, 1, 3, 1, [2, 2, 2, 2], 2, "Relu", False),    # dilation 2
+    (1, 8, 17, 19, 1, 3, 2, [0, 1, 1, 0], 1, None, False),      # asymmetric padding
+    (16, 128, 20, 20, 1, 3, 1, [1, 1, 1, 1], 1, None, False),   # the YOLO PSA position encoding
+]
+
+
+@pytest.mark.parametrize("case", DW_CASES, ids=[f"dw{i}" for i in range(len(DW_CASES))])
+def test_depthwise_conv_bitwise(gpu, case):
+    from spinnv2_amd.runtime import Model
+
+    n, c, h, w, mult, k, s, pads, d, act, res = case
+    g = models.single_conv(n, c, h, w, c * mult, k, s, dilation=d, group=c, act=act, residual=res, pads=pads)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        got = m.get_output(0)
+        assert m.kernel_name(0) == "conv_dw_f32", m.kernel_name(0)
+    want = run_oracle(blob, xs)[0]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 # ResNet-101 layers at their real shapes, batch 1 (split-K path) and batch 8
 RESNET_LAYERS = [
     (64, 56, 64, 3, 1, 1),     # s1 3x3
@@ -291,12 +324,14 @@ def test_graph_mode_matches_eager(gpu):
             np.testing.assert_array_equal(m.get_output(0), eager)
 
 
-# Every tile configuration (the fp32 table of conv_f32.hip: 8 shallow-k
-# tiles, then 4 deep-k ones), with and without split-K (each slice writes its
-# partial tile; splitk_epilogue sums them in slice order and applies the
-# epilogue), on a ragged residual conv; forced through the tuning overrides.
-F32_CFGS = 12
-SPLIT_CASES = [(cfg, split) for cfg in range(F32_CFGS) for split in (1, 3, 8)]
+# Every implicit-GEMM tile configuration (the fp32 table of conv_f32.hip: 8
+# shallow-k tiles, 4 deep-k ones, then after the two skinny kernels 3 tiles
+# of 32 rows), with and without split-K (each slice writes its partial tile;
+# splitk_epilogue sums them in slice order and applies the epilogue), on a
+# ragged residual conv; forced through the tuning overrides.
+F32_IGEMM_CFGS = [*range(12), 14, 15, 16]
+F32_SKINNY_CFGS = [12, 13]
+SPLIT_CASES = [(cfg, split) for cfg in F32_IGEMM_CFGS for split in (1, 3, 8)]
 
 
 @pytest.mark.parametrize("cfg,split", SPLIT_CASES, ids=[f"cfg{c}_split{s}" for c, s in SPLIT_CASES])
@@ -324,7 +359,7 @@ SKINNY_CASES = [
 ]
 
 
-@pytest.mark.parametrize("cfg", [F32_CFGS, F32_CFGS + 1])
+@pytest.mark.parametrize("cfg", F32_SKINNY_CFGS)
 @pytest.mark.parametrize("name,build", SKINNY_CASES, ids=[c[0] for c in SKINNY_CASES])
 def test_skinny_configs(gpu, monkeypatch, cfg, name, build):
     from spinnv2_amd.runtime import Model
@@ -339,7 +374,7 @@ def test_skinny_configs(gpu, monkeypatch, cfg, name, build):
         m.run()
         got = m.get_output(0)
         name = m.kernel_name(0)
-    assert f"conv_skinny_f32<16x16,w{4 if cfg == F32_CFGS else 8}" in name, name
+    assert f"conv_skinny_f32<16x16,w{4 if cfg == F32_SKINNY_CFGS[0] else 8}" in name, name
     want = run_oracle(blob, xs)[0]
     assert tnorm_err(got, want) <= FP32_TOL
 
@@ -349,7 +384,7 @@ def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
     a forced skinny configuration (its chunks would straddle taps)."""
     from spinnv2_amd.runtime import Model
 
-    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_CFGS))
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_SKINNY_CFGS[0]))
     g = models.single_conv(1, 72, 11, 13, 40, 3, 1, 1)
     blob = write_spk(g, "mi355x")
     xs = rng_inputs(g)
@@ -361,7 +396,7 @@ def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
 
 
-@pytest.mark.parametrize("cfg", range(F32_CFGS))
+@pytest.mark.parametrize("cfg", F32_IGEMM_CFGS)
 def test_conv_hybrid_schedule(gpu, monkeypatch, cfg):
     """Hybrid schedule (whole tiles for a multiple of the CU count, the last
     n-tile columns split over k and summed by splitk_epilogue) on a layer
