@@ -1211,16 +1211,20 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
         if (hipEventElapsedTime(&ms, e0, e1) != hipSuccess) return 1e300;
         return 1e3 * ms / reps;
     };
+    // Each timing covers about 100 us of back-to-back launches (1 to 20 of
+    // them): a batch-1 candidate runs for a few microseconds, where one
+    // launch's time is mostly event and launch noise.
+    auto reps_for = [](double t) { return std::max(1, std::min(20, static_cast<int>(100.0 / std::max(t, 1.0)))); };
     bool ok = true;
     for (Cand &cd : keep) {
-        (void)time_it(cd, 1);  // warm-up (first launch of a kernel variant)
-        cd.t = time_it(cd, 1);
+        const double t1 = time_it(cd, 1);  // also the warm-up (first launch of a kernel variant)
+        cd.t = t1 >= 1e300 ? t1 : time_it(cd, reps_for(t1));
         if (cd.t >= 1e300) ok = false;
     }
     std::sort(keep.begin(), keep.end(), [](const Cand &a, const Cand &b) { return a.t < b.t; });
     const size_t finalists = std::min<size_t>(keep.size(), 4);
     for (size_t i = 0; i < finalists && ok; i++) {
-        const double t = time_it(keep[i], 3);
+        const double t = time_it(keep[i], 3 * reps_for(keep[i].t));
         keep[i].t = std::min(keep[i].t, t);
     }
     std::sort(keep.begin(), keep.begin() + finalists, [](const Cand &a, const Cand &b) { return a.t < b.t; });
