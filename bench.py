@@ -126,6 +126,68 @@ def copy_calibration(mib: int, reps: int) -> None:
     buf.free()
 
 
+# GEMM views (M = output features, K, N = columns) of ResNet-101 b=64 layers
+# and one large square problem, for the vendor-library calibration
+VENDOR_GEMM_SHAPES = [
+    ("s3_3x3_as_gemm", 256, 2304, 12544),
+    ("s3_1x1_reduce", 256, 1024, 12544),
+    ("s3_1x1_expand", 1024, 256, 12544),
+    ("s4_3x3_as_gemm", 512, 4608, 3136),
+    ("square_4096", 4096, 4096, 4096),
+]
+
+
+def vendor_gemm(reps: int) -> dict:
+    """Calibration, not the product: fp32 GEMM TFLOP/s of the vendor library
+    (torch.matmul on ROCm, TF32-style reduced precision off) beside this
+    runtime's Gemm node on the same problem (Y[N, M] = X[N, K] W[K, M]; the
+    node's HIP-graph replay, wall-clocked), on the GEMM shapes of ResNet-101's
+    stage-3/4 layers (what its convs compute, without the gather) and a square
+    problem."""
+    import torch
+
+    from spinnv2_amd.runtime import DeviceBuffer, Model, load_library
+    from spinnv2_amd.spk import models, write_spk
+
+    torch.backends.cuda.matmul.allow_tf32 = False
+    lib = load_library()
+    out = []
+    for name, M, K, N in VENDOR_GEMM_SHAPES:
+        flop = 2.0 * M * K * N
+        a = torch.randn(M, K, device="cuda:0")
+        b = torch.randn(K, N, device="cuda:0")
+        for _ in range(3):
+            c = a @ b
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            c = a @ b
+        e1.record()
+        torch.cuda.synchronize()
+        t_vendor = e0.elapsed_time(e1) / reps * 1e-3
+        del a, b, c
+        g = models.single_gemm(N, K, M, bias=False)
+        m = Model(write_spk(g, "mi355x"), lib=lib)
+        x = models.make_input(g.tensors[g.inputs[0]].shape)
+        xb = DeviceBuffer(x.nbytes, lib)
+        xb.upload(x)
+        m.bind_input(0, xb)
+        m.set_graph_mode(True)
+        for _ in range(3):
+            m.run()
+        lib.spkv2_device_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            m.run()
+        lib.spkv2_device_synchronize()
+        t_ours = (time.perf_counter() - t0) / reps
+        out.append({"shape": name, "M": M, "K": K, "N": N, "vendor_tflops": round(flop / t_vendor / 1e12, 1),
+                    "spkv2_gemm_tflops": round(flop / t_ours / 1e12, 1), "spkv2_kernel": m.kernel_name(0)})
+        m.close()
+        xb.free()
+    return {"vendor_gemm": out, "peak_tflops": 157.3}
+
+
 def pmc_traffic(name: str = "conv_igemm_f32_resnet101_b64_traffic.txt") -> dict | None:
     """HBM bytes of the conv kernels per step, from a committed rocprofv3
     --pmc summary (FETCH_SIZE and WRITE_SIZE passes scaled by the copy
@@ -414,6 +476,8 @@ def main() -> None:
     ap.add_argument("--yolo-batch", type=int, choices=(1, 16), default=None,
                     help="with --yolo-only: only this batch (a profile of one shape)")
     ap.add_argument("--elementwise-only", action="store_true", help="run only the memory-bound op section")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only compare fp32 GEMM rates with the vendor library (torch.matmul) on ResNet shapes")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the plain copy kernel over this many MiB (PMC counter calibration)")
     args = ap.parse_args()
@@ -423,6 +487,9 @@ def main() -> None:
         sys.exit(2)
     if args.copy_calibration_mib:
         copy_calibration(args.copy_calibration_mib, args.steps)
+        return
+    if args.vendor_gemm:
+        print(json.dumps(vendor_gemm(max(args.steps, 20))), flush=True)
         return
 
     from spinnv2_amd.runtime import DeviceBuffer, Model, load_library

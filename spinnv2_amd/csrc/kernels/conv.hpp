@@ -27,12 +27,14 @@ int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeo
 
 enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV_DW_F32 = 3 };
 
-// The k -> offset rule of an fp32 implicit-GEMM B source per tap, for the
-// skinny kernel: k = c * taps + tap sits at c * cstride + (tap / KW) * tap_h
-// + (tap % KW) * tap_w elements from the column's base; C = 0 when the layer
-// has no such form.
-struct SkinnyGeom {
+// How an fp32 implicit-GEMM B source is laid out beyond its k-offset table.
+// Per tap, for the skinny kernel: k = c * taps + tap sits at c * cstride +
+// (tap / KW) * tap_h + (tap % KW) * tap_w elements from the column's base (C
+// = 0 when the layer has no such form).  kvec: k is contiguous in aligned
+// groups of four (16-byte loads along k).
+struct GatherGeom {
     int C = 0, cstride = 0, KW = 1, tap_h = 0, tap_w = 0;
+    bool kvec = false;
 };
 
 struct ConvPlan {
@@ -43,7 +45,7 @@ struct ConvPlan {
     int m_tiles, n_tiles, k_tiles;
     int splitk, kt_per_split;  // split-K factor and k-tiles per slice
     int dp_tiles, ws_n0;       // hybrid schedule: whole tiles first, partials only from column ws_n0 on
-    SkinnyGeom sk;  // fp32 path: the B source's per-tap rule (skinny configurations)
+    GatherGeom gather;  // fp32 path: the B source's layout (skinny configurations, KVEC loads)
     int K, Kpad;
     void *wpack;         // device: packed weight panels (fp32 or int8)
     void *ktab;          // device: per-k gather table (byte offsets into the B source)

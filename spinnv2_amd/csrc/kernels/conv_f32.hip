@@ -146,7 +146,10 @@ struct IgemmArgs {
 // wave-uniform SGPR from the per-layer table, and each element is a single
 // buffer_load with (voffset, soffset) = (col(n), koff[k]).  Columns past N
 // and k past K use out-of-range offsets and load 0.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+// KVEC: the B source holds k contiguously in aligned groups of four (a Gemm
+// whose A is [rows][K] with K a multiple of 4), so each lane's four k of a
+// column are one 16-byte load instead of four scalar ones.
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool KVEC = false>
 __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     constexpr int TM = BM / (32 * WAVES_M);
     constexpr int TN = BN / (32 * WAVES_N);
@@ -243,8 +246,20 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
     {                                                                                                                \
         /* the table has two tiles of out-of-range entries past Kpad */                                           \
         const int *ko = a.koff + (KT) * BK + bgrp * KPT;                                                              \
-        _Pragma("unroll") for (int j = 0; j < KPT; j++) BR[j] = __builtin_bit_cast(                                  \
-            float, __builtin_amdgcn_raw_buffer_load_b32(xrs, col, ko[j], 0));                                        \
+        if constexpr (KVEC) {                                                                                        \
+            /* the four k of a quad are all below K or all past it (K % 4 == 0) */                                  \
+            _Pragma("unroll") for (int j = 0; j < KPT; j += 4) {                                                     \
+                const floatx4 v_ =                                                                                   \
+                    __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, col, ko[j], 0));          \
+                BR[j] = v_[0];                                                                                       \
+                BR[j + 1] = v_[1];                                                                                   \
+                BR[j + 2] = v_[2];                                                                                   \
+                BR[j + 3] = v_[3];                                                                                   \
+            }                                                                                                        \
+        } else {                                                                                                     \
+            _Pragma("unroll") for (int j = 0; j < KPT; j++) BR[j] = __builtin_bit_cast(                              \
+                float, __builtin_amdgcn_raw_buffer_load_b32(xrs, col, ko[j], 0));                                    \
+        }                                                                                                            \
     }
 #define IGEMM_STORE_B(BUF, BR)                                                                                       \
     {                                                                                                                \
@@ -768,11 +783,13 @@ struct TileCfg {
     int BM, BN, BK;  // skinny kernel: 16, 16 and the 64-k chunk
     const char *name;
     IgemmKernel kernel;
+    IgemmKernel kernel_kvec;  // the same tile with 16-byte B loads along k (KVEC)
     double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
     int skinny_waves = 0;  // > 0: conv_skinny_f32 with this many waves (no split-K)
 };
 
-#define CFG(BM, BN, BK, EFF) {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, 2, 2>, EFF}
+#define CFG(BM, BN, BK, EFF) \
+    {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, 2, 2>, conv_igemm_f32<BM, BN, BK, 2, 2, true>, EFF}
 const TileCfg kCfgs[] = {
     CFG(128, 128, 16, 0.85), CFG(128, 128, 32, 0.85), CFG(64, 128, 16, 0.90), CFG(64, 128, 32, 0.88),
     CFG(128, 64, 16, 1.00),  CFG(128, 64, 32, 0.95),  CFG(64, 64, 16, 0.96),  CFG(64, 64, 32, 0.98),
@@ -781,14 +798,14 @@ const TileCfg kCfgs[] = {
     // latency per 16 k
     CFG(64, 64, 64, 0.95),   CFG(64, 64, 128, 0.95), CFG(128, 64, 64, 0.95),  CFG(64, 128, 64, 0.90),
     // 16 x 16 tiles, k over 4 or 8 waves: small outputs without split-K
-    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, 1.0, 4},
-    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, 1.0, 8},
+    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, conv_skinny_f32<4>, 1.0, 4},
+    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, conv_skinny_f32<8>, 1.0, 8},
     // 32-row tiles, the four waves side by side along n: layers with 16-48
     // output channels (YOLO) fill half or more of the MFMA rows instead of
     // a quarter to three quarters of a 64-row tile
-    {32, 128, 16, "32x128x16", conv_igemm_f32<32, 128, 16, 1, 4>, 0.90},
-    {32, 128, 32, "32x128x32", conv_igemm_f32<32, 128, 32, 1, 4>, 0.90},
-    {32, 256, 16, "32x256x16", conv_igemm_f32<32, 256, 16, 1, 4>, 0.90},
+    {32, 128, 16, "32x128x16", conv_igemm_f32<32, 128, 16, 1, 4>, conv_igemm_f32<32, 128, 16, 1, 4, true>, 0.90},
+    {32, 128, 32, "32x128x32", conv_igemm_f32<32, 128, 32, 1, 4>, conv_igemm_f32<32, 128, 32, 1, 4, true>, 0.90},
+    {32, 256, 16, "32x256x16", conv_igemm_f32<32, 256, 16, 1, 4>, conv_igemm_f32<32, 256, 16, 1, 4, true>, 0.90},
 };
 #undef CFG
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
@@ -926,12 +943,12 @@ struct GatherSpec {
     int x_img_stride;  // elements between images of the B source
     std::function<int(int)> koff;  // byte offset of k < K
     std::string key;   // everything the timing depends on
-    SkinnyGeom sk;     // the same rule per tap (skinny kernel)
+    GatherGeom gather;  // the same rule per tap (skinny kernel), 16-byte k loads (KVEC)
 };
 
 // The skinny kernel takes a layer whose channels per tap are a multiple of
 // its 64-k chunk (so a chunk never straddles two taps).
-bool skinny_fits(const GatherSpec &gs) { return gs.sk.C > 0 && gs.sk.C % 64 == 0; }
+bool skinny_fits(const GatherSpec &gs) { return gs.gather.C > 0 && gs.gather.C % 64 == 0; }
 
 // Configuration c can run the layer.
 bool cfg_fits(int c, const GatherSpec &gs) {
@@ -953,7 +970,7 @@ std::vector<int> build_koff(const GatherSpec &gs, int BK) {
 // an already prepared (padded) B source, then the split-K epilogue.
 static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
                         int x_bytes, int x_img_stride, const float *wpack, const int *koff, const float *bias,
-                        const float *res, float *y, float alpha, float *ws, const SkinnyGeom &sk,
+                        const float *res, float *y, float alpha, float *ws, const GatherGeom &gg,
                         const ConvPlan *handoff = nullptr) {
     const TileCfg &t = kCfgs[cfg];
     IgemmArgs a{};
@@ -996,15 +1013,15 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     if (t.skinny_waves > 0) {
         // the kernel's chunks never straddle taps: checked here as well as
         // at planning, since a chunk past its tap would read other channels
-        if (sk.C <= 0 || sk.C % 64 != 0 || tc.k_tiles * 64 != sk.C * (g.KH * g.KW)) {
+        if (gg.C <= 0 || gg.C % 64 != 0 || tc.k_tiles * 64 != gg.C * (g.KH * g.KW)) {
             set_last_error_text("conv_skinny_f32: layer without whole 64-channel chunks per tap");
             return SPKV2_E_UNSUPPORTED;
         }
-        a.sk_C = sk.C;
-        a.sk_cstride = sk.cstride;
-        a.sk_KW = sk.KW;
-        a.sk_tap_h = sk.tap_h;
-        a.sk_tap_w = sk.tap_w;
+        a.sk_C = gg.C;
+        a.sk_cstride = gg.cstride;
+        a.sk_KW = gg.KW;
+        a.sk_tap_h = gg.tap_h;
+        a.sk_tap_w = gg.tap_w;
         a.ws = nullptr;
         t.kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0, st>>>(a);
         return launch_status("conv_skinny_f32");
@@ -1012,7 +1029,7 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     const dim3 grid = tc.dp_tiles > 0
                           ? dim3(static_cast<unsigned>(tc.dp_tiles + (tiles - tc.dp_tiles) * tc.splitk), 1)
                           : dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(tc.splitk));
-    t.kernel<<<grid, dim3(256), 0, st>>>(a);
+    (gg.kvec ? t.kernel_kvec : t.kernel)<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.ws_ld;
@@ -1204,7 +1221,7 @@ bool tune_tiles(hipStream_t st, const ConvGeom &g, const GatherSpec &gs, int *cf
         if (hipEventRecord(e0, st) != hipSuccess) return 1e300;
         for (int r = 0; r < reps; r++)
             if (launch_igemm(st, cd.cfg, cd.tc, g, gs.Wp, xs, gs.x_bytes, gs.x_img_stride, wp, ko, bias, res, y, 1.0f,
-                             ws, gs.sk) != 0)
+                             ws, gs.gather) != 0)
                 return 1e300;
         if (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess) return 1e300;
         float ms = 0.0f;
@@ -1390,9 +1407,9 @@ static int plan_tiles_and_weights(hipStream_t st, const ConvGeom &g, const Gathe
     plan->dp_tiles = tc.dp_tiles;
     plan->ws_n0 = tc.ws_n0;
     if (partial_bytes(plan) >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;
-    plan->sk = gs.sk;
+    plan->gather = gs.gather;
     if (t.skinny_waves > 0) {
-        if (int rc = upload_packed_skinny(w_host, g.M, gs.sk.C, gs.K / gs.sk.C, plan->m_tiles, plan->k_tiles,
+        if (int rc = upload_packed_skinny(w_host, g.M, gs.gather.C, gs.K / gs.gather.C, plan->m_tiles, plan->k_tiles,
                                           &plan->wpack))
             return rc;
     } else if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack)) {
@@ -1436,11 +1453,11 @@ int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvP
         return ((c * Hp + kh * g.dh) * Wp + kw * g.dw) * 4;
     };
     gs.key = shape_key("conv", g, plan, gs.x_img_stride);
-    gs.sk.C = g.C;
-    gs.sk.cstride = Hp * Wp;
-    gs.sk.KW = g.KW;
-    gs.sk.tap_h = g.dh * Wp;
-    gs.sk.tap_w = g.dw;
+    gs.gather.C = g.C;
+    gs.gather.cstride = Hp * Wp;
+    gs.gather.KW = g.KW;
+    gs.gather.tap_h = g.dh * Wp;
+    gs.gather.tap_w = g.dw;
     if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = plan->pad_bytes + partial_bytes(plan);
     return 0;
@@ -1459,8 +1476,9 @@ int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int 
     gs.x_img_stride = k_stride == 1 ? g.C : 1;
     gs.koff = [k_stride](int k) { return k * k_stride * 4; };
     gs.key = shape_key(k_stride == 1 ? "gemm" : "gemm_ta", g, plan, gs.x_img_stride);
-    gs.sk.C = g.C;  // one tap
-    gs.sk.cstride = k_stride;
+    gs.gather.C = g.C;  // one tap
+    gs.gather.cstride = k_stride;
+    gs.gather.kvec = k_stride == 1 && g.C % 4 == 0;  // A is [rows][K]: four k of a row are 16 contiguous bytes
     if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = partial_bytes(plan);
     return 0;
@@ -1529,7 +1547,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     const bool give = p->pad_out && handoff;
     return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
                         static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
-                        give && !p->y_needed ? nullptr : y, alpha, ws, p->sk, give ? p : nullptr);
+                        give && !p->y_needed ? nullptr : y, alpha, ws, p->gather, give ? p : nullptr);
 }
 
 // fp32 handoff.  When this padded conv's input is the only output of an

@@ -346,6 +346,19 @@ def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
+@pytest.mark.parametrize("cfg", F32_IGEMM_CFGS)
+@pytest.mark.parametrize("k", [136, 130])
+def test_gemm_every_tile_config(gpu, monkeypatch, cfg, k):
+    """Gemm through every implicit-GEMM tile: with K a multiple of 4 the B
+    operand (A, [rows][K]) is loaded 16 bytes along k at a time (the KVEC
+    instances), otherwise one element at a time; ragged M and N."""
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    g = models.single_gemm(70, k, 90, alpha=0.75)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    assert tnorm_err(run_gpu(blob, xs)[0], run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 # The skinny configurations (16 x 16 tiles, k over 4 or 8 waves summed in
 # LDS; entries 12 and 13 of the fp32 table) on layers whose channels per tap
 # are multiples of 64: ragged M and N, padding, stride, dilation, residual,
