@@ -45,6 +45,65 @@ __global__ void __launch_bounds__(256) permute_kernel(const float *__restrict__ 
     }
 }
 
+// Permutations that keep the last axis: every output row (the last axis, L
+// elements) is one contiguous input row.  One workgroup per output row
+// (grid-stride over rows), lanes along the row, 16-byte accesses when L
+// and the row starts allow them.
+__global__ void __launch_bounds__(256) permute_rows(const float *__restrict__ x, float *__restrict__ y, size_t rows,
+                                                    int L, StrideMap m) {
+    const bool vec = (L & 3) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+    for (size_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        // the output row's coordinates over ranks 0 .. rank-2 give the source row
+        size_t t = r;
+        int64_t off = 0;
+        for (int d = m.rank - 2; d >= 0; d--) {
+            const int64_t c = static_cast<int64_t>(t % m.ydim[d]);
+            t /= m.ydim[d];
+            off += c * m.src[d];
+        }
+        const float *src = x + off;
+        float *dst = y + r * static_cast<size_t>(L);
+        if (vec && (off & 3) == 0) {
+            const floatx4 *s4 = reinterpret_cast<const floatx4 *>(src);
+            floatx4 *d4 = reinterpret_cast<floatx4 *>(dst);
+            for (int i = threadIdx.x; i < L / 4; i += 256) d4[i] = s4[i];
+        } else {
+            for (int i = threadIdx.x; i < L; i += 256) dst[i] = src[i];
+        }
+    }
+}
+
+// Permutations that swap the last two axes and keep the rest: batched
+// transposes y[b][c][r] = x[b][r][c] of R x C matrices.  A workgroup moves a
+// 32 x 32 tile through LDS (row pitch 33: the column reads hit 32 different
+// banks), reading rows of x and writing rows of y coalesced.
+constexpr int kTp = 32;
+
+__global__ void __launch_bounds__(256) transpose_tiles(const float *__restrict__ x, float *__restrict__ y, int R, int C,
+                                                       int tiles_c, int tiles_per_mat, size_t total_tiles) {
+    __shared__ float tile[kTp][kTp + 1];
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8 threads
+    for (size_t t = blockIdx.x; t < total_tiles; t += gridDim.x) {
+        const size_t b = t / tiles_per_mat;
+        const int tm = static_cast<int>(t - b * tiles_per_mat);
+        const int r0 = (tm / tiles_c) * kTp, c0 = (tm % tiles_c) * kTp;
+        const float *xb = x + b * static_cast<size_t>(R) * C;
+        float *yb = y + b * static_cast<size_t>(R) * C;
+        __syncthreads();  // the previous tile's reads of `tile` are done
+#pragma unroll
+        for (int i = 0; i < kTp; i += 8) {
+            const int r = r0 + ty + i, c = c0 + tx;
+            if (r < R && c < C) tile[ty + i][tx] = xb[static_cast<size_t>(r) * C + c];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kTp; i += 8) {
+            const int c = c0 + ty + i, r = r0 + tx;
+            if (r < R && c < C) yb[static_cast<size_t>(c) * R + r] = tile[tx][ty + i];
+        }
+    }
+}
+
 // y[i] = x[coords(i) mod xdim]  (reference shape/tile.c:13-19)
 __global__ void __launch_bounds__(256) tile_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n,
                                                    StrideMap m) {
@@ -353,9 +412,32 @@ int transpose_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     }
     const size_t n = elem_count(yr);
     if (n == 0) return 0;
+    const int rank = xr->rank;
+    auto perm = [&](int d) { return attr.extra_count > 0 ? static_cast<int>(attr.extra[d]) : d; };
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    bool keeps_last = rank >= 2 && perm(rank - 1) == rank - 1;
+    bool swaps_last2 = rank >= 2 && perm(rank - 1) == rank - 2 && perm(rank - 2) == rank - 1;
+    for (int d = 0; d + 2 < rank; d++) swaps_last2 = swaps_last2 && perm(d) == d;
+    if (keeps_last && xr->shape[rank - 1] >= 64) {
+        set_kernel_name(ctx, node, "transpose_rows");
+        const int L = static_cast<int>(xr->shape[rank - 1]);
+        const size_t rows = n / static_cast<size_t>(L);
+        hipLaunchKernelGGL(permute_rows, dim3(static_cast<unsigned>(std::min<size_t>(rows, 65536))), dim3(256), 0,
+                           ctx->stream, x, y, rows, L, m);
+        return launch_status("transpose");
+    }
+    if (swaps_last2) {
+        set_kernel_name(ctx, node, "transpose_tiles");
+        const int R = static_cast<int>(xr->shape[rank - 2]), C = static_cast<int>(xr->shape[rank - 1]);
+        const int tiles_r = (R + kTp - 1) / kTp, tiles_c = (C + kTp - 1) / kTp;
+        const size_t total = n / (static_cast<size_t>(R) * C) * tiles_r * tiles_c;
+        hipLaunchKernelGGL(transpose_tiles, dim3(static_cast<unsigned>(std::min<size_t>(total, 65536))), dim3(256), 0,
+                           ctx->stream, x, y, R, C, tiles_c, tiles_r * tiles_c, total);
+        return launch_status("transpose");
+    }
     set_kernel_name(ctx, node, "transpose");
-    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream,
-                       dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]), n, m);
+    hipLaunchKernelGGL(permute_kernel, dim3(grid_for(n, 256)), dim3(256), 0, ctx->stream, x, y, n, m);
     return launch_status("transpose");
 }
 

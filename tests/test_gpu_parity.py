@@ -881,7 +881,12 @@ def test_fp32_pad_handoff_is_bit_identical(gpu, monkeypatch):
 # against the oracle (they move values without arithmetic).
 INDEX_CASES = [
     ("Transpose", [2, 64, 40, 40], dict(perm=[0, 2, 3, 1])),
-    ("Transpose", [1, 144, 8400], dict(perm=[0, 2, 1])),
+    ("Transpose", [1, 144, 8400], dict(perm=[0, 2, 1])),         # last two swapped: 32 x 32 LDS tiles
+    ("Transpose", [2, 3, 45, 70], dict(perm=[0, 1, 3, 2])),      # ragged tiles, batch of 6
+    ("Transpose", [2, 4, 8400], dict(perm=[0, 2, 1])),           # 4-row matrices
+    ("Transpose", [2, 4, 16, 8400], dict(perm=[0, 2, 1, 3])),    # last axis kept: row copies, 16-byte
+    ("Transpose", [3, 5, 7, 100], dict(perm=[2, 0, 1, 3])),
+    ("Transpose", [2, 3, 130], dict(perm=[1, 0, 2])),            # rows of 130: scalar copies
     ("Tile", [1, 8, 1, 50], dict(reps=[2, 1, 30, 1])),
     ("Split", [1, 128, 40, 40], dict(sizes=[64, 64], axis=1)),
     ("Split", [1, 64, 8400], dict(sizes=[16, 16, 32], axis=1)),
