@@ -35,6 +35,12 @@ enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV
 struct GatherGeom {
     int C = 0, cstride = 0, KW = 1, tap_h = 0, tap_w = 0;
     bool kvec = false;
+    // implicit padding: the B source is the unpadded input (H x W, padded by
+    // ph / pw at the top / left), every tap bounds-checked through the tap
+    // table ktap (device, owned by the plan)
+    bool chk = false;
+    int chk_H = 0, chk_W = 0, chk_ph = 0, chk_pw = 0;
+    const int *ktap = nullptr;
 };
 
 struct ConvPlan {

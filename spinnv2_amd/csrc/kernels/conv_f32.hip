@@ -93,6 +93,7 @@ void conv_plan_free(void *p) {
     if (plan->scales) (void)hipFree(plan->scales);
     if (plan->q_in) (void)hipFree(plan->q_in);
     if (plan->pad_in) (void)hipFree(plan->pad_in);
+    if (plan->gather.ktap) (void)hipFree(const_cast<int *>(plan->gather.ktap));
     delete plan;
 }
 
@@ -134,6 +135,10 @@ struct IgemmArgs {
     // (kh, kw) = (tap / sk_KW, tap % sk_KW) kh * sk_tap_h + kw * sk_tap_w
     // elements past tap 0
     int sk_C, sk_cstride, sk_KW, sk_tap_h, sk_tap_w;
+    // implicit padding (kModeChk): per-k tap table ((kh*dh) << 16 | kw*dw,
+    // 0x7fff7fff past K), the unpadded input's extent and the padding
+    const int *__restrict__ ktap;
+    int chk_H, chk_W, chk_ph, chk_pw;
 };
 
 
@@ -146,11 +151,19 @@ struct IgemmArgs {
 // wave-uniform SGPR from the per-layer table, and each element is a single
 // buffer_load with (voffset, soffset) = (col(n), koff[k]).  Columns past N
 // and k past K use out-of-range offsets and load 0.
-// KVEC: the B source holds k contiguously in aligned groups of four (a Gemm
-// whose A is [rows][K] with K a multiple of 4), so each lane's four k of a
-// column are one 16-byte load instead of four scalar ones.
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, bool KVEC = false>
+// MODE kModeKvec: the B source holds k contiguously in aligned groups of four
+// (a Gemm whose A is [rows][K] with K a multiple of 4), so each lane's four
+// k of a column are one 16-byte load instead of four scalar ones.
+// MODE kModeChk (implicit padding): the B source is the unpadded input, and
+// each element is bounds-checked: tap table entry (kh*dh, kw*dw) of k against
+// the lane's column base (oh*sh - ph, ow*sw - pw); taps outside the input
+// load 0, so a padded conv needs no zero-padded copy of its input.
+constexpr int kModePlain = 0, kModeKvec = 1, kModeChk = 2;
+
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int MODE = kModePlain>
 __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
+    constexpr bool KVEC = MODE == kModeKvec;
+    constexpr bool CHK = MODE == kModeChk;
     constexpr int TM = BM / (32 * WAVES_M);
     constexpr int TN = BN / (32 * WAVES_N);
     constexpr int K8 = BK / 8;
@@ -213,6 +226,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 
     {
         int col = kOobOffset;
+        int ihb = 0x40000000, iwb = 0;  // CHK: the column's input row / column at tap (0, 0)
         {
             const int n = nt * BN + bcol;
             if (n < a.Ntot) {
@@ -220,7 +234,13 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 const int sp = n - img * a.OHW;
                 const int oh = sp / a.OW;
                 const int ow = sp - oh * a.OW;
-                col = (img * a.x_img_stride + oh * a.sh * a.Wp + ow * a.sw) * 4;
+                if constexpr (CHK) {
+                    ihb = oh * a.sh - a.chk_ph;
+                    iwb = ow * a.sw - a.chk_pw;
+                    col = (img * a.x_img_stride + ihb * a.Wp + iwb) * 4;  // may be negative: used only in bounds
+                } else {
+                    col = (img * a.x_img_stride + oh * a.sh * a.Wp + ow * a.sw) * 4;
+                }
             }
         }
 
@@ -255,6 +275,16 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 BR[j + 1] = v_[1];                                                                                   \
                 BR[j + 2] = v_[2];                                                                                   \
                 BR[j + 3] = v_[3];                                                                                   \
+            }                                                                                                        \
+        } else if constexpr (CHK) {                                                                                  \
+            /* past K the tap entry is out of every input, so those k load 0 too */                                 \
+            const int *kt_ = a.ktap + (KT) * BK + bgrp * KPT;                                                         \
+            _Pragma("unroll") for (int j = 0; j < KPT; j++) {                                                        \
+                const int tp_ = kt_[j];                                                                              \
+                const bool in_ = static_cast<unsigned>(ihb + (tp_ >> 16)) < static_cast<unsigned>(a.chk_H) &&         \
+                                 static_cast<unsigned>(iwb + (tp_ & 0xffff)) < static_cast<unsigned>(a.chk_W);        \
+                BR[j] = __builtin_bit_cast(                                                                          \
+                    float, __builtin_amdgcn_raw_buffer_load_b32(xrs, in_ ? col + ko[j] : kOobOffset, 0, 0));         \
             }                                                                                                        \
         } else {                                                                                                     \
             _Pragma("unroll") for (int j = 0; j < KPT; j++) BR[j] = __builtin_bit_cast(                              \
@@ -783,13 +813,16 @@ struct TileCfg {
     int BM, BN, BK;  // skinny kernel: 16, 16 and the 64-k chunk
     const char *name;
     IgemmKernel kernel;
-    IgemmKernel kernel_kvec;  // the same tile with 16-byte B loads along k (KVEC)
+    IgemmKernel kernel_kvec;  // the same tile with 16-byte B loads along k (kModeKvec)
+    IgemmKernel kernel_chk;   // the same tile with implicit padding (kModeChk)
     double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
     int skinny_waves = 0;  // > 0: conv_skinny_f32 with this many waves (no split-K)
 };
 
-#define CFG(BM, BN, BK, EFF) \
-    {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, 2, 2>, conv_igemm_f32<BM, BN, BK, 2, 2, true>, EFF}
+#define CFGW(BM, BN, BK, WM, WN, EFF)                                                                        \
+    {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, WM, WN, kModePlain>,                          \
+     conv_igemm_f32<BM, BN, BK, WM, WN, kModeKvec>, conv_igemm_f32<BM, BN, BK, WM, WN, kModeChk>, EFF}
+#define CFG(BM, BN, BK, EFF) CFGW(BM, BN, BK, 2, 2, EFF)
 const TileCfg kCfgs[] = {
     CFG(128, 128, 16, 0.85), CFG(128, 128, 32, 0.85), CFG(64, 128, 16, 0.90), CFG(64, 128, 32, 0.88),
     CFG(128, 64, 16, 1.00),  CFG(128, 64, 32, 0.95),  CFG(64, 64, 16, 0.96),  CFG(64, 64, 32, 0.98),
@@ -798,16 +831,15 @@ const TileCfg kCfgs[] = {
     // latency per 16 k
     CFG(64, 64, 64, 0.95),   CFG(64, 64, 128, 0.95), CFG(128, 64, 64, 0.95),  CFG(64, 128, 64, 0.90),
     // 16 x 16 tiles, k over 4 or 8 waves: small outputs without split-K
-    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, conv_skinny_f32<4>, 1.0, 4},
-    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, conv_skinny_f32<8>, 1.0, 8},
+    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, conv_skinny_f32<4>, conv_skinny_f32<4>, 1.0, 4},
+    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, conv_skinny_f32<8>, conv_skinny_f32<8>, 1.0, 8},
     // 32-row tiles, the four waves side by side along n: layers with 16-48
     // output channels (YOLO) fill half or more of the MFMA rows instead of
     // a quarter to three quarters of a 64-row tile
-    {32, 128, 16, "32x128x16", conv_igemm_f32<32, 128, 16, 1, 4>, conv_igemm_f32<32, 128, 16, 1, 4, true>, 0.90},
-    {32, 128, 32, "32x128x32", conv_igemm_f32<32, 128, 32, 1, 4>, conv_igemm_f32<32, 128, 32, 1, 4, true>, 0.90},
-    {32, 256, 16, "32x256x16", conv_igemm_f32<32, 256, 16, 1, 4>, conv_igemm_f32<32, 256, 16, 1, 4, true>, 0.90},
+    CFGW(32, 128, 16, 1, 4, 0.90), CFGW(32, 128, 32, 1, 4, 0.90), CFGW(32, 256, 16, 1, 4, 0.90),
 };
 #undef CFG
+#undef CFGW
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // threads per workgroup of configuration c
@@ -1029,7 +1061,12 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     const dim3 grid = tc.dp_tiles > 0
                           ? dim3(static_cast<unsigned>(tc.dp_tiles + (tiles - tc.dp_tiles) * tc.splitk), 1)
                           : dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(tc.splitk));
-    (gg.kvec ? t.kernel_kvec : t.kernel)<<<grid, dim3(256), 0, st>>>(a);
+    a.ktap = gg.ktap;
+    a.chk_H = gg.chk_H;
+    a.chk_W = gg.chk_W;
+    a.chk_ph = gg.chk_ph;
+    a.chk_pw = gg.chk_pw;
+    (gg.kvec ? t.kernel_kvec : gg.chk ? t.kernel_chk : t.kernel)<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.ws_ld;
@@ -1488,7 +1525,8 @@ std::string igemm_name(const ConvPlan *p) {
     if (kCfgs[p->cfg].skinny_waves > 0)
         return std::string("conv_skinny_f32<16x16,w") + std::to_string(kCfgs[p->cfg].skinny_waves) +
                (p->padded ? ",pad" : "") + ">";
-    return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") +
+    return std::string("conv_igemm_f32<") + kCfgs[p->cfg].name +
+           (p->gather.chk ? ",ipad" : p->padded ? ",pad" : "") +
            ",splitk=" + std::to_string(p->splitk) + (p->dp_tiles ? ",dp=" + std::to_string(p->dp_tiles) : "") + ">";
 }
 
@@ -1529,7 +1567,10 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     // with the handoffs not live (a fault event armed, or the kernel registry
     // changed since prepare) every tensor is materialized and padded here
     const bool handoff = handoffs_live(ctx);
-    if (p->padded && p->pad_in && handoff) {
+    int Wp = p->Wp;
+    if (p->gather.chk) {
+        Wp = g.W;  // implicit padding: the kernel reads the unpadded input, taps checked
+    } else if (p->padded && p->pad_in && handoff) {
         xs = p->pad_in;  // written, zero halo included, by the producer's epilogue
         x_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.C * p->Hp * p->Wp * 4);
         x_img_stride = g.C * p->Hp * p->Wp;
@@ -1545,9 +1586,58 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     }
     float *ws = p->workspace > 0 ? reinterpret_cast<float *>(wsb + p->pad_bytes) : nullptr;
     const bool give = p->pad_out && handoff;
-    return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, p->Wp, xs, x_bytes, x_img_stride,
+    return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, Wp, xs, x_bytes, x_img_stride,
                         static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
                         give && !p->y_needed ? nullptr : y, alpha, ws, p->gather, give ? p : nullptr);
+}
+
+// Implicit padding.  A padded conv whose input no producer hands over in
+// padded form, and whose gather per output pixel is short (C*KH*KW <= 160:
+// RGB stems, 3x3 convs of up to 16 channels), reads the unpadded input with
+// every tap bounds-checked (kModeChk) instead of copying it into a
+// zero-padded buffer first: the k -> offset table is rebuilt for the
+// unpadded input, a tap table gives (kh*dh, kw*dw) per k, and the padded
+// copy's workspace is dropped.  For longer gathers the checks on every
+// element cost more than the copy saves (a 64-channel 3x3 conv at 80x80,
+// batch 16: 170 against 124 us with its copy), so they keep the copy; so
+// do the skinny kernel (it reads a padded input) and inputs 16384 or more
+// rows or columns tall (the tap table packs a tap into 16 bits).
+// SPKV2_IMPLICIT_PAD=0 keeps the copy everywhere, =1 takes the checks
+// wherever they apply.
+static int use_implicit_padding(ConvPlan *plan) {
+    const ConvGeom &g = plan->g;
+    if (!plan->padded || plan->pad_in || kCfgs[plan->cfg].skinny_waves > 0) return 0;
+    if (g.H >= 16384 || g.W >= 16384 || (g.KH - 1) * g.dh >= 32768 || (g.KW - 1) * g.dw >= 32768) return 0;
+    const char *e = getenv("SPKV2_IMPLICIT_PAD");
+    if (e && e[0] == '0') return 0;
+    if (!(e && e[0] == '1') && g.C * g.KH * g.KW > 160) return 0;
+    const int BK = plan->BK;
+    const int K = g.C * g.KH * g.KW;
+    const size_t entries = static_cast<size_t>(plan->Kpad) + 2 * BK;  // as build_koff: two tiles past Kpad
+    std::vector<int> koff(entries, kOobOffset), ktap(entries, 0x7fff7fff);
+    for (int k = 0; k < K; k++) {
+        const int c = k / (g.KH * g.KW), r = k % (g.KH * g.KW);
+        const int th = (r / g.KW) * g.dh, tw = (r % g.KW) * g.dw;
+        koff[k] = ((c * g.H + th) * g.W + tw) * 4;
+        ktap[k] = (th << 16) | tw;
+    }
+    void *kt = nullptr, *tt = nullptr;
+    if (int rc = upload_koff(koff, &kt)) return rc;
+    if (int rc = upload_koff(ktap, &tt)) {
+        (void)hipFree(kt);
+        return rc;
+    }
+    if (plan->ktab) (void)hipFree(plan->ktab);
+    plan->ktab = kt;
+    plan->gather.ktap = static_cast<const int *>(tt);
+    plan->gather.chk = true;
+    plan->gather.chk_H = g.H;
+    plan->gather.chk_W = g.W;
+    plan->gather.chk_ph = g.ph;
+    plan->gather.chk_pw = g.pw;
+    plan->workspace -= plan->pad_bytes;
+    plan->pad_bytes = 0;
+    return 0;
 }
 
 // fp32 handoff.  When this padded conv's input is the only output of an
@@ -1709,6 +1799,7 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
         } else {
             rc = plan_igemm_f32(ctx->stream, g, w, plan);
             if (rc == 0) rc = setup_pad_handoff(ctx, node, plan);
+            if (rc == 0) rc = use_implicit_padding(plan);
             if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan) + (plan->pad_in ? "+handoff" : ""));
         }
     } else if (dw_fits(g)) {

@@ -346,6 +346,45 @@ def test_conv_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
+# Padded convs whose input no producer hands over padded: implicit padding
+# (every tap bounds-checked against the unpadded input; forced here with
+# SPKV2_IMPLICIT_PAD=1, by default only for short gathers) or, with
+# SPKV2_IMPLICIT_PAD=0, a zero-padded copy first.
+# (N, Cin, H, W, Cout, k, stride, pads [t, l, b, r], dilation, residual)
+PAD_CASES = [
+    (2, 16, 13, 11, 40, 3, 1, [1, 1, 1, 1], 1, True),
+    (1, 3, 37, 29, 16, 3, 2, [1, 1, 1, 1], 1, False),   # YOLO-stem-like: 3 channels, stride 2
+    (1, 3, 30, 30, 64, 7, 2, [3, 3, 3, 3], 1, False),   # ResNet-stem-like
+    (1, 8, 17, 19, 24, 3, 1, [0, 2, 1, 0], 1, False),   # asymmetric
+    (1, 8, 20, 20, 24, 3, 1, [2, 2, 2, 2], 2, True),    # dilation 2
+]
+
+
+@pytest.mark.parametrize("implicit", ["1", "0"])
+@pytest.mark.parametrize("cfg", [6, 7, 8, 14])
+@pytest.mark.parametrize("case", PAD_CASES, ids=[f"pad{i}" for i in range(len(PAD_CASES))])
+def test_padded_conv_implicit_and_copied(gpu, monkeypatch, case, cfg, implicit):
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    monkeypatch.setenv("SPKV2_IMPLICIT_PAD", implicit)
+    n, c, h, w, m, k, s, pads, d, res = case
+    g = models.single_conv(n, c, h, w, m, k, s, dilation=d, act="Relu", residual=res, pads=pads)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as mdl:
+        for i, x in enumerate(xs):
+            mdl.set_input(i, x)
+        mdl.run()
+        got = mdl.get_output(0)
+        name = mdl.kernel_name(0)
+    if implicit == "1":
+        assert ",ipad" in name, name
+    else:
+        assert ",pad" in name and ",ipad" not in name, name
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 @pytest.mark.parametrize("cfg", F32_IGEMM_CFGS)
 @pytest.mark.parametrize("k", [136, 130])
 def test_gemm_every_tile_config(gpu, monkeypatch, cfg, k):
