@@ -1066,7 +1066,9 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     a.chk_W = gg.chk_W;
     a.chk_ph = gg.chk_ph;
     a.chk_pw = gg.chk_pw;
-    (gg.kvec ? t.kernel_kvec : gg.chk ? t.kernel_chk : t.kernel)<<<grid, dim3(256), 0, st>>>(a);
+    // 16-byte B loads need a 16-byte aligned source (a caller-bound input may not be)
+    const bool kvec = gg.kvec && (reinterpret_cast<uintptr_t>(xs) & 15) == 0;
+    (kvec ? t.kernel_kvec : gg.chk ? t.kernel_chk : t.kernel)<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_f32")) return rc;
     if (tc.splitk > 1) {
         const size_t total = static_cast<size_t>(g.M) * a.ws_ld;
