@@ -123,6 +123,7 @@ struct IgemmArgs {
     int M, OW, OHW, Ntot;
     int sh, sw;
     int x_img_stride;                // elements between images in x
+    int y_img_stride;                // elements between images in y and the residual
     int m_tiles, k_tiles, kt_per_split;
     int act;
     float alpha;
@@ -405,7 +406,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 const int n = nt * BN + (wn * TN + j) * 32 + row;
                 const int img = n / a.OHW;
                 const int sp = n - img * a.OHW;
-                obase[j] = n < a.Ntot ? (img * a.M * a.OHW + sp) * 4 : kOobOffset;
+                obase[j] = n < a.Ntot ? (img * a.y_img_stride + sp) * 4 : kOobOffset;
             }
             float *const any = a.y ? a.y : a.yp;
             const __amdgpu_buffer_rsrc_t yrs =
@@ -543,7 +544,7 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     const bool eown = tid < 256 && em < a.M && en < a.Ntot;
     const int eimg = eown ? en / a.OHW : 0;
     const int esp = en - eimg * a.OHW;
-    const size_t eyi = (static_cast<size_t>(eimg) * a.M + em) * a.OHW + esp;
+    const size_t eyi = static_cast<size_t>(eimg) * a.y_img_stride + static_cast<size_t>(em) * a.OHW + esp;
     const float ebias = eown && a.bias ? a.bias[em] : 0.0f;
     const float eres = eown && a.res ? a.res[eyi] : 0.0f;
 
@@ -631,7 +632,9 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
             const int img = (n + e) / OHW;
-            rv[e] = res ? res[(static_cast<size_t>(img) * M + m) * OHW + (n + e - img * OHW)] : 0.0f;
+            rv[e] = res ? res[static_cast<size_t>(img) * h.y_img_stride + static_cast<size_t>(m) * OHW +
+                              (n + e - img * OHW)]
+                        : 0.0f;
         }
         // up to 16 slices' loads in flight before the first add (one round
         // trip for splitk <= 16); the adds stay in slice order
@@ -651,7 +654,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             if (bias) o += bm;
             const int img = (n + e) / OHW;
             const int sp = n + e - img * OHW;
-            const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
+            const size_t yi = static_cast<size_t>(img) * h.y_img_stride + static_cast<size_t>(m) * OHW + sp;
             if (res) o += rv[e];
             o = apply_act(o, act);
             if (h.yp) {
@@ -668,10 +671,12 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
 // grid.x over the elements of a plane (32-bit index math), so small
 // batches still spread over the GPU.
 __global__ void __launch_bounds__(256) pad_nchw(const float *__restrict__ x, float *__restrict__ xp, unsigned planes,
-                                                int H, int W, int Hp, int Wp, int pt, int pl) {
+                                                unsigned C, size_t x_img, int H, int W, int Hp, int Wp, int pt,
+                                                int pl) {
     const unsigned plane_sz = static_cast<unsigned>(Hp * Wp);
     for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
-        const float *src = x + static_cast<size_t>(plane) * H * W;
+        // images x_img elements apart (more than C planes: a channel slice)
+        const float *src = x + (plane / C) * x_img + static_cast<size_t>(plane % C) * H * W;
         float *dst = xp + static_cast<size_t>(plane) * plane_sz;
         for (unsigned r = blockIdx.x * 256 + threadIdx.x; r < plane_sz; r += gridDim.x * 256) {
             const int hq = static_cast<int>(r / static_cast<unsigned>(Wp));
@@ -1000,10 +1005,18 @@ std::vector<int> build_koff(const GatherSpec &gs, int BK) {
 
 // Launches the implicit GEMM of configuration cfg with tile counts tc over
 // an already prepared (padded) B source, then the split-K epilogue.
+// y's layout when it is a channel slice of a larger buffer (a Concat's):
+// elements between images and the byte extent from y; 0 for the natural
+// M x OH x OW images (the residual, when there is one, always has those).
+struct YLayout {
+    int img = 0;
+    int bytes = 0;
+};
+
 static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
                         int x_bytes, int x_img_stride, const float *wpack, const int *koff, const float *bias,
                         const float *res, float *y, float alpha, float *ws, const GatherGeom &gg,
-                        const ConvPlan *handoff = nullptr) {
+                        const ConvPlan *handoff = nullptr, YLayout yl = YLayout{}) {
     const TileCfg &t = kCfgs[cfg];
     IgemmArgs a{};
     a.x = xs;
@@ -1039,7 +1052,8 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
         a.yp_pt = handoff->pad_pt;
         a.yp_pl = handoff->pad_pl;
     }
-    a.y_bytes = static_cast<int>(g.y_elems * 4);
+    a.y_bytes = yl.bytes > 0 ? yl.bytes : static_cast<int>(g.y_elems * 4);
+    a.y_img_stride = yl.img > 0 ? yl.img : g.M * a.OHW;
     a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
     const int tiles = tc.m_tiles * tc.n_tiles;
     if (t.skinny_waves > 0) {
@@ -1560,12 +1574,11 @@ uint8_t *plan_workspace(const Spkv2Context *ctx, const ConvPlan *p) {
 // x_img_stride: elements between consecutive "images" of the B source (a
 // Gemm with trans_a reads A as [K][rows]: stride 1).
 static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res,
-                          float *y, float alpha, int x_img_stride) {
+                          float *y, float alpha, int x_img_stride, int x_bytes, YLayout yl) {
     const ConvGeom &g = p->g;
     uint8_t *wsb = plan_workspace(ctx, p);
     if (p->workspace > 0 && !wsb) return SPKV2_E_UNSUPPORTED;
     const float *xs = x;
-    int x_bytes = static_cast<int>(g.x_elems * 4);
     // with the handoffs not live (a fault event armed, or the kernel registry
     // changed since prepare) every tensor is materialized and padded here
     const bool handoff = handoffs_live(ctx);
@@ -1580,7 +1593,8 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
         float *xp = reinterpret_cast<float *>(wsb);
         const unsigned planes = static_cast<unsigned>(g.N * g.C);
         hipLaunchKernelGGL(pad_nchw, plane_grid(static_cast<size_t>(p->Hp) * p->Wp, planes), dim3(256), 0,
-                           ctx->stream, x, xp, planes, g.H, g.W, p->Hp, p->Wp, p->pt, p->pl);
+                           ctx->stream, x, xp, planes, static_cast<unsigned>(g.C), static_cast<size_t>(x_img_stride),
+                           g.H, g.W, p->Hp, p->Wp, p->pt, p->pl);
         if (int rc = launch_status("pad_nchw")) return rc;
         xs = xp;
         x_bytes = static_cast<int>(static_cast<size_t>(planes) * p->Hp * p->Wp * 4);
@@ -1590,7 +1604,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
     const bool give = p->pad_out && handoff;
     return launch_igemm(ctx->stream, p->cfg, plan_counts(p), g, Wp, xs, x_bytes, x_img_stride,
                         static_cast<const float *>(p->wpack), static_cast<const int *>(p->ktab), bias, res,
-                        give && !p->y_needed ? nullptr : y, alpha, ws, p->gather, give ? p : nullptr);
+                        give && !p->y_needed ? nullptr : y, alpha, ws, p->gather, give ? p : nullptr, yl);
 }
 
 // Implicit padding.  A padded conv whose input no producer hands over in
@@ -1688,13 +1702,39 @@ static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, Con
 
 int run_igemm_f32(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, const float *res, float *y,
                   float alpha) {
-    return run_igemm_impl(ctx, p, x, bias, res, y, alpha, p->g.C * p->g.H * p->g.W);
+    return run_igemm_impl(ctx, p, x, bias, res, y, alpha, p->g.C * p->g.H * p->g.W, static_cast<int>(p->g.x_elems * 4),
+                          YLayout{});
 }
 
 // Gemm entry: no residual, caller-chosen row stride of the B source.
 int run_igemm_f32_strided(Spkv2Context *ctx, const ConvPlan *p, const float *x, const float *bias, float *y,
                           float alpha, int x_img_stride) {
-    return run_igemm_impl(ctx, p, x, bias, nullptr, y, alpha, x_img_stride);
+    return run_igemm_impl(ctx, p, x, bias, nullptr, y, alpha, x_img_stride, static_cast<int>(p->g.x_elems * 4),
+                          YLayout{});
+}
+
+// A conv node's run: its input and output through their channel-slice
+// views when they have them (a Concat's buffer; never with a residual, so
+// the residual keeps y's natural layout).
+static int run_igemm_node(Spkv2Context *ctx, const ConvPlan *p, const Spkv2NodeRecord *node) {
+    const ConvGeom &g = p->g;
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    int x_img = g.C * g.H * g.W, x_bytes = static_cast<int>(g.x_elems * 4);
+    if (const Spkv2TensorView *v = live_view(ctx, node->inputs[0])) {
+        x = reinterpret_cast<const float *>(v->base);
+        x_img = static_cast<int>(v->img_elems);
+        x_bytes = static_cast<int>(v->extent);
+    }
+    float *y = dptr<float>(ctx, node->outputs[0]);
+    YLayout yl;
+    if (const Spkv2TensorView *v = live_view(ctx, node->outputs[0])) {
+        if (g.has_res) return SPKV2_E_UNSUPPORTED;  // not set up that way
+        y = reinterpret_cast<float *>(v->base);
+        yl.img = static_cast<int>(v->img_elems);
+        yl.bytes = static_cast<int>(v->extent);
+    }
+    return run_igemm_impl(ctx, p, x, g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr,
+                          g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr, y, 1.0f, x_img, x_bytes, yl);
 }
 
 // The depthwise kernel takes group convs with one input channel per group and
@@ -1821,11 +1861,7 @@ int conv_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratch) {
     ConvPlan *plan = static_cast<ConvPlan *>(ctx->plans[node->id]);
     if (!plan) return SPKV2_E_UNSUPPORTED;  // prepare did not run for this node
     switch (plan->path) {
-    case CONV_IGEMM_F32:
-        return run_igemm_f32(ctx, plan, dptr<const float>(ctx, node->inputs[0]),
-                             plan->g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr,
-                             plan->g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr,
-                             dptr<float>(ctx, node->outputs[0]), 1.0f);
+    case CONV_IGEMM_F32: return run_igemm_node(ctx, plan, node);
     case CONV_DIRECT_F32: return run_direct(ctx, node, plan->g);
     case CONV_DW_F32: return run_dw(ctx, node, plan->g);
     case CONV_IGEMM_I8: return conv_i8_run(ctx, node, plan, nullptr);

@@ -70,6 +70,25 @@ __global__ void __launch_bounds__(256) binary_same4(const float4 *__restrict__ a
     }
 }
 
+// The same-shape op over image-strided operands (channel slices of a
+// Concat buffer): grid.y walks the images, grid.x the float4s of one image.
+template <int OP>
+__global__ void __launch_bounds__(256) binary_img4(const float4 *__restrict__ a, const float4 *__restrict__ b,
+                                                   float4 *__restrict__ y, unsigned images, size_t per4, size_t as4,
+                                                   size_t bs4, size_t ys4, int act) {
+    for (unsigned img = blockIdx.y; img < images; img += gridDim.y)
+        for (size_t j = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; j < per4;
+             j += static_cast<size_t>(gridDim.x) * 256) {
+            const float4 u = a[img * as4 + j], v = b[img * bs4 + j];
+            float4 r;
+            r.x = apply_act(bin<OP>(u.x, v.x), act);
+            r.y = apply_act(bin<OP>(u.y, v.y), act);
+            r.z = apply_act(bin<OP>(u.z, v.z), act);
+            r.w = apply_act(bin<OP>(u.w, v.w), act);
+            y[img * ys4 + j] = r;
+        }
+}
+
 template <int OP>
 __global__ void __launch_bounds__(256) binary_bcast(const float *__restrict__ a, const float *__restrict__ b,
                                                     float *__restrict__ y, size_t n, BcastDesc d, int act) {
@@ -591,6 +610,29 @@ int binary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const float *a = dptr<const float>(ctx, node->inputs[0]), *b = dptr<const float>(ctx, node->inputs[1]);
     float *y = dptr<float>(ctx, node->outputs[0]);
     hipStream_t s = ctx->stream;
+    const Spkv2TensorView *av = live_view(ctx, node->inputs[0]), *bv = live_view(ctx, node->inputs[1]),
+                          *yv = live_view(ctx, node->outputs[0]);
+    if (av || bv || yv) {
+        // an Add over channel slices of Concat buffers (same-shape NCHW,
+        // images a multiple of 4 elements, as set up at prepare)
+        if (node->op_type != SPKV2_OP_ADD || yr->rank != 4) return SPKV2_E_UNSUPPORTED;
+        const unsigned images = yr->shape[0];
+        const size_t per = elem_count(yr) / std::max(images, 1u);
+        const size_t as = av ? av->img_elems : per, bs = bv ? bv->img_elems : per, ys = yv ? yv->img_elems : per;
+        if (av) a = reinterpret_cast<const float *>(av->base);
+        if (bv) b = reinterpret_cast<const float *>(bv->base);
+        if (yv) y = reinterpret_cast<float *>(yv->base);
+        if (((per | as | bs | ys) & 3) != 0 ||
+            ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y)) & 15))
+            return SPKV2_E_UNSUPPORTED;
+        set_kernel_name(ctx, node, "binary_img4");
+        if (per == 0 || images == 0) return 0;
+        const dim3 grid(static_cast<unsigned>(std::min<size_t>((per / 4 + 255) / 256, 1024)), std::min(images, 65535u));
+        hipLaunchKernelGGL((binary_img4<BIN_ADD>), grid, dim3(256), 0, s, reinterpret_cast<const float4 *>(a),
+                           reinterpret_cast<const float4 *>(b), reinterpret_cast<float4 *>(y), images, per / 4, as / 4,
+                           bs / 4, ys / 4, act);
+        return launch_status("binary_img4");
+    }
     set_kernel_name(ctx, node, "binary");
     switch (node->op_type) {
     case SPKV2_OP_ADD: return launch_binary<BIN_ADD>(s, ar, br, yr, a, b, y, act);
@@ -655,15 +697,29 @@ int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     for (int i = axis + 1; i < yr->rank; i++) inner *= yr->shape[i];
     const size_t y_axis = yr->shape[axis];
     float *y = dptr<float>(ctx, node->outputs[0]);
+    size_t y_stride = y_axis * inner;
+    // channel-slice views (set up at prepare for axis 1): the output is the
+    // Concat buffer, and the inputs that are views into it are in place
+    const Spkv2TensorView *ov = live_view(ctx, node->outputs[0]);
+    if (ov) {
+        if (axis != 1) return SPKV2_E_UNSUPPORTED;
+        y = reinterpret_cast<float *>(ov->base);
+        y_stride = static_cast<size_t>(ov->img_elems);
+    }
     size_t axis_off = 0;
-    set_kernel_name(ctx, node, "concat");
+    set_kernel_name(ctx, node, ov ? "concat_views" : "concat");
     for (uint16_t i = 0; i < node->input_count; i++) {
         const Spkv2TensorRecord *xr = rec(ctx, node->inputs[i]);
         const float *x = dptr<const float>(ctx, node->inputs[i]);
         const size_t block = static_cast<size_t>(xr->shape[axis]) * inner;
+        size_t x_stride = block;
+        if (const Spkv2TensorView *xv = live_view(ctx, node->inputs[i])) {
+            x = reinterpret_cast<const float *>(xv->base);
+            x_stride = static_cast<size_t>(xv->img_elems);
+        }
         float *dst = y + axis_off * inner;
-        if (!(outer == 1 && dst == x) && outer * block > 0)
-            if (int rc = strided_block_copy(ctx->stream, x, dst, outer, block, block, 0, y_axis * inner)) return rc;
+        if (!((outer == 1 || x_stride == y_stride) && dst == x) && outer * block > 0)
+            if (int rc = strided_block_copy(ctx->stream, x, dst, outer, block, x_stride, 0, y_stride)) return rc;
         axis_off += xr->shape[axis];
     }
     return 0;

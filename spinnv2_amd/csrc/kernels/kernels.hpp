@@ -52,6 +52,10 @@ int topk_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, size_t block, size_t x_stride,
                        size_t x_base, size_t y_stride);
 
+// channel-slice views of Concats at batch > 1 (views.cpp), after every
+// node's prepare
+int setup_concat_views(Spkv2Context *ctx);
+
 // reliability helpers used by the executor
 int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);
 int minmax(hipStream_t s, const float *x, size_t n, float *dev_out4);

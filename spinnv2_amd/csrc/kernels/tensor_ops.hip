@@ -266,7 +266,7 @@ __global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, 
                                                    float *__restrict__ indices, size_t inner, int dim, int k,
                                                    int largest) {
     __shared__ uint32_t hist[256];
-    __shared__ uint32_t s_prefix, s_remaining, s_count, s_ambiguous;
+    __shared__ uint32_t s_prefix, s_remaining, s_count;
     __shared__ unsigned long long keys[kTopkMaxK];
     __shared__ HeapPair heap[kTopkMaxK];
     __shared__ float rowbuf[kTopkRowLds];
@@ -488,6 +488,12 @@ int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     for (int i = axis + 1; i < xr->rank; i++) inner *= xr->shape[i];
     const size_t x_axis = xr->shape[axis];
     size_t axis_offset = 0;
+    // every output a channel-slice view of the input (set up at prepare):
+    // the outputs already are the input's channel ranges
+    if (node->id < ctx->view_split.size() && ctx->view_split[node->id] && live_view(ctx, node->inputs[0])) {
+        set_kernel_name(ctx, node, "split_views");
+        return 0;
+    }
     set_kernel_name(ctx, node, "split");
     for (uint16_t k = 0; k < node->output_count; k++) {
         const Spkv2TensorRecord *yr = rec(ctx, node->outputs[k]);

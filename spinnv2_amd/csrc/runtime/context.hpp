@@ -20,6 +20,16 @@ struct Spkv2TensorSlot {
     uint8_t *data = nullptr;  // device address (or a caller-bound device buffer)
 };
 
+// A channel-slice view: an fp32 NCHW activation that lives as a channel
+// range of a Concat's device buffer instead of at its own arena offset, so
+// the Concat need not copy it.  img_elems: elements between images; extent:
+// bytes from base to the end of the tensor's last image.
+struct Spkv2TensorView {
+    uint8_t *base = nullptr;
+    int64_t img_elems = 0;
+    size_t extent = 0;
+};
+
 struct Spkv2Context {
     // ---- the package (host memory, zero-copy views into the blob) ----
     uint8_t *owned_model = nullptr;
@@ -109,6 +119,13 @@ struct Spkv2Context {
     // INT8 accumulator capture (test hook): per node, a device buffer that
     // each run of an int8 conv fills with its raw int32 accumulators
     std::vector<int32_t *> acc_capture;
+    // Channel-slice views set up at prepare (Concat along channels at batch
+    // > 1), in force only while the handoffs are: per tensor (base null:
+    // none), per node whether it is a Split whose outputs are all views of
+    // its input (nothing to copy), and the Concat buffers (owned).
+    std::vector<Spkv2TensorView> views;
+    std::vector<uint8_t> view_split;
+    std::vector<void *> view_buffers;
 };
 
 // ---- internal helpers shared by the runtime translation units ----
@@ -137,6 +154,13 @@ inline bool builtin_runs(const Spkv2Context *ctx, uint32_t node_id) {
 // the handoff relies on).  When they are not, every producer writes its
 // output and every consumer reads it, as the reference does.
 inline bool handoffs_live(const Spkv2Context *ctx) { return !ctx->fault_event.enabled && ctx->winners_match; }
+
+// The channel-slice view a built-in kernel reads or writes a tensor through
+// in this run, or null (the tensor is at its own slot).
+inline const Spkv2TensorView *live_view(const Spkv2Context *ctx, uint32_t tensor_id) {
+    if (tensor_id >= ctx->views.size() || !ctx->views[tensor_id].base || !handoffs_live(ctx)) return nullptr;
+    return &ctx->views[tensor_id];
+}
 void set_last_error(const char *what, hipError_t err);
 void set_last_error_text(const std::string &text);
 int hip_check(hipError_t err, const char *what);

@@ -169,6 +169,7 @@ void destroy(Spkv2Context *ctx) {
         if (ctx->dev_flag) (void)hipFree(ctx->dev_flag);
         for (int32_t *p : ctx->acc_capture)
             if (p) (void)hipFree(p);
+        for (void *p : ctx->view_buffers) (void)hipFree(p);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     }
     spkv2_platform_free(ctx->node_cache);
