@@ -351,17 +351,26 @@ __global__ void __launch_bounds__(256) avgpool_kernel(PoolArgs a) {
     }
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+// Wave-wide sum / max through DPP lane moves (no LDS round trips): an
+// inclusive scan within each 16-lane row (row_shr 1, 2, 4, 8), then row 0's
+// total into row 1 and row 2's into row 3 (row_bcast 15), then rows 0-1's
+// into rows 2-3 (row_bcast 31); lane 63 ends with the whole wave's, read
+// back as a scalar.  Lanes a move has no source for, or whose row it
+// leaves out, take the identity.
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce(float v) {
+    const int id = __float_as_int(MAX ? -INFINITY : 0.0f);
+    auto step = [&](float o) { v = MAX ? (o > v ? o : v) : v + o; };
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x111, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x112, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x114, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x118, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x142, 0xa, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x143, 0xc, 0xf, false)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
-__device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) {
-        const float o = __shfl_xor(v, off, 64);
-        v = o > v ? o : v;
-    }
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return wave_reduce<false>(v); }
+__device__ __forceinline__ float wave_max(float v) { return wave_reduce<true>(v); }
 
 // One wave per contiguous row of `len` elements.  MODE 0: mean of x/denom
 // terms (ReduceMean, reference reduce.c:37-40); 1: max (ReduceMax);
@@ -432,12 +441,12 @@ __global__ void __launch_bounds__(256) softmax_rows(const float *__restrict__ x,
     m = wave_max(m);
     float s = 0.0f;
     for (int i = lane; i < dim; i += 64) {
-        const float e = expf(xr[i] - m);
+        const float e = __expf(xr[i] - m);
         yr[i] = e;
         s += e;
     }
-    s = wave_sum(s);
-    for (int i = lane; i < dim; i += 64) yr[i] = yr[i] / s;
+    const float r = 1.0f / wave_sum(s);
+    for (int i = lane; i < dim; i += 64) yr[i] = yr[i] * r;
 }
 
 // Rows of at most 2048 values that are a multiple of 4 long: one wave per
@@ -466,16 +475,16 @@ __global__ void __launch_bounds__(256) softmax_rows_reg(const float *__restrict_
         if (t * 64 + lane < quads) {
 #pragma unroll
             for (int e = 0; e < 4; e++) {
-                v[t][e] = expf(v[t][e] - m);
+                v[t][e] = __expf(v[t][e] - m);
                 s += v[t][e];
             }
         }
     }
-    s = wave_sum(s);
+    const float r = 1.0f / wave_sum(s);
 #pragma unroll
     for (int t = 0; t < 8; t++) {
         const int q = t * 64 + lane;
-        if (q < quads) yr[q] = floatx4{v[t][0] / s, v[t][1] / s, v[t][2] / s, v[t][3] / s};
+        if (q < quads) yr[q] = floatx4{v[t][0] * r, v[t][1] * r, v[t][2] * r, v[t][3] * r};
     }
 }
 
@@ -492,11 +501,12 @@ __global__ void __launch_bounds__(256) softmax_strided(const float *__restrict__
         for (int d = 0; d < dim; d++) m = fmaxf(m, xc[static_cast<size_t>(d) * inner]);
         float s = 0.0f;
         for (int d = 0; d < dim; d++) {
-            const float e = expf(xc[static_cast<size_t>(d) * inner] - m);
+            const float e = __expf(xc[static_cast<size_t>(d) * inner] - m);
             yc[static_cast<size_t>(d) * inner] = e;
             s += e;
         }
-        for (int d = 0; d < dim; d++) yc[static_cast<size_t>(d) * inner] = yc[static_cast<size_t>(d) * inner] / s;
+        const float r = 1.0f / s;
+        for (int d = 0; d < dim; d++) yc[static_cast<size_t>(d) * inner] = yc[static_cast<size_t>(d) * inner] * r;
     }
 }
 
