@@ -966,7 +966,10 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     char key[256];
     snprintf(key, sizeof(key), "i8|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d", g.N, g.C, g.H, g.W, g.M, g.KH, g.KW,
              g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, g.has_bias ? 1 : 0, g.has_res ? 1 : 0, g.act);
-    if (tuned_lookup(key, cfg_out, split_out) && *cfg_out < kNumI8Cfgs) return true;
+    // a stored choice is taken only if this layer's K layout allows it (a
+    // tune DB written by another build may name another configuration)
+    if (tuned_lookup(key, cfg_out, split_out) && *cfg_out >= 0 && *cfg_out < kNumI8Cfgs && i8_cfg_fits(L, *cfg_out))
+        return true;
     const int Ntot = g.N * g.OH * g.OW;
     const int Kbytes = L.groups * 16;
     struct Cand {
