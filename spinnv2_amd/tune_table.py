@@ -10,6 +10,7 @@ times its candidates and appends its choice to the output file
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
     python -m spinnv2_amd.tune_table --int8-network [table.tune]
+    python -m spinnv2_amd.tune_table --f32-network [table.tune]
 
 INT8 entries (keys starting `i8|`) already in the committed table are kept
 unless --retune-int8 is given: the INT8 tuner times each layer alone with an
@@ -25,7 +26,9 @@ events per node, 3 warmup + 10 runs); a shape whose layout does not allow
 the configuration falls back to the tuner, which appends its own choice to
 the DB, so those shapes are left out of that configuration's figures.  A
 shape's entry changes when another configuration's summed node time over
-its nodes beats the current one by more than 2%.
+its nodes beats the current one by more than 2%.  --f32-network does the
+same for ResNet-101 b=64 over the fp32 tile configurations and hybrid
+schedules (F32_SWEEP).
 """
 
 from __future__ import annotations
@@ -93,33 +96,54 @@ def int8_key(g, n) -> str:
     """The INT8 tuner's key of a conv node (conv_i8.hip, tune_i8)."""
     x, w, y = g.shape(n.inputs[0]), g.tensors[n.inputs[1]].shape, g.shape(n.outputs[0])
     st, dl = n.attrs.get("strides", [1, 1]), n.attrs.get("dilations", [1, 1])
-    fa = n.attrs.get("fused_activation", 0)
-    act = {"Relu": 1, "SiLU": 2}.get(fa, 0) if isinstance(fa, str) else int(fa or 0)
     return (f"i8|{x[0]},{x[1]},{x[2]},{x[3]}|{w[0]},{w[2]},{w[3]},{y[2]},{y[3]},{st[0]},{st[1]},{dl[0]},{dl[1]}|"
-            f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{act}")
+            f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}")
 
 
-def _int8_child(blob: str, table: str, cfg: int, out: str) -> None:
-    """One configuration of the in-network sweep (cfg < 0: the table as is)."""
+def f32_key(g, n) -> str:
+    """The fp32 tuner's key of a group-1 conv node (conv_f32.hip, shape_key
+    and plan_igemm_f32's padded-input geometry)."""
+    N, C, H, W = g.shape(n.inputs[0])
+    M, _, KH, KW = g.tensors[n.inputs[1]].shape
+    OH, OW = g.shape(n.outputs[0])[2:]
+    sh, sw = n.attrs.get("strides", [1, 1])
+    dh, dw = n.attrs.get("dilations", [1, 1])
+    ph, pw = n.attrs.get("pads", [0, 0, 0, 0])[:2]
+    hspan, wspan = (OH - 1) * sh + (KH - 1) * dh + 1, (OW - 1) * sw + (KW - 1) * dw + 1
+    padded = ph > 0 or pw > 0 or hspan - ph > H or wspan - pw > W
+    Hp, Wp = (max(H + ph, hspan), max(W + pw, wspan)) if padded else (H, W)
+    return (f"conv|{N},{C},{H},{W}|{M},{KH},{KW},{OH},{OW},{sh},{sw},{dh}|{dw},{Hp},{Wp}|{C * Hp * Wp},"
+            f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}")
+
+
+def _act(n) -> int:
+    fa = n.attrs.get("fused_activation", 0)
+    return {"Relu": 1, "SiLU": 2}.get(fa, 0) if isinstance(fa, str) else int(fa or 0)
+
+
+def _sweep_child(blob: str, cand: str, out: str) -> None:
+    """One candidate of an in-network sweep: every key in blob + '.keys' set
+    to `cand` ("cfg split", or "table": the committed table as is) through a
+    private tune DB; writes each conv node's time and the keys that fell back
+    to the tuner (their layout does not allow the candidate)."""
     import json
 
     import numpy as np
 
-    if cfg >= 0:
+    keys = json.loads(Path(blob + ".keys").read_text())
+    if cand != "table":
         db = out + ".tune"
-        keys = json.loads(Path(blob + ".keys").read_text())
-        with open(db, "w") as f:
-            for k in keys:
-                f.write(f"{k} {cfg} 1\n")
+        Path(db).write_text("".join(f"{k} {cand}\n" for k in keys))
         os.environ["SPKV2_TUNE_TABLE"] = "0"
         os.environ["SPKV2_TUNE_DB"] = db
     from .runtime import DeviceBuffer, Model, load_library
+
+    meta = json.loads(Path(blob + ".ids").read_text())
+    lib = load_library()
+    m = Model(Path(blob).read_bytes(), lib=lib)
     from .spk import models
 
-    lib = load_library()
-    ids = json.loads(Path(blob + ".ids").read_text())
-    m = Model(Path(blob).read_bytes(), lib=lib)
-    x = models.make_input([64, 3, 224, 224])
+    x = models.make_input(meta["input"])
     buf = DeviceBuffer(x.nbytes, lib)
     buf.upload(np.ascontiguousarray(x))
     m.bind_input(0, buf)
@@ -131,24 +155,75 @@ def _int8_child(blob: str, table: str, cfg: int, out: str) -> None:
         m.run()
     lib.spkv2_device_synchronize()
     times = {}
-    for i in ids:
+    for i in meta["ids"]:
         ms, c = m.node_time(i)
         times[i] = ms / max(c, 1) * 1e3
     m.close()
     buf.free()
     fell_back = set()
-    if cfg >= 0:
+    if cand != "table":
         for line in Path(out + ".tune").read_text().splitlines()[len(keys):]:
             if line.split():
                 fell_back.add(line.split()[0])
     Path(out).write_text(json.dumps({"times": times, "fell_back": sorted(fell_back)}))
 
 
-def int8_network(table: Path) -> None:
+def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: str) -> None:
+    """Times every candidate (cfg, split) on the network in a process of its
+    own and rewrites the table entries of `keys` (node id -> key) whose
+    summed node time some candidate beats by more than 2%.  A candidate with
+    no key taking it ends the sweep (past the last configuration)."""
     import json
     import subprocess
     import tempfile
 
+    current = {}
+    for line in table.read_text().splitlines():
+        p = line.split()
+        if len(p) == 3:
+            current[p[0]] = (int(p[1]), int(p[2]))
+    allkeys = sorted(set(keys.values()))
+    runs = {}
+    with tempfile.TemporaryDirectory() as d:
+        bp = os.path.join(d, "net.spk")
+        Path(bp).write_bytes(blob)
+        Path(bp + ".ids").write_text(json.dumps({"ids": sorted(keys), "input": list(g.shape(g.inputs[0]))}))
+        Path(bp + ".keys").write_text(json.dumps(allkeys))
+        for cand in ["table", *[f"{c} {s}" for c, s in candidates]]:
+            out = os.path.join(d, "cand.json")
+            r = subprocess.run([sys.executable, "-m", "spinnv2_amd.tune_table", "--sweep-child", bp, cand, out],
+                               capture_output=True, text=True)
+            if r.returncode != 0:
+                raise RuntimeError(f"{label} sweep, candidate {cand}:\n{r.stderr[-2000:]}")
+            res = json.loads(Path(out).read_text())
+            if cand != "table" and set(res["fell_back"]) >= set(allkeys):
+                break
+            runs[cand] = res
+            print(f"{label}: candidate {cand} timed", flush=True)
+    base = runs.pop("table")
+    changed = {}
+    for key in allkeys:
+        nodes = [str(i) for i, k in keys.items() if k == key]
+        now = sum(base["times"][i] for i in nodes)
+        best, pick = now, None
+        for cand, r in runs.items():
+            if key in r["fell_back"]:
+                continue
+            t = sum(r["times"][i] for i in nodes)
+            if t < best:
+                best, pick = t, cand
+        if pick and tuple(map(int, pick.split())) != current.get(key) and best < 0.98 * now:
+            changed[key] = pick
+            print(f"{key}: {current.get(key)} -> {pick} ({now:.1f} -> {best:.1f} us over {len(nodes)} nodes)")
+    lines = []
+    for line in table.read_text().splitlines():
+        p = line.split()
+        lines.append(f"{p[0]} {changed[p[0]]}" if p and p[0] in changed else line)
+    table.write_text("".join(l + "\n" for l in lines))
+    print(f"{label}: {len(changed)} entries changed -> {table}")
+
+
+def int8_network(table: Path) -> None:
     from .spk import models, write_spk
     from .spk.quantize import calibrate_activation_scales, quantize_conv_weights
 
@@ -157,62 +232,31 @@ def int8_network(table: Path) -> None:
     act = calibrate_activation_scales(g1, samples)
     g = models.resnet(50, 64)
     blob = write_spk(g, "mi355x", quant_params=quantize_conv_weights(g) + act)
-    convs = [n for n in g.nodes if n.op_type == "Conv"]
-    keys = {n.id: int8_key(g, n) for n in convs}
-    current = {}
-    for line in table.read_text().splitlines():
-        p = line.split()
-        if len(p) == 3 and p[0].startswith("i8|64,"):
-            current[p[0]] = int(p[1])
-    runs = {}
-    with tempfile.TemporaryDirectory() as d:
-        bp = os.path.join(d, "net.spk")
-        Path(bp).write_bytes(blob)
-        Path(bp + ".ids").write_text(json.dumps([n.id for n in convs]))
-        Path(bp + ".keys").write_text(json.dumps(sorted(set(keys.values()))))
-        cfg = -1
-        while True:
-            out = os.path.join(d, f"cfg{cfg}.json")
-            r = subprocess.run([sys.executable, "-m", "spinnv2_amd.tune_table", "--int8-child", bp, str(table),
-                                str(cfg), out], capture_output=True, text=True)
-            if r.returncode != 0:
-                raise RuntimeError(f"int8 sweep, configuration {cfg}:\n{r.stderr[-2000:]}")
-            res = json.loads(Path(out).read_text())
-            # past the last configuration no shape takes the index (every
-            # configuration fits the 1x1 layers)
-            if cfg >= 0 and set(res["fell_back"]) >= set(keys.values()):
-                break
-            runs[cfg] = res
-            print(f"int8 network: configuration {cfg} timed", flush=True)
-            cfg += 1
-    base = runs.pop(-1)
-    changed = {}
-    for key in sorted(set(keys.values())):
-        nodes = [str(i) for i, k in keys.items() if k == key]
-        now = sum(base["times"][i] for i in nodes)
-        best, pick = now, current.get(key)
-        for c, r in runs.items():
-            if key in r["fell_back"]:
-                continue
-            t = sum(r["times"][i] for i in nodes)
-            if t < best:
-                best, pick = t, c
-        if pick != current.get(key) and best < 0.98 * now:
-            changed[key] = pick
-            print(f"{key}: {current.get(key)} -> {pick} ({now:.1f} -> {best:.1f} us over {len(nodes)} nodes)")
-    lines = []
-    for line in table.read_text().splitlines():
-        p = line.split()
-        lines.append(f"{p[0]} {changed[p[0]]} 1" if p and p[0] in changed else line)
-    table.write_text("".join(l + "\n" for l in lines))
-    print(f"{len(changed)} INT8 entries changed -> {table}")
+    keys = {n.id: int8_key(g, n) for n in g.nodes if n.op_type == "Conv"}
+    network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64")
+
+
+# fp32 candidates: every configuration but the skinny ones (batch-1 tiles)
+# whole-tile, and the hybrid schedules the tuner picks for ResNet-101 b=64
+# (1000 + slices per remaining tile) on the 64-row ones
+F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16)] + \
+            [(c, s) for c in (2, 6, 7) for s in (1004, 1008, 1016)] + [(6, 3)]
+
+
+def f32_network(table: Path) -> None:
+    from .spk import models, write_spk
+
+    g = models.resnet(101, 64)
+    blob = write_spk(g, "mi355x")
+    keys = {n.id: f32_key(g, n) for n in g.nodes if n.op_type == "Conv" and n.attrs.get("group", 1) == 1}
+    network_sweep(g, blob, keys, F32_SWEEP, table, "resnet101 b=64")
 
 
 if __name__ == "__main__":
-    if len(sys.argv) == 6 and sys.argv[1] == "--int8-child":
-        _int8_child(sys.argv[2], sys.argv[3], int(sys.argv[4]), sys.argv[5])
-    elif "--int8-network" in sys.argv[1:]:
+    if len(sys.argv) == 5 and sys.argv[1] == "--sweep-child":
+        _sweep_child(sys.argv[2], sys.argv[3], sys.argv[4])
+    elif "--int8-network" in sys.argv[1:] or "--f32-network" in sys.argv[1:]:
         rest = [a for a in sys.argv[1:] if not a.startswith("--")]
-        int8_network(Path(rest[0]) if rest else DEFAULT_OUT)
+        (int8_network if "--int8-network" in sys.argv[1:] else f32_network)(Path(rest[0]) if rest else DEFAULT_OUT)
     else:
         main()
