@@ -10,7 +10,7 @@ times its candidates and appends its choice to the output file
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
     python -m spinnv2_amd.tune_table --int8-network [table.tune]
-    python -m spinnv2_amd.tune_table --f32-network [table.tune]
+    python -m spinnv2_amd.tune_table --f32-network [--yolo] [table.tune]
 
 INT8 entries (keys starting `i8|`) already in the committed table are kept
 unless --retune-int8 is given: the INT8 tuner times each layer alone with an
@@ -27,8 +27,8 @@ the configuration falls back to the tuner, which appends its own choice to
 the DB, so those shapes are left out of that configuration's figures.  A
 shape's entry changes when another configuration's summed node time over
 its nodes beats the current one by more than 2%.  --f32-network does the
-same for ResNet-101 b=64 over the fp32 tile configurations and hybrid
-schedules (F32_SWEEP).
+same for ResNet-101 b=64 (or, with --yolo, YOLOv10n b=16) over the fp32
+tile configurations and hybrid schedules (F32_SWEEP).
 """
 
 from __future__ import annotations
@@ -117,8 +117,9 @@ def f32_key(g, n) -> str:
 
 
 def _act(n) -> int:
-    fa = n.attrs.get("fused_activation", 0)
-    return {"Relu": 1, "SiLU": 2}.get(fa, 0) if isinstance(fa, str) else int(fa or 0)
+    from .spk import format as F
+
+    return int(F.ACTIVATION[n.attrs.get("fused_activation")])
 
 
 def _sweep_child(blob: str, cand: str, out: str) -> None:
@@ -243,13 +244,14 @@ F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16)]
             [(c, s) for c in (2, 6, 7) for s in (1004, 1008, 1016)] + [(6, 3)]
 
 
-def f32_network(table: Path) -> None:
+def f32_network(table: Path, net: str = "resnet101") -> None:
     from .spk import models, write_spk
 
-    g = models.resnet(101, 64)
+    g = models.yolo_v10n(16) if net == "yolo" else models.resnet(101, 64)
     blob = write_spk(g, "mi355x")
     keys = {n.id: f32_key(g, n) for n in g.nodes if n.op_type == "Conv" and n.attrs.get("group", 1) == 1}
-    network_sweep(g, blob, keys, F32_SWEEP, table, "resnet101 b=64")
+    cands = F32_SWEEP + ([(c, s) for c in (14, 15, 16) for s in (1004, 1008, 1016)] if net == "yolo" else [])
+    network_sweep(g, blob, keys, cands, table, "yolov10n b=16" if net == "yolo" else "resnet101 b=64")
 
 
 if __name__ == "__main__":
@@ -257,6 +259,10 @@ if __name__ == "__main__":
         _sweep_child(sys.argv[2], sys.argv[3], sys.argv[4])
     elif "--int8-network" in sys.argv[1:] or "--f32-network" in sys.argv[1:]:
         rest = [a for a in sys.argv[1:] if not a.startswith("--")]
-        (int8_network if "--int8-network" in sys.argv[1:] else f32_network)(Path(rest[0]) if rest else DEFAULT_OUT)
+        table = Path(rest[0]) if rest else DEFAULT_OUT
+        if "--int8-network" in sys.argv[1:]:
+            int8_network(table)
+        else:
+            f32_network(table, "yolo" if "--yolo" in sys.argv[1:] else "resnet101")
     else:
         main()
