@@ -10,7 +10,7 @@ times its candidates and appends its choice to the output file
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
     python -m spinnv2_amd.tune_table --int8-network [table.tune]
-    python -m spinnv2_amd.tune_table --f32-network [--yolo] [table.tune]
+    python -m spinnv2_amd.tune_table --f32-network [--yolo | --b1] [table.tune]
 
 INT8 entries (keys starting `i8|`) already in the committed table are kept
 unless --retune-int8 is given: the INT8 tuner times each layer alone with an
@@ -27,8 +27,9 @@ the configuration falls back to the tuner, which appends its own choice to
 the DB, so those shapes are left out of that configuration's figures.  A
 shape's entry changes when another configuration's summed node time over
 its nodes beats the current one by more than 2%.  --f32-network does the
-same for ResNet-101 b=64 (or, with --yolo, YOLOv10n b=16) over the fp32
-tile configurations and hybrid schedules (F32_SWEEP).
+same for ResNet-101 b=64 (with --yolo YOLOv10n b=16, with --b1 ResNet-101
+b=1) over the fp32 tile configurations and schedules (F32_SWEEP,
+F32_SWEEP_B1).
 """
 
 from __future__ import annotations
@@ -169,11 +170,12 @@ def _sweep_child(blob: str, cand: str, out: str) -> None:
     Path(out).write_text(json.dumps({"times": times, "fell_back": sorted(fell_back)}))
 
 
-def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: str) -> None:
+def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: str, open_ended: bool = False) -> None:
     """Times every candidate (cfg, split) on the network in a process of its
     own and rewrites the table entries of `keys` (node id -> key) whose
-    summed node time some candidate beats by more than 2%.  A candidate with
-    no key taking it ends the sweep (past the last configuration)."""
+    summed node time some candidate beats by more than 2%.  With open_ended
+    (configuration indices counted up without a known end) a candidate no
+    key takes ends the sweep; otherwise it is only skipped."""
     import json
     import subprocess
     import tempfile
@@ -198,7 +200,9 @@ def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: st
                 raise RuntimeError(f"{label} sweep, candidate {cand}:\n{r.stderr[-2000:]}")
             res = json.loads(Path(out).read_text())
             if cand != "table" and set(res["fell_back"]) >= set(allkeys):
-                break
+                if open_ended:
+                    break
+                continue
             runs[cand] = res
             print(f"{label}: candidate {cand} timed", flush=True)
     base = runs.pop("table")
@@ -234,7 +238,7 @@ def int8_network(table: Path) -> None:
     g = models.resnet(50, 64)
     blob = write_spk(g, "mi355x", quant_params=quantize_conv_weights(g) + act)
     keys = {n.id: int8_key(g, n) for n in g.nodes if n.op_type == "Conv"}
-    network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64")
+    network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
 
 
 # fp32 candidates: every configuration but the skinny ones (batch-1 tiles)
@@ -244,14 +248,22 @@ F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16)]
             [(c, s) for c in (2, 6, 7) for s in (1004, 1008, 1016)] + [(6, 3)]
 
 
+# batch 1: every configuration, whole tiles and split-K (the skinny ones
+# split k over their waves instead)
+F32_SWEEP_B1 = [(c, s) for c in range(17) for s in (1, 2, 3, 4, 6, 8, 12, 16) if s == 1 or c not in (12, 13)]
+
+
 def f32_network(table: Path, net: str = "resnet101") -> None:
     from .spk import models, write_spk
 
-    g = models.yolo_v10n(16) if net == "yolo" else models.resnet(101, 64)
+    g = {"yolo": lambda: models.yolo_v10n(16), "resnet101_b1": lambda: models.resnet(101, 1)}.get(
+        net, lambda: models.resnet(101, 64))()
     blob = write_spk(g, "mi355x")
     keys = {n.id: f32_key(g, n) for n in g.nodes if n.op_type == "Conv" and n.attrs.get("group", 1) == 1}
-    cands = F32_SWEEP + ([(c, s) for c in (14, 15, 16) for s in (1004, 1008, 1016)] if net == "yolo" else [])
-    network_sweep(g, blob, keys, cands, table, "yolov10n b=16" if net == "yolo" else "resnet101 b=64")
+    cands = F32_SWEEP_B1 if net == "resnet101_b1" else \
+        F32_SWEEP + ([(c, s) for c in (14, 15, 16) for s in (1004, 1008, 1016)] if net == "yolo" else [])
+    network_sweep(g, blob, keys, cands, table, {"yolo": "yolov10n b=16", "resnet101_b1": "resnet101 b=1"}.get(
+        net, "resnet101 b=64"))
 
 
 if __name__ == "__main__":
@@ -263,6 +275,7 @@ if __name__ == "__main__":
         if "--int8-network" in sys.argv[1:]:
             int8_network(table)
         else:
-            f32_network(table, "yolo" if "--yolo" in sys.argv[1:] else "resnet101")
+            f32_network(table, "yolo" if "--yolo" in sys.argv[1:] else "resnet101_b1" if "--b1" in sys.argv[1:]
+                        else "resnet101")
     else:
         main()
