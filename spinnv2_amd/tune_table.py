@@ -9,7 +9,7 @@ times its candidates and appends its choice to the output file
 (SPKV2_TUNE_DB); the file is then sorted and de-duplicated.
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
-    python -m spinnv2_amd.tune_table --int8-network [table.tune]
+    python -m spinnv2_amd.tune_table --int8-network [--b1] [table.tune]
     python -m spinnv2_amd.tune_table --f32-network [--yolo | --b1] [table.tune]
 
 INT8 entries (keys starting `i8|`) already in the committed table are kept
@@ -228,17 +228,21 @@ def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: st
     print(f"{label}: {len(changed)} entries changed -> {table}")
 
 
-def int8_network(table: Path) -> None:
+def int8_network(table: Path, batch: int = 64) -> None:
     from .spk import models, write_spk
     from .spk.quantize import calibrate_activation_scales, quantize_conv_weights
 
     g1 = models.resnet(50, 1)
     samples = [models.make_input(g1.tensors[g1.inputs[0]].shape, 1000 + i) for i in range(16)]
     act = calibrate_activation_scales(g1, samples)
-    g = models.resnet(50, 64)
+    g = models.resnet(50, batch)
     blob = write_spk(g, "mi355x", quant_params=quantize_conv_weights(g) + act)
     keys = {n.id: int8_key(g, n) for n in g.nodes if n.op_type == "Conv"}
-    network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
+    if batch == 1:  # every configuration with split-K too (23 configurations)
+        network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (1, 2, 3, 4, 6, 8, 12, 16)], table,
+                      "int8 resnet50 b=1")
+    else:
+        network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
 
 
 # fp32 candidates: every configuration but the skinny ones (batch-1 tiles)
@@ -273,7 +277,7 @@ if __name__ == "__main__":
         rest = [a for a in sys.argv[1:] if not a.startswith("--")]
         table = Path(rest[0]) if rest else DEFAULT_OUT
         if "--int8-network" in sys.argv[1:]:
-            int8_network(table)
+            int8_network(table, 1 if "--b1" in sys.argv[1:] else 64)
         else:
             f32_network(table, "yolo" if "--yolo" in sys.argv[1:] else "resnet101_b1" if "--b1" in sys.argv[1:]
                         else "resnet101")
