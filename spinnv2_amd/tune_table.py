@@ -9,7 +9,7 @@ times its candidates and appends its choice to the output file
 (SPKV2_TUNE_DB); the file is then sorted and de-duplicated.
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
-    python -m spinnv2_amd.tune_table --int8-network [--b1] [table.tune]
+    python -m spinnv2_amd.tune_table --int8-network [--b1 | --splitk] [table.tune]
     python -m spinnv2_amd.tune_table --f32-network [--yolo | --b1] [table.tune]
 
 INT8 entries (keys starting `i8|`) already in the committed table are kept
@@ -241,6 +241,8 @@ def int8_network(table: Path, batch: int = 64) -> None:
     if batch == 1:  # every configuration with split-K too (23 configurations)
         network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (1, 2, 3, 4, 6, 8, 12, 16)], table,
                       "int8 resnet50 b=1")
+    elif "--splitk" in sys.argv[1:]:  # the 23 configurations with split-K 2, 3, 4
+        network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (2, 3, 4)], table, "int8 resnet50 b=64")
     else:
         network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
 
