@@ -103,6 +103,12 @@ struct PoolPlan {
     float q_inv_scale;
     int q_readers;
     bool y_needed;
+    // When the pooled input comes from an int8 conv with Relu that nothing
+    // else reads: that conv's epilogue quantizes it (consumers' scale, round
+    // half to even) into this unpadded NHWC buffer [N][H][W][C] (owned), and
+    // the pool takes the maximum of the int8 values (quantization is
+    // monotone, so that is the quantized maximum).
+    int8_t *q_src;
 };
 
 void pool_plan_free(void *p);

@@ -325,6 +325,44 @@ __global__ void __launch_bounds__(256) maxpool3s2_q8(const float *__restrict__ x
     *reinterpret_cast<uintx4 *>(dst) = uintx4{w[0], w[1], w[2], w[3]};
 }
 
+// The pooling of maxpool3s2_q8 over an input its producer already quantized
+// with the consumers' scale and round-half-even rounding (the pooled tensor
+// has no half-away tail when its channels are a multiple of 64): int8 NHWC
+// [N][H][W][C] in, the consumers' zero-padded NHWC int8 buffer out.  The
+// quantization is monotone, so the maximum of the quantized in-bounds taps
+// is the quantized maximum of the fp32 taps, byte for byte.  One thread per
+// (output pixel, 16 channels): 9 taps of 16 bytes, one 16-byte store.
+__global__ void __launch_bounds__(256) maxpool3s2_i8(const int8_t *__restrict__ xq_in, int8_t *__restrict__ xq,
+                                                     unsigned pixels, int C16, int H, int W, int OH, int OW, int Hp,
+                                                     int Wp, int Cp, int pt, int pl) {
+    typedef signed char char16 __attribute__((ext_vector_type(16)));
+    const size_t total = static_cast<size_t>(pixels) * C16;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * 256) {
+        const int c16 = static_cast<int>(i % C16);
+        const size_t pix = i / C16;
+        const int ow = static_cast<int>(pix % OW);
+        const size_t t = pix / OW;
+        const int oh = static_cast<int>(t % OH);
+        const size_t img = t / OH;
+        char16 m = static_cast<char16>(static_cast<signed char>(-128));
+#pragma unroll
+        for (int kh = 0; kh < 3; kh++) {
+            const int ih = 2 * oh - 1 + kh;
+            if (ih < 0 || ih >= H) continue;
+#pragma unroll
+            for (int kw = 0; kw < 3; kw++) {
+                const int iw = 2 * ow - 1 + kw;
+                if (iw < 0 || iw >= W) continue;
+                const char16 v = *reinterpret_cast<const char16 *>(
+                    xq_in + ((img * H + ih) * W + iw) * (static_cast<size_t>(C16) * 16) + c16 * 16);
+                m = __builtin_elementwise_max(m, v);
+            }
+        }
+        *reinterpret_cast<char16 *>(xq + ((img * Hp + oh + pt) * Wp + ow + pl) * Cp + c16 * 16) = m;
+    }
+}
+
 // reference pool/avgpool.c:21-45: mean over the in-bounds taps
 __global__ void __launch_bounds__(256) avgpool_kernel(PoolArgs a) {
     const size_t total = static_cast<size_t>(a.N) * a.C * a.OH * a.OW;
@@ -763,8 +801,10 @@ static bool is_pool3s2_x4(const PoolArgs &p) {
 }
 
 void pool_plan_free(void *p) {
-    // q_out belongs to the first consuming conv
-    delete static_cast<PoolPlan *>(p);
+    // q_out belongs to the first consuming conv, q_src to this plan
+    PoolPlan *plan = static_cast<PoolPlan *>(p);
+    if (plan->q_src) (void)hipFree(plan->q_src);
+    delete plan;
 }
 
 // A MaxPool that the fused pooling + int8 quantization kernel can run gets a
@@ -786,6 +826,63 @@ int maxpool_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) 
     return 0;
 }
 
+// After every node's prepare: a MaxPool whose output every reader takes in
+// int8 (no fp32 output needed) and whose input is the only output of an
+// int8 conv with Relu, read by nothing else, gets that input in int8: the
+// conv's epilogue quantizes it with the pool consumers' scale (their
+// rounding is half to even throughout: 64-channel planes leave no tail)
+// into the plan's NHWC buffer, and the conv skips its fp32 output.  Relu
+// keeps NaN out (the fp32 pool would skip a NaN tap; its int8 value is 0).
+// Off for protected packages and under SPKV2_I8_HANDOFF=0, bypassed like
+// every handoff while handoffs_live() is false.
+int setup_pool_int8_inputs(Spkv2Context *ctx) {
+    if (ctx->protection_count > 0) return 0;
+    if (const char *e = getenv("SPKV2_I8_HANDOFF"))
+        if (e[0] == '0') return 0;
+    for (uint32_t id = 0; id < ctx->header.num_nodes; id++) {
+        const Spkv2NodeRecord *node = &ctx->node_records[id];
+        if (node->op_type != SPKV2_OP_MAXPOOL || !builtin_runs(ctx, id) || ctx->plan_dtors[id] != pool_plan_free) continue;
+        PoolPlan *q = static_cast<PoolPlan *>(ctx->plans[id]);
+        PoolArgs p;
+        if (!q || !q->q_out || q->y_needed || q->q_src || pool_args(ctx, node, &p) != 0) continue;
+        if (!is_pool3s2_x4(p) || p.C % 64 != 0 || q->q_split < p.C * p.OH * p.OW) continue;
+        const uint32_t t = node->inputs[0];
+        const Spkv2NodeRecord *prod = nullptr;
+        int readers = 0;
+        for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+            const Spkv2NodeRecord *n = &ctx->node_records[i];
+            for (uint16_t k = 0; k < n->input_count; k++)
+                if (n->inputs[k] == t) readers++;
+            for (uint16_t k = 0; k < n->output_count; k++)
+                if (n->outputs[k] == t) prod = n;
+        }
+        bool is_output = false;
+        for (size_t i = 0; i < ctx->output_count; i++)
+            if (ctx->output_ids[i] == t) is_output = true;
+        if (!prod || prod->id >= id || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1 || readers != 1 ||
+            is_output || !builtin_runs(ctx, prod->id) || ctx->plan_dtors[prod->id] != conv_plan_free)
+            continue;
+        ConvPlan *cp = static_cast<ConvPlan *>(ctx->plans[prod->id]);
+        if (!cp || cp->path != CONV_IGEMM_I8 || cp->q_out || cp->g.act != 1 || cp->g.M != p.C || cp->g.N != p.N ||
+            cp->g.OH != p.H || cp->g.OW != p.W)
+            continue;
+        const size_t bytes = static_cast<size_t>(p.N) * p.H * p.W * p.C;
+        if (bytes >= 0x7fff0000ULL) continue;  // the epilogue's byte offsets are 31-bit
+        if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&q->q_src), bytes), "hipMalloc int8 pool input"))
+            return rc;
+        cp->q_out = q->q_src;
+        cp->q_Hp = p.H;
+        cp->q_Wp = p.W;
+        cp->q_Cp = p.C;
+        cp->q_pt = cp->q_pl = 0;
+        cp->q_split = 0x7fffffff;  // round half to even everywhere
+        cp->q_inv_scale = q->q_inv_scale;
+        cp->q_readers = 1;
+        cp->y_needed = false;
+    }
+    return 0;
+}
+
 int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     PoolArgs p;
     if (int rc = pool_args(ctx, node, &p)) return rc;
@@ -797,6 +894,17 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const PoolPlan *q = ctx->plan_dtors[node->id] == pool_plan_free
                             ? static_cast<const PoolPlan *>(ctx->plans[node->id])
                             : nullptr;
+    if (q && q->q_out && q->q_src && handoffs_live(ctx) && is_pool3s2_x4(p) && p.C % 64 == 0) {
+        // the producer quantized the input for this pool's consumers
+        set_kernel_name(ctx, node, "maxpool3s2_i8");
+        const size_t pixels = static_cast<size_t>(p.N) * p.OH * p.OW;
+        const size_t work = pixels * (p.C / 16);
+        if (pixels > 0xffffffffULL) return SPKV2_E_UNSUPPORTED;
+        hipLaunchKernelGGL(maxpool3s2_i8, dim3(grid_for(work, 256)), dim3(256), 0, ctx->stream, q->q_src, q->q_out,
+                           static_cast<unsigned>(pixels), p.C / 16, p.H, p.W, p.OH, p.OW, q->q_Hp, q->q_Wp, q->q_Cp,
+                           q->q_pt, q->q_pl);
+        return launch_status("maxpool");
+    }
     if (q && q->q_out && handoffs_live(ctx) && is_pool3s2_x4(p) && p.C % 64 == 0) {
         set_kernel_name(ctx, node, q->y_needed ? "maxpool3s2_q8+y" : "maxpool3s2_q8");
         const dim3 grid(static_cast<unsigned>((p.OH * p.OW + 63) / 64), static_cast<unsigned>(p.C / 64),

@@ -55,6 +55,8 @@ int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, si
 // channel-slice views of Concats at batch > 1 (views.cpp), after every
 // node's prepare
 int setup_concat_views(Spkv2Context *ctx);
+// int8 conv -> MaxPool -> int8 convs: the conv hands the pool int8 (eltwise.hip)
+int setup_pool_int8_inputs(Spkv2Context *ctx);
 
 // reliability helpers used by the executor
 int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);

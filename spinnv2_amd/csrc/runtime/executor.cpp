@@ -426,6 +426,7 @@ extern "C" int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t
             if (ws > workspace) workspace = ws;
         }
         if (int rc = spk::kern::setup_concat_views(ctx)) return rc;
+        if (int rc = spk::kern::setup_pool_int8_inputs(ctx)) return rc;
         if (workspace > 0) {
             if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&ctx->workspace), workspace), "hipMalloc workspace"))
                 return rc;

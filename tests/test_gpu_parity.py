@@ -765,9 +765,10 @@ POOL_CASES = [([2, 16, 24, 32], 64, False, False), ([1, 16, 20, 24], 128, True, 
 @pytest.mark.parametrize("case", range(len(POOL_CASES)))
 def test_int8_maxpool_handoff_bit_exact(gpu, monkeypatch, case, handoff):
     """A MaxPool read by int8 convs quantizes its output for them in the
-    pooling kernel (fp32 written only where something else reads it):
-    every output bit-exact against the oracle, eager and with a fault event
-    armed (then the pool writes fp32 and each conv quantizes)."""
+    pooling kernel (fp32 written only where something else reads it), and
+    when only int8 convs read it, its producing int8 conv hands it int8 in
+    turn: every output bit-exact against the oracle, eager and with a fault
+    event armed (then the pool writes fp32 and each conv quantizes)."""
     from spinnv2_amd.runtime import FaultEvent, Model
 
     monkeypatch.setenv("SPKV2_I8_HANDOFF", handoff)
@@ -791,7 +792,9 @@ def test_int8_maxpool_handoff_bit_exact(gpu, monkeypatch, case, handoff):
         m.run()
         armed = [m.get_output(i) for i in range(n_out)]
     if handoff == "1":
-        assert pool_name == ("maxpool3s2_q8+y" if third or pool_out else "maxpool3s2_q8"), pool_name
+        # with no fp32 reader of the pooled tensor, the first conv also hands
+        # the pool its input in int8 (pooling quantized values)
+        assert pool_name == ("maxpool3s2_q8+y" if third or pool_out else "maxpool3s2_i8"), pool_name
         assert ",handoff" in names[1] and ",shared" in names[2], names
     else:
         assert pool_name == "maxpool3s2_x4", pool_name
