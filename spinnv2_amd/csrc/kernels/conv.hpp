@@ -86,6 +86,7 @@ struct ConvPlan {
     // conv: producer side (not owned) and consumer side (owned).
     float *pad_out;
     int pad_Hp, pad_Wp, pad_pt, pad_pl;
+    int pad_m0, pad_C;  // producer side: only channels pad_m0 .. + pad_C - 1 go over (pad_C 0: all)
     float *pad_in;
 };
 

@@ -131,6 +131,7 @@ struct IgemmArgs {
     // input (NCHW, Hp x Wp planes); y may then be null (no other reader)
     float *__restrict__ yp;
     int yp_bytes, yp_Wp, yp_pt, yp_pl, yp_plane;
+    int yp_m0, yp_C;  // the handed-off channels: m0 .. m0 + C - 1 of y, the target's channels 0 .. C - 1
     // skinny kernel: k = tap * sk_C + c (a tap's channels consecutive);
     // channel c of a tap is c * sk_cstride elements past channel 0, tap
     // (kh, kw) = (tap / sk_KW, tap % sk_KW) kh * sk_tap_h + kw * sk_tap_w
@@ -427,7 +428,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                 const int sp = n - img * a.OHW;
                 const int oh = sp / a.OW;
                 const int ow = sp - oh * a.OW;
-                pbase[j] = n < a.Ntot ? (img * a.M * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl) * 4
+                pbase[j] = n < a.Ntot ? (img * a.yp_C * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl) * 4
                                       : kOobOffset;
             }
             // one 32x32 block at a time: its 16 bias and 16 residual loads are
@@ -466,9 +467,11 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                     if (a.yp) {
 #pragma unroll
                         for (int r = 0; r < 16; r++) {
-                            const int m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), prs,
-                                                                  m < a.M ? pbase[j] + m * plane4 : kOobOffset, 0, 0);
+                            const unsigned mc = static_cast<unsigned>(mrow[i] + 8 * (r >> 2) + (r & 3) - a.yp_m0);
+                            __builtin_amdgcn_raw_buffer_store_b32(
+                                __float_as_uint(v[r]), prs,
+                                mc < static_cast<unsigned>(a.yp_C) ? pbase[j] + static_cast<int>(mc) * plane4 : kOobOffset,
+                                0, 0);
                         }
                     }
                     if (a.y) {
@@ -599,10 +602,11 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
         if (a.bias) v += ebias;
         if (a.res) v += eres;
         v = apply_act(v, a.act);
-        if (a.yp) {
+        if (a.yp && static_cast<unsigned>(em - a.yp_m0) < static_cast<unsigned>(a.yp_C)) {
             const int oh = esp / a.OW;
             const int ow = esp - oh * a.OW;
-            a.yp[(static_cast<size_t>(eimg) * a.M + em) * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl] = v;
+            a.yp[(static_cast<size_t>(eimg) * a.yp_C + em - a.yp_m0) * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow +
+                 a.yp_pl] = v;
         }
         if (a.y) a.y[eyi] = v;
     }
@@ -657,9 +661,10 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             const size_t yi = static_cast<size_t>(img) * h.y_img_stride + static_cast<size_t>(m) * OHW + sp;
             if (res) o += rv[e];
             o = apply_act(o, act);
-            if (h.yp) {
+            if (h.yp && static_cast<unsigned>(m - h.yp_m0) < static_cast<unsigned>(h.yp_C)) {
                 const int oh = sp / h.OW, ow = sp - (sp / h.OW) * h.OW;
-                h.yp[(static_cast<size_t>(img) * M + m) * h.yp_plane + (oh + h.yp_pt) * h.yp_Wp + ow + h.yp_pl] = o;
+                h.yp[(static_cast<size_t>(img) * h.yp_C + m - h.yp_m0) * h.yp_plane + (oh + h.yp_pt) * h.yp_Wp + ow +
+                     h.yp_pl] = o;
             }
             if (y) y[yi] = o;
         }
@@ -1047,7 +1052,9 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     if (handoff) {
         a.yp = handoff->pad_out;
         a.yp_plane = handoff->pad_Hp * handoff->pad_Wp;
-        a.yp_bytes = static_cast<int>(static_cast<size_t>(g.N) * g.M * a.yp_plane * 4);
+        a.yp_m0 = handoff->pad_C > 0 ? handoff->pad_m0 : 0;
+        a.yp_C = handoff->pad_C > 0 ? handoff->pad_C : g.M;
+        a.yp_bytes = static_cast<int>(static_cast<size_t>(g.N) * a.yp_C * a.yp_plane * 4);
         a.yp_Wp = handoff->pad_Wp;
         a.yp_pt = handoff->pad_pt;
         a.yp_pl = handoff->pad_pl;
@@ -1657,7 +1664,9 @@ static int use_implicit_padding(ConvPlan *plan) {
 }
 
 // fp32 handoff.  When this padded conv's input is the only output of an
-// earlier fp32 implicit-GEMM conv, that conv stores its result straight into
+// earlier fp32 implicit-GEMM conv, or one output of a channel Split of such
+// a conv's output (then that conv stores only the Split output's channel
+// range), that conv stores its result straight into
 // a zero-padded buffer owned by this plan (halo zeroed once here, never
 // written), and this conv skips its padding pass.  The producer still writes
 // the unpadded tensor when anything else reads it.  Packages with a
@@ -1677,13 +1686,34 @@ static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, Con
             for (uint16_t k = 0; k < n->output_count; k++)
                 if (n->outputs[k] == t) prod = n;
     }
+    // through a channel Split (a C2f block's halves): the conv whose output
+    // the Split cuts hands over the channel range of this conv's input
+    int m0 = 0;
+    bool via_split = false;
+    if (prod && prod->op_type == SPKV2_OP_SPLIT && prod->input_count >= 1 && builtin_runs(ctx, prod->id)) {
+        Spkv2AttrRecord attr;
+        const Spkv2TensorRecord *sr = rec(ctx, prod->inputs[0]);
+        if (spkv2_ctx_get_attr(ctx, prod, &attr) != 0 || sr->rank != 4 || (attr.axis < 0 ? attr.axis + 4 : attr.axis) != 1)
+            return 0;
+        for (uint16_t k = 0; k < prod->output_count && prod->outputs[k] != t; k++) m0 += rec(ctx, prod->outputs[k])->shape[1];
+        const uint32_t s_in = prod->inputs[0];
+        const Spkv2NodeRecord *sp = prod;
+        prod = nullptr;
+        for (uint32_t i = 0; i < sp->id; i++) {
+            const Spkv2NodeRecord *n = &ctx->node_records[i];
+            for (uint16_t k = 0; k < n->output_count; k++)
+                if (n->outputs[k] == s_in) prod = n;
+        }
+        via_split = true;
+    }
     if (!prod || prod->op_type != SPKV2_OP_CONV || prod->output_count != 1) return 0;
     if (!builtin_runs(ctx, prod->id) || !builtin_runs(ctx, node->id)) return 0;  // a user kernel runs one end
     if (ctx->plan_dtors[prod->id] != conv_plan_free) return 0;
     ConvPlan *pp = static_cast<ConvPlan *>(ctx->plans[prod->id]);
     if (!pp || pp->path != CONV_IGEMM_F32 || pp->pad_out) return 0;
     const ConvGeom &g = plan->g;
-    if (pp->g.N != g.N || pp->g.M != g.C || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
+    if (pp->g.N != g.N || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
+    if (via_split ? m0 + g.C > pp->g.M : pp->g.M != g.C) return 0;
     bool is_output = false;
     for (size_t i = 0; i < ctx->output_count; i++)
         if (ctx->output_ids[i] == t) is_output = true;
@@ -1696,7 +1726,9 @@ static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, Con
     pp->pad_Wp = plan->Wp;
     pp->pad_pt = plan->pt;
     pp->pad_pl = plan->pl;
-    pp->y_needed = readers > 1 || is_output;
+    pp->pad_m0 = m0;
+    pp->pad_C = via_split ? g.C : 0;
+    pp->y_needed = via_split || readers > 1 || is_output;  // through a Split: the Split reads all of it
     return 0;
 }
 

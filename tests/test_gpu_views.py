@@ -152,3 +152,29 @@ def test_yolo_v10n_views_against_oracle(gpu, monkeypatch, batch):
     want = [np.asarray(o) for o in OracleExecutor(blob).run(*xs)]
     for n in range(batch):  # anchor indices repeat across images: one image at a time
         check_detections([a.reshape(w.shape)[n] for a, w in zip(got, want)], [w[n] for w in want])
+
+
+def test_split_pad_handoff_bit_identical(gpu, monkeypatch):
+    """A padded 3x3 conv reading one output of a channel Split takes its
+    zero-padded input from the conv the Split cuts (that conv stores the
+    channel range into it): every output equals the copying path bit for
+    bit, with and without the channel-slice views."""
+    g = _c2f_graph(batch=2, widths=(32, 64))
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    split_outs = {t for n in g.nodes if n.op_type == "Split" for t in n.outputs}
+    readers = [n.id for n in g.nodes if n.op_type == "Conv" and n.inputs[0] in split_outs]
+    assert readers
+    outs = {}
+    for views in ("1", "0"):
+        monkeypatch.setenv("SPKV2_CONCAT_VIEWS", views)
+        for flag in ("1", "0"):
+            monkeypatch.setenv("SPKV2_PAD_HANDOFF", flag)
+            out, names = _run(blob, xs, len(g.nodes))
+            outs[views, flag] = out
+            if flag == "1":
+                assert all(names[i].endswith("+handoff") for i in readers), [names[i] for i in readers]
+            else:
+                assert not any(names[i].endswith("+handoff") for i in readers)
+    for k, v in outs.items():
+        np.testing.assert_array_equal(v.view(np.uint32), outs["0", "0"].view(np.uint32), err_msg=str(k))
