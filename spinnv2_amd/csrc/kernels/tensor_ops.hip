@@ -192,7 +192,7 @@ __global__ void __launch_bounds__(256) gather_elements_kernel(const float *__res
 // ---------------------------------------------------------------- TopK
 
 constexpr int kTopkMaxK = 1024;
-constexpr int kTopkRowLds = 16384;  // rows up to this length are staged in LDS for the heap replay
+constexpr int kTopkRowLds = 16384;  // rows up to this length are staged in LDS
 
 // order-preserving key of a float: larger float -> larger unsigned
 __device__ __forceinline__ uint32_t fkey(float v) {
@@ -205,104 +205,207 @@ struct HeapPair {
     uint32_t idx;
 };
 
-// The reference's selection, replayed exactly by one thread (used only when
-// values tie across the k-th place, where the heap's history decides which
-// of the tied elements survive): heap of the first k, sift-down from k/2-1,
-// then every later element replaces the root when strictly better
-// (reference tensor/topk.c:71-101).
-// `row` holds the row's values (LDS when it fits, else the input itself with
-// stride `inner`).  Run by one wave: lane 0 builds and sifts the heap, and
-// the wave scans 64 elements at a time for the next one that enters (strictly
-// better than the current root), so runs of elements that cannot enter cost
-// one ballot; after each insertion the rest of the 64 are checked against
-// the new root, which keeps the reference's element-by-element order.
-__device__ void topk_heap_replay(const float *__restrict__ row, size_t inner, int dim, int k, int largest,
-                                 HeapPair *h, int lane) {
-    auto better = [&](float a, float b) { return largest ? (a < b) : (a > b); };  // "a sinks below b"
-    auto sift = [&](int i) {
-        for (;;) {
-            int l = 2 * i + 1, r = 2 * i + 2, m = i;
-            if (l < k && better(h[l].v, h[m].v)) m = l;
-            if (r < k && better(h[r].v, h[m].v)) m = r;
-            if (m == i) break;
-            const HeapPair t = h[i];
-            h[i] = h[m];
-            h[m] = t;
-            i = m;
+// The reference's sift-down from node i of a heap of n (tensor/topk.c:8-30):
+// the smaller child (the larger one for largest = 0) moves up while it is
+// strictly better-placed than the sifted element, the left child winning
+// ties.  The sifted element is carried down and stored once.
+__device__ __forceinline__ void topk_sift(HeapPair *h, int n, int i, int largest) {
+    const HeapPair e = h[i];
+    for (;;) {
+        const int l = 2 * i + 1;
+        if (l >= n) break;
+        const int r = l + 1;
+        // both children in one round trip (the right one clamped into the heap)
+        const HeapPair cl = h[l];
+        const HeapPair cr = h[min(r, n - 1)];
+        int m = i;
+        HeapPair mv = e;
+        if (largest ? (cl.v < mv.v) : (cl.v > mv.v)) {
+            m = l;
+            mv = cl;
         }
-    };
-    if (lane == 0) {
-        for (int d = 0; d < k; d++) h[d] = HeapPair{row[static_cast<size_t>(d) * inner], static_cast<uint32_t>(d)};
-        for (int i = k / 2 - 1; i >= 0; i--) sift(i);
-    }
-    __builtin_amdgcn_wave_barrier();
-    float root = h[0].v;
-    for (int d0 = k; d0 < dim; d0 += 64) {
-        const int d = d0 + lane;
-        const bool live = d < dim;
-        const float v = live ? row[static_cast<size_t>(d) * inner] : 0.0f;
-        unsigned long long m = __ballot(live && (largest ? (v > root) : (v < root)));
-        while (m) {
-            const int j = __ffsll(static_cast<long long>(m)) - 1;
-            const float vj = __shfl(v, j);
-            if (lane == 0) {
-                h[0] = HeapPair{vj, static_cast<uint32_t>(d0 + j)};
-                sift(0);
-            }
-            __builtin_amdgcn_wave_barrier();
-            root = h[0].v;
-            m = __ballot(live && lane > j && (largest ? (v > root) : (v < root)));
+        if (r < n && (largest ? (cr.v < mv.v) : (cr.v > mv.v))) {
+            m = r;
+            mv = cr;
         }
+        if (m == i) break;
+        h[i] = mv;
+        i = m;
     }
+    h[i] = e;
 }
 
-// One workgroup per (outer, inner) row.  Radix select over order-preserving
-// keys finds the k-th best value T; when exactly k elements are at least as
-// good as T (no tie straddles the k-th place, the usual case) they are the
-// reference's selection; otherwise the reference's heap is replayed.  The
-// selection is then sorted by (value, best first; index ascending), the
-// reference's comparator (tensor/topk.c:28-41), with a bitonic sort in LDS.
-__global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, float *__restrict__ values,
-                                                   float *__restrict__ indices, size_t inner, int dim, int k,
-                                                   int largest) {
+// The reference's insertion (tensor/topk.c:87-92 and 97-101): e replaces
+// the root and is sifted down (topk_sift's rule), two levels per round trip
+// to LDS (a node's children and grandchildren are read together; only the
+// path's nodes are written).  Returns the value left at the root.
+__device__ __forceinline__ float topk_sift_root(HeapPair *h, int n, HeapPair e, int largest) {
+    auto above = [&](float a, float b) { return largest ? (a < b) : (a > b); };  // a belongs above b
+    int i = 0;
+    float rootv = e.v;
+    for (;;) {
+        const int l = 2 * i + 1;
+        if (l >= n) break;
+        const int g = 2 * l + 1;  // children of l: g, g + 1; of l + 1: g + 2, g + 3
+        const HeapPair c0 = h[l], c1 = h[min(l + 1, n - 1)];
+        const HeapPair g0 = h[min(g, n - 1)], g1 = h[min(g + 1, n - 1)];
+        const HeapPair g2 = h[min(g + 2, n - 1)], g3 = h[min(g + 3, n - 1)];
+        int m = i;
+        HeapPair mv = e;
+        if (above(c0.v, mv.v)) {
+            m = l;
+            mv = c0;
+        }
+        if (l + 1 < n && above(c1.v, mv.v)) {
+            m = l + 1;
+            mv = c1;
+        }
+        if (m == i) break;
+        h[i] = mv;
+        if (i == 0) rootv = mv.v;
+        const bool left = m == l;
+        i = m;
+        const int l2 = 2 * i + 1;
+        if (l2 >= n) break;
+        const HeapPair d0 = left ? g0 : g2, d1 = left ? g1 : g3;
+        m = i;
+        mv = e;
+        if (above(d0.v, mv.v)) {
+            m = l2;
+            mv = d0;
+        }
+        if (l2 + 1 < n && above(d1.v, mv.v)) {
+            m = l2 + 1;
+            mv = d1;
+        }
+        if (m == i) break;
+        h[i] = mv;
+        i = m;
+    }
+    h[i] = e;
+    return rootv;
+}
+
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / 64;
+
+// Inclusive prefix sum of v over the workgroup's threads in thread order:
+// shuffles within each wave, the wave totals through LDS.
+__device__ __forceinline__ uint32_t topk_scan(uint32_t v, uint32_t *wsum, int tid) {
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t u = __shfl_up(v, o);
+        if (lane >= o) v += u;
+    }
+    if (lane == 63) wsum[wave] = v;
+    __syncthreads();
+    for (int w = 0; w < wave; w++) v += wsum[w];
+    return v;
+}
+
+// One workgroup of 1024 threads per (outer, inner) row.  Radix select over
+// order-preserving keys finds the k-th best value T; when exactly k elements
+// are at least as good as T (no tie straddles the k-th place, the usual
+// case) they are the reference's selection; otherwise the reference's heap
+// is replayed.  The selection is then ordered by (value, best first; index
+// ascending), the reference's comparator (tensor/topk.c:28-41): its k keys
+// (value key, inverted index) are distinct, so each one's output position is
+// the number of keys above it.
+//
+// Rows of up to kTopkRowLds elements are read from memory once, into LDS
+// (several loads per thread in flight), and every later pass reads LDS.  The
+// replay of the reference's heap (tensor/topk.c:71-101) when values tie
+// across the k-th place:
+//   * the heap of the first k elements is built by all threads, Floyd's
+//     sift-downs level by level from the deepest (the nodes of one level
+//     root disjoint subtrees, so their order within the level is free, and
+//     every deeper level precedes them, as in the reference's descending
+//     loop);
+//   * the heap's root only gets better as elements enter, so an element no
+//     better than the root after heapify never enters: all threads mark the
+//     others first (a bit per element), and one wave walks only the marked
+//     ones in element order, testing 64 at a time against the current root;
+//     lane 0 inserts the first that enters and the rest are re-tested
+//     against the new root.
+template <bool STAGED>
+__global__ void __launch_bounds__(kTopkThreads) topk_kernel(const float *__restrict__ x, float *__restrict__ values,
+                                                            float *__restrict__ indices, size_t inner, int dim, int k,
+                                                            int largest) {
     __shared__ uint32_t hist[256];
+    __shared__ uint32_t wsum[kTopkWaves];
     __shared__ uint32_t s_prefix, s_remaining, s_count;
     __shared__ unsigned long long keys[kTopkMaxK];
     __shared__ HeapPair heap[kTopkMaxK];
-    __shared__ float rowbuf[kTopkRowLds];
+    __shared__ unsigned long long cmask[STAGED ? kTopkRowLds / 64 : 1];
+    __shared__ float rowbuf[STAGED ? kTopkRowLds : 1];
     const size_t row = blockIdx.x;
     const size_t o = row / inner, in = row % inner;
     const size_t base = o * static_cast<size_t>(dim) * inner + in;
     const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     // -0 and +0 compare equal in the reference: give them one key
     auto key_of = [&](float v) -> uint32_t {
         const uint32_t kk = fkey(v == 0.0f ? 0.0f : v);
         return largest ? kk : ~kk;
     };
+    // (a compile-time choice: a run-time one merges both into generic loads)
+    auto at = [&](int d) -> float {
+        if constexpr (STAGED)
+            return rowbuf[d];
+        else
+            return x[base + static_cast<size_t>(d) * inner];
+    };
+
+    if constexpr (STAGED) {
+        constexpr int U = 4;
+        for (int d0 = 0; d0 < dim; d0 += kTopkThreads * U) {
+            float v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int d = d0 + u * kTopkThreads + tid;
+                v[u] = d < dim ? x[base + static_cast<size_t>(d) * inner] : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int d = d0 + u * kTopkThreads + tid;
+                if (d < dim) rowbuf[d] = v[u];
+            }
+        }
+    }
 
     uint32_t prefix = 0, mask = 0, remaining = static_cast<uint32_t>(k), eq_count = 0;
     for (int pass = 0; pass < 4; pass++) {
         const int shift = 24 - 8 * pass;
-        hist[tid] = 0;
+        if (tid < 256) hist[tid] = 0;
         __syncthreads();
-        for (int d = tid; d < dim; d += 256) {
-            const uint32_t kk = key_of(x[base + static_cast<size_t>(d) * inner]);
-            if ((kk & mask) == prefix) atomicAdd(&hist[(kk >> shift) & 255u], 1u);
+        for (int d0 = 0; d0 < dim; d0 += kTopkThreads) {
+            const int d = d0 + tid;
+            const uint32_t kk = d < dim ? key_of(at(d)) : 0u;
+            const bool act = d < dim && (kk & mask) == prefix;
+            const uint32_t bin = (kk >> shift) & 255u;
+            // a wave whose counted elements all fall in one bin (ties) adds
+            // them with one atomic
+            const unsigned long long am = __ballot(act);
+            if (am == 0ull) continue;
+            const int first = __ffsll(static_cast<long long>(am)) - 1;
+            const uint32_t b0 = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(bin), first));
+            if (__ballot(act && bin == b0) == am) {
+                if (lane == first) atomicAdd(&hist[b0], static_cast<uint32_t>(__popcll(am)));
+            } else if (act) {
+                atomicAdd(&hist[bin], 1u);
+            }
         }
         __syncthreads();
-        if (tid == 0) {
-            uint32_t cum = 0;
-            int digit = 0;
-            for (int b = 255; b >= 0; b--) {
-                if (cum + hist[b] >= remaining) {
-                    digit = b;
-                    break;
-                }
-                cum += hist[b];
-            }
-            s_prefix = prefix | (static_cast<uint32_t>(digit) << shift);
-            s_remaining = remaining - cum;
-            s_count = hist[digit];
+        // digit: the largest b whose suffix count S(b) = hist[b] + ... +
+        // hist[255] reaches `remaining` (thread t < 256 holds bin 255 - t)
+        const uint32_t b = 255u - static_cast<uint32_t>(tid & 255);
+        const uint32_t hb = tid < 256 ? hist[b] : 0u;
+        const uint32_t S = topk_scan(hb, wsum, tid);
+        if (tid < 256 && S >= remaining && S - hb < remaining) {
+            s_prefix = prefix | (b << shift);
+            s_remaining = remaining - (S - hb);
+            s_count = hb;
         }
         __syncthreads();
         prefix = s_prefix;
@@ -313,57 +416,98 @@ __global__ void __launch_bounds__(256) topk_kernel(const float *__restrict__ x, 
     }
     // T = prefix; `remaining` of the eq_count elements equal to T are needed
     const bool ambiguous = eq_count != remaining;
-    int kp = 1;
-    while (kp < k) kp <<= 1;
-    for (int i = tid; i < kp; i += 256) keys[i] = 0ull;  // padding sorts last
     if (tid == 0) s_count = 0;
     __syncthreads();
     if (!ambiguous) {
-        for (int d = tid; d < dim; d += 256) {
-            const uint32_t kk = key_of(x[base + static_cast<size_t>(d) * inner]);
-            if (kk >= prefix) {
-                const uint32_t slot = atomicAdd(&s_count, 1u);
-                keys[slot] = (static_cast<unsigned long long>(kk) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(d));
-            }
+        for (int d0 = 0; d0 < dim; d0 += kTopkThreads) {
+            const int d = d0 + tid;
+            const uint32_t kk = d < dim ? key_of(at(d)) : 0u;
+            const bool sel = d < dim && kk >= prefix;
+            const unsigned long long sm = __ballot(sel);
+            if (sm == 0ull) continue;
+            const int first = __ffsll(static_cast<long long>(sm)) - 1;
+            uint32_t slot = 0;
+            if (lane == first) slot = atomicAdd(&s_count, static_cast<uint32_t>(__popcll(sm)));
+            slot = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(slot), first));
+            const uint32_t below = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(sm >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(sm), 0u));
+            if (sel) keys[slot + below] = (static_cast<unsigned long long>(kk) << 32) | (0xFFFFFFFFu - static_cast<uint32_t>(d));
         }
     } else {
-        // the replay is one thread's sequential scan: stage the row in LDS
-        // first (all threads), so its reads cost LDS latency, not memory's
-        const bool staged = dim <= kTopkRowLds;
-        if (staged)
-            for (int d = tid; d < dim; d += 256) rowbuf[d] = x[base + static_cast<size_t>(d) * inner];
+        for (int i = tid; i < k; i += kTopkThreads) heap[i] = HeapPair{at(i), static_cast<uint32_t>(i)};
         __syncthreads();
-        if (tid < 64) {
-            if (staged)
-                topk_heap_replay(rowbuf, 1, dim, k, largest, heap, tid);
-            else
-                topk_heap_replay(x + base, inner, dim, k, largest, heap, tid);
-            for (int i = tid; i < k; i += 64)
-                keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
+        const int last = k / 2 - 1;  // the reference sifts nodes last .. 0
+        for (int D = last >= 0 ? 31 - __clz(last + 1) : -1; D >= 0; D--) {
+            const int hi = min((2 << D) - 2, last);
+            for (int i = (1 << D) - 1 + tid; i <= hi; i += kTopkThreads) topk_sift(heap, k, i, largest);
+            __syncthreads();
         }
-    }
-    __syncthreads();
-    // bitonic sort, descending
-    for (int size = 2; size <= kp; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < kp; i += 256) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const unsigned long long a = keys[i], b = keys[j];
-                    if (desc ? (a < b) : (a > b)) {
-                        keys[i] = b;
-                        keys[j] = a;
+        const float root0 = heap[0].v;
+        if constexpr (STAGED) {
+            const int nblk = (dim - k + 63) / 64;
+            for (int bk = wave; bk < nblk; bk += kTopkWaves) {
+                const int d = k + 64 * bk + lane;
+                const float v = d < dim ? rowbuf[d] : 0.0f;
+                const unsigned long long cm = __ballot(d < dim && (largest ? (v > root0) : (v < root0)));
+                if (lane == 0) cmask[bk] = cm;
+            }
+            __syncthreads();
+            if (wave == 0) {
+                float root = root0;
+                for (int b0 = 0; b0 < nblk; b0 += 64) {
+                    const unsigned long long mine = b0 + lane < nblk ? cmask[b0 + lane] : 0ull;
+                    unsigned long long nz = __ballot(mine != 0ull);
+                    while (nz) {
+                        const int jb = __ffsll(static_cast<long long>(nz)) - 1;
+                        nz &= nz - 1;
+                        const unsigned long long cm = __shfl(mine, jb);
+                        const int d0 = k + 64 * (b0 + jb);
+                        const bool cand = (cm >> lane) & 1ull;
+                        const float v = cand ? rowbuf[d0 + lane] : 0.0f;
+                        unsigned long long m = __ballot(cand && (largest ? (v > root) : (v < root)));
+                        while (m) {
+                            const int j = __ffsll(static_cast<long long>(m)) - 1;
+                            const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+                            float r = 0.0f;
+                            if (lane == 0) r = topk_sift_root(heap, k, HeapPair{vj, static_cast<uint32_t>(d0 + j)}, largest);
+                            root = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+                            m = __ballot(cand && lane > j && (largest ? (v > root) : (v < root)));
+                        }
                     }
                 }
             }
-            __syncthreads();
+        } else if (wave == 0) {  // rows beyond the LDS: the same walk over every element, from memory
+            float root = root0;
+            for (int d0 = k; d0 < dim; d0 += 64) {
+                const int d = d0 + lane;
+                const bool live = d < dim;
+                const float v = live ? x[base + static_cast<size_t>(d) * inner] : 0.0f;
+                unsigned long long m = __ballot(live && (largest ? (v > root) : (v < root)));
+                while (m) {
+                    const int j = __ffsll(static_cast<long long>(m)) - 1;
+                    const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+                    float r = 0.0f;
+                    if (lane == 0) r = topk_sift_root(heap, k, HeapPair{vj, static_cast<uint32_t>(d0 + j)}, largest);
+                    root = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(r), 0));
+                    m = __ballot(live && lane > j && (largest ? (v > root) : (v < root)));
+                }
+            }
         }
+        __syncthreads();
+        for (int i = tid; i < k; i += kTopkThreads)
+            keys[i] = (static_cast<unsigned long long>(key_of(heap[i].v)) << 32) | (0xFFFFFFFFu - heap[i].idx);
     }
-    for (int j = tid; j < k; j += 256) {
-        const uint32_t d = 0xFFFFFFFFu - static_cast<uint32_t>(keys[j] & 0xFFFFFFFFull);
-        const size_t out = (o * static_cast<size_t>(k) + j) * inner + in;
-        values[out] = x[base + static_cast<size_t>(d) * inner];
+    __syncthreads();
+    // output position of each selected key: the number of keys above it
+    // (descending order, as the reference's comparator sorts)
+    for (int i = tid; i < k; i += kTopkThreads) {
+        const unsigned long long ki = keys[i];
+        int rank = 0;
+#pragma unroll 8
+        for (int j = 0; j < k; j++) rank += keys[j] > ki ? 1 : 0;
+        const uint32_t d = 0xFFFFFFFFu - static_cast<uint32_t>(ki & 0xFFFFFFFFull);
+        const size_t out = (o * static_cast<size_t>(k) + rank) * inner + in;
+        values[out] = at(static_cast<int>(d));
         indices[out] = static_cast<float>(d);
     }
 }
@@ -605,7 +749,8 @@ int topk_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     if (rows == 0) return 0;
     if (rows > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
     set_kernel_name(ctx, node, "topk");
-    hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream,
+    auto kernel = dim <= kTopkRowLds ? topk_kernel<true> : topk_kernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(rows)), dim3(kTopkThreads), 0, ctx->stream,
                        dptr<const float>(ctx, node->inputs[0]), dptr<float>(ctx, node->outputs[0]),
                        dptr<float>(ctx, node->outputs[1]), inner, dim, k, attr.largest ? 1 : 0);
     return launch_status("topk");

@@ -944,6 +944,8 @@ INDEX_CASES = [
     ("TopK", [1, 8400], dict(k=300, axis=-1, largest=1)),
     ("TopK", [4, 24000], dict(k=300, axis=1, largest=1)),
     ("TopK", [3, 1000, 5], dict(k=17, axis=1, largest=0)),
+    ("TopK", [5, 130], dict(k=1, axis=1, largest=1)),
+    ("TopK", [2, 70], dict(k=65, axis=-1, largest=0)),
     ("ReduceMax", [1, 80, 8400], dict(axes=[1], keepdims=0)),
 ]
 
@@ -967,9 +969,12 @@ def test_concat_strided_bitwise(gpu, batch, chans):
 
 
 # TopK also on inputs rounded to a coarse grid, so values tie across the
-# k-th place and the reference's heap history decides the selection
+# k-th place and the reference's heap history decides the selection, and on
+# rows of one repeated value (a detector whose class scores all saturate to
+# 1.0: the first k elements survive, no element enters the heap)
 INDEX_RUNS = [(op, shape, kw, "normal") for op, shape, kw in INDEX_CASES] + \
-    [(op, shape, kw, "ties") for op, shape, kw in INDEX_CASES if op == "TopK"]
+    [(op, shape, kw, "ties") for op, shape, kw in INDEX_CASES if op == "TopK"] + \
+    [(op, shape, kw, "const") for op, shape, kw in INDEX_CASES if op == "TopK"]
 
 
 @pytest.mark.parametrize("op,shape,kw,dist", INDEX_RUNS,
@@ -979,6 +984,8 @@ def test_index_ops_bitwise(gpu, op, shape, kw, dist):
     xs = rng_inputs(g)
     if dist == "ties":
         xs = [np.round(x * 2).astype(np.float32) / 2 for x in xs]
+    elif dist == "const":
+        xs = [np.ones_like(x) for x in xs]
     got = run_gpu(write_spk(g, "mi355x"), xs, outputs=len(g.outputs))
     want = run_oracle(write_spk(g, "mi355x"), xs)
     for a_, b_ in zip(got, want):
