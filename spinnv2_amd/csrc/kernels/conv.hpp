@@ -25,7 +25,7 @@ struct ConvGeom {
 
 int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeom *g);
 
-enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV_DW_F32 = 3 };
+enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV_DW_F32 = 3, CONV_SMALLK_F32 = 4 };
 
 // How an fp32 implicit-GEMM B source is laid out beyond its k-offset table.
 // Per tap, for the skinny kernel: k = c * taps + tap sits at c * cstride +
@@ -83,11 +83,14 @@ struct ConvPlan {
     int8_t *q_in;
     int8_t *q_shared;
     // fp32 handoff, the same for the zero-padded NCHW input of a padded
-    // conv: producer side (not owned) and consumer side (owned).
+    // conv: producer side (not owned) and consumer side (owned, unless
+    // pad_in_shared: a later consumer of the same tensor with the same
+    // padded geometry reads the first consumer's buffer).
     float *pad_out;
     int pad_Hp, pad_Wp, pad_pt, pad_pl;
     int pad_m0, pad_C;  // producer side: only channels pad_m0 .. + pad_C - 1 go over (pad_C 0: all)
     float *pad_in;
+    bool pad_in_shared;
 };
 
 void conv_plan_free(void *p);

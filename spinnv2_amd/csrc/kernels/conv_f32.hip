@@ -92,7 +92,7 @@ void conv_plan_free(void *p) {
     if (plan->ktab) (void)hipFree(plan->ktab);
     if (plan->scales) (void)hipFree(plan->scales);
     if (plan->q_in) (void)hipFree(plan->q_in);
-    if (plan->pad_in) (void)hipFree(plan->pad_in);
+    if (plan->pad_in && !plan->pad_in_shared) (void)hipFree(plan->pad_in);
     if (plan->gather.ktap) (void)hipFree(const_cast<int *>(plan->gather.ktap));
     delete plan;
 }
@@ -745,6 +745,119 @@ __global__ void __launch_bounds__(256) conv_direct_f32(DirectArgs a) {
         }
         if (a.res) sum += a.res[idx];
         a.y[idx] = apply_act(sum, a.act);
+    }
+}
+
+// ------------------------------------------------ small-gather stem kernel
+
+// Convs with a few input channels (C <= 4: RGB stems) and a short gather per
+// output pixel (C*KH*KW <= 64) whose output channels fit one thread
+// (M <= 64).  As an implicit GEMM such a layer is one or two k-tiles per
+// output tile with most MFMA rows empty, bound by its prologue and epilogue;
+// here each wave takes 64 consecutive output pixels of one output row, one
+// per lane, and each lane keeps all MT (>= M) output channels in registers:
+// per tap one input load (the row test is wave-uniform, the column test per
+// lane) and MT weights read from LDS as broadcast 16-byte reads.  Each output
+// is summed from the bias in the reference's order (c, kh, kw), out-of-bounds
+// taps skipped (runtime/kernels/reference/conv/conv.c:3-62), one fused
+// multiply-add per tap; then residual, activation, and the stores: y and/or
+// the consuming conv's zero-padded input (the fp32 pad handoff).
+constexpr int kSmallkMaxC = 4;
+constexpr int kSmallkMaxK = 64;
+
+struct SmallkArgs {
+    const float *__restrict__ x;
+    const float *__restrict__ w;  // OIHW: [M][K]
+    const float *__restrict__ bias;
+    const float *__restrict__ res;
+    float *__restrict__ y;   // null: only the handoff is stored
+    float *__restrict__ yp;  // the consuming conv's zero-padded input, or null
+    int N, C, H, W, M, KH, KW, OH, OW;
+    int sh, sw, ph, pw, dh, dw, act;
+    int segs;     // 64-pixel segments per output row
+    int x_bytes;  // extent of x for the bounds-checked loads
+    int yp_Hp, yp_Wp, yp_pt, yp_pl, yp_m0, yp_C;
+};
+
+template <int MT>
+__global__ void __launch_bounds__(256) conv_smallk_f32(SmallkArgs a) {
+    __shared__ __attribute__((aligned(16))) float wl[kSmallkMaxK * MT];  // [k][m], zero past M
+    __shared__ int toff[kSmallkMaxK];                                    // element offset of tap k from tap 0
+    __shared__ int tdd[kSmallkMaxK];                                     // (kh*dh) << 16 | kw*dw
+    const int K = a.C * a.KH * a.KW;
+    for (int i = threadIdx.x; i < K * MT; i += 256) {
+        const int k = i / MT, m = i - k * MT;
+        wl[i] = m < a.M ? a.w[m * K + k] : 0.0f;
+    }
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const int taps = a.KH * a.KW;
+        const int c = k / taps, r = k - c * taps;
+        const int dy = (r / a.KW) * a.dh, dx = (r % a.KW) * a.dw;
+        toff[k] = (c * a.H + dy) * a.W + dx;
+        tdd[k] = (dy << 16) | dx;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const long long item = static_cast<long long>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // (n, oh, segment)
+    if (item >= static_cast<long long>(a.N) * a.OH * a.segs) return;
+    const int seg = static_cast<int>(item % a.segs);
+    const int rest = static_cast<int>(item / a.segs);
+    const int oh = rest % a.OH, n = rest / a.OH;
+    const int ow = seg * 64 + lane;
+    const bool live = ow < a.OW;
+    const int ihb = oh * a.sh - a.ph, iwb = ow * a.sw - a.pw;
+    const int base = (n * a.C * a.H + ihb) * a.W + iwb;  // tap (0, 0, 0); used only for taps in bounds
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[m] = a.bias && m < a.M ? a.bias[m] : 0.0f;
+    // KC taps at a time: all their loads in flight together (taps outside
+    // the input, and past K, load from an out-of-range offset and are skipped)
+    constexpr int KC = 16;
+    for (int k0 = 0; k0 < K; k0 += KC) {
+        float xv[KC];
+        unsigned okm = 0;
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            const int k = min(k0 + j, K - 1);
+            const int dd = tdd[k];
+            const bool ok = k0 + j < K && live &&
+                            static_cast<unsigned>(ihb + (dd >> 16)) < static_cast<unsigned>(a.H) &&
+                            static_cast<unsigned>(iwb + (dd & 0xffff)) < static_cast<unsigned>(a.W);
+            xv[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                  xrs, ok ? (base + toff[k]) * 4 : kOobOffset, 0, 0));
+            okm |= static_cast<unsigned>(ok) << j;
+        }
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            if (k0 + j >= K) break;
+            if ((okm >> j) & 1u) {  // lanes whose tap is outside the input skip it (exec mask)
+                const floatx4 *wr = reinterpret_cast<const floatx4 *>(&wl[(k0 + j) * MT]);
+#pragma unroll
+                for (int q = 0; q < MT / 4; q++) {
+                    const floatx4 wv = wr[q];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) acc[4 * q + u] = fmaf(xv[j], wv[u], acc[4 * q + u]);
+                }
+            }
+        }
+    }
+    if (!live) return;
+    const size_t plane = static_cast<size_t>(a.OH) * a.OW;
+    const size_t ybase = static_cast<size_t>(n) * a.M * plane + static_cast<size_t>(oh) * a.OW + ow;
+    const size_t pplane = static_cast<size_t>(a.yp_Hp) * a.yp_Wp;
+    const size_t pbase = static_cast<size_t>(n) * a.yp_C * pplane + static_cast<size_t>(oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl;
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        if (m < a.M) {  // (a constant trip count: acc stays in registers)
+            float v = acc[m];
+            if (a.res) v += a.res[ybase + m * plane];
+            v = apply_act(v, a.act);
+            if (a.y) a.y[ybase + m * plane] = v;
+            const unsigned mc = static_cast<unsigned>(m - a.yp_m0);
+            if (a.yp && mc < static_cast<unsigned>(a.yp_C)) a.yp[pbase + mc * pplane] = v;
+        }
     }
 }
 
@@ -1486,18 +1599,30 @@ static std::string shape_key(const char *kind, const ConvGeom &g, const ConvPlan
     return buf;
 }
 
-// Plans an fp32 implicit GEMM for convolution g (group 1) with weights
-// w_host[M][C*KH*KW].  When some tap falls outside the input, the input is
-// first copied into a zero-padded buffer so the kernel needs no bounds tests.
-int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvPlan *plan) {
-    const int K = g.C * g.KH * g.KW;
+// Rows and columns of the zero-padded input conv g reads, from the top /
+// left padding on (its taps' span, at least the input's), when it needs one.
+static bool padded_extent(const ConvGeom &g, int *Hp, int *Wp) {
     const int hspan = (g.OH - 1) * g.sh + (g.KH - 1) * g.dh + 1;  // rows the taps touch, from -ph
     const int wspan = (g.OW - 1) * g.sw + (g.KW - 1) * g.dw + 1;
-    plan->padded = g.ph > 0 || g.pw > 0 || hspan - g.ph > g.H || wspan - g.pw > g.W;
+    *Hp = std::max(g.H + g.ph, hspan);
+    *Wp = std::max(g.W + g.pw, wspan);
+    return g.ph > 0 || g.pw > 0 || hspan - g.ph > g.H || wspan - g.pw > g.W;
+}
+
+// Plans an fp32 implicit GEMM for convolution g (group 1) with weights
+// w_host[M][C*KH*KW].  When some tap falls outside the input, the input is
+// first copied into a zero-padded buffer so the kernel needs no bounds tests;
+// min_Hp / min_Wp enlarge that buffer's planes (a geometry shared with the
+// other padded readers of the same input).
+int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvPlan *plan, int min_Hp = 0,
+                   int min_Wp = 0) {
+    const int K = g.C * g.KH * g.KW;
+    int ext_h = 0, ext_w = 0;
+    plan->padded = padded_extent(g, &ext_h, &ext_w);
     plan->pt = plan->padded ? g.ph : 0;
     plan->pl = plan->padded ? g.pw : 0;
-    plan->Hp = plan->padded ? std::max(g.H + g.ph, hspan) : g.H;
-    plan->Wp = plan->padded ? std::max(g.W + g.pw, wspan) : g.W;
+    plan->Hp = plan->padded ? std::max(ext_h, min_Hp) : g.H;
+    plan->Wp = plan->padded ? std::max(ext_w, min_Wp) : g.W;
     const int64_t xp_elems = static_cast<int64_t>(g.N) * g.C * plan->Hp * plan->Wp;
     if (xp_elems * 4 >= 0x7fff0000LL) return SPKV2_E_UNSUPPORTED;  // byte offsets are 31-bit
     plan->pad_bytes = plan->padded ? align256(static_cast<size_t>(xp_elems) * 4) : 0;
@@ -1663,6 +1788,38 @@ static int use_implicit_padding(ConvPlan *plan) {
     return 0;
 }
 
+static bool smallk_fits(const ConvGeom &g);
+
+// The padded planes every padded fp32 implicit-GEMM conv reading this
+// node's input plans with, when that input comes straight from a conv: the
+// largest any of them needs (with the same top / left padding), so that they
+// can all read one zero-padded copy, the pad handoff's buffer.  0 x 0 when
+// the input has another producer.
+static void shared_pad_extent(const Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom &g, int *Hp,
+                              int *Wp) {
+    *Hp = *Wp = 0;
+    const uint32_t t = node->inputs[0];
+    bool from_conv = false;
+    for (uint32_t i = 0; i < node->id && i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *n = &ctx->node_records[i];
+        for (uint16_t k = 0; k < n->output_count; k++)
+            if (n->outputs[k] == t) from_conv = n->op_type == SPKV2_OP_CONV;
+    }
+    if (!from_conv) return;
+    for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
+        const Spkv2NodeRecord *n = &ctx->node_records[i];
+        if (n->op_type != SPKV2_OP_CONV || n->input_count < 2 || n->inputs[0] != t) continue;
+        ConvGeom r;
+        if (read_conv_geom(ctx, n, &r) != 0 || r.group != 1 || r.w_dtype != SPKV2_DTYPE_FP32 ||
+            r.x_dtype != SPKV2_DTYPE_FP32 || smallk_fits(r) || r.ph != g.ph || r.pw != g.pw)
+            continue;
+        int h = 0, w = 0;
+        if (!padded_extent(r, &h, &w)) continue;
+        *Hp = std::max(*Hp, h);
+        *Wp = std::max(*Wp, w);
+    }
+}
+
 // fp32 handoff.  When this padded conv's input is the only output of an
 // earlier fp32 implicit-GEMM conv, or one output of a channel Split of such
 // a conv's output (then that conv stores only the Split output's channel
@@ -1710,10 +1867,22 @@ static int setup_pad_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, Con
     if (!builtin_runs(ctx, prod->id) || !builtin_runs(ctx, node->id)) return 0;  // a user kernel runs one end
     if (ctx->plan_dtors[prod->id] != conv_plan_free) return 0;
     ConvPlan *pp = static_cast<ConvPlan *>(ctx->plans[prod->id]);
-    if (!pp || pp->path != CONV_IGEMM_F32 || pp->pad_out) return 0;
+    if (!pp || (pp->path != CONV_IGEMM_F32 && pp->path != CONV_SMALLK_F32)) return 0;
     const ConvGeom &g = plan->g;
     if (pp->g.N != g.N || pp->g.OH != g.H || pp->g.OW != g.W) return 0;
     if (via_split ? m0 + g.C > pp->g.M : pp->g.M != g.C) return 0;
+    if (pp->pad_out) {
+        // the producer already hands this tensor to an earlier consumer: a
+        // consumer with the same padded geometry and channel range reads
+        // that consumer's buffer (the producer writes y as well, since the
+        // tensor has more than one reader)
+        if (pp->pad_Hp == plan->Hp && pp->pad_Wp == plan->Wp && pp->pad_pt == plan->pt && pp->pad_pl == plan->pl &&
+            pp->pad_m0 == m0 && pp->pad_C == (via_split ? g.C : 0)) {
+            plan->pad_in = pp->pad_out;
+            plan->pad_in_shared = true;
+        }
+        return 0;
+    }
     bool is_output = false;
     for (size_t i = 0; i < ctx->output_count; i++)
         if (ctx->output_ids[i] == t) is_output = true;
@@ -1817,6 +1986,68 @@ static int run_dw(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom
     return launch_status("conv_dw_f32");
 }
 
+// The small-gather stem kernel takes ungrouped convs with at most
+// kSmallkMaxC input channels, a gather of at most kSmallkMaxK taps and at
+// most 64 output channels (SPKV2_CONV_SMALLK=0 keeps them on the implicit
+// GEMM).
+static bool smallk_fits(const ConvGeom &g) {
+    if (const char *e = getenv("SPKV2_CONV_SMALLK"))
+        if (e[0] == '0') return false;
+    return g.group == 1 && g.C <= kSmallkMaxC && g.C * g.KH * g.KW <= kSmallkMaxK && g.M <= 64 &&
+           g.H < 32768 && g.W < 32768 && (g.KH - 1) * g.dh < 32768 && (g.KW - 1) * g.dw < 32768;
+}
+
+static int run_smallk(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *p) {
+    const ConvGeom &g = p->g;
+    SmallkArgs a{};
+    a.x = dptr<const float>(ctx, node->inputs[0]);
+    a.w = dptr<const float>(ctx, node->inputs[1]);
+    a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
+    a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
+    a.y = dptr<float>(ctx, node->outputs[0]);
+    a.N = g.N;
+    a.C = g.C;
+    a.H = g.H;
+    a.W = g.W;
+    a.M = g.M;
+    a.KH = g.KH;
+    a.KW = g.KW;
+    a.OH = g.OH;
+    a.OW = g.OW;
+    a.sh = g.sh;
+    a.sw = g.sw;
+    a.ph = g.ph;
+    a.pw = g.pw;
+    a.dh = g.dh;
+    a.dw = g.dw;
+    a.act = g.act;
+    a.segs = (g.OW + 63) / 64;
+    a.x_bytes = static_cast<int>(g.x_elems * 4);
+    // with the handoffs not live every tensor is materialized as written
+    if (p->pad_out && handoffs_live(ctx)) {
+        a.yp = p->pad_out;
+        a.yp_Hp = p->pad_Hp;
+        a.yp_Wp = p->pad_Wp;
+        a.yp_pt = p->pad_pt;
+        a.yp_pl = p->pad_pl;
+        a.yp_m0 = p->pad_C > 0 ? p->pad_m0 : 0;
+        a.yp_C = p->pad_C > 0 ? p->pad_C : g.M;
+        if (!p->y_needed) a.y = nullptr;
+    }
+    const long long waves = static_cast<long long>(g.N) * g.OH * a.segs;
+    if (waves <= 0) return 0;
+    const long long blocks = (waves + 3) / 4;
+    if (blocks > 0x7fffffffLL) return SPKV2_E_UNSUPPORTED;
+    const dim3 grid(static_cast<unsigned>(blocks));
+    if (g.M <= 16)
+        hipLaunchKernelGGL(conv_smallk_f32<16>, grid, dim3(256), 0, ctx->stream, a);
+    else if (g.M <= 32)
+        hipLaunchKernelGGL(conv_smallk_f32<32>, grid, dim3(256), 0, ctx->stream, a);
+    else
+        hipLaunchKernelGGL(conv_smallk_f32<64>, grid, dim3(256), 0, ctx->stream, a);
+    return launch_status("conv_smallk_f32");
+}
+
 static int run_direct(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvGeom &g) {
     DirectArgs a{};
     a.x = dptr<const float>(ctx, node->inputs[0]);
@@ -1866,12 +2097,17 @@ int conv_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
         rc = conv_i8_prepare(ctx, node, plan);
     } else if (g.w_dtype != SPKV2_DTYPE_FP32 || g.x_dtype != SPKV2_DTYPE_FP32) {
         rc = SPKV2_E_UNSUPPORTED;
+    } else if (smallk_fits(g)) {
+        plan->path = CONV_SMALLK_F32;
+        set_kernel_name(ctx, node, "conv_smallk_f32");
     } else if (g.group == 1) {
         const float *w = reinterpret_cast<const float *>(host_weight_data(ctx, node->inputs[1]));
         if (!w) {
             rc = SPKV2_E_UNSUPPORTED;  // weights produced at run time
         } else {
-            rc = plan_igemm_f32(ctx->stream, g, w, plan);
+            int hp = 0, wp = 0;
+            shared_pad_extent(ctx, node, g, &hp, &wp);
+            rc = plan_igemm_f32(ctx->stream, g, w, plan, hp, wp);
             if (rc == 0) rc = setup_pad_handoff(ctx, node, plan);
             if (rc == 0) rc = use_implicit_padding(plan);
             if (rc == 0) set_kernel_name(ctx, node, igemm_name(plan) + (plan->pad_in ? "+handoff" : ""));
@@ -1897,6 +2133,7 @@ int conv_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratch) {
     case CONV_DIRECT_F32: return run_direct(ctx, node, plan->g);
     case CONV_DW_F32: return run_dw(ctx, node, plan->g);
     case CONV_IGEMM_I8: return conv_i8_run(ctx, node, plan, nullptr);
+    case CONV_SMALLK_F32: return run_smallk(ctx, node, plan);
     }
     return SPKV2_E_UNSUPPORTED;
 }

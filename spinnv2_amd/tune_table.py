@@ -8,12 +8,14 @@ the built-in table ignored (SPKV2_TUNE_TABLE=0), so the prepare-time tuner
 times its candidates and appends its choice to the output file
 (SPKV2_TUNE_DB); the file is then sorted and de-duplicated.
 
-    python -m spinnv2_amd.tune_table [out.tune] [--retune-int8]
+    python -m spinnv2_amd.tune_table [out.tune] [--retune-int8 | --missing] [--no-int8]
     python -m spinnv2_amd.tune_table --int8-network [--b1 | --splitk] [table.tune]
     python -m spinnv2_amd.tune_table --f32-network [--yolo | --b1] [table.tune]
 
-INT8 entries (keys starting `i8|`) already in the committed table are kept
-unless --retune-int8 is given: the INT8 tuner times each layer alone with an
+With --missing every entry of the committed table is kept and only layer
+shapes it lacks are tuned (the table stays in force, so the tuner runs for
+those alone); --no-int8 leaves the INT8 networks out.  INT8 entries (keys starting `i8|`) already in the committed
+table are kept unless --retune-int8 is given: the INT8 tuner times each layer alone with an
 fp32 epilogue, while in the network most int8 convs hand int8 to the next
 conv instead, and on ResNet-50 b=64 a regenerated set of INT8 choices ran the
 network at 1.97 ms per step against 1.80 for the kept one.
@@ -41,19 +43,21 @@ from pathlib import Path
 DEFAULT_OUT = Path(__file__).resolve().parent / "lib" / "mi355x.tune"
 
 
-def networks():
-    """(label, graph, quant params) of every benchmark configuration."""
+def networks(int8: bool = True):
+    """(label, graph, quant params) of every benchmark configuration (without
+    the INT8 ones when int8 is false)."""
     from .spk import models
     from .spk.quantize import calibrate_activation_scales, quantize_conv_weights
 
     for depth, batch in ((101, 64), (101, 1), (18, 32), (18, 1)):
         yield f"resnet{depth} b={batch}", models.resnet(depth, batch), None
-    g1 = models.resnet(50, 1)
-    samples = [models.make_input(g1.tensors[g1.inputs[0]].shape, 1000 + i) for i in range(16)]
-    act = calibrate_activation_scales(g1, samples)
-    for batch in (64, 1):
-        g = models.resnet(50, batch)
-        yield f"int8 resnet50 b={batch}", g, quantize_conv_weights(g) + act
+    if int8:
+        g1 = models.resnet(50, 1)
+        samples = [models.make_input(g1.tensors[g1.inputs[0]].shape, 1000 + i) for i in range(16)]
+        act = calibrate_activation_scales(g1, samples)
+        for batch in (64, 1):
+            g = models.resnet(50, batch)
+            yield f"int8 resnet50 b={batch}", g, quantize_conv_weights(g) + act
     for batch in (16, 1):
         yield f"yolov10n b={batch}", models.yolo_v10n(batch), None
 
@@ -61,15 +65,17 @@ def networks():
 def main() -> None:
     args = [a for a in sys.argv[1:] if not a.startswith("--")]
     retune_int8 = "--retune-int8" in sys.argv[1:]
+    missing = "--missing" in sys.argv[1:]
     out = Path(args[0]) if args else DEFAULT_OUT
     kept = {}
     if not retune_int8 and DEFAULT_OUT.exists():
         for line in DEFAULT_OUT.read_text().splitlines():
-            if line.startswith("i8|") and len(line.split()) == 3:
+            if (missing or line.startswith("i8|")) and len(line.split()) == 3:
                 kept[line.split()[0]] = line
     tmp = out.with_suffix(".partial")
     tmp.unlink(missing_ok=True)
-    os.environ["SPKV2_TUNE_TABLE"] = "0"
+    # --missing: the table stays in force, so only shapes it lacks are tuned
+    os.environ["SPKV2_TUNE_TABLE"] = "1" if missing else "0"
     os.environ["SPKV2_TUNE_DB"] = str(tmp)
     for k in ("SPKV2_CONV_CFG", "SPKV2_CONV_SPLITK", "SPKV2_CONV_HYBRID", "SPKV2_CONV_TUNE", "SPKV2_I8_CFG",
               "SPKV2_I8_SPLITK"):
@@ -78,18 +84,18 @@ def main() -> None:
     from .spk import write_spk
 
     lib = load_library()
-    for label, g, qp in networks():
+    for label, g, qp in networks(int8="--no-int8" not in sys.argv[1:]):
         with Model(write_spk(g, "mi355x", quant_params=qp), lib=lib):
             pass
         print(f"tuned {label}", flush=True)
     lines = {}
-    for line in tmp.read_text().splitlines():
+    for line in (tmp.read_text() if tmp.exists() else "").splitlines():
         parts = line.split()
         if len(parts) == 3:
             lines[parts[0]] = line
     lines.update(kept)
     out.write_text("".join(lines[k] + "\n" for k in sorted(lines)))
-    tmp.unlink()
+    tmp.unlink(missing_ok=True)
     print(f"{len(lines)} layer shapes -> {out}")
 
 
@@ -101,18 +107,50 @@ def int8_key(g, n) -> str:
             f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}")
 
 
-def f32_key(g, n) -> str:
-    """The fp32 tuner's key of a group-1 conv node (conv_f32.hip, shape_key
-    and plan_igemm_f32's padded-input geometry)."""
-    N, C, H, W = g.shape(n.inputs[0])
-    M, _, KH, KW = g.tensors[n.inputs[1]].shape
+def _padded_extent(g, n):
+    """(padded, Hp, Wp) of a conv node's own zero-padded input (conv_f32.hip,
+    padded_extent)."""
+    _, _, H, W = g.shape(n.inputs[0])
+    _, _, KH, KW = g.tensors[n.inputs[1]].shape
     OH, OW = g.shape(n.outputs[0])[2:]
     sh, sw = n.attrs.get("strides", [1, 1])
     dh, dw = n.attrs.get("dilations", [1, 1])
     ph, pw = n.attrs.get("pads", [0, 0, 0, 0])[:2]
     hspan, wspan = (OH - 1) * sh + (KH - 1) * dh + 1, (OW - 1) * sw + (KW - 1) * dw + 1
     padded = ph > 0 or pw > 0 or hspan - ph > H or wspan - pw > W
-    Hp, Wp = (max(H + ph, hspan), max(W + pw, wspan)) if padded else (H, W)
+    return padded, max(H + ph, hspan), max(W + pw, wspan)
+
+
+def _smallk(g, n) -> bool:
+    """Whether the small-gather stem kernel takes the conv (conv_f32.hip, smallk_fits)."""
+    C = g.shape(n.inputs[0])[1]
+    M, _, KH, KW = g.tensors[n.inputs[1]].shape
+    return n.attrs.get("group", 1) == 1 and C <= 4 and C * KH * KW <= 64 and M <= 64
+
+
+def f32_key(g, n) -> str:
+    """The fp32 tuner's key of a group-1 conv node (conv_f32.hip, shape_key
+    and plan_igemm_f32's padded-input geometry: the largest any padded conv
+    reader of the same conv output needs, shared_pad_extent)."""
+    N, C, H, W = g.shape(n.inputs[0])
+    M, _, KH, KW = g.tensors[n.inputs[1]].shape
+    OH, OW = g.shape(n.outputs[0])[2:]
+    sh, sw = n.attrs.get("strides", [1, 1])
+    dh, dw = n.attrs.get("dilations", [1, 1])
+    pads = n.attrs.get("pads", [0, 0, 0, 0])[:2]
+    padded, Hp, Wp = _padded_extent(g, n)
+    if padded:
+        prod = [p for p in g.nodes if p.id < n.id and n.inputs[0] in p.outputs]
+        if prod and prod[-1].op_type == "Conv":
+            for r in g.nodes:
+                if (r.op_type != "Conv" or r.inputs[0] != n.inputs[0] or r.attrs.get("group", 1) != 1 or _smallk(g, r)
+                        or r.attrs.get("pads", [0, 0, 0, 0])[:2] != pads):
+                    continue
+                rp, rh, rw = _padded_extent(g, r)
+                if rp:
+                    Hp, Wp = max(Hp, rh), max(Wp, rw)
+    else:
+        Hp, Wp = H, W
     return (f"conv|{N},{C},{H},{W}|{M},{KH},{KW},{OH},{OW},{sh},{sw},{dh}|{dw},{Hp},{Wp}|{C * Hp * Wp},"
             f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}")
 
@@ -265,7 +303,8 @@ def f32_network(table: Path, net: str = "resnet101") -> None:
     g = {"yolo": lambda: models.yolo_v10n(16), "resnet101_b1": lambda: models.resnet(101, 1)}.get(
         net, lambda: models.resnet(101, 64))()
     blob = write_spk(g, "mi355x")
-    keys = {n.id: f32_key(g, n) for n in g.nodes if n.op_type == "Conv" and n.attrs.get("group", 1) == 1}
+    keys = {n.id: f32_key(g, n) for n in g.nodes
+            if n.op_type == "Conv" and n.attrs.get("group", 1) == 1 and not _smallk(g, n)}
     cands = F32_SWEEP_B1 if net == "resnet101_b1" else \
         F32_SWEEP + ([(c, s) for c in (14, 15, 16) for s in (1004, 1008, 1016)] if net == "yolo" else [])
     network_sweep(g, blob, keys, cands, table, {"yolo": "yolov10n b=16", "resnet101_b1": "resnet101 b=1"}.get(

@@ -368,6 +368,7 @@ def test_padded_conv_implicit_and_copied(gpu, monkeypatch, case, cfg, implicit):
 
     monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
     monkeypatch.setenv("SPKV2_IMPLICIT_PAD", implicit)
+    monkeypatch.setenv("SPKV2_CONV_SMALLK", "0")  # the 3-channel stem shapes on the implicit GEMM
     n, c, h, w, m, k, s, pads, d, res = case
     g = models.single_conv(n, c, h, w, m, k, s, dilation=d, act="Relu", residual=res, pads=pads)
     blob = write_spk(g, "mi355x")
@@ -383,6 +384,81 @@ def test_padded_conv_implicit_and_copied(gpu, monkeypatch, case, cfg, implicit):
     else:
         assert ",pad" in name and ",ipad" not in name, name
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+# Small-gather stems (conv_smallk_f32: at most 4 input channels and 64 taps,
+# at most 64 output channels; one output pixel per lane, every output channel
+# in registers), against the oracle and against the implicit GEMM.
+# (N, Cin, H, W, Cout, k, stride, pads [t, l, b, r], dilation, residual, act)
+SMALLK_CASES = [
+    (2, 3, 37, 29, 16, 3, 2, [1, 1, 1, 1], 1, False, "Silu"),  # YOLO stem
+    (1, 1, 28, 28, 6, 5, 1, [0, 0, 0, 0], 1, False, "Relu"),   # LeNet conv1
+    (3, 4, 20, 70, 40, 4, 1, [2, 1, 1, 2], 1, True, "Relu"),   # 64 taps, asymmetric pads, residual
+    (1, 2, 33, 130, 64, 3, 1, [2, 2, 2, 2], 2, False, None),   # dilation 2, rows of 3 segments
+    (2, 3, 9, 9, 24, 3, 3, [0, 0, 0, 0], 1, True, "Relu"),     # stride 3, short rows
+]
+
+
+@pytest.mark.parametrize("case", SMALLK_CASES, ids=[f"smallk{i}" for i in range(len(SMALLK_CASES))])
+def test_smallk_stem_conv(gpu, monkeypatch, case):
+    from spinnv2_amd.runtime import Model
+
+    n, c, h, w, m, k, s, pads, d, res, act = case
+    g = models.single_conv(n, c, h, w, m, k, s, dilation=d, act=act, residual=res, pads=pads)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    print(f"[smallk] case {case}", flush=True)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SPKV2_CONV_SMALLK", flag)
+        with Model(blob) as mdl:
+            for i, x in enumerate(xs):
+                mdl.set_input(i, x)
+            mdl.run()
+            outs[flag] = mdl.get_output(0)
+            name = mdl.kernel_name(0)
+        assert (name == "conv_smallk_f32") == (flag == "1"), name
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(outs["1"], want) <= FP32_TOL
+    assert tnorm_err(outs["1"], outs["0"]) <= FP32_TOL
+
+
+def test_smallk_stem_handoff_graph_mode(gpu, monkeypatch):
+    """A stem on the small-gather kernel hands its output to the padded 3x3
+    conv after it (stored straight into that conv's zero-padded input, the
+    tensor itself not written when nothing else reads it); eager, HIP-graph
+    replays and the handoff switched off agree bit for bit."""
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    p = models.Params(9)
+    g = Graph("stem_handoff")
+    x = g.input("x", [2, 3, 48, 40])
+    a = g.silu(g.conv(x, p.he((16, 3, 3, 3)), p.normal(16, 0.01), stride=2, pad=1))
+    b = g.silu(g.conv(a, p.he((32, 16, 3, 3)), p.normal(32, 0.01), stride=2, pad=1))
+    g.mark_output(b)
+    run_default_pipeline(g)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SPKV2_PAD_HANDOFF", flag)
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            eager = m.get_output(0)
+            names = [m.kernel_name(nd.id) for nd in g.nodes if nd.op_type == "Conv"]
+            m.set_graph_mode(True)
+            for _ in range(3):
+                m.set_input(0, xs[0])
+                m.run()
+                np.testing.assert_array_equal(m.get_output(0), eager)
+        outs[flag] = eager
+        assert names[0] == "conv_smallk_f32", names
+        assert names[1].endswith("+handoff") == (flag == "1"), names
+    np.testing.assert_array_equal(outs["1"], outs["0"])
+    assert tnorm_err(outs["1"], run_oracle(blob, xs)[0]) <= FP32_TOL
 
 
 @pytest.mark.parametrize("cfg", F32_IGEMM_CFGS)
