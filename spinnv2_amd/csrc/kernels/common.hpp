@@ -20,10 +20,15 @@ typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
 typedef int intx16 __attribute__((ext_vector_type(16)));
 
 // Fused activation codes of the SPK attr record (0 none, 1 Relu, 2 SiLU),
-// as the reference applies them (kernel_common.c:100-108).
+// as the reference applies them (kernel_common.c:100-108).  SiLU
+// v / (1 + exp(-v)) is evaluated with the hardware exponential (v_exp_f32
+// on v * log2(e)) and reciprocal (v_rcp_f32), within a few ulp of the
+// reference's expf and division for |v| up to ~20 (relative error below
+// ~|v| * 2^-24 from the exponent's rounding) and with its special values:
+// +inf -> +inf, -inf -> NaN, NaN -> NaN, v below ~-88.7 -> -0.
 __device__ __forceinline__ float apply_act(float v, int act) {
     if (act == 1) return v > 0.0f ? v : 0.0f;
-    if (act == 2) return v / (1.0f + expf(-v));
+    if (act == 2) return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
     return v;
 }
 

@@ -141,6 +141,7 @@ struct IgemmArgs {
     // 0x7fff7fff past K), the unpadded input's extent and the padding
     const int *__restrict__ ktap;
     int chk_H, chk_W, chk_ph, chk_pw;
+    int th_steps;  // thin kernel: K / 4 MFMA steps (k' = tap * sk_C + c)
 };
 
 
@@ -612,6 +613,182 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     }
 }
 
+// Thin implicit GEMM, for layers with few output channels and many output
+// pixels (YOLO's 16- and 32-channel layers at 80x80 to 320x320): MB blocks
+// of 16 rows by 256 columns per workgroup, each wave 64 of the columns as
+// four 16x16 blocks on v_mfma_f32_16x16x4f32.  The waves share nothing, so
+// there is no LDS and no barrier: each lane loads its B elements straight
+// into registers and its A elements from the packed weights (the same for
+// the four waves: L1 hits), with two 16-k chunks of loads in flight.
+//
+// k order k' = tap * C + c (C a multiple of 4): MFMA step s takes its k
+// slot g (lanes 16g..16g+15) from channel 4 * (s % (C/4)) + g of tap
+// s / (C/4), so the B element of a lane's column n sits at col(n) (per
+// lane, with g's channel) plus a tap and channel-quad offset that is the
+// same for the wave.  Steps past K / 4 load nothing (0) and meet zero
+// weights.  Packed weights [m_tiles][k_tiles][MB][64 lanes][4 steps]: lane
+// (g, r) of block b holds row 16b + r at k' = 16 kt + 4 step + g.  Columns
+// past N and rows past M use out-of-range offsets (loads give 0, stores are
+// dropped), as in conv_igemm_f32.
+template <int MB>
+__global__ void __launch_bounds__(256) conv_thin_f32(IgemmArgs a) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int mt = bid % a.m_tiles;
+    const int nt = bid / a.m_tiles;
+    const int cs4 = a.sk_cstride * 4;
+    const int n0 = nt * 256 + wave * 64;
+    int col[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + l16;
+        col[j] = kOobOffset;
+        if (n < a.Ntot) {
+            const int img = n / a.OHW;
+            const int sp = n - img * a.OHW;
+            const int oh = sp / a.OW;
+            const int ow = sp - oh * a.OW;
+            col[j] = (img * a.x_img_stride + oh * a.sh * a.Wp + ow * a.sw) * 4 + g * cs4;
+        }
+    }
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
+    const int CQ = a.sk_C >> 2;
+    const floatx4 *wsrc = reinterpret_cast<const floatx4 *>(a.wp) + static_cast<size_t>(mt) * a.k_tiles * MB * 64 + lane;
+
+    floatx4 acc[MB][4];
+#pragma unroll
+    for (int b = 0; b < MB; b++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[b][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    constexpr int P = 3;  // chunks in flight: 3 x (16 + MB) loads, within the 63 vmcnt counts
+    floatx4 av[P][MB];
+    float bv[P][4][4];  // [set][step][column block]
+
+    // Chunks are loaded in order, so the next step's tap (kh, kw) and channel
+    // quad are counters advanced once per step (wave-uniform; no division
+    // in the loop, whose scalar unit the CU's waves share).
+    int s_next = 0, st_cq = 0, st_kh = 0, st_kw = 0;
+    // chunk KT (4 steps) into (AV, BV); past the last chunk a valid chunk of
+    // weights and no B elements (steps past K / 4) are loaded, never used
+#define TH_LOAD(KT, AV, BV)                                                                                       \
+    {                                                                                                             \
+        const int kt_ = min((KT), a.k_tiles - 1);                                                                 \
+        _Pragma("unroll") for (int b = 0; b < MB; b++) AV[b] = wsrc[(static_cast<size_t>(kt_) * MB + b) * 64];   \
+        _Pragma("unroll") for (int st = 0; st < 4; st++) {                                                        \
+            if (s_next < a.th_steps) {                                                                            \
+                const int so_ = (st_kh * a.sk_tap_h + st_kw * a.sk_tap_w) * 4 + st_cq * 4 * cs4;                 \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) BV[st][j] =                                         \
+                    __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, col[j], so_, 0));         \
+            } else {                                                                                              \
+                _Pragma("unroll") for (int j = 0; j < 4; j++) BV[st][j] = 0.0f;                                   \
+            }                                                                                                     \
+            s_next++;                                                                                             \
+            if (++st_cq == CQ) {                                                                                  \
+                st_cq = 0;                                                                                        \
+                if (++st_kw == a.sk_KW) {                                                                         \
+                    st_kw = 0;                                                                                    \
+                    st_kh++;                                                                                      \
+                }                                                                                                 \
+            }                                                                                                     \
+        }                                                                                                         \
+    }
+#define TH_MMA(AV, BV)                                                                                            \
+    _Pragma("unroll") for (int st = 0; st < 4; st++) _Pragma("unroll") for (int b = 0; b < MB; b++)               \
+        _Pragma("unroll") for (int j = 0; j < 4; j++) acc[b][j] =                                                 \
+            __builtin_amdgcn_mfma_f32_16x16x4f32(AV[b][st], BV[st][j], acc[b][j], 0, 0, 0);
+
+    // a ring of P register sets: chunk i in set i % P, loaded P - 1 chunks
+    // ahead of its multiply (the loop is unrolled by P so set indices are
+    // constants)
+#pragma unroll
+    for (int p = 0; p < P - 1; p++) TH_LOAD(p, av[p], bv[p]);
+    for (int k0 = 0; k0 < a.k_tiles; k0 += P) {
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            TH_LOAD(k0 + p + P - 1, av[(p + P - 1) % P], bv[(p + P - 1) % P]);
+            if (k0 + p < a.k_tiles) { TH_MMA(av[p], bv[p]); }
+        }
+    }
+#undef TH_LOAD
+#undef TH_MMA
+
+    // 16x16 accumulator layout: lane (g, l16) holds rows 4g..4g+3 of column l16
+    const int ohw4 = a.OHW * 4;
+    int obase[4], pbase[4];
+    const int plane4 = a.yp_plane * 4;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int n = n0 + 16 * j + l16;
+        obase[j] = kOobOffset;
+        pbase[j] = kOobOffset;
+        if (n < a.Ntot) {
+            const int img = n / a.OHW;
+            const int sp = n - img * a.OHW;
+            const int oh = sp / a.OW;
+            const int ow = sp - oh * a.OW;
+            obase[j] = (img * a.y_img_stride + sp) * 4;
+            pbase[j] = (img * a.yp_C * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow + a.yp_pl) * 4;
+        }
+    }
+    float *const any = a.y ? a.y : a.yp;
+    const __amdgpu_buffer_rsrc_t yrs =
+        __builtin_amdgcn_make_buffer_rsrc(any, static_cast<short>(0), a.y ? a.y_bytes : 0, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        a.yp ? a.yp : any, static_cast<short>(0), a.yp ? a.yp_bytes : 0, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.res ? a.res : any), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufferWord3);
+    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.bias ? a.bias : any), static_cast<short>(0), a.bias ? a.M * 4 : 0, kBufferWord3);
+#pragma unroll
+    for (int b = 0; b < MB; b++) {
+        const int m0 = mt * 16 * MB + 16 * b + 4 * g;  // this lane's first row in block b
+        floatx4 bias4 = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (a.bias) {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                bias4[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(brs, (m0 + r) * 4, 0, 0));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            floatx4 v = acc[b][j];
+            if (a.alpha != 1.0f) v *= a.alpha;
+            if (a.bias) v += bias4;
+            if (a.res) {
+                floatx4 rv;
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rrs, m0 + r < a.M ? obase[j] + (m0 + r) * ohw4 : kOobOffset, 0, 0));
+                v += rv;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; r++) v[r] = apply_act(v[r], a.act);
+            if (a.yp) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const unsigned mc = static_cast<unsigned>(m0 + r - a.yp_m0);
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(v[r]), prs,
+                        mc < static_cast<unsigned>(a.yp_C) ? pbase[j] + static_cast<int>(mc) * plane4 : kOobOffset, 0, 0);
+                }
+            }
+            if (a.y) {
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
+                                                          m0 + r < a.M ? obase[j] + (m0 + r) * ohw4 : kOobOffset, 0, 0);
+            }
+        }
+    }
+}
+
 // Sums split-K partials in slice order, then applies the epilogue.  Each
 // thread owns VEC consecutive columns of one row (VEC = 4 when the partial
 // columns start and end on multiples of 4: 16-byte loads).
@@ -940,6 +1117,7 @@ struct TileCfg {
     IgemmKernel kernel_chk;   // the same tile with implicit padding (kModeChk)
     double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
     int skinny_waves = 0;  // > 0: conv_skinny_f32 with this many waves (no split-K)
+    int thin_mb = 0;       // > 0: conv_thin_f32 with this many 16-row blocks (no split-K)
 };
 
 #define CFGW(BM, BN, BK, WM, WN, EFF)                                                                        \
@@ -960,6 +1138,10 @@ const TileCfg kCfgs[] = {
     // output channels (YOLO) fill half or more of the MFMA rows instead of
     // a quarter to three quarters of a 64-row tile
     CFGW(32, 128, 16, 1, 4, 0.90), CFGW(32, 128, 32, 1, 4, 0.90), CFGW(32, 256, 16, 1, 4, 0.90),
+    // thin tiles: 16 or 32 rows by 256 columns, one wave per 64 columns, no
+    // LDS (layers with 16-32 output channels and many pixels)
+    {16, 256, 16, "thin16x256", conv_thin_f32<1>, conv_thin_f32<1>, conv_thin_f32<1>, 1.0, 0, 1},
+    {32, 256, 16, "thin32x256", conv_thin_f32<2>, conv_thin_f32<2>, conv_thin_f32<2>, 1.0, 0, 2},
 };
 #undef CFG
 #undef CFGW
@@ -1020,10 +1202,11 @@ TileCounts tile_counts(int c, int M, int Ntot, int K, int split) {
     tc.m_tiles = (M + t.BM - 1) / t.BM;
     tc.n_tiles = (Ntot + t.BN - 1) / t.BN;
     tc.k_tiles = (K + t.BK - 1) / t.BK;
-    const int req = t.skinny_waves > 0 ? 1 : split >= kHybrid ? split - kHybrid : split;  // skinny: no split-K
+    const bool whole = t.skinny_waves > 0 || t.thin_mb > 0;  // skinny, thin: no split-K
+    const int req = whole ? 1 : split >= kHybrid ? split - kHybrid : split;
     tc.kt_per_split = (tc.k_tiles + req - 1) / req;
     tc.splitk = (tc.k_tiles + tc.kt_per_split - 1) / tc.kt_per_split;
-    if (split >= kHybrid && t.skinny_waves == 0) {
+    if (split >= kHybrid && !whole) {
         // whole tiles: the largest multiple of the CU count that is whole
         // n-tile columns (so the remaining tiles are the last columns)
         const int tiles = tc.m_tiles * tc.n_tiles;
@@ -1061,6 +1244,15 @@ double model_us(int c, const TileCounts &tc, int M, int Ntot) {
         const long rounds = (wgs + slots - 1) / slots;
         const int chunks = (tc.k_tiles + t.skinny_waves - 1) / t.skinny_waves;
         return static_cast<double>(rounds) * (chunks * 16 * 32 / 2400.0 + 1.0) + 2.0;
+    }
+    if (t.thin_mb > 0) {
+        // a wave's 16-k chunk is 16 * MB MFMAs of 32 cycles; the busiest
+        // CU's waves per SIMD share its MFMA pipe; ~1 us of latency per round
+        const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles;
+        const long slots = static_cast<long>(cus) * resident_wgs(c);
+        const long rounds = (wgs + slots - 1) / slots;
+        const long per_cu = std::min<long>(resident_wgs(c), (wgs + cus - 1) / cus);
+        return static_cast<double>(rounds) * (per_cu * tc.k_tiles * 16.0 * t.thin_mb * 32 / 2400.0 + 1.0) + 2.0;
     }
     const long wgs = static_cast<long>(tc.m_tiles) * tc.n_tiles * tc.splitk;
     const long slots = static_cast<long>(cus) * resident_wgs(c);
@@ -1105,9 +1297,14 @@ struct GatherSpec {
 // its 64-k chunk (so a chunk never straddles two taps).
 bool skinny_fits(const GatherSpec &gs) { return gs.gather.C > 0 && gs.gather.C % 64 == 0; }
 
+// The thin kernel takes a layer whose channels per tap are a multiple of
+// its 4-k MFMA step.
+bool thin_fits(const GatherSpec &gs) { return gs.gather.C > 0 && gs.gather.C % 4 == 0 && gs.K % 4 == 0; }
+
 // Configuration c can run the layer.
 bool cfg_fits(int c, const GatherSpec &gs) {
-    return resident_wgs(c) > 0 && (kCfgs[c].skinny_waves == 0 || skinny_fits(gs));
+    return resident_wgs(c) > 0 && (kCfgs[c].skinny_waves == 0 || skinny_fits(gs)) &&
+           (kCfgs[c].thin_mb == 0 || thin_fits(gs));
 }
 
 std::vector<int> build_koff(const GatherSpec &gs, int BK) {
@@ -1191,6 +1388,24 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
         a.ws = nullptr;
         t.kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0, st>>>(a);
         return launch_status("conv_skinny_f32");
+    }
+    if (t.thin_mb > 0) {
+        // k' = tap * C + c in whole 4-channel steps: checked here as well as
+        // at planning, since a step past its tap would read other channels
+        const int K = gg.C * g.KH * g.KW;
+        if (gg.C <= 0 || gg.C % 4 != 0 || gg.chk || tc.k_tiles * 16 < K || tc.k_tiles * 16 >= K + 16) {
+            set_last_error_text("conv_thin_f32: layer without whole 4-channel steps per tap");
+            return SPKV2_E_UNSUPPORTED;
+        }
+        a.sk_C = gg.C;
+        a.sk_cstride = gg.cstride;
+        a.sk_KW = gg.KW;
+        a.sk_tap_h = gg.tap_h;
+        a.sk_tap_w = gg.tap_w;
+        a.th_steps = K / 4;
+        a.ws = nullptr;
+        t.kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(256), 0, st>>>(a);
+        return launch_status("conv_thin_f32");
     }
     const dim3 grid = tc.dp_tiles > 0
                           ? dim3(static_cast<unsigned>(tc.dp_tiles + (tiles - tc.dp_tiles) * tc.splitk), 1)
@@ -1538,6 +1753,27 @@ int upload_packed_skinny(const float *w, int M, int C, int taps, int m_tiles, in
     return hip_check(hipMemcpy(*out, packed.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy packed weights");
 }
 
+// Packs w[m][c][tap] (k = c * taps + tap, the reference's order) for the
+// thin kernel: k' = tap * C + c, tile [m_tiles][k_tiles][MB][64 lanes][4
+// steps] holding, for lane (g, r) of 16-row block b, row 16b + r at
+// k' = 16 kt + 4 step + g.  Rows past M and k' past K are zero.
+int upload_packed_thin(const float *w, int M, int C, int taps, int MB, int m_tiles, int k_tiles, void **out) {
+    std::vector<float> packed(static_cast<size_t>(m_tiles) * k_tiles * MB * 256, 0.0f);
+    const int K = C * taps;
+    for (int m = 0; m < M; m++) {
+        const int mt = m / (16 * MB), b = (m % (16 * MB)) / 16, r = m % 16;
+        for (int kp = 0; kp < K; kp++) {
+            const int tap = kp / C, c = kp % C;
+            const int kt = kp / 16, st = (kp % 16) / 4, g = kp % 4;
+            packed[(((static_cast<size_t>(mt) * k_tiles + kt) * MB + b) * 64 + g * 16 + r) * 4 + st] =
+                w[(static_cast<size_t>(m) * C + c) * taps + tap];
+        }
+    }
+    const size_t bytes = packed.size() * sizeof(float);
+    if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc packed weights")) return rc;
+    return hip_check(hipMemcpy(*out, packed.data(), bytes, hipMemcpyHostToDevice), "hipMemcpy packed weights");
+}
+
 int upload_koff(const std::vector<int> &koff, void **out) {
     const size_t bytes = koff.size() * sizeof(int);
     if (int rc = hip_check(hipMalloc(out, bytes), "hipMalloc koff")) return rc;
@@ -1584,6 +1820,10 @@ static int plan_tiles_and_weights(hipStream_t st, const ConvGeom &g, const Gathe
     if (t.skinny_waves > 0) {
         if (int rc = upload_packed_skinny(w_host, g.M, gs.gather.C, gs.K / gs.gather.C, plan->m_tiles, plan->k_tiles,
                                           &plan->wpack))
+            return rc;
+    } else if (t.thin_mb > 0) {
+        if (int rc = upload_packed_thin(w_host, g.M, gs.gather.C, gs.K / gs.gather.C, t.thin_mb, plan->m_tiles,
+                                        plan->k_tiles, &plan->wpack))
             return rc;
     } else if (int rc = upload_packed_f32(w_host, g.M, gs.K, t.BM, t.BK, plan->m_tiles, plan->k_tiles, &plan->wpack)) {
         return rc;
@@ -1670,6 +1910,8 @@ int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int 
 }
 
 std::string igemm_name(const ConvPlan *p) {
+    if (kCfgs[p->cfg].thin_mb > 0)
+        return std::string("conv_thin_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") + ">";
     if (kCfgs[p->cfg].skinny_waves > 0)
         return std::string("conv_skinny_f32<16x16,w") + std::to_string(kCfgs[p->cfg].skinny_waves) +
                (p->padded ? ",pad" : "") + ">";
@@ -1754,7 +1996,7 @@ static int run_igemm_impl(Spkv2Context *ctx, const ConvPlan *p, const float *x, 
 // wherever they apply.
 static int use_implicit_padding(ConvPlan *plan) {
     const ConvGeom &g = plan->g;
-    if (!plan->padded || plan->pad_in || kCfgs[plan->cfg].skinny_waves > 0) return 0;
+    if (!plan->padded || plan->pad_in || kCfgs[plan->cfg].skinny_waves > 0 || kCfgs[plan->cfg].thin_mb > 0) return 0;
     if (g.H >= 16384 || g.W >= 16384 || (g.KH - 1) * g.dh >= 32768 || (g.KW - 1) * g.dw >= 32768) return 0;
     const char *e = getenv("SPKV2_IMPLICIT_PAD");
     if (e && e[0] == '0') return 0;

@@ -386,6 +386,35 @@ def test_padded_conv_implicit_and_copied(gpu, monkeypatch, case, cfg, implicit):
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
 
 
+@pytest.mark.parametrize("smallk", ["1", "0"])
+def test_silu_activation_accuracy(gpu, monkeypatch, smallk):
+    """The fused SiLU (hardware exponential and reciprocal) against
+    v / (1 + exp(-v)) in float64: a 1x1 conv with weight 1 and bias 0 passes
+    every input through unchanged, then the activation; within 1e-5 relative
+    (0.5e-5 absolute near 0) on a grid over [-100, 100], and the special
+    values exactly (+inf, -inf -> NaN, NaN, -0 below about -88.7).  Both the
+    small-gather kernel and the implicit GEMM's epilogue."""
+    from spinnv2_amd.spk.graph import Graph
+    from spinnv2_amd.spk.passes import run_default_pipeline
+
+    monkeypatch.setenv("SPKV2_CONV_SMALLK", smallk)
+    grid = np.concatenate([np.linspace(-100, 100, 20001), [-88.5, -89.0, -90.0, 0.0, -0.0, 1e-30, -1e-30, 87.0, 89.0]])
+    specials = np.array([np.inf, -np.inf, np.nan])
+    x = np.concatenate([grid, specials, np.zeros(128 - (grid.size + 3) % 128)]).astype(np.float32)
+    g = Graph("silu")
+    xi = g.input("x", [1, 1, x.size // 128, 128])
+    g.mark_output(g.silu(g.conv(xi, np.ones((1, 1, 1, 1), np.float32), np.zeros(1, np.float32))))
+    run_default_pipeline(g)
+    got = run_gpu(write_spk(g, "mi355x"), [x.reshape(1, 1, -1, 128)])[0].ravel()
+    xd = x.astype(np.float64)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = xd / (1.0 + np.exp(-xd))
+    fin = np.isfinite(xd)
+    np.testing.assert_allclose(got[fin], want[fin], rtol=1e-5, atol=0.5e-5)
+    assert got[grid.size] == np.inf and np.isnan(got[grid.size + 1]) and np.isnan(got[grid.size + 2])
+    assert np.all(got[:grid.size][x[:grid.size] < -89.0] == 0.0)
+
+
 # Small-gather stems (conv_smallk_f32: at most 4 input channels and 64 taps,
 # at most 64 output channels; one output pixel per lane, every output channel
 # in registers), against the oracle and against the implicit GEMM.
@@ -521,6 +550,60 @@ def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
         m.run()
         got = m.get_output(0)
         assert "skinny" not in m.kernel_name(0)
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+# The thin kernel (entries 17 and 18 of the fp32 table: 16 or 32 rows by
+# 256 columns, one wave per 64 columns, no LDS) on layers whose channels per
+# tap are multiples of 4: ragged M and N, padding, stride, dilation,
+# residual, SiLU, and Gemm with alpha and with transA.
+F32_THIN_CFGS = [17, 18]
+THIN_CASES = [
+    ("conv3x3_res", lambda: models.single_conv(2, 72, 11, 13, 40, 3, 1, 1, act="Relu", residual=True)),
+    ("conv1x1_s2", lambda: models.single_conv(1, 32, 14, 14, 24, 1, 2, 0, act=None)),
+    ("conv3x3_s2_dil2", lambda: models.single_conv(1, 16, 15, 15, 16, 3, 2, 2, dilation=2, act="Relu")),
+    ("conv3x3_silu_wide", lambda: models.single_conv(2, 16, 40, 36, 32, 3, 1, 1, act="Silu")),
+    ("conv5x5_c8", lambda: models.single_conv(3, 8, 17, 19, 20, 5, 1, 2, act="Relu")),
+    ("gemm_alpha", lambda: models.single_gemm(3, 192, 70, alpha=0.5)),
+    ("gemm_trans_a", lambda: models.single_gemm(5, 128, 33, trans_a=1)),
+]
+
+
+@pytest.mark.parametrize("cfg", F32_THIN_CFGS)
+@pytest.mark.parametrize("name,build", THIN_CASES, ids=[c[0] for c in THIN_CASES])
+def test_thin_configs(gpu, monkeypatch, cfg, name, build):
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(cfg))
+    g = build()
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    print(f"[thin] cfg {cfg} case {name}", flush=True)
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        got = m.get_output(0)
+        kname = m.kernel_name(0)
+    assert f"conv_thin_f32<thin{16 if cfg == F32_THIN_CFGS[0] else 32}x256" in kname, kname
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(got, want) <= FP32_TOL
+
+
+def test_thin_config_refused_off_4_channel_steps(gpu, monkeypatch):
+    """A layer whose channels per tap are not a multiple of 4 does not take a
+    forced thin configuration (a step would straddle two taps)."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_THIN_CFGS[0]))
+    g = models.single_conv(1, 6, 11, 13, 16, 3, 1, 1)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        m.set_input(0, xs[0])
+        m.run()
+        got = m.get_output(0)
+        assert "thin" not in m.kernel_name(0)
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
 
 

@@ -99,6 +99,24 @@ def test_c2f_views_skinny_kernel(gpu, monkeypatch):
     assert "concat_views" in names
 
 
+def test_c2f_views_thin_kernel(gpu, monkeypatch):
+    """The thin kernel (no LDS, one wave per 64 columns) reading and writing
+    through views and handoffs: every conv that can take it is forced onto
+    it; views on equal views off bit for bit, and the oracle within
+    tolerance."""
+    monkeypatch.setenv("SPKV2_CONV_CFG", "18")
+    g = _c2f_graph(batch=2, c_in=16, hw=20, widths=(32, 64))
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    on, names = _run(blob, xs, len(g.nodes))
+    monkeypatch.setenv("SPKV2_CONCAT_VIEWS", "0")
+    off, _ = _run(blob, xs, len(g.nodes))
+    np.testing.assert_array_equal(on.view(np.uint32), off.view(np.uint32))
+    assert sum("conv_thin_f32" in n for n in names) >= 6, names
+    assert "concat_views" in names
+    assert tnorm_err(on, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 def test_c2f_views_graph_mode_and_fault_path(gpu):
     """HIP-graph replays with the views equal eager; with a fault event
     armed (an injection that never fires) the views are off and every
