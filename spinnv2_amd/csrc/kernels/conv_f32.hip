@@ -1142,6 +1142,9 @@ const TileCfg kCfgs[] = {
     // LDS (layers with 16-32 output channels and many pixels)
     {16, 256, 16, "thin16x256", conv_thin_f32<1>, conv_thin_f32<1>, conv_thin_f32<1>, 1.0, 0, 1},
     {32, 256, 16, "thin32x256", conv_thin_f32<2>, conv_thin_f32<2>, conv_thin_f32<2>, 1.0, 0, 2},
+    // 96-row tiles, the four waves side by side along n, each three 32x32
+    // blocks: 65-96 output channels (YOLO's 80-class head) in one m-tile
+    CFGW(96, 128, 16, 1, 4, 0.90), CFGW(96, 128, 32, 1, 4, 0.90),
 };
 #undef CFG
 #undef CFGW

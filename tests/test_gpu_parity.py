@@ -326,10 +326,11 @@ def test_graph_mode_matches_eager(gpu):
 
 # Every implicit-GEMM tile configuration (the fp32 table of conv_f32.hip: 8
 # shallow-k tiles, 4 deep-k ones, then after the two skinny kernels 3 tiles
-# of 32 rows), with and without split-K (each slice writes its partial tile;
+# of 32 rows, and after the two thin ones 2 tiles of 96 rows), with and
+# without split-K (each slice writes its partial tile;
 # splitk_epilogue sums them in slice order and applies the epilogue), on a
 # ragged residual conv; forced through the tuning overrides.
-F32_IGEMM_CFGS = [*range(12), 14, 15, 16]
+F32_IGEMM_CFGS = [*range(12), 14, 15, 16, 19, 20]
 F32_SKINNY_CFGS = [12, 13]
 SPLIT_CASES = [(cfg, split) for cfg in F32_IGEMM_CFGS for split in (1, 3, 8)]
 
