@@ -124,6 +124,7 @@ struct IgemmArgs {
     int sh, sw;
     int x_img_stride;                // elements between images in x
     int y_img_stride;                // elements between images in y and the residual
+    int y_cstride;                   // elements between channels in y (OHW unless y is a view)
     int m_tiles, k_tiles, kt_per_split;
     int act;
     float alpha;
@@ -402,7 +403,8 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
             return;  // splitk_epilogue sums the partials
         }
         {
-            const int ohw4 = a.OHW * 4;
+            const int ohw4 = a.OHW * 4;      // the residual's channel stride (natural layout)
+            const int ycs4 = a.y_cstride * 4;  // y's
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const int n = nt * BN + (wn * TN + j) * 32 + row;
@@ -482,7 +484,7 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
                             // __float_as_uint takes the element by value (a bit
                             // cast applied to a vector element reads element 0)
                             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
-                                                                  m < a.M ? obase[j] + m * ohw4 : kOobOffset, 0, 0);
+                                                                  m < a.M ? obase[j] + m * ycs4 : kOobOffset, 0, 0);
                         }
                     }
                 }
@@ -548,7 +550,8 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     const bool eown = tid < 256 && em < a.M && en < a.Ntot;
     const int eimg = eown ? en / a.OHW : 0;
     const int esp = en - eimg * a.OHW;
-    const size_t eyi = static_cast<size_t>(eimg) * a.y_img_stride + static_cast<size_t>(em) * a.OHW + esp;
+    // (y's channel stride: a residual comes only with y's natural layout)
+    const size_t eyi = static_cast<size_t>(eimg) * a.y_img_stride + static_cast<size_t>(em) * a.y_cstride + esp;
     const float ebias = eown && a.bias ? a.bias[em] : 0.0f;
     const float eres = eown && a.res ? a.res[eyi] : 0.0f;
 
@@ -783,7 +786,8 @@ __global__ void __launch_bounds__(256) conv_thin_f32(IgemmArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; r++)
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[r]), yrs,
-                                                          m0 + r < a.M ? obase[j] + (m0 + r) * ohw4 : kOobOffset, 0, 0);
+                                                          m0 + r < a.M ? obase[j] + (m0 + r) * a.y_cstride * 4 : kOobOffset,
+                                                          0, 0);
             }
         }
     }
@@ -835,7 +839,7 @@ __global__ void __launch_bounds__(256) splitk_epilogue(const float *__restrict__
             if (bias) o += bm;
             const int img = (n + e) / OHW;
             const int sp = n + e - img * OHW;
-            const size_t yi = static_cast<size_t>(img) * h.y_img_stride + static_cast<size_t>(m) * OHW + sp;
+            const size_t yi = static_cast<size_t>(img) * h.y_img_stride + static_cast<size_t>(m) * h.y_cstride + sp;
             if (res) o += rv[e];
             o = apply_act(o, act);
             if (h.yp && static_cast<unsigned>(m - h.yp_m0) < static_cast<unsigned>(h.yp_C)) {
@@ -1329,6 +1333,7 @@ std::vector<int> build_koff(const GatherSpec &gs, int BK) {
 struct YLayout {
     int img = 0;
     int bytes = 0;
+    int cstride = 0;  // elements between channels; 0: OH x OW
 };
 
 static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const ConvGeom &g, int Wp, const float *xs,
@@ -1374,6 +1379,7 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
     }
     a.y_bytes = yl.bytes > 0 ? yl.bytes : static_cast<int>(g.y_elems * 4);
     a.y_img_stride = yl.img > 0 ? yl.img : g.M * a.OHW;
+    a.y_cstride = yl.cstride > 0 ? yl.cstride : a.OHW;
     a.ws_bytes = static_cast<int>(partial_bytes_of(tc, g.M, a.Ntot));
     const int tiles = tc.m_tiles * tc.n_tiles;
     if (t.skinny_waves > 0) {
@@ -2178,6 +2184,7 @@ static int run_igemm_node(Spkv2Context *ctx, const ConvPlan *p, const Spkv2NodeR
         y = reinterpret_cast<float *>(v->base);
         yl.img = static_cast<int>(v->img_elems);
         yl.bytes = static_cast<int>(v->extent);
+        yl.cstride = static_cast<int>(v->ch_elems);
     }
     return run_igemm_impl(ctx, p, x, g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr,
                           g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr, y, 1.0f, x_img, x_bytes, yl);

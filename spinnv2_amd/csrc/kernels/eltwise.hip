@@ -726,6 +726,10 @@ int unary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
 // Flatten / Reshape / Cast / Unsqueeze: a byte copy unless the planner
 // aliased output and input (reference shape/copy.c, shape/flatten.c).
 int copy_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    if (view_elided(ctx, node->id)) {  // a detection-head chain's Reshape: its data already sit in place
+        set_kernel_name(ctx, node, "copy_elided");
+        return 0;
+    }
     const size_t bytes = node->op_type == SPKV2_OP_FLATTEN ? rec(ctx, node->inputs[0])->size_bytes
                                                            : rec(ctx, node->outputs[0])->size_bytes;
     set_kernel_name(ctx, node, "copy");
@@ -735,6 +739,10 @@ int copy_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
 // reference tensor/concat.c; inputs the planner placed inside the output
 // (memory_plan.py Concat aliases) are already in place and are skipped.
 int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    if (view_elided(ctx, node->id)) {  // a detection-head chain's Concat: its inputs were written in place
+        set_kernel_name(ctx, node, "concat_elided");
+        return 0;
+    }
     Spkv2AttrRecord attr;
     if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
     const Spkv2TensorRecord *yr = rec(ctx, node->outputs[0]);

@@ -638,12 +638,21 @@ int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         set_kernel_name(ctx, node, "split_views");
         return 0;
     }
+    // the input as a view in its natural layout (the buffer a detection-head
+    // chain's convs wrote in place)
+    const float *x = dptr<const float>(ctx, node->inputs[0]);
+    if (const Spkv2TensorView *v = live_view(ctx, node->inputs[0])) {
+        if (v->img_elems != static_cast<int64_t>(x_axis * inner) || (v->ch_elems != 0 && axis == 1 &&
+                                                                    v->ch_elems != static_cast<int64_t>(inner)))
+            return SPKV2_E_UNSUPPORTED;  // not set up that way
+        x = reinterpret_cast<const float *>(v->base);
+    }
     set_kernel_name(ctx, node, "split");
     for (uint16_t k = 0; k < node->output_count; k++) {
         const Spkv2TensorRecord *yr = rec(ctx, node->outputs[k]);
         const size_t block = static_cast<size_t>(yr->shape[axis]) * inner;
         if (axis_offset + yr->shape[axis] > x_axis) return -11;
-        if (int rc = strided_block_copy(ctx->stream, dptr<const float>(ctx, node->inputs[0]),
+        if (int rc = strided_block_copy(ctx->stream, x,
                                         dptr<float>(ctx, node->outputs[k]), outer, block, x_axis * inner,
                                         axis_offset * inner, block))
             return rc;

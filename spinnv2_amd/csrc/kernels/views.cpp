@@ -51,6 +51,14 @@ bool movable(const Spkv2Context *ctx, const Uses &u, uint32_t t) {
            !ctx->views[t].base;
 }
 
+// movable, of rank r (movable itself asks for an NCHW activation)
+bool movable_rank(const Spkv2Context *ctx, const Uses &u, uint32_t t, int r) {
+    const Spkv2TensorRecord *x = rec(ctx, t);
+    return x->rank == r && x->dtype == SPKV2_DTYPE_FP32 && x->role == SPKV2_ROLE_ACTIVATION &&
+           x->memory_class == SPKV2_MEMORY_ACTIVATION_ARENA && !u.graph_io[t] && x->size_bytes > 0 &&
+           !ctx->views[t].base;
+}
+
 int axis_of(const Spkv2Context *ctx, const Spkv2NodeRecord *n, int rank) {
     Spkv2AttrRecord attr;
     if (spkv2_ctx_get_attr(ctx, n, &attr) != 0) return -1;
@@ -146,12 +154,101 @@ bool place_input(const Spkv2Context *ctx, const Uses &u, const Spkv2NodeRecord *
     return true;
 }
 
+// Detection-head chains (YOLO's head): per level, a channel Concat of convs
+// (box and class branches), flattened by a Reshape [N, C, H, W] ->
+// [N, C, H*W]; the levels joined by a Concat along axis 2 into [N, C, L];
+// that read by one channel Split (box and class again).  The convs write
+// their outputs straight into one buffer laid out as the [N, C, L] tensor
+// (channel stride L, each level at its offset along L), the per-level
+// Concats, the Reshapes and the level Concat have nothing left to do, and the
+// Split reads the buffer.  Every intermediate must have exactly one reader
+// (the next node of the chain).
+void setup_head_views(Spkv2Context *ctx, const Uses &u) {
+    const uint32_t nn = ctx->header.num_nodes;
+    auto sole_reader = [&](uint32_t t, uint32_t node) {
+        return u.readers[t].size() == 1 && u.readers[t][0].first == node;
+    };
+    for (uint32_t id = 0; id < nn; id++) {
+        const Spkv2NodeRecord *k2 = &ctx->node_records[id];
+        if (k2->op_type != SPKV2_OP_CONCAT || !builtin_runs(ctx, id) || k2->output_count != 1) continue;
+        const uint32_t o = k2->outputs[0];
+        const Spkv2TensorRecord *orr = rec(ctx, o);
+        if (!movable_rank(ctx, u, o, 3) || axis_of(ctx, k2, 3) != 2 || u.readers[o].size() != 1) continue;
+        const uint32_t sp = u.readers[o][0].first;
+        const Spkv2NodeRecord *split = &ctx->node_records[sp];
+        if (split->op_type != SPKV2_OP_SPLIT || !builtin_runs(ctx, sp) || u.readers[o][0].second != 0 ||
+            axis_of(ctx, split, 3) != 1)
+            continue;
+        const int64_t N = orr->shape[0], C = orr->shape[1], L = orr->shape[2];
+        const int64_t zbytes = N * C * L * 4;
+        if (zbytes >= (int64_t(1) << 31)) continue;
+        struct Place {
+            uint32_t t;
+            int64_t off;  // elements from the buffer's start
+        };
+        std::vector<Place> places;
+        std::vector<uint32_t> elide;
+        int64_t l0 = 0;
+        bool ok = true;
+        for (uint16_t i = 0; i < k2->input_count && ok; i++) {
+            const uint32_t r = k2->inputs[i];
+            const int pr = u.producer[r];
+            ok = movable_rank(ctx, u, r, 3) && sole_reader(r, id) && pr >= 0 &&
+                 ctx->node_records[pr].op_type == SPKV2_OP_RESHAPE && builtin_runs(ctx, static_cast<uint32_t>(pr));
+            if (!ok) break;
+            const Spkv2TensorRecord *rr = rec(ctx, r);
+            const uint32_t c = ctx->node_records[pr].inputs[0];
+            const int pk = u.producer[c];
+            ok = rr->shape[0] == N && rr->shape[1] == C && movable_rank(ctx, u, c, 4) &&
+                 sole_reader(c, static_cast<uint32_t>(pr)) && pk >= 0 &&
+                 ctx->node_records[pk].op_type == SPKV2_OP_CONCAT && builtin_runs(ctx, static_cast<uint32_t>(pk));
+            if (!ok) break;
+            const Spkv2TensorRecord *cr = rec(ctx, c);
+            const Spkv2NodeRecord *k1 = &ctx->node_records[pk];
+            const int64_t HW = static_cast<int64_t>(cr->shape[2]) * cr->shape[3];
+            ok = cr->shape[0] == N && cr->shape[1] == C && HW == rr->shape[2] && k1->output_count == 1 &&
+                 axis_of(ctx, k1, 4) == 1;
+            int64_t c0 = 0;
+            for (uint16_t j = 0; j < k1->input_count && ok; j++) {
+                const uint32_t t = k1->inputs[j];
+                const Spkv2TensorRecord *tr = rec(ctx, t);
+                // a conv writer (its epilogues take a channel stride; the
+                // Add kernel's image-strided form does not)
+                ok = movable_rank(ctx, u, t, 4) && sole_reader(t, static_cast<uint32_t>(pk)) &&
+                     strided_writer(ctx, u, t) && u.producer[t] >= 0 &&
+                     f32_conv(ctx, static_cast<uint32_t>(u.producer[t])) && tr->shape[0] == N &&
+                     tr->shape[2] == cr->shape[2] && tr->shape[3] == cr->shape[3];
+                if (ok) places.push_back({t, c0 * L + l0});
+                c0 += tr->shape[1];
+            }
+            ok = ok && c0 == C;
+            elide.push_back(static_cast<uint32_t>(pk));
+            elide.push_back(static_cast<uint32_t>(pr));
+            l0 += HW;
+        }
+        if (!ok || l0 != L || places.empty()) continue;
+        void *z = nullptr;
+        if (hipMalloc(&z, static_cast<size_t>(zbytes)) != hipSuccess) {
+            (void)hipGetLastError();
+            continue;  // the chain keeps its copies
+        }
+        ctx->view_buffers.push_back(z);
+        uint8_t *zb = static_cast<uint8_t *>(z);
+        for (const Place &pl : places)
+            ctx->views[pl.t] = Spkv2TensorView{zb + pl.off * 4, C * L, static_cast<size_t>(zbytes - pl.off * 4), L};
+        ctx->views[o] = Spkv2TensorView{zb, C * L, static_cast<size_t>(zbytes), L};
+        for (uint32_t e : elide) ctx->view_elide[e] = 1;
+        ctx->view_elide[id] = 1;
+    }
+}
+
 }  // namespace
 
 int setup_concat_views(Spkv2Context *ctx) {
     const uint32_t nt = ctx->header.num_tensors, nn = ctx->header.num_nodes;
     ctx->views.assign(nt, Spkv2TensorView{});
     ctx->view_split.assign(nn, 0);
+    ctx->view_elide.assign(nn, 0);
     if (ctx->protection_count > 0) return 0;  // protected packages keep every tensor where the reference has it
     if (const char *e = getenv("SPKV2_CONCAT_VIEWS"))
         if (e[0] == '0') return 0;
@@ -212,6 +309,7 @@ int setup_concat_views(Spkv2Context *ctx) {
         ctx->views[o] = Spkv2TensorView{zb, CZ * HW, static_cast<size_t>(zbytes)};
         for (uint32_t s : pl.splits) ctx->view_split[s] = 1;
     }
+    setup_head_views(ctx, u);
     return 0;
 }
 

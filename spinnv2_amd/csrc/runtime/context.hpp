@@ -26,8 +26,9 @@ struct Spkv2TensorSlot {
 // bytes from base to the end of the tensor's last image.
 struct Spkv2TensorView {
     uint8_t *base = nullptr;
-    int64_t img_elems = 0;
-    size_t extent = 0;
+    int64_t img_elems = 0;  // elements between images
+    size_t extent = 0;      // bytes from base to the end of the buffer
+    int64_t ch_elems = 0;   // elements between channels (0: the tensor's own plane size)
 };
 
 struct Spkv2Context {
@@ -120,11 +121,13 @@ struct Spkv2Context {
     // each run of an int8 conv fills with its raw int32 accumulators
     std::vector<int32_t *> acc_capture;
     // Channel-slice views set up at prepare (Concat along channels at batch
-    // > 1), in force only while the handoffs are: per tensor (base null:
-    // none), per node whether it is a Split whose outputs are all views of
-    // its input (nothing to copy), and the Concat buffers (owned).
+    // > 1, detection-head chains), in force only while the handoffs are: per
+    // tensor (base null: none), per node whether it is a Split whose outputs
+    // are all views of its input (nothing to copy) or a node whose output
+    // the views already hold (nothing to run), and the buffers (owned).
     std::vector<Spkv2TensorView> views;
     std::vector<uint8_t> view_split;
+    std::vector<uint8_t> view_elide;  // nodes whose output the views already hold: nothing to run
     std::vector<void *> view_buffers;
 };
 
@@ -160,6 +163,9 @@ inline bool handoffs_live(const Spkv2Context *ctx) { return !ctx->fault_event.en
 inline const Spkv2TensorView *live_view(const Spkv2Context *ctx, uint32_t tensor_id) {
     if (tensor_id >= ctx->views.size() || !ctx->views[tensor_id].base || !handoffs_live(ctx)) return nullptr;
     return &ctx->views[tensor_id];
+}
+inline bool view_elided(const Spkv2Context *ctx, uint32_t node_id) {
+    return node_id < ctx->view_elide.size() && ctx->view_elide[node_id] && handoffs_live(ctx);
 }
 void set_last_error(const char *what, hipError_t err);
 void set_last_error_text(const std::string &text);

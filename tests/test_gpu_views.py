@@ -163,6 +163,10 @@ def test_yolo_v10n_views_against_oracle(gpu, monkeypatch, batch):
             runs[flag] = ([m.get_output(i) for i in range(4)], [m.kernel_name(i) for i in range(len(g.nodes))])
     got, names = runs["1"]
     assert (names.count("split_views"), names.count("concat_views")) == YOLO_VIEWS[batch], names
+    # the detection head: three level Concats and the level join elided, the
+    # three Reshapes too; the convs wrote the [N, 144, L] buffer in place
+    assert (names.count("concat_elided"), names.count("copy_elided")) == (4, 3), names
+    assert "concat_elided" not in runs["0"][1]
     for a_, b_ in zip(got, runs["0"][0]):
         np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
     from oracle.spk_exec import OracleExecutor
@@ -170,6 +174,32 @@ def test_yolo_v10n_views_against_oracle(gpu, monkeypatch, batch):
     want = [np.asarray(o) for o in OracleExecutor(blob).run(*xs)]
     for n in range(batch):  # anchor indices repeat across images: one image at a time
         check_detections([a.reshape(w.shape)[n] for a, w in zip(got, want)], [w[n] for w in want])
+
+
+@pytest.mark.parametrize("force", [("SPKV2_CONV_SPLITK", "3"), ("SPKV2_CONV_CFG", "18"), ("SPKV2_CONV_CFG", "12")],
+                         ids=["splitk3", "thin32", "skinny"])
+def test_yolo_head_views_every_epilogue(gpu, monkeypatch, force):
+    """The detection head's convs write the [N, 144, L] buffer with channel
+    stride L through every epilogue that can take them (split-K partials
+    summed by splitk_epilogue, the thin and the skinny kernels): outputs
+    equal the copying path bit for bit."""
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv(*force)
+    g = models.yolo_v10n(batch=2, image=160, topk=50)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g, dist="uniform")
+    print(f"[views] yolo head {force}", flush=True)
+    runs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("SPKV2_CONCAT_VIEWS", flag)
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            runs[flag] = ([m.get_output(i) for i in range(4)], [m.kernel_name(i) for i in range(len(g.nodes))])
+    assert runs["1"][1].count("concat_elided") == 4, runs["1"][1]
+    for a_, b_ in zip(runs["1"][0], runs["0"][0]):
+        np.testing.assert_array_equal(a_.view(np.uint32), b_.view(np.uint32))
 
 
 def test_split_pad_handoff_bit_identical(gpu, monkeypatch):
