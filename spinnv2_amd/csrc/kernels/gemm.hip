@@ -11,6 +11,7 @@
 //
 // MatMul (reference mm/matmul.c:3-49): batched, numpy-broadcast leading
 // dimensions; one thread per output element, k inner, lanes along n.
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -60,28 +61,35 @@ struct MatmulArgs {
 
 constexpr int kMmTile = 64, kMmBK = 16, kMmLd = kMmBK + 1;
 
+// Matrix indices into a and b of batch z of y (numpy broadcasting: a
+// leading dim of 1 repeats).
+__device__ __forceinline__ void matmul_batch(const MatmulArgs &p, int z, size_t *ab, size_t *bb) {
+    int coords[8] = {0};
+    int t = z;
+    for (int d = p.yrank - 3; d >= 0; d--) {
+        coords[d] = t % p.yshape[d];
+        t /= p.yshape[d];
+    }
+    *ab = 0;
+    *bb = 0;
+    for (int d = 0; d + 2 < p.arank; d++) {
+        const int yd = p.yrank - p.arank + d;
+        *ab = *ab * p.ashape[d] + (p.ashape[d] == 1 || yd < 0 ? 0 : coords[yd]);
+    }
+    for (int d = 0; d + 2 < p.brank; d++) {
+        const int yd = p.yrank - p.brank + d;
+        *bb = *bb * p.bshape[d] + (p.bshape[d] == 1 || yd < 0 ? 0 : coords[yd]);
+    }
+}
+
 __global__ void __launch_bounds__(256) matmul_mfma(MatmulArgs p) {
     __shared__ float As[2][kMmTile * kMmLd];
     __shared__ float Bs[2][kMmTile * kMmLd];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * kMmTile, n0 = blockIdx.x * kMmTile;
-    // batch coordinates of y, broadcast into a and b
-    int coords[8] = {0};
-    int t = blockIdx.z;
-    for (int d = p.yrank - 3; d >= 0; d--) {
-        coords[d] = t % p.yshape[d];
-        t /= p.yshape[d];
-    }
     size_t ab = 0, bb = 0;
-    for (int d = 0; d + 2 < p.arank; d++) {
-        const int yd = p.yrank - p.arank + d;
-        ab = ab * p.ashape[d] + (p.ashape[d] == 1 || yd < 0 ? 0 : coords[yd]);
-    }
-    for (int d = 0; d + 2 < p.brank; d++) {
-        const int yd = p.yrank - p.brank + d;
-        bb = bb * p.bshape[d] + (p.bshape[d] == 1 || yd < 0 ? 0 : coords[yd]);
-    }
+    matmul_batch(p, blockIdx.z, &ab, &bb);
     const size_t M = p.M, N = p.N, K = p.K;
     const float *A = p.a + ab * M * K;
     const float *B = p.b + bb * K * N;
@@ -139,6 +147,63 @@ __global__ void __launch_bounds__(256) matmul_mfma(MatmulArgs p) {
     for (int r = 0; r < 16; r++) {
         const int m = m0 + wm * 32 + 8 * (r >> 2) + 4 * kh + (r & 3);
         if (m < p.M && col < p.N) Y[static_cast<size_t>(m) * N + col] = acc[r];
+    }
+}
+
+// Batched MatMul for grids too small to fill the GPU with 64x64 tiles (the
+// PSA attention products at batch 1): one 32x32 tile per workgroup, its k
+// range cut into four contiguous quarters (whole groups of 8 k), one per
+// wave.  Each wave accumulates the whole tile over its quarter on
+// v_mfma_f32_32x32x2f32 with its operands loaded straight into registers,
+// four groups of loads in flight (lanes 0-31 take k = 8g + t and lanes 32-63
+// k = 8g + 4 + t for MFMA step t of group g, for A and B alike, so every k
+// is summed once); the four partial tiles are then summed through LDS in
+// wave order, so the result does not depend on timing.
+__global__ void __launch_bounds__(256) matmul_ksplit(MatmulArgs p) {
+    __shared__ float red[4][1024];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int row = lane & 31, half = lane >> 5;
+    const int m0 = blockIdx.y * 32, n0 = blockIdx.x * 32;
+    size_t ab = 0, bb = 0;
+    matmul_batch(p, blockIdx.z, &ab, &bb);
+    const size_t M = p.M, N = p.N, K = p.K;
+    const float *A = p.a + ab * M * K;
+    const float *B = p.b + bb * K * N;
+    float *Y = p.y + static_cast<size_t>(blockIdx.z) * M * N;
+    const int groups = (p.K + 7) / 8;
+    const int per = (groups + 3) / 4;
+    const int g0 = wave * per, g1 = min(g0 + per, groups);
+    const int am = m0 + row, bn = n0 + row;
+    const bool arow = am < p.M, bcol = bn < p.N;
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    for (int gi = g0; gi < g1; gi += 4) {
+        float av[4][4], bv[4][4];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int k = (gi + u) * 8 + 4 * half + t;
+                const bool ok = gi + u < g1 && k < p.K;
+                av[u][t] = ok && arow ? A[static_cast<size_t>(am) * K + k] : 0.0f;
+                bv[u][t] = ok && bcol ? B[static_cast<size_t>(k) * N + bn] : 0.0f;
+            }
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av[u][t], bv[u][t], acc, 0, 0, 0);
+    }
+    // accumulator layout: column lane & 31, rows 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+    for (int r = 0; r < 16; r++) red[wave][(8 * (r >> 2) + 4 * half + (r & 3)) * 32 + row] = acc[r];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = tid * 4 + i;
+        const int m = m0 + (e >> 5), n = n0 + (e & 31);
+        const float v = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
+        if (m < p.M && n < p.N) Y[static_cast<size_t>(m) * N + n] = v;
     }
 }
 
@@ -227,6 +292,14 @@ int matmul_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     if (M > 0x7fffffffULL || N > 0x7fffffffULL || K > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
     const uint64_t mt = (M + kMmTile - 1) / kMmTile, nt = (N + kMmTile - 1) / kMmTile;
     if (mt > 65535 || batch > 65535 || nt > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
+    // 64x64 tiles for fewer than half the CUs: 32x32 tiles with k split over
+    // the waves instead (measured on the PSA attention products: 14 tiles at
+    // batch 1 27 -> 15 us of node time; 224 tiles at batch 16 the 64x64
+    // kernel is faster);
+    // SPKV2_MATMUL_KSPLIT=0 / 1 forces either
+    const uint64_t mt32 = (M + 31) / 32, nt32 = (N + 31) / 32;
+    bool ksplit = mt * nt * batch < 128 && mt32 <= 65535;
+    if (const char *e = getenv("SPKV2_MATMUL_KSPLIT")) ksplit = e[0] == '1' ? mt32 <= 65535 : false;
     MatmulArgs p{};
     p.a = dptr<const float>(ctx, node->inputs[0]);
     p.b = dptr<const float>(ctx, node->inputs[1]);
@@ -241,6 +314,13 @@ int matmul_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         p.yshape[i] = static_cast<int>(yr->shape[i]);
         p.ashape[i] = static_cast<int>(ar->shape[i]);
         p.bshape[i] = static_cast<int>(br->shape[i]);
+    }
+    if (ksplit) {
+        set_kernel_name(ctx, node, "matmul_ksplit_f32<32x32>");
+        hipLaunchKernelGGL(matmul_ksplit, dim3(static_cast<unsigned>(nt32), static_cast<unsigned>(mt32),
+                                               static_cast<unsigned>(batch)),
+                           dim3(256), 0, ctx->stream, p);
+        return launch_status("matmul");
     }
     set_kernel_name(ctx, node, "matmul_mfma_f32<64x64x16>");
     hipLaunchKernelGGL(matmul_mfma, dim3(static_cast<unsigned>(nt), static_cast<unsigned>(mt),

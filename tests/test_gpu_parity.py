@@ -416,6 +416,41 @@ def test_silu_activation_accuracy(gpu, monkeypatch, smallk):
     assert np.all(got[:grid.size][x[:grid.size] < -89.0] == 0.0)
 
 
+# Batched MatMul through both kernels: 64x64 LDS tiles and 32x32 tiles with
+# k split over the waves (chosen when the 64x64 grid is small; forced here):
+# plain 2-D, batched, broadcasting both ways, a constant B, ragged tiles,
+# K not a multiple of 8 or of 32, and the PSA attention products.
+MATMUL_CASES = [
+    dict(a_shape=[5, 7], b_shape=[7, 3]),
+    dict(a_shape=[2, 3, 8, 16], b_shape=[2, 3, 16, 5]),
+    dict(a_shape=[2, 1, 4, 6], b_shape=[3, 6, 5]),
+    dict(a_shape=[3, 70, 33], b_shape=[33, 65]),
+    dict(a_shape=[4, 33, 17], b_shape=[17, 9], const_b=True),
+    dict(a_shape=[1, 2, 400, 32], b_shape=[1, 2, 32, 400]),
+    dict(a_shape=[1, 2, 64, 400], b_shape=[1, 2, 400, 400]),
+    dict(a_shape=[2, 40, 1001], b_shape=[1001, 37]),
+]
+
+
+@pytest.mark.parametrize("ksplit", ["1", "0"])
+@pytest.mark.parametrize("kw", MATMUL_CASES, ids=[f"mm{i}" for i in range(len(MATMUL_CASES))])
+def test_matmul_both_kernels(gpu, monkeypatch, kw, ksplit):
+    from spinnv2_amd.runtime import Model
+
+    monkeypatch.setenv("SPKV2_MATMUL_KSPLIT", ksplit)
+    g = models.matmul_op(**kw)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        got = m.get_output(0)
+        name = m.kernel_name(0)
+    assert ("ksplit" in name) == (ksplit == "1"), name
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 # Small-gather stems (conv_smallk_f32: at most 4 input channels and 64 taps,
 # at most 64 output channels; one output pixel per lane, every output channel
 # in registers), against the oracle and against the implicit GEMM.
