@@ -548,6 +548,38 @@ __global__ void __launch_bounds__(256) softmax_strided(const float *__restrict__
     }
 }
 
+// The same for a short axis (dim <= D: YOLO's 16-bin DFL softmax): the
+// column stays in registers, so it is read once with every load in flight and
+// written once; the arithmetic and its order are softmax_strided's.
+template <int D>
+__global__ void __launch_bounds__(256) softmax_strided_reg(const float *__restrict__ x, float *__restrict__ y,
+                                                           size_t outer, int dim, size_t inner) {
+    const size_t cols = outer * inner;
+    for (size_t c = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; c < cols; c += static_cast<size_t>(gridDim.x) * 256) {
+        const size_t o = c / inner, in = c - o * inner;
+        const float *xc = x + o * dim * inner + in;
+        float *yc = y + o * dim * inner + in;
+        float v[D];
+#pragma unroll
+        for (int d = 0; d < D; d++) v[d] = d < dim ? xc[static_cast<size_t>(d) * inner] : -INFINITY;
+        float m = -INFINITY;
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < dim) m = fmaxf(m, v[d]);
+        float s = 0.0f;
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < dim) {
+                v[d] = __expf(v[d] - m);
+                s += v[d];
+            }
+        const float r = 1.0f / s;
+#pragma unroll
+        for (int d = 0; d < D; d++)
+            if (d < dim) yc[static_cast<size_t>(d) * inner] = v[d] * r;
+    }
+}
+
 // Nearest resize with the reference index rule (reference shape/resize.c:15-26).
 __global__ void __launch_bounds__(256) resize_nearest(const float *__restrict__ x, float *__restrict__ y, int N, int C,
                                                       int H, int W, int OH, int OW, float scale_h, float scale_w) {
@@ -983,7 +1015,8 @@ int softmax_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     else if (inner == 1)
         hipLaunchKernelGGL(softmax_rows, dim3(blocks_for(outer, 4)), dim3(256), 0, ctx->stream, x, y, outer, dim);
     else
-        hipLaunchKernelGGL(softmax_strided, dim3(grid_for(outer * inner, 256)), dim3(256), 0, ctx->stream, x, y, outer,
+        hipLaunchKernelGGL(dim <= 16 ? softmax_strided_reg<16> : dim <= 32 ? softmax_strided_reg<32> : softmax_strided,
+                           dim3(grid_for(outer * inner, 256)), dim3(256), 0, ctx->stream, x, y, outer,
                            dim, inner);
     return launch_status("softmax");
 }

@@ -149,6 +149,9 @@ FLOAT_OPS = [
     ("Softmax", [5, 2048], dict(axis=-1)),     # register-resident rows at their limit
     ("Softmax", [3, 2052], dict(axis=-1)),     # longer rows: three passes
     ("Softmax", [3, 6, 7], dict(axis=-1)),     # rows not a multiple of 4
+    ("Softmax", [2, 16, 4, 300], dict(axis=1)),  # DFL-like: 16 strided bins in registers
+    ("Softmax", [2, 24, 70], dict(axis=1)),    # strided, 24 of up to 32 in registers
+    ("Softmax", [2, 40, 33], dict(axis=1)),    # strided, longer than the register forms
     ("ReduceMean", [4, 2048, 7, 7], dict(axes=[2, 3])),
     ("ReduceMean", [2, 6, 5, 4], dict(axes=[1])),
     ("GlobalAveragePool", [2, 32, 7, 7], {}),
