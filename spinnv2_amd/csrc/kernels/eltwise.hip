@@ -105,6 +105,24 @@ __global__ void __launch_bounds__(256) binary_bcast(const float *__restrict__ a,
     }
 }
 
+// One operand a single element (a tensor times a constant: YOLO's attention
+// scale): 16-byte accesses, the reference's operand order kept
+// (scalar_first: the scalar is the left operand).
+template <int OP>
+__global__ void __launch_bounds__(256) binary_scalar4(const float4 *__restrict__ t, const float *__restrict__ sc,
+                                                      float4 *__restrict__ y, size_t n4, int act, int scalar_first) {
+    const float c = *sc;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += static_cast<size_t>(gridDim.x) * 256) {
+        const float4 u = t[i];
+        float4 r;
+        r.x = apply_act(scalar_first ? bin<OP>(c, u.x) : bin<OP>(u.x, c), act);
+        r.y = apply_act(scalar_first ? bin<OP>(c, u.y) : bin<OP>(u.y, c), act);
+        r.z = apply_act(scalar_first ? bin<OP>(c, u.z) : bin<OP>(u.z, c), act);
+        r.w = apply_act(scalar_first ? bin<OP>(c, u.w) : bin<OP>(u.w, c), act);
+        y[i] = r;
+    }
+}
+
 template <int OP>
 int launch_binary(hipStream_t s, const Spkv2TensorRecord *ar, const Spkv2TensorRecord *br, const Spkv2TensorRecord *yr,
                   const float *a, const float *b, float *y, int act) {
@@ -113,10 +131,18 @@ int launch_binary(hipStream_t s, const Spkv2TensorRecord *ar, const Spkv2TensorR
     const bool same = elem_count(ar) == n && elem_count(br) == n && ar->rank == yr->rank && br->rank == yr->rank;
     const bool aligned = ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
                            reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+    const bool a_scalar = elem_count(ar) == 1 && elem_count(br) == n;
+    const bool b_scalar = elem_count(br) == 1 && elem_count(ar) == n;
+    const float *t = a_scalar ? b : a;
+    const bool t_aligned = ((reinterpret_cast<uintptr_t>(t) | reinterpret_cast<uintptr_t>(y)) & 15) == 0;
     if (same && aligned && n % 4 == 0) {
         hipLaunchKernelGGL((binary_same4<OP>), dim3(grid_for(n / 4, 256)), dim3(256), 0, s,
                            reinterpret_cast<const float4 *>(a), reinterpret_cast<const float4 *>(b),
                            reinterpret_cast<float4 *>(y), n / 4, act);
+    } else if ((a_scalar || b_scalar) && t_aligned && n % 4 == 0) {
+        hipLaunchKernelGGL((binary_scalar4<OP>), dim3(grid_for(n / 4, 256)), dim3(256), 0, s,
+                           reinterpret_cast<const float4 *>(t), a_scalar ? a : b, reinterpret_cast<float4 *>(y), n / 4,
+                           act, a_scalar ? 1 : 0);
     } else {
         BcastDesc d;
         make_bcast(ar, br, yr, &d);

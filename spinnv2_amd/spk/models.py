@@ -182,7 +182,7 @@ def single_op(op: str, shape, **kw) -> Graph:
             return g
     elif op in ("Mul", "Sub", "Div", "Mod"):
         b = g.input("b", kw.get("b_shape", shape))
-        y = g.binary(op, x, b)
+        y = g.binary(op, b, x) if kw.get("swap") else g.binary(op, x, b)
     elif op == "Resize":
         y = g.resize(x, kw.get("scale", 2))
     elif op == "Softmax":

@@ -130,6 +130,11 @@ EXACT_OPS = [
     ("MaxPool", [1, 3, 16, 8], dict(k=3, s=2, p=1)),
     ("Resize", [2, 3, 6, 10], dict(scale=2)),
     ("Resize", [2, 3, 5, 7], dict(scale=2)),
+    # one operand a single element (16-byte path), either order; odd size (generic path)
+    ("Mul", [2, 3, 40, 40], dict(b_shape=[1])),
+    ("Sub", [2, 3, 40, 40], dict(b_shape=[1], swap=True)),
+    ("Div", [2, 8, 10, 10], dict(b_shape=[1], swap=True)),
+    ("Mul", [3, 5, 7], dict(b_shape=[1])),
 ]
 
 
