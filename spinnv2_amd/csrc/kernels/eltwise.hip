@@ -153,6 +153,20 @@ int launch_binary(hipStream_t s, const Spkv2TensorRecord *ar, const Spkv2TensorR
 
 enum UnOp { UN_RELU = 0, UN_SIGMOID, UN_CLIP, UN_LEAKY };
 
+// 1 / (1 + exp(-v)) on the hardware exponential and reciprocal, as the
+// conv epilogues' SiLU: within a few ulp of the reference's expf and
+// division, with its special values (+inf -> 1, -inf and v below about
+// -88.7 -> 0, NaN -> NaN).
+__device__ __forceinline__ float sigmoid_hw(float v) { return __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
+
+// Sigmoid over 16-byte groups (n a multiple of 4, aligned operands).
+__global__ void __launch_bounds__(256) sigmoid4(const float4 *__restrict__ x, float4 *__restrict__ y, size_t n4) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n4; i += static_cast<size_t>(gridDim.x) * 256) {
+        const float4 u = x[i];
+        y[i] = float4{sigmoid_hw(u.x), sigmoid_hw(u.y), sigmoid_hw(u.z), sigmoid_hw(u.w)};
+    }
+}
+
 template <int OP>
 __global__ void __launch_bounds__(256) unary_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n,
                                                     const float *__restrict__ lo, const float *__restrict__ hi,
@@ -162,7 +176,7 @@ __global__ void __launch_bounds__(256) unary_kernel(const float *__restrict__ x,
     for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += static_cast<size_t>(gridDim.x) * 256) {
         float v = x[i];
         if constexpr (OP == UN_RELU) v = v > 0.0f ? v : 0.0f;                  // relu.c:11
-        if constexpr (OP == UN_SIGMOID) v = 1.0f / (1.0f + expf(-v));          // sigmoid.c:11
+        if constexpr (OP == UN_SIGMOID) v = sigmoid_hw(v);                      // sigmoid.c:11
         if constexpr (OP == UN_CLIP) {                                         // clip_leakyrelu.c:23-27
             if (v < minv) v = minv;
             if (v > maxv) v = maxv;
@@ -762,7 +776,11 @@ int unary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     switch (node->op_type) {
     case SPKV2_OP_RELU: hipLaunchKernelGGL(unary_kernel<UN_RELU>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, 0.0f); break;
     case SPKV2_OP_SIGMOID:
-        hipLaunchKernelGGL(unary_kernel<UN_SIGMOID>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, 0.0f);
+        if (n % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y)) & 15) == 0)
+            hipLaunchKernelGGL(sigmoid4, dim3(grid_for(n / 4, 256)), dim3(256), 0, s, reinterpret_cast<const float4 *>(x),
+                               reinterpret_cast<float4 *>(y), n / 4);
+        else
+            hipLaunchKernelGGL(unary_kernel<UN_SIGMOID>, grid, dim3(256), 0, s, x, y, n, nullptr, nullptr, 0.0f);
         break;
     case SPKV2_OP_CLIP: {
         const float *lo = node->input_count >= 2 ? dptr<const float>(ctx, node->inputs[1]) : nullptr;

@@ -162,6 +162,7 @@ FLOAT_OPS = [
     ("GlobalAveragePool", [2, 32, 7, 7], {}),
     ("AveragePool", [1, 4, 9, 9], dict(k=3, s=2, p=1)),
     ("Sigmoid", [2, 300], {}),
+    ("Sigmoid", [3, 7, 5], {}),                # odd size: one element per thread
     ("Mul", [2, 8, 4, 4], dict(b_shape=[8, 1, 1])),
 ]
 
@@ -457,6 +458,19 @@ def test_matmul_both_kernels(gpu, monkeypatch, kw, ksplit):
         name = m.kernel_name(0)
     assert ("ksplit" in name) == (ksplit == "1"), name
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+def test_sigmoid_accuracy(gpu):
+    """Sigmoid (hardware exponential and reciprocal, 16-byte path) against
+    1 / (1 + exp(-v)) in float64: within 1e-5 relative on a grid over
+    [-100, 100]; +inf -> 1, -inf -> 0, NaN -> NaN."""
+    grid = np.linspace(-100, 100, 20001)
+    x = np.concatenate([grid, [np.inf, -np.inf, np.nan], np.zeros(1)]).astype(np.float32)
+    g = models.single_op("Sigmoid", [1, x.size])
+    got = run_gpu(write_spk(g, "mi355x"), [x.reshape(1, -1)])[0].ravel()
+    want = 1.0 / (1.0 + np.exp(-grid))
+    np.testing.assert_allclose(got[:grid.size], want, rtol=1e-5, atol=1e-30)
+    assert got[grid.size] == 1.0 and got[grid.size + 1] == 0.0 and np.isnan(got[grid.size + 2])
 
 
 # Small-gather stems (conv_smallk_f32: at most 4 input channels and 64 taps,
