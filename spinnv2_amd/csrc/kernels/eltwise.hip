@@ -450,6 +450,32 @@ __device__ __forceinline__ float wave_reduce(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return wave_reduce<false>(v); }
 __device__ __forceinline__ float wave_max(float v) { return wave_reduce<true>(v); }
 
+// Max over short contiguous rows (len <= 128: YOLO's 80 class scores per
+// anchor): 16 lanes per row, four rows per wave; each lane keeps the max of
+// its elements (v > acc, so NaN never wins, as row_reduce), then four DPP
+// shifts within the 16-lane row leave the row's max in its lane 15.
+__global__ void __launch_bounds__(256) row_max16(const float *__restrict__ x, float *__restrict__ y, size_t rows,
+                                                 int len) {
+    const int l16 = threadIdx.x & 15;
+    const size_t row = (static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x) >> 4;
+    const bool live = row < rows;
+    float acc = -INFINITY;
+    if (live) {
+        const float *xr = x + row * len;
+        for (int i = l16; i < len; i += 16) {
+            const float v = xr[i];
+            acc = v > acc ? v : acc;
+        }
+    }
+    const int id = __float_as_int(-INFINITY);
+    auto step = [&](float o) { acc = o > acc ? o : acc; };
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(acc), 0x111, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(acc), 0x112, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(acc), 0x114, 0xf, 0xf, false)));
+    step(__int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(acc), 0x118, 0xf, 0xf, false)));
+    if (live && l16 == 15) y[row] = acc;
+}
+
 // One wave per contiguous row of `len` elements.  MODE 0: mean of x/denom
 // terms (ReduceMean, reference reduce.c:37-40); 1: max (ReduceMax);
 // 2: sum * inv (GlobalAveragePool, avgpool.c:62-67).
@@ -1116,7 +1142,10 @@ int reduce_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         for (int i = 0; i < first; i++) rows *= xr->shape[i];
         for (int i = first; i < rank; i++) len *= xr->shape[i];
         if (rows * len == 0) return 0;
-        if (is_max)
+        if (is_max && len <= 128)
+            hipLaunchKernelGGL(row_max16, dim3(blocks_for(rows, 16)), dim3(256), 0, ctx->stream, x, y, rows,
+                               static_cast<int>(len));
+        else if (is_max)
             hipLaunchKernelGGL(row_reduce<1>, dim3(blocks_for(rows, 4)), dim3(256), 0, ctx->stream, x, y, rows,
                                static_cast<int>(len), denom);
         else

@@ -1164,6 +1164,11 @@ INDEX_CASES = [
     ("TopK", [5, 130], dict(k=1, axis=1, largest=1)),
     ("TopK", [2, 70], dict(k=65, axis=-1, largest=0)),
     ("ReduceMax", [1, 80, 8400], dict(axes=[1], keepdims=0)),
+    # the last axis: 16 lanes per row up to 128 (YOLO's 80 scores, ragged 7, the limit), a wave beyond
+    ("ReduceMax", [2, 300, 80], dict(axes=[2], keepdims=0)),
+    ("ReduceMax", [3, 33, 7], dict(axes=[2], keepdims=0)),
+    ("ReduceMax", [2, 17, 128], dict(axes=[2], keepdims=0)),
+    ("ReduceMax", [2, 17, 129], dict(axes=[2], keepdims=0)),
 ]
 
 
