@@ -1185,12 +1185,14 @@ int reduce_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
 // floor(o / 2) index): each thread reads 2 input columns (8 bytes) and
 // writes them doubled to both output rows (two 16-byte stores).
 __global__ void __launch_bounds__(256) resize2x_x2(const float *__restrict__ x, float *__restrict__ y, unsigned planes,
-                                                   int H, int W) {
+                                                   int H, int W, unsigned C, size_t y_img) {
     const unsigned pairs = static_cast<unsigned>(H * (W / 2));
     const int OW = 2 * W;
     for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
         const float *xp = x + static_cast<size_t>(plane) * H * W;
-        float *yp = y + static_cast<size_t>(plane) * 4 * H * W;
+        // y's images y_img elements apart (a Concat buffer's channel slice, or C * 4HW)
+        const unsigned img = plane / C;
+        float *yp = y + img * y_img + static_cast<size_t>(plane - img * C) * 4 * H * W;
         for (unsigned q = blockIdx.x * 256 + threadIdx.x; q < pairs; q += gridDim.x * 256) {
             const int ih = static_cast<int>(q / static_cast<unsigned>(W / 2));
             const int iw = 2 * (static_cast<int>(q) - ih * (W / 2));
@@ -1216,10 +1218,17 @@ int resize_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         if (pairs > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
         const dim3 grid(static_cast<unsigned>(std::min<size_t>((pairs + 255) / 256, 1024)),
                         static_cast<unsigned>(std::min<size_t>(planes, 65535)));
-        hipLaunchKernelGGL(resize2x_x2, grid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]),
-                           dptr<float>(ctx, node->outputs[0]), static_cast<unsigned>(planes), H, W);
+        float *y = dptr<float>(ctx, node->outputs[0]);
+        size_t y_img = static_cast<size_t>(C) * OH * OW;
+        if (const Spkv2TensorView *v = live_view(ctx, node->outputs[0])) {  // written into a Concat's buffer
+            y = reinterpret_cast<float *>(v->base);
+            y_img = static_cast<size_t>(v->img_elems);
+        }
+        hipLaunchKernelGGL(resize2x_x2, grid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]), y,
+                           static_cast<unsigned>(planes), H, W, static_cast<unsigned>(C), y_img);
         return launch_status("resize");
     }
+    if (live_view(ctx, node->outputs[0])) return SPKV2_E_UNSUPPORTED;  // views only for the 2x path
     const float scale_h = static_cast<float>(OH) / static_cast<float>(H);
     const float scale_w = static_cast<float>(OW) / static_cast<float>(W);
     set_kernel_name(ctx, node, "resize_nearest");

@@ -11,7 +11,8 @@
 // of that buffer, the other readers read it there (a "view": base pointer,
 // elements between images), and the Concat copies only what is left:
 //   * an input written by an fp32 implicit-GEMM conv (without a residual: its
-//     residual keeps y's natural layout) or by a same-shape Add is placed;
+//     residual keeps y's natural layout), by a same-shape Add or by a 2x
+//     nearest Resize is placed;
 //   * an input that is one output of a channel Split whose outputs are
 //     consecutive inputs of the Concat (YOLO's C2f blocks) is placed with all
 //     of them, the Split's input covering their ranges: the Split itself then
@@ -90,6 +91,18 @@ bool same_shape_add(const Spkv2Context *ctx, uint32_t id) {
     return true;
 }
 
+// A 2x nearest Resize of an fp32 NCHW tensor that resize_run's 2x kernel
+// runs (even width, same N and C), which takes y's image stride.
+bool resize2x(const Spkv2Context *ctx, uint32_t id) {
+    const Spkv2NodeRecord *n = &ctx->node_records[id];
+    if (n->op_type != SPKV2_OP_RESIZE || !builtin_runs(ctx, id) || n->input_count < 1 || n->output_count != 1)
+        return false;
+    const Spkv2TensorRecord *x = rec(ctx, n->inputs[0]), *y = rec(ctx, n->outputs[0]);
+    return x->rank == 4 && y->rank == 4 && x->dtype == SPKV2_DTYPE_FP32 && y->dtype == SPKV2_DTYPE_FP32 &&
+           y->shape[0] == x->shape[0] && y->shape[1] == x->shape[1] && y->shape[2] == 2 * x->shape[2] &&
+           y->shape[3] == 2 * x->shape[3] && x->shape[3] % 2 == 0;
+}
+
 // The producer of t can write it through a view.
 bool strided_writer(const Spkv2Context *ctx, const Uses &u, uint32_t t) {
     const int p = u.producer[t];
@@ -97,7 +110,7 @@ bool strided_writer(const Spkv2Context *ctx, const Uses &u, uint32_t t) {
     const Spkv2NodeRecord *n = &ctx->node_records[p];
     if (const ConvPlan *cp = f32_conv(ctx, static_cast<uint32_t>(p)))
         return !cp->g.has_res && n->output_count == 1 && n->outputs[0] == t;
-    return same_shape_add(ctx, static_cast<uint32_t>(p));
+    return same_shape_add(ctx, static_cast<uint32_t>(p)) || resize2x(ctx, static_cast<uint32_t>(p));
 }
 
 // Every reader of t but `owner` reads it through a view (a conv as its
