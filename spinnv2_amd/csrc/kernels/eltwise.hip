@@ -218,6 +218,7 @@ struct PoolArgs {
     const float *__restrict__ x;
     float *__restrict__ y;
     int N, C, H, W, OH, OW, kh, kw, sh, sw, ph, pw;
+    size_t x_img, y_img;  // elements between images (maxpool_kernel; C*H*W and C*OH*OW unless views)
 };
 
 // reference pool/maxpool.c:20-40: -inf start, out-of-bounds taps skipped.
@@ -227,8 +228,9 @@ __global__ void __launch_bounds__(256) maxpool_kernel(PoolArgs a) {
     const unsigned planes = static_cast<unsigned>(a.N * a.C);
     const unsigned per_plane = static_cast<unsigned>(a.OH * a.OW);
     for (unsigned plane = blockIdx.y; plane < planes; plane += gridDim.y) {
-        const float *xp = a.x + static_cast<size_t>(plane) * a.H * a.W;
-        float *yp = a.y + static_cast<size_t>(plane) * per_plane;
+        const unsigned img = plane / static_cast<unsigned>(a.C), c = plane - img * static_cast<unsigned>(a.C);
+        const float *xp = a.x + img * a.x_img + static_cast<size_t>(c) * a.H * a.W;
+        float *yp = a.y + img * a.y_img + static_cast<size_t>(c) * per_plane;
         for (unsigned r = blockIdx.x * 256 + threadIdx.x; r < per_plane; r += gridDim.x * 256) {
             const int oh = static_cast<int>(r / static_cast<unsigned>(a.OW));
             const int ow = static_cast<int>(r) - oh * a.OW;
@@ -902,6 +904,8 @@ static int pool_args(Spkv2Context *ctx, const Spkv2NodeRecord *node, PoolArgs *p
     p->sw = attr.strides[1];
     p->ph = attr.pads[0];
     p->pw = attr.pads[1];
+    p->x_img = static_cast<size_t>(p->C) * p->H * p->W;
+    p->y_img = static_cast<size_t>(p->C) * p->OH * p->OW;
     return 0;
 }
 
@@ -1004,6 +1008,9 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const PoolPlan *q = ctx->plan_dtors[node->id] == pool_plan_free
                             ? static_cast<const PoolPlan *>(ctx->plans[node->id])
                             : nullptr;
+    // views are set up for stride-1 pools only, which take the generic kernel
+    if ((live_view(ctx, node->inputs[0]) || live_view(ctx, node->outputs[0])) && is_pool3s2_x4(p))
+        return SPKV2_E_UNSUPPORTED;
     if (q && q->q_out && q->q_src && handoffs_live(ctx) && is_pool3s2_x4(p) && p.C % 64 == 0) {
         // the producer quantized the input for this pool's consumers
         set_kernel_name(ctx, node, "maxpool3s2_i8");
@@ -1039,6 +1046,16 @@ int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     if (per_plane > 0x7fffffffULL || planes > 0x7fffffffULL) return SPKV2_E_UNSUPPORTED;
     const dim3 grid(static_cast<unsigned>(std::min<size_t>((per_plane + 255) / 256, 1024)),
                     static_cast<unsigned>(std::min<size_t>(planes, 65535)));
+    // input and output through their channel-slice views when they have them
+    // (SPPF's stride-1 pools: a Concat's buffer)
+    if (const Spkv2TensorView *v = live_view(ctx, node->inputs[0])) {
+        p.x = reinterpret_cast<const float *>(v->base);
+        p.x_img = static_cast<size_t>(v->img_elems);
+    }
+    if (const Spkv2TensorView *v = live_view(ctx, node->outputs[0])) {
+        p.y = reinterpret_cast<float *>(v->base);
+        p.y_img = static_cast<size_t>(v->img_elems);
+    }
     hipLaunchKernelGGL(maxpool_kernel, grid, dim3(256), 0, ctx->stream, p);
     return launch_status("maxpool");
 }

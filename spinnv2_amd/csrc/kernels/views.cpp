@@ -17,9 +17,10 @@
 //     consecutive inputs of the Concat (YOLO's C2f blocks) is placed with all
 //     of them, the Split's input covering their ranges: the Split itself then
 //     has nothing to copy;
-//   * every other reader of a placed tensor must be such a conv (as its x)
-//     or Add, so it can read through the view; the Concat's output is the
-//     buffer itself, so its readers must be too.
+//   * every other reader of a placed tensor must be such a conv (as its x),
+//     an Add or a stride-1 MaxPool (SPPF's, which also writes its output
+//     into the buffer), so it can read through the view; the Concat's
+//     output is the buffer itself, so its readers must be too.
 // Every channel of a buffer has exactly one writer per run (its placed
 // tensor's producer, or the Concat's copy), so no other tensor's data is
 // ever overwritten there.  Like the other handoffs the views are in force
@@ -103,6 +104,18 @@ bool resize2x(const Spkv2Context *ctx, uint32_t id) {
            y->shape[3] == 2 * x->shape[3] && x->shape[3] % 2 == 0;
 }
 
+// A stride-1 MaxPool of an fp32 NCHW tensor (SPPF's): maxpool_run takes it
+// on its generic kernel, which reads and writes through image strides.
+bool stride1_maxpool(const Spkv2Context *ctx, uint32_t id) {
+    const Spkv2NodeRecord *n = &ctx->node_records[id];
+    if (n->op_type != SPKV2_OP_MAXPOOL || !builtin_runs(ctx, id) || n->input_count < 1 || n->output_count != 1)
+        return false;
+    Spkv2AttrRecord attr;
+    if (spkv2_ctx_get_attr(ctx, n, &attr) != 0 || attr.strides[0] != 1 || attr.strides[1] != 1) return false;
+    const Spkv2TensorRecord *x = rec(ctx, n->inputs[0]), *y = rec(ctx, n->outputs[0]);
+    return x->rank == 4 && y->rank == 4 && x->dtype == SPKV2_DTYPE_FP32 && y->dtype == SPKV2_DTYPE_FP32;
+}
+
 // The producer of t can write it through a view.
 bool strided_writer(const Spkv2Context *ctx, const Uses &u, uint32_t t) {
     const int p = u.producer[t];
@@ -110,7 +123,8 @@ bool strided_writer(const Spkv2Context *ctx, const Uses &u, uint32_t t) {
     const Spkv2NodeRecord *n = &ctx->node_records[p];
     if (const ConvPlan *cp = f32_conv(ctx, static_cast<uint32_t>(p)))
         return !cp->g.has_res && n->output_count == 1 && n->outputs[0] == t;
-    return same_shape_add(ctx, static_cast<uint32_t>(p)) || resize2x(ctx, static_cast<uint32_t>(p));
+    return same_shape_add(ctx, static_cast<uint32_t>(p)) || resize2x(ctx, static_cast<uint32_t>(p)) ||
+           stride1_maxpool(ctx, static_cast<uint32_t>(p));
 }
 
 // Every reader of t but `owner` reads it through a view (a conv as its
@@ -124,6 +138,7 @@ bool readers_ok(const Spkv2Context *ctx, const Uses &u, uint32_t t, uint32_t own
         }
         if (f32_conv(ctx, id) && slot == 0) continue;
         if (same_shape_add(ctx, id)) continue;
+        if (stride1_maxpool(ctx, id) && slot == 0) continue;
         return false;
     }
     return true;

@@ -138,10 +138,11 @@ def test_c2f_views_graph_mode_and_fault_path(gpu):
 
 
 # batch -> (Splits, Concats) without copies: the eight C2f blocks' Splits;
-# at batch 1 only the Concats whose every input is placed (the C2f ones and
-# the PAN Concat whose other input is a conv's: the 2x Resize writes its
-# upsampled input in place), at batch 2 also those with inputs left to copy
-YOLO_VIEWS = {1: (8, 9), 2: (8, 12)}
+# at batch 1 only the Concats whose every input is placed (the C2f ones,
+# SPPF's -- its stride-1 MaxPools read and write the buffer -- and the PAN
+# Concat whose other input is a conv's: the 2x Resize writes its upsampled
+# input in place), at batch 2 also those with inputs left to copy
+YOLO_VIEWS = {1: (8, 10), 2: (8, 13)}
 
 
 @pytest.mark.parametrize("batch", sorted(YOLO_VIEWS))
