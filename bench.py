@@ -10,10 +10,14 @@ Reported:
   value          images/sec at batch 64 over the timed K steps (the node
                  loop captured into a HIP graph during warmup and replayed;
                  --eager times the plain node loop instead);
-  roofline       conv implicit-GEMM throughput: sum of conv FLOP per step /
-                 sum of conv node device time per step, from HIP events
-                 around every node on the run stream in a separate eager pass
-                 of W + K steps, against the fp32 MFMA peak;
+  roofline       conv implicit-GEMM throughput: conv FLOP per step / the
+                 summed kernel-trace durations of the conv nodes' launches
+                 per step (the committed rocprofv3 summary of this workload),
+                 against the fp32 MFMA peak; beside it the live figures of
+                 this run: HIP events around every node on the run stream in
+                 a separate eager pass of W + K steps, and the timed step;
+  graph_matches_eager  the timed graph replay's output is bit-identical to
+                 the eager pass's output of the same input;
   b1_*           batch-1 latency and images/sec (HIP-graph replay);
   cpu_baseline   the reference runtime (cpu_generic package: naive conv on
                  x86) on one batch-1 image, timed on the host;
@@ -203,9 +207,16 @@ def pmc_traffic(name: str = "conv_igemm_f32_resnet101_b64_traffic.txt") -> dict 
     return vals or None
 
 
-def batch1_latency(depth: int, steps: int, lib, eager: bool = False) -> float:
+def bit_identical(a: np.ndarray, b: np.ndarray) -> bool:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and bool(np.array_equal(a.view(np.uint32), b.view(np.uint32)))
+
+
+def batch1_latency(depth: int, steps: int, lib, eager: bool = False) -> tuple[float, bool]:
     """Batch-1 latency: ms per spkv2_run of a HIP-graph-captured node loop
-    (the plain node loop with eager), input already resident on the device."""
+    (the plain node loop with eager), input already resident on the device;
+    and whether the last timed run's output is bit-identical to an eager
+    run's before it."""
     from spinnv2_amd.runtime import DeviceBuffer, Model
     from spinnv2_amd.spk import models, write_spk
 
@@ -215,6 +226,8 @@ def batch1_latency(depth: int, steps: int, lib, eager: bool = False) -> float:
     x1buf = DeviceBuffer(x1.nbytes, lib)
     x1buf.upload(x1)
     m1.bind_input(0, x1buf)
+    m1.run()
+    eager_out = m1.get_output(0)
     m1.set_graph_mode(not eager)
     for _ in range(5):
         m1.run()
@@ -224,9 +237,10 @@ def batch1_latency(depth: int, steps: int, lib, eager: bool = False) -> float:
         m1.run()
     lib.spkv2_device_synchronize()
     b1_ms = (time.perf_counter() - t0) * 1e3 / steps
+    same = bit_identical(m1.get_output(0), eager_out)
     m1.close()
     x1buf.free()
-    return b1_ms
+    return b1_ms, same
 
 
 def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, node_report: bool = False,
@@ -284,6 +298,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
         m.run()
     lib.spkv2_device_synchronize()
     m.set_profiling(False)
+    eager_out = m.get_output(0)
     m.set_graph_mode(not eager)
     for _ in range(warmup):
         m.run()
@@ -293,6 +308,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
         m.run()
     lib.spkv2_device_synchronize()
     elapsed = time.perf_counter() - t0
+    graph_same = bit_identical(m.get_output(0), eager_out)
     m.set_graph_mode(False)
     conv_ms = 0.0
     for nid in ops:
@@ -335,6 +351,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     tops = total_ops / (conv_ms * 1e-3) / 1e12
     out = {"workload": "resnet50_int8_224", "batch": batch, "images_per_sec": batch * steps / elapsed,
            "ms_per_step": elapsed * 1e3 / steps, "timed_mode": "eager" if eager else "hip_graph",
+           "graph_matches_eager": graph_same,
            "semantics": "reference kernel_conv_int8 (conv_int8.c:121-210): per-channel symmetric int8 weights, "
                         "per-tensor symmetric activations (zero point 0), int32 accumulate, float dequantize + "
                         "bias + fp32 residual + Relu; fp32 tensors between nodes",
@@ -352,6 +369,8 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
         b1 = DeviceBuffer(x1.nbytes, lib)
         b1.upload(x1)
         m1.bind_input(0, b1)
+        m1.run()
+        eager1 = m1.get_output(0)
         m1.set_graph_mode(not eager)
         for _ in range(5):
             m1.run()
@@ -361,6 +380,7 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
             m1.run()
         lib.spkv2_device_synchronize()
         out["b1_ms_per_image"] = (time.perf_counter() - t0) * 1e3 / b1_steps
+        out["b1_graph_matches_eager"] = bit_identical(m1.get_output(0), eager1)
         m1.close()
         b1.free()
     return out
@@ -551,6 +571,7 @@ def main() -> None:
     lib.spkv2_device_synchronize()
     profiled_elapsed = time.perf_counter() - t0
     m.set_profiling(False)
+    eager_logits = m.get_output(0)
     # the timed region: the node loop captured once into a HIP graph (during
     # warmup) and replayed, input resident in HBM
     if not args.eager:
@@ -563,8 +584,10 @@ def main() -> None:
         m.run()
     lib.spkv2_device_synchronize()
     elapsed = time.perf_counter() - t0
+    logits = m.get_output(0)
+    graph_same = bit_identical(logits, eager_logits)
     m.set_graph_mode(False)
-    logits = m.get_output(0).reshape(args.batch, -1)
+    logits = logits.reshape(args.batch, -1)
     # host-buffer interface (spkv2_set_input / spkv2_get_output copy over PCIe
     # each step): reported beside, never as, the value
     pcie_ips = None
@@ -596,9 +619,20 @@ def main() -> None:
     xin.free()
     ms_per_step = elapsed * 1e3 / args.steps
     conv_tflops = conv_flops / (conv_ms * 1e-3) / 1e12
+    # Roofline time basis: the summed kernel-trace durations of every launch
+    # of the conv nodes (GEMM, split-K epilogue, padding) per step, from the
+    # committed rocprofv3 summary of this workload, so the fraction
+    # reproduces from profiles/.  Beside it, two live figures of this run:
+    # per-node HIP events (event overhead and launch gaps inside the node:
+    # an upper bound of the conv time) and the whole timed graph step (every
+    # kernel of the network: a looser upper bound).
+    kstats = (pmc_traffic("conv_igemm_f32_resnet101_b64_kernel_stats.txt")
+              if (args.depth, args.batch) == (101, 64) else None)
+    trace_ms = kstats.get("conv_kernels_ms_per_run") if kstats else None
+    roof_tflops = conv_flops / (trace_ms * 1e-3) / 1e12 if trace_ms else conv_tflops
 
     # ---------------------------------------------------------- batch 1
-    b1_ms = batch1_latency(args.depth, args.b1_steps, lib, args.eager) if args.b1_steps > 0 else None
+    b1_ms, b1_same = batch1_latency(args.depth, args.b1_steps, lib, args.eager) if args.b1_steps > 0 else (None, None)
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
     ew = None if args.no_elementwise else elementwise(lib)
@@ -627,13 +661,26 @@ def main() -> None:
         "b1_images_per_sec": 1e3 / b1_ms if b1_ms else None,
         "conv_ms_per_step": conv_ms,
         "node_ms_per_step": total_node_ms,
-        "roofline": {"bound": "mfma", "achieved": conv_tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": conv_tflops / FP32_MFMA_PEAK_TFLOPS,
+        "graph_matches_eager": graph_same,
+        "b1_graph_matches_eager": b1_same,
+        "roofline": {"bound": "mfma", "achieved": roof_tflops, "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": roof_tflops / FP32_MFMA_PEAK_TFLOPS,
+                     "basis": ("summed kernel-trace durations of the conv nodes' launches per step "
+                               "(profiles/conv_igemm_f32_resnet101_b64_kernel_stats.txt, result conv_kernels_ms_per_run)"
+                               if trace_ms else "HIP events around every conv node (no committed trace for this shape)"),
+                     "kernel_ms_per_step": trace_ms,
+                     "event_basis": {"conv_ms_per_step": conv_ms, "tflops": conv_tflops,
+                                     "frac": conv_tflops / FP32_MFMA_PEAK_TFLOPS,
+                                     "note": "HIP events per node, eager pass of this run: an upper bound of the time"},
+                     "step_basis": {"ms_per_step": ms_per_step,
+                                    "tflops": conv_flops / (ms_per_step * 1e-3) / 1e12,
+                                    "frac": conv_flops / (ms_per_step * 1e-3) / 1e12 / FP32_MFMA_PEAK_TFLOPS,
+                                    "note": "conv FLOP over the whole timed graph step (all kernels)"},
                      "traffic": traffic.get("conv_hbm_bytes_per_step") if traffic else None,
                      "traffic_basis": "HBM bytes of all conv launches of one step (rocprofv3 FETCH_SIZE + "
                                       "WRITE_SIZE, copy-kernel scaled; profiles/)" if traffic else None,
                      "algorithmic_bytes": conv_alg_bytes,
-                     "kernel": "conv_igemm_f32 (all conv nodes; HIP events per node on the run stream)"},
+                     "kernel": "conv_igemm_f32 (all conv nodes)"},
         "cpu_baseline": base,
         "cpu_baseline_simd": base_simd,
         "int8": int8,

@@ -98,6 +98,7 @@ class Package:
                 w = np.frombuffer(raw, dtype=dt).reshape(t.shape)
                 self.weights[t.id] = w.astype(np.float32) if t.dtype == 3 else w.copy()
         self.quant = {}
+        self.zero_points = {}
         if 9 in secs:
             qoff, qsize = secs[9]
             first = _QP.unpack_from(blob, qoff)
@@ -105,6 +106,9 @@ class Package:
             for i in range(count):
                 tid, scheme, axis, nch, doff = _QP.unpack_from(blob, qoff + i * _QP.size)
                 self.quant[tid] = np.frombuffer(blob[qoff + doff: qoff + doff + 4 * nch], dtype="<f4").copy()
+                # int32 zero points follow the scales (reference spk_writer.py quantization section)
+                zoff = qoff + doff + 4 * nch
+                self.zero_points[tid] = np.frombuffer(blob[zoff: zoff + 4 * nch], dtype="<i4").copy()
         meta = json.loads(blob[secs[1][0]: secs[1][0] + secs[1][1]].decode())
         self.inputs = [t.id for t in self.tensors if t.role == 1]
         self.outputs = list(meta.get("outputs", [t.id for t in self.tensors if t.role == 2]))
@@ -143,7 +147,55 @@ class OracleExecutor:
         vals[n.outputs[0]] = y
         return y
 
+    def _is_q8(self, tid) -> bool:
+        """An int8 activation tensor (the INT8 configuration with int8
+        tensors between nodes)."""
+        t = self.pkg.tensors[tid]
+        return t.dtype == 2 and t.role != 3
+
+    def _qz(self, tid):
+        return float(self.pkg.quant[tid][0]), int(self.pkg.zero_points[tid][0])
+
+    def _conv_q8(self, n, vals):
+        """Conv of the INT8 configuration (spk_oracle.c oracle_q8_conv): int8
+        (or fp32, quantized on load) input with (s_x, z_x), per-channel int8
+        weights, int32 accumulation, fixed-point requantization into int8
+        with (s_y, z_y), int8 residual with (s_r, z_r), Relu clamp."""
+        lib = self.lib
+        x = vals[n.inputs[0]]
+        w = vals[n.inputs[1]]
+        b = vals[n.inputs[2]] if len(n.inputs) > 2 else None
+        sx, zx = self._qz(n.inputs[0])
+        sy, zy = self._qz(n.outputs[0])
+        if x.dtype != np.int8:
+            xf = np.ascontiguousarray(x, dtype=np.float32)
+            x = np.zeros(xf.shape, np.int8)
+            lib.oracle_q8_quantize(_f(xf), _f(x), ctypes.c_size_t(xf.size), ctypes.c_float(sx), zx)
+        r, sr, zr = None, 0.0, 0
+        if len(n.inputs) > 3:
+            r = np.ascontiguousarray(vals[n.inputs[3]])
+            assert r.dtype == np.int8, "the INT8 configuration's residual is an int8 tensor"
+            sr, zr = self._qz(n.inputs[3])
+        M = w.shape[0]
+        sw = np.ascontiguousarray(self.pkg.quant[n.inputs[1]][:M], dtype=np.float32)
+        bq, m1, m2, shf = (np.zeros(M, np.int32) for _ in range(4))
+        rc = lib.oracle_q8_requant_params(ctypes.c_float(sx), _f(sw), ctypes.c_float(sy), ctypes.c_float(sr),
+                                          _f(np.ascontiguousarray(b, dtype=np.float32) if b is not None else None),
+                                          M, _f(bq), _f(m1), _f(m2), _f(shf))
+        assert rc == 0, "requantization shift out of range"
+        y = self._out(n, vals, np.int8)
+        acc = np.zeros(y.shape, np.int32)
+        N, C, H, W = x.shape
+        _, _, KH, KW = w.shape
+        a = n.attr
+        lib.oracle_q8_conv(_f(np.ascontiguousarray(x)), zx, _f(w), _f(bq), _f(m1), _f(m2), _f(shf), _f(r), zr, zy,
+                           int(a["act"] == 1), _f(y), _f(acc), N, C, H, W, M, KH, KW, y.shape[2], y.shape[3],
+                           a["strides"][0], a["strides"][1], a["pads"][0], a["pads"][1], a["dil"][0], a["dil"][1])
+        self.acc[n.id] = acc
+
     def _conv(self, n, vals):
+        if self._is_q8(n.outputs[0]) or self._is_q8(n.inputs[0]):
+            return self._conv_q8(n, vals)
         x = vals[n.inputs[0]]
         w = vals[n.inputs[1]]
         b = vals[n.inputs[2]] if len(n.inputs) > 2 else None
@@ -197,14 +249,31 @@ class OracleExecutor:
                       a["strides"][1], a["pads"][0], a["pads"][1])
 
     def _maxpool(self, n, vals):
+        if vals[n.inputs[0]].dtype == np.int8:
+            assert self._is_q8(n.outputs[0]) and self._qz(n.inputs[0]) == self._qz(n.outputs[0])
+            x = vals[n.inputs[0]]
+            y = self._out(n, vals, np.int8)
+            a = n.attr
+            self.lib.oracle_q8_maxpool(_f(x), _f(y), *x.shape, y.shape[2], y.shape[3], a["kernel"][0],
+                                       a["kernel"][1], a["strides"][0], a["strides"][1], a["pads"][0], a["pads"][1])
+            return
         x, y, g = self._pool_args(n, vals)
         self.lib.oracle_maxpool_f32(_f(x), _f(y), *g)
+
+    def _plane_mean_q8(self, n, vals):
+        x = vals[n.inputs[0]]
+        y = self._out(n, vals)
+        s, z = self._qz(n.inputs[0])
+        self.lib.oracle_q8_plane_mean(_f(x), _f(y), ctypes.c_size_t(x.shape[0] * x.shape[1]), x.shape[2] * x.shape[3],
+                                      ctypes.c_float(s), z)
 
     def _averagepool(self, n, vals):
         x, y, g = self._pool_args(n, vals)
         self.lib.oracle_avgpool_f32(_f(x), _f(y), *g)
 
     def _globalaveragepool(self, n, vals):
+        if vals[n.inputs[0]].dtype == np.int8:
+            return self._plane_mean_q8(n, vals)
         x = vals[n.inputs[0]]
         y = self._out(n, vals)
         self.lib.oracle_global_avgpool_f32(_f(x), _f(y), x.shape[0], x.shape[1], x.shape[2] * x.shape[3])
@@ -266,6 +335,12 @@ class OracleExecutor:
         self.lib.oracle_reduce_f32(_f(x), shp, x.ndim, ctypes.c_uint32(mask), int(is_max), _f(y))
 
     def _reducemean(self, n, vals):
+        x = vals[n.inputs[0]]
+        if x.dtype == np.int8:
+            a = n.attr
+            axes = sorted(v % x.ndim for v in a["extra"][:a["extra_count"]])
+            assert x.ndim == 4 and axes == [2, 3], "int8 ReduceMean over the spatial axes only"
+            return self._plane_mean_q8(n, vals)
         self._reduce(n, vals, False)
 
     def _reducemax(self, n, vals):

@@ -366,6 +366,152 @@ int oracle_conv2d_int8(const float *x, const int8_t *wq, const float *w_scales, 
     return 0;
 }
 
+/* ------------------------------------------- INT8 with int8 tensors (Q8)
+ *
+ * The INT8 configuration the benchmark names (per-channel symmetric int8
+ * weights, per-tensor asymmetric int8 activations between nodes, int32
+ * accumulation, fixed-point requantization with round-half-away, fused Relu
+ * clamp).  The reference runtime has no such mode: its INT8 conv keeps fp32
+ * tensors between nodes with zero point 0 (conv_int8.c:121-210,
+ * compiler/quantization/calibrate.py:16).  This is the mode's definition,
+ * restated independently of the device code; tests/test_oracle_q8.py pins it
+ * with int64 brute force, the zero-point identity, and exact rationals. */
+
+/* t / 2^s rounded to nearest, ties away from zero (s >= 1) */
+int64_t oracle_q8_round_shift(int64_t t, int s) {
+    const int64_t half = (int64_t)1 << (s - 1);
+    if (t >= 0) return (t + half) >> s;
+    return -((-t + half) >> s);
+}
+
+static double rha_double(double v) { return v >= 0.0 ? floor(v + 0.5) : -floor(-v + 0.5); }
+
+/* Per output channel m: bias_q[m] = round_half_away(bias[m] / (s_x s_w[m]))
+ * clamped to +-2^30, and the fixed-point multipliers of
+ *   R1 = (s_x s_w[m]) / s_y  (accumulator -> output units)
+ *   R2 = s_r / s_y           (residual -> output units; 0 without one)
+ * with one shift S[m] for both: S = 31 - e where max(R1, R2) = f 2^e,
+ * f in [0.5, 1), and Mi = floor(Ri 2^S + 0.5), one less S if that reaches
+ * 2^31.  Returns -1 when S leaves [1, 62]. */
+int oracle_q8_requant_params(float s_x, const float *s_w, float s_y, float s_r, const float *bias, int M,
+                             int32_t *bias_q, int32_t *m1, int32_t *m2, int32_t *shift) {
+    for (int m = 0; m < M; m++) {
+        const double r1 = ((double)s_x * (double)s_w[m]) / (double)s_y;
+        const double r2 = s_r > 0.0f ? (double)s_r / (double)s_y : 0.0;
+        const double rmax = r1 > r2 ? r1 : r2;
+        int e = 0;
+        (void)frexp(rmax, &e);
+        int sh = 31 - e;
+        double a = floor(ldexp(r1, sh) + 0.5), b = floor(ldexp(r2, sh) + 0.5);
+        if (a >= 2147483648.0 || b >= 2147483648.0) {
+            sh -= 1;
+            a = floor(ldexp(r1, sh) + 0.5);
+            b = floor(ldexp(r2, sh) + 0.5);
+        }
+        if (sh < 1 || sh > 62) return -1;
+        m1[m] = (int32_t)a;
+        m2[m] = (int32_t)b;
+        shift[m] = sh;
+        double bq = bias ? rha_double((double)bias[m] / ((double)s_x * (double)s_w[m])) : 0.0;
+        if (bq > 1073741824.0) bq = 1073741824.0;
+        if (bq < -1073741824.0) bq = -1073741824.0;
+        bias_q[m] = (int32_t)bq;
+    }
+    return 0;
+}
+
+/* fp32 -> int8 with (s, z): sat8(roundf(x * (1/s)) + z), NaN -> z */
+void oracle_q8_quantize(const float *x, int8_t *q, size_t count, float scale, int zp) {
+    const float inv = 1.0f / scale;
+    for (size_t i = 0; i < count; i++) {
+        const float t = x[i] * inv;
+        int v = zp;
+        if (t == t) {
+            float r = roundf(t);
+            if (r < -512.0f) r = -512.0f;
+            if (r > 512.0f) r = 512.0f;
+            v = (int)r + zp;
+        }
+        q[i] = (int8_t)(v < -128 ? -128 : v > 127 ? 127 : v);
+    }
+}
+
+/* one requantized output: q = rha((acc + bq) m1 + (r - z_r) m2, S) + z_y,
+ * Relu as max(q, z_y), saturated */
+int oracle_q8_requant_one(int32_t acc, int32_t bq, int32_t m1, int32_t m2, int32_t sh, int r, int zy, int relu) {
+    const int64_t t = ((int64_t)acc + bq) * (int64_t)m1 + (int64_t)r * (int64_t)m2;
+    int64_t q = oracle_q8_round_shift(t, sh) + zy;
+    if (relu && q < zy) q = zy;
+    return (int)(q < -128 ? -128 : q > 127 ? 127 : q);
+}
+
+/* Conv over NCHW int8 x with zero point zx: acc = sum over in-bounds taps of
+ * w (x - zx) (out-of-bounds taps are real zeros), then requantized into y
+ * (NCHW int8, zero point zy) with the residual res (NCHW int8, zero point
+ * zr) when given.  acc_out (optional) receives the int32 accumulators. */
+void oracle_q8_conv(const int8_t *x, int zx, const int8_t *wq, const int32_t *bias_q, const int32_t *m1,
+                    const int32_t *m2, const int32_t *shift, const int8_t *res, int zr, int zy, int relu, int8_t *y,
+                    int32_t *acc_out, int N, int C, int H, int W, int M, int KH, int KW, int OH, int OW, int sh,
+                    int sw, int ph, int pw, int dh, int dw) {
+#pragma omp parallel for collapse(2) schedule(static)
+    for (int n = 0; n < N; n++) {
+        for (int m = 0; m < M; m++) {
+            for (int oh = 0; oh < OH; oh++) {
+                for (int ow = 0; ow < OW; ow++) {
+                    int64_t s = 0;
+                    for (int c = 0; c < C; c++)
+                        for (int kh = 0; kh < KH; kh++) {
+                            const int ih = oh * sh - ph + kh * dh;
+                            if (ih < 0 || ih >= H) continue;
+                            for (int kw = 0; kw < KW; kw++) {
+                                const int iw = ow * sw - pw + kw * dw;
+                                if (iw < 0 || iw >= W) continue;
+                                s += (int64_t)wq[(((size_t)m * C + c) * KH + kh) * KW + kw] *
+                                     ((int64_t)x[(((size_t)n * C + c) * H + ih) * W + iw] - zx);
+                            }
+                        }
+                    const size_t yi = (((size_t)n * M + m) * OH + oh) * OW + ow;
+                    if (acc_out) acc_out[yi] = (int32_t)s;
+                    const int r = res ? (int)res[yi] - zr : 0;
+                    y[yi] = (int8_t)oracle_q8_requant_one((int32_t)s, bias_q[m], m1[m], m2[m], shift[m], r, zy, relu);
+                }
+            }
+        }
+    }
+}
+
+/* MaxPool over NCHW int8 (one (s, z) for input and output): the maximum of
+ * the in-bounds taps */
+void oracle_q8_maxpool(const int8_t *x, int8_t *y, int N, int C, int H, int W, int OH, int OW, int kh, int kw, int sh,
+                       int sw, int ph, int pw) {
+    for (size_t plane = 0; plane < (size_t)N * C; plane++)
+        for (int oh = 0; oh < OH; oh++)
+            for (int ow = 0; ow < OW; ow++) {
+                int best = -129;
+                for (int i = 0; i < kh; i++) {
+                    const int ih = oh * sh - ph + i;
+                    if (ih < 0 || ih >= H) continue;
+                    for (int j = 0; j < kw; j++) {
+                        const int iw = ow * sw - pw + j;
+                        if (iw < 0 || iw >= W) continue;
+                        const int v = x[(plane * H + ih) * W + iw];
+                        if (v > best) best = v;
+                    }
+                }
+                y[(plane * OH + oh) * OW + ow] = (int8_t)(best < -128 ? -128 : best);
+            }
+}
+
+/* mean over each of `planes` planes of `hw` int8 values with (s, z), to
+ * fp32: (float)(((double)sum(q - z) * s) / hw) */
+void oracle_q8_plane_mean(const int8_t *x, float *y, size_t planes, int hw, float scale, int zp) {
+    for (size_t p = 0; p < planes; p++) {
+        int64_t sum = 0;
+        for (int i = 0; i < hw; i++) sum += (int64_t)x[p * hw + i] - zp;
+        y[p] = (float)(((double)sum * (double)scale) / (double)hw);
+    }
+}
+
 /* ------------------------------------------------------------------ TopK */
 
 typedef struct {

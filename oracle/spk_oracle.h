@@ -90,6 +90,22 @@ int oracle_conv2d_int8(const float *x, const int8_t *wq, const float *w_scales, 
                        const float *res, float *y, int32_t *acc_out, int N, int C, int H, int W, int M, int KH,
                        int KW, int OH, int OW, int sh, int sw, int ph, int pw, int dh, int dw, int act);
 
+/* INT8 with int8 tensors between nodes (the benchmark's INT8 configuration;
+ * no reference counterpart): asymmetric per-tensor activations, fixed-point
+ * requantization with round-half-away (spk_oracle.c) */
+int64_t oracle_q8_round_shift(int64_t t, int s);
+int oracle_q8_requant_params(float s_x, const float *s_w, float s_y, float s_r, const float *bias, int M,
+                             int32_t *bias_q, int32_t *m1, int32_t *m2, int32_t *shift);
+void oracle_q8_quantize(const float *x, int8_t *q, size_t count, float scale, int zp);
+int oracle_q8_requant_one(int32_t acc, int32_t bq, int32_t m1, int32_t m2, int32_t sh, int r, int zy, int relu);
+void oracle_q8_conv(const int8_t *x, int zx, const int8_t *wq, const int32_t *bias_q, const int32_t *m1,
+                    const int32_t *m2, const int32_t *shift, const int8_t *res, int zr, int zy, int relu, int8_t *y,
+                    int32_t *acc_out, int N, int C, int H, int W, int M, int KH, int KW, int OH, int OW, int sh,
+                    int sw, int ph, int pw, int dh, int dw);
+void oracle_q8_maxpool(const int8_t *x, int8_t *y, int N, int C, int H, int W, int OH, int OW, int kh, int kw, int sh,
+                       int sw, int ph, int pw);
+void oracle_q8_plane_mean(const int8_t *x, float *y, size_t planes, int hw, float scale, int zp);
+
 #ifdef __cplusplus
 }
 #endif

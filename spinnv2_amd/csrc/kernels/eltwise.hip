@@ -89,6 +89,18 @@ __global__ void __launch_bounds__(256) binary_img4(const float4 *__restrict__ a,
         }
 }
 
+// The same over scalar elements, for views whose bases or image strides are
+// not whole float4s (e.g. a channel offset times an odd plane size).
+template <int OP>
+__global__ void __launch_bounds__(256) binary_img1(const float *__restrict__ a, const float *__restrict__ b,
+                                                   float *__restrict__ y, unsigned images, size_t per, size_t as,
+                                                   size_t bs, size_t ys, int act) {
+    for (unsigned img = blockIdx.y; img < images; img += gridDim.y)
+        for (size_t j = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; j < per;
+             j += static_cast<size_t>(gridDim.x) * 256)
+            y[img * ys + j] = apply_act(bin<OP>(a[img * as + j], b[img * bs + j]), act);
+}
+
 template <int OP>
 __global__ void __launch_bounds__(256) binary_bcast(const float *__restrict__ a, const float *__restrict__ b,
                                                     float *__restrict__ y, size_t n, BcastDesc d, int act) {
@@ -761,8 +773,9 @@ int binary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const Spkv2TensorView *av = live_view(ctx, node->inputs[0]), *bv = live_view(ctx, node->inputs[1]),
                           *yv = live_view(ctx, node->outputs[0]);
     if (av || bv || yv) {
-        // an Add over channel slices of Concat buffers (same-shape NCHW,
-        // images a multiple of 4 elements, as set up at prepare)
+        // an Add over channel slices of Concat buffers (same-shape NCHW, as
+        // set up at prepare): float4s when every base and image stride
+        // allows, scalar elements otherwise
         if (node->op_type != SPKV2_OP_ADD || yr->rank != 4) return SPKV2_E_UNSUPPORTED;
         const unsigned images = yr->shape[0];
         const size_t per = elem_count(yr) / std::max(images, 1u);
@@ -771,8 +784,13 @@ int binary_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         if (bv) b = reinterpret_cast<const float *>(bv->base);
         if (yv) y = reinterpret_cast<float *>(yv->base);
         if (((per | as | bs | ys) & 3) != 0 ||
-            ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y)) & 15))
-            return SPKV2_E_UNSUPPORTED;
+            ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(y)) & 15)) {
+            set_kernel_name(ctx, node, "binary_img1");
+            if (per == 0 || images == 0) return 0;
+            const dim3 grid(static_cast<unsigned>(std::min<size_t>((per + 255) / 256, 1024)), std::min(images, 65535u));
+            hipLaunchKernelGGL((binary_img1<BIN_ADD>), grid, dim3(256), 0, s, a, b, y, images, per, as, bs, ys, act);
+            return launch_status("binary_img1");
+        }
         set_kernel_name(ctx, node, "binary_img4");
         if (per == 0 || images == 0) return 0;
         const dim3 grid(static_cast<unsigned>(std::min<size_t>((per / 4 + 255) / 256, 1024)), std::min(images, 65535u));

@@ -75,14 +75,15 @@ const ConvPlan *f32_conv(const Spkv2Context *ctx, uint32_t id) {
     return p && p->path == CONV_IGEMM_F32 ? p : nullptr;
 }
 
-// An Add of two same-shape fp32 NCHW tensors whose images are whole float4s
-// (binary_run's image-strided kernel).
+// An Add of two same-shape fp32 NCHW tensors (binary_run's image-strided
+// kernels: float4s when every view base and image stride is 16-byte
+// aligned, scalar elements otherwise).
 bool same_shape_add(const Spkv2Context *ctx, uint32_t id) {
     const Spkv2NodeRecord *n = &ctx->node_records[id];
     if (n->op_type != SPKV2_OP_ADD || !builtin_runs(ctx, id) || n->input_count != 2 || n->output_count != 1)
         return false;
     const Spkv2TensorRecord *y = rec(ctx, n->outputs[0]);
-    if (y->rank != 4 || y->dtype != SPKV2_DTYPE_FP32 || (y->shape[1] * y->shape[2] * y->shape[3]) % 4 != 0) return false;
+    if (y->rank != 4 || y->dtype != SPKV2_DTYPE_FP32) return false;
     for (int k = 0; k < 2; k++) {
         const Spkv2TensorRecord *r = rec(ctx, n->inputs[k]);
         if (r->rank != 4 || r->dtype != SPKV2_DTYPE_FP32) return false;
@@ -327,7 +328,10 @@ int setup_concat_views(Spkv2Context *ctx) {
             if (placed < k->input_count) continue;
         }
         void *z = nullptr;
-        if (int rc = hip_check(hipMalloc(&z, static_cast<size_t>(zbytes)), "hipMalloc concat buffer")) return rc;
+        if (hipMalloc(&z, static_cast<size_t>(zbytes)) != hipSuccess) {
+            (void)hipGetLastError();
+            continue;  // an optimization only: this Concat keeps its copies
+        }
         ctx->view_buffers.push_back(z);
         uint8_t *zb = static_cast<uint8_t *>(z);
         for (const auto &[t, ch] : pl.channel) {

@@ -1,13 +1,17 @@
 """Digests rocprofv3 CSV output into the short text summaries kept in profiles/.
 
     python -m spinnv2_amd.rocprof_summary stats   <kernel_stats.csv> --runs N [--match conv_igemm_i8]
+           [--group NAME --include SUBSTR [--include ...] [--exclude SUBSTR ...]]
     python -m spinnv2_amd.rocprof_summary traffic --fetch <pmc.csv> --write <pmc.csv>
            --copy-fetch <pmc.csv> --copy-write <pmc.csv> --copy-bytes B --runs N --match conv_igemm
     python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
            [--mops SQ_INSTS_VALU_MFMA_MOPS_I8 --peak 5000]
 
 `stats` divides rocprofv3 --kernel-trace --stats totals by the number of
-spkv2_run calls the profiled command made (N), giving per-run kernel time.
+spkv2_run calls the profiled command made (N), giving per-run kernel time;
+--group totals the kernels whose name contains any --include and none of
+the --exclude substrings (e.g. every launch of the conv nodes: the GEMM,
+split-K epilogue and padding kernels, without the classifier Gemm's).
 `traffic` sums FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the
 kernels whose name contains --match, per run, and scales each counter by
 bytes / counter of a plain copy kernel of known size profiled the same way;
@@ -36,7 +40,8 @@ def short_name(name: str) -> str:
     return re.sub(r"\(.*\)$", "", name)
 
 
-def stats(path: str, runs: int, match: str | None = None) -> str:
+def stats(path: str, runs: int, match: str | None = None, group: str | None = None,
+          include: list[str] | None = None, exclude: list[str] | None = None) -> str:
     rows = list(csv.DictReader(open(path)))
     total = sum(float(r["TotalDurationNs"]) for r in rows)
     out = [f"{'kernel':48s} {'calls/run':>9s} {'avg us':>9s} {'ms/run':>9s} {'share':>7s}"]
@@ -52,6 +57,16 @@ def stats(path: str, runs: int, match: str | None = None) -> str:
         out.append("")
         out.append(f"result {match}_ms_per_run = {ms:.6f}")
         out.append(f"result {match}_calls_per_run = {calls:.1f}")
+    if group:
+        inc, exc = include or [], exclude or []
+        sel = [r for r in rows if any(s in short_name(r["Name"]) for s in inc)
+               and not any(s in short_name(r["Name"]) for s in exc)]
+        ms = sum(float(r["TotalDurationNs"]) for r in sel) / runs / 1e6
+        calls = sum(int(r["Calls"]) for r in sel) / runs
+        out.append("")
+        out.append(f"group {group}: names containing any of {inc}" + (f", none of {exc}" if exc else ""))
+        out.append(f"result {group}_ms_per_run = {ms:.6f}")
+        out.append(f"result {group}_calls_per_run = {calls:.1f}")
     return "\n".join(out)
 
 
@@ -158,6 +173,9 @@ def main() -> None:
     s.add_argument("csv")
     s.add_argument("--runs", type=int, required=True)
     s.add_argument("--match", default=None, help="also total the kernels whose name contains this")
+    s.add_argument("--group", default=None, help="name of a kernel group totalled from --include / --exclude")
+    s.add_argument("--include", action="append", default=[], help="group member: name contains this")
+    s.add_argument("--exclude", action="append", default=[], help="not a group member: name contains this")
     t = sub.add_parser("traffic")
     for k in ("fetch", "write", "copy_fetch", "copy_write"):
         t.add_argument("--" + k.replace("_", "-"), dest=k, required=True)
@@ -173,7 +191,7 @@ def main() -> None:
     m.add_argument("--peak", type=float, default=157.3, help="T ops/s of the counted MFMA type (fp32: 157.3)")
     m.add_argument("--mops", default="SQ_INSTS_VALU_MFMA_MOPS_F32", help="MFMA work counter (units of 512 ops)")
     a = ap.parse_args()
-    print({"stats": lambda: stats(a.csv, a.runs, a.match), "traffic": lambda: traffic(a),
+    print({"stats": lambda: stats(a.csv, a.runs, a.match, a.group, a.include, a.exclude), "traffic": lambda: traffic(a),
            "mfma": lambda: mfma(a)}[a.cmd]())
 
 

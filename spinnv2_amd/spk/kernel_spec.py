@@ -54,17 +54,19 @@ PROFILES = {
                            "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
     "cpu_ref": {"name": "cpu_ref", "backends": ["ref"], "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
     # the reference's ARM profile (compiler/target/profiles/cpu_arm_neon.json):
-    # Conv tokens int8, pointwise, depthwise, Winograd F(4,3), im2col
+    # Conv tokens int8, pointwise, depthwise, Winograd F(4,3), im2col; its
+    # 32 MiB scratch limit (the 64 MiB activation limit is not checked by
+    # this writer's planner, for any profile)
     "cpu_arm_neon": {"name": "cpu_arm_neon", "backends": ["ref", "cpu", "simd"], "bnns": False,
                      "conv_kinds": ["pointwise_1x1", "depthwise_direct", "winograd_f43"],
-                     "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
+                     "scratch_arena_max": 33554432, "activation_arena_max": 0},
     # the two conv kinds the reference runtime keeps (spkv2_format.h:130-131,
     # kernels.c:75-77) but no reference profile selects: Winograd F(2,3) for
     # 3x3/s1/p1 and the 3x3/s2/p1 direct conv; packages carrying them must
     # still run unchanged
     "cpu_arm_neon_exp": {"name": "cpu_arm_neon_exp", "backends": ["ref", "cpu", "simd"], "bnns": False,
                          "conv_kinds": ["pointwise_1x1", "depthwise_direct", "winograd_3x3s1", "conv3x3s2_direct"],
-                         "scratch_arena_max": 1 << 30, "activation_arena_max": 0},
+                         "scratch_arena_max": 33554432, "activation_arena_max": 0},
 }
 
 

@@ -228,3 +228,36 @@ def test_split_pad_handoff_bit_identical(gpu, monkeypatch):
                 assert not any(names[i].endswith("+handoff") for i in readers)
     for k, v in outs.items():
         np.testing.assert_array_equal(v.view(np.uint32), outs["0", "0"].view(np.uint32), err_msg=str(k))
+
+
+@pytest.mark.parametrize("batch", [1, 2])
+def test_unaligned_add_view_scalar_path(gpu, monkeypatch, batch):
+    """An Add placed in a Concat buffer at a channel offset whose byte
+    offset is not a multiple of 16 (2 channels of 5x5 planes before it) and
+    with odd image strides: binary_run takes its scalar image-strided kernel
+    (binary_img1), bit-identical to the copying path."""
+    p = models.Params(5)
+    g = Graph("unaligned_add_view")
+    x = g.input("x", [batch, 3, 5, 5])
+    a = g.conv(x, p.he((2, 3, 1, 1)), p.normal(2, 0.01))
+    # Relu on both convs keeps the Add from fusing into either
+    b1 = g.relu(g.conv(x, p.he((4, 3, 3, 3)), p.normal(4, 0.01), pad=1))
+    b2 = g.relu(g.conv(x, p.he((4, 3, 1, 1)), p.normal(4, 0.01)))
+    s = g.add(b1, b2)
+    z = g.concat([a, s], axis=1)
+    y = g.conv(z, p.he((3, 6, 3, 3)), p.normal(3, 0.01), pad=1)
+    g.mark_output(y)
+    run_default_pipeline(g)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    print(f"[views] unaligned Add view batch {batch}", flush=True)
+    monkeypatch.setenv("SPKV2_CONCAT_VIEWS", "1")
+    on, names_on = _run(blob, xs, len(g.nodes))
+    monkeypatch.setenv("SPKV2_CONCAT_VIEWS", "0")
+    off, names_off = _run(blob, xs, len(g.nodes))
+    np.testing.assert_array_equal(on.view(np.uint32), off.view(np.uint32))
+    assert "Add" in [n.op_type for n in g.nodes]
+    assert "binary_img1" in names_on or batch == 1, names_on
+    assert "binary_img1" not in names_off
+    want = run_oracle(blob, xs)[0]
+    assert tnorm_err(on, want) <= FP32_TOL

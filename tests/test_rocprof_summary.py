@@ -91,3 +91,16 @@ def test_mfma_int8_counter(tmp_path):
     assert _result(out, "conv_igemm_i8_mfma_tflops") == pytest.approx(5.12)
     assert _result(out, "conv_igemm_i8_mfma_frac_of_peak") == pytest.approx(5.12 / 5000, abs=1e-4)
     assert _result(out, "conv_igemm_i8_mfma_busy_frac") == pytest.approx(0.25)
+
+
+def test_stats_group_include_exclude(tmp_path):
+    p = _write(tmp_path / "s.csv", ["Name", "Calls", "TotalDurationNs", "AverageNs"],
+               [["void spk::kern::conv_igemm_f32<64, 64, 16, 2, 2, 0>(spk::kern::IgemmArgs)", 20, 2_000_000, 100_000],
+                ["void spk::kern::conv_igemm_f32<64, 64, 16, 2, 2, 1>(spk::kern::IgemmArgs)", 10, 100_000, 10_000],
+                ["splitk_epilogue<4>", 10, 500_000, 50_000],
+                ["maxpool3s2_x4", 10, 300_000, 30_000]])
+    out = rs.stats(p, runs=10, group="conv_kernels", include=["conv_igemm_f32", "splitk_epilogue"],
+                   exclude=["conv_igemm_f32<64, 64, 16, 2, 2, 1>"])
+    # 2.0 ms + 0.5 ms over 10 runs; the KVEC Gemm and the pool are not members
+    assert _result(out, "conv_kernels_ms_per_run") == pytest.approx(0.25)
+    assert _result(out, "conv_kernels_calls_per_run") == pytest.approx(3.0)
