@@ -46,6 +46,10 @@ void *spkv2_ctx_stream(const Spkv2Context *ctx);
 /* quantization record of a tensor and its host-resident scale array (NULL if none) */
 const Spkv2QuantParamRecord *spkv2_ctx_find_quant_param(const Spkv2Context *ctx, uint32_t tensor_id);
 const float *spkv2_ctx_quant_scales(const Spkv2Context *ctx, const Spkv2QuantParamRecord *qp);
+/* the record's int32 zero points, which follow its scales in the
+ * quantization section (reference compiler/packager/spk_writer.py writes
+ * them there; its runtime reads only the scales), NULL if out of range */
+const int32_t *spkv2_ctx_quant_zero_points(const Spkv2Context *ctx, const Spkv2QuantParamRecord *qp);
 /* per-node cache slot (device allocations made at prepare time) and its destructor */
 int spkv2_ctx_node_cache(Spkv2Context *ctx, uint32_t node_id, void ***slot, void (***dtor)(void *));
 
@@ -109,6 +113,13 @@ int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable);
  * SPKV2_E_UNSUPPORTED (spkv2_mi355x_last_error says why).  Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU race. */
 int spkv2_mi355x_conv_int8_accumulators_noalloc(Spkv2Context *ctx, uint32_t node_id, int32_t *out, size_t size);
+/* No counterpart in the reference (its INT8 mode keeps fp32 tensors between
+ * nodes).  In the INT8 configuration with int8 tensors between nodes, copy
+ * one int8 activation tensor (package dtype int8, role activation), laid out
+ * NCHW, to host memory `out` (the runtime keeps it as zero-point-padded NHWC
+ * on the device).  Call after spkv2_run.  size must be N*C*H*W; -1 for a
+ * tensor that is not such a tensor. */
+int spkv2_mi355x_read_int8_tensor(Spkv2Context *ctx, uint32_t tensor_id, int8_t *out, size_t size);
 
 #ifdef __cplusplus
 }

@@ -25,7 +25,16 @@ struct ConvGeom {
 
 int read_conv_geom(const Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvGeom *g);
 
-enum ConvPath { CONV_IGEMM_F32 = 0, CONV_DIRECT_F32 = 1, CONV_IGEMM_I8 = 2, CONV_DW_F32 = 3, CONV_SMALLK_F32 = 4 };
+// CONV_Q8: the int8 implicit GEMM of CONV_IGEMM_I8 in the INT8 configuration
+// with int8 tensors between nodes (fixed-point requantizing epilogue)
+enum ConvPath {
+    CONV_IGEMM_F32 = 0,
+    CONV_DIRECT_F32 = 1,
+    CONV_IGEMM_I8 = 2,
+    CONV_DW_F32 = 3,
+    CONV_SMALLK_F32 = 4,
+    CONV_Q8 = 5
+};
 
 // How an fp32 implicit-GEMM B source is laid out beyond its k-offset table.
 // Per tap, for the skinny kernel: k = c * taps + tap sits at c * cstride +
@@ -59,6 +68,11 @@ struct ConvPlan {
     bool padded;         // fp32 path: the input is copied into a padded workspace buffer first
     size_t pad_bytes;    // fp32 path: workspace bytes of that padded copy
     float *scales;       // device, int8 path: w_scale[m] * x_scale
+    // device, CONV_Q8: per output channel, five int32 rows of M:
+    // -z_x * sum(w[m]), that plus bias_q[m], the multipliers m1[m], m2[m]
+    // and the shift (requantization constants computed at prepare)
+    int *qrow;
+    int x_zp;            // CONV_Q8: the input's zero point
     float x_scale;       // int8 path: activation scale
     int quant_split;     // int8 path: first element index of the per-image tail (round half away)
     size_t workspace;    // bytes of device workspace needed per run

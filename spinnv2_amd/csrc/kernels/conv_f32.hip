@@ -91,6 +91,7 @@ void conv_plan_free(void *p) {
     if (plan->wpack) (void)hipFree(plan->wpack);
     if (plan->ktab) (void)hipFree(plan->ktab);
     if (plan->scales) (void)hipFree(plan->scales);
+    if (plan->qrow) (void)hipFree(plan->qrow);
     if (plan->q_in) (void)hipFree(plan->q_in);
     if (plan->pad_in && !plan->pad_in_shared) (void)hipFree(plan->pad_in);
     if (plan->gather.ktap) (void)hipFree(const_cast<int *>(plan->gather.ktap));
@@ -2384,7 +2385,8 @@ int conv_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratch) {
     case CONV_IGEMM_F32: return run_igemm_node(ctx, plan, node);
     case CONV_DIRECT_F32: return run_direct(ctx, node, plan->g);
     case CONV_DW_F32: return run_dw(ctx, node, plan->g);
-    case CONV_IGEMM_I8: return conv_i8_run(ctx, node, plan, nullptr);
+    case CONV_IGEMM_I8:
+    case CONV_Q8: return conv_i8_run(ctx, node, plan, nullptr);
     case CONV_SMALLK_F32: return run_smallk(ctx, node, plan);
     }
     return SPKV2_E_UNSUPPORTED;
@@ -2402,7 +2404,7 @@ int conv_direct_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *scratc
 int conv_int8_accumulators(Spkv2Context *ctx, const Spkv2NodeRecord *node, int32_t *dev_out) {
     if (ctx->plan_dtors[node->id] != conv_plan_free) return SPKV2_E_UNSUPPORTED;
     ConvPlan *plan = static_cast<ConvPlan *>(ctx->plans[node->id]);
-    if (!plan || plan->path != CONV_IGEMM_I8) return SPKV2_E_UNSUPPORTED;
+    if (!plan || (plan->path != CONV_IGEMM_I8 && plan->path != CONV_Q8)) return SPKV2_E_UNSUPPORTED;
     return conv_i8_run(ctx, node, plan, dev_out);
 }
 

@@ -53,9 +53,18 @@ constexpr int kOob = 0x7fff0000;
 // c < C, 0 elsewhere.  A block covers 64 padded pixels x 64 channels,
 // transposed through LDS so reads (along w) and writes (along c) are both
 // contiguous.
+// In the INT8 configuration with int8 tensors between nodes (q8) every
+// value is sat8(roundf(v) + zp) and the halo and padded channels hold zp.
+__device__ __forceinline__ int quantize_q8(float v, float inv_scale, int zp) {
+    const float t = v * inv_scale;
+    if (t != t) return zp;
+    const float r = fminf(fmaxf(roundf(t), -512.0f), 512.0f);
+    return min(max(static_cast<int>(r) + zp, -128), 127);
+}
+
 __global__ void __launch_bounds__(256) quantize_pad_nhwc(const float *__restrict__ x, int8_t *__restrict__ xq, int C,
                                                          int H, int W, int Hp, int Wp, int Cp, int pt, int pl,
-                                                         float inv_scale, int split) {
+                                                         float inv_scale, int split, int zp, int q8) {
     __shared__ int8_t tile[64][64 + 4];
     const int img = blockIdx.z;
     const int p0 = blockIdx.x * 64;
@@ -71,15 +80,19 @@ __global__ void __launch_bounds__(256) quantize_pad_nhwc(const float *__restrict
                         static_cast<unsigned>(w) < static_cast<unsigned>(W);
     for (int cc = threadIdx.x >> 6; cc < 64; cc += 4) {
         const int c = c0 + cc;
-        int8_t q = 0;
+        int8_t q = static_cast<int8_t>(zp);
         if (inside && c < C) {
             const int idx = c * HW + h * W + w;  // NCHW index inside the image
-            const float v = xi[idx] * inv_scale;
-            float r;
-            if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
-            else r = idx < split ? rintf(v) : roundf(v);
-            r = fminf(fmaxf(r, -128.0f), 127.0f);
-            q = static_cast<int8_t>(static_cast<int>(r));
+            if (q8) {
+                q = static_cast<int8_t>(quantize_q8(xi[idx], inv_scale, zp));
+            } else {
+                const float v = xi[idx] * inv_scale;
+                float r;
+                if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
+                else r = idx < split ? rintf(v) : roundf(v);
+                r = fminf(fmaxf(r, -128.0f), 127.0f);
+                q = static_cast<int8_t>(static_cast<int>(r));
+            }
         }
         tile[cc][tp] = q;
     }
@@ -104,7 +117,8 @@ __global__ void __launch_bounds__(256) quantize_pad_nhwc(const float *__restrict
 // bytes as dwords, instead of 64-channel tiles that would sit mostly idle.
 __global__ void __launch_bounds__(256) quantize_pad_nhwc_narrow(const float *__restrict__ x, int8_t *__restrict__ xq,
                                                                 int C, int H, int W, int Hp, int Wp, int Cp, int pt,
-                                                                int pl, float inv_scale, int split, int images) {
+                                                                int pl, float inv_scale, int split, int images, int zp,
+                                                                int q8) {
     const int HW = H * W;
     const int HWp = Hp * Wp;
     const size_t total = static_cast<size_t>(images) * HWp;
@@ -123,15 +137,19 @@ __global__ void __launch_bounds__(256) quantize_pad_nhwc_narrow(const float *__r
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const int c = c0 + b;
-                int8_t q = 0;
+                int8_t q = static_cast<int8_t>(zp);
                 if (inside && c < C) {
                     const int idx = c * HW + h * W + w;  // NCHW index inside the image
-                    const float v = xi[idx] * inv_scale;
-                    float r;
-                    if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
-                    else r = idx < split ? rintf(v) : roundf(v);
-                    r = fminf(fmaxf(r, -128.0f), 127.0f);
-                    q = static_cast<int8_t>(static_cast<int>(r));
+                    if (q8) {
+                        q = static_cast<int8_t>(quantize_q8(xi[idx], inv_scale, zp));
+                    } else {
+                        const float v = xi[idx] * inv_scale;
+                        float r;
+                        if (v != v) r = 0.0f;  // NaN quantizes to 0 (the ARM conversions)
+                        else r = idx < split ? rintf(v) : roundf(v);
+                        r = fminf(fmaxf(r, -128.0f), 127.0f);
+                        q = static_cast<int8_t>(static_cast<int>(r));
+                    }
                 }
                 word |= static_cast<uint32_t>(static_cast<uint8_t>(q)) << (8 * b);
             }
@@ -161,7 +179,30 @@ struct I8Args {
     int8_t *__restrict__ q_out;
     int q_bytes, q_Hp, q_Wp, q_Cp, q_pt, q_pl, q_split;
     float q_inv;
+    // INT8 configuration with int8 tensors between nodes (q8 = 1): mode 0
+    // requantizes in fixed point into q_out (an int8 tensor's padded NHWC
+    // buffer, zero point y_zp) instead of dequantizing; qrow holds five rows
+    // of M int32 (-z_x * sum(w), that plus bias_q, m1, m2, shift); the
+    // residual is the int8 tensor r8 (zero point r_zp); mode 2 adds the
+    // first row, giving sum(w (x - z_x)).
+    int q8;
+    const int *__restrict__ qrow;
+    const int8_t *__restrict__ r8;
+    int r_bytes, r_Hp, r_Wp, r_Cp, r_pt, r_pl, r_zp;
+    int y_zp;
 };
+
+// Fixed-point requantization of one output (the INT8 configuration):
+// t = (acc + c) m1 + rd m2 in int64, rounded to nearest with ties away from
+// zero by the shift, plus the output zero point, Relu as a clamp at it,
+// saturated.  (t + half - [t < 0]) >> sh equals sign(t) ((|t| + half) >> sh).
+__device__ __forceinline__ int q8_requant(int acc, int c, int m1, int m2, int sh, int rd, int zy, bool relu) {
+    const int64_t t = (static_cast<int64_t>(acc) + c) * m1 + static_cast<int64_t>(rd) * m2;
+    const int64_t half = int64_t(1) << (sh - 1);
+    int v = static_cast<int>((t + half - (t < 0 ? 1 : 0)) >> sh) + zy;
+    if (relu) v = max(v, zy);
+    return min(max(v, -128), 127);
+}
 
 // The reference's activation quantization of one value (conv_int8.c:26-55):
 // round half to even below `split` (the 16-wide vector body), half away
@@ -177,10 +218,10 @@ __device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even)
 
 constexpr int i8_stage_bytes(int BM, int BN);
 template <int BM>
-__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_sc, float *s_bi);
+__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par);
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
-                                            int lane, const float *s_sc, const float *s_bi, int8_t *s_q);
+                                            int lane, const float *s_par, int8_t *s_q);
 
 template <int BM, int BN, int BK, int BMAP>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
@@ -194,7 +235,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int OPS = 2 * (BM + BN) * LDK;
     constexpr int SMEM = OPS > i8_stage_bytes(BM, BN) ? OPS : i8_stage_bytes(BM, BN);
     __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
-    __shared__ float s_par[2 * BM];
+    __shared__ float s_par[4 * BM];  // per-row epilogue constants
     int8_t(*As)[BM * LDK] = reinterpret_cast<int8_t(*)[BM * LDK]>(smem);
     int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem + 2 * BM * LDK);
 
@@ -314,7 +355,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     if (kt0 >= kt1) return;  // empty split-K slice
-    i8_load_row_params<BM>(a, mt * BM, s_par, s_par + BM);  // read after the loop's barriers
+    i8_load_row_params<BM>(a, mt * BM, s_par);  // read after the loop's barriers
     I8_LOAD_TILE(kt0, ar0, br0);
     I8_LOAD_TILE(kt0 + 1, ar1, br1);
     I8_STORE_TILE(0, ar0, br0);
@@ -332,7 +373,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #undef I8_COMPUTE
 #undef I8_LOAD_TILE
 #undef I8_STORE_TILE
-    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, s_par + BM, smem);
+    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
 }
 
 // Workgroup-shared memory of the int8 GEMM kernels' epilogue: the tile's
@@ -341,12 +382,23 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 // that aliases the k-loop's operand buffers (free once the loop is done).
 constexpr int i8_stage_bytes(int BM, int BN) { return BN * (BM + 16); }
 
+// s_par: [BM] combined scales and [BM] biases, or with q8 four [BM] int32
+// rows (c, m1, m2, shift), each a row of the plan's qrow table.
 template <int BM>
-__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_sc, float *s_bi) {
+__device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par) {
+    if (a.q8) {
+        int *s_i = reinterpret_cast<int *>(s_par);
+        for (int i = threadIdx.x; i < BM; i += 256) {
+            const int m = mt0 + i;
+#pragma unroll
+            for (int r = 0; r < 4; r++) s_i[r * BM + i] = m < a.M ? a.qrow[(r + 1) * a.M + m] : 1;
+        }
+        return;
+    }
     for (int i = threadIdx.x; i < BM; i += 256) {
         const int m = mt0 + i;
-        s_sc[i] = m < a.M ? a.scales[m] : 0.0f;
-        s_bi[i] = a.bias && m < a.M ? a.bias[m] : 0.0f;
+        s_par[i] = m < a.M ? a.scales[m] : 0.0f;
+        s_par[BM + i] = a.bias && m < a.M ? a.bias[m] : 0.0f;
     }
 }
 
@@ -355,12 +407,13 @@ __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, flo
 // tile at (mt0, nt0) (blockIdx.y is the split-K slice).  mode 1 stores int32
 // partials, mode 2 the raw accumulators as NCHW, mode 0 dequantizes (+ bias,
 // residual, activation) into y and/or requantizes into the consumer's padded
-// NHWC int8 buffer: through the LDS staging area when its channel pitch is a
+// NHWC int8 buffer -- or with q8 requantizes in fixed point into the output
+// int8 tensor -- through the LDS staging area when its channel pitch is a
 // multiple of 16, so each pixel's channels of the tile leave as contiguous
 // 16-byte pieces (the other waves' channels of the same pixel beside them).
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
-                                            int lane, const float *s_sc, const float *s_bi, int8_t *s_q) {
+                                            int lane, const float *s_par, int8_t *s_q) {
     const int m0 = mt0 + wmo, n0 = nt0 + wno;
     const int row = lane & 31;
     // 32x32 accumulator layout: lane holds column (lane & 31) and rows
@@ -411,19 +464,27 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                    __builtin_amdgcn_raw_buffer_store_b32(acc[i][j][r], wrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
+                    // q8: the halo holds z_x, so sum(w x) - z_x sum(w) = sum(w (x - z_x))
+                    const int v = acc[i][j][r] + (a.q8 && m < M ? a.qrow[m] : 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(v, wrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
                 }
         return;
     }
-    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(a.y ? a.y : const_cast<float *>(a.scales), static_cast<short>(0),
-                                                                         a.y ? a.y_bytes : 0, kBufWord3);
+    const int8_t *dummy = reinterpret_cast<const int8_t *>(a.wp);  // base of the unused resources (0 records)
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
+        a.y ? static_cast<void *>(a.y) : const_cast<int8_t *>(dummy), static_cast<short>(0), a.y ? a.y_bytes : 0,
+        kBufWord3);
     const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(a.res ? a.res : a.scales), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
+        a.res ? const_cast<float *>(a.res) : const_cast<float *>(reinterpret_cast<const float *>(dummy)),
+        static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
     const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
         a.q_out ? a.q_out : const_cast<int8_t *>(a.xq), static_cast<short>(0), a.q_out ? a.q_bytes : 0, kBufWord3);
-    // handoff: byte offset of this lane's pixel in the consumer's padded NHWC
-    // buffer, and its spatial index (for the NCHW rounding split)
-    unsigned qbase[TN];
+    const __amdgpu_buffer_rsrc_t r8s = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(a.r8 ? a.r8 : dummy), static_cast<short>(0), a.r8 ? a.r_bytes : 0, kBufWord3);
+    // handoff / q8 output: byte offset of this lane's pixel in the padded
+    // NHWC int8 buffer, and its spatial index (for the NCHW rounding split);
+    // q8 residual: the pixel's offset in the residual's padded NHWC buffer
+    unsigned qbase[TN], rbase[TN];
     int qsp[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -435,61 +496,98 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
         qsp[j] = sp;
         qbase[j] = n < a.Ntot ? static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp)
                               : static_cast<unsigned>(kOob);
+        rbase[j] = n < a.Ntot && a.r8
+                       ? static_cast<unsigned>(((img * a.r_Hp + oh + a.r_pt) * a.r_Wp + ow + a.r_pl) * a.r_Cp)
+                       : static_cast<unsigned>(kOob);
     }
-    // staged handoff (workgroup-uniform): the staging area aliases the
+    // staged int8 stores (workgroup-uniform): the staging area aliases the
     // k-loop's LDS operands, so every wave must be past its last read
     const bool stage = a.q_out && a.q_Cp % 16 == 0;
     constexpr int SQ = BM + 16;  // staging row pitch: an odd multiple of 16 bytes
     if (stage) __syncthreads();
+    const float *s_sc = s_par, *s_bi = s_par + BM;
+    const int *s_i = reinterpret_cast<const int *>(s_par);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         // per-row constants of this block (LDS), for all TN blocks
         floatx16 sc, bi;
+        intx16 qc, qm1, qm2, qsh;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * (r >> 2) + (r & 3);
-            sc[r] = s_sc[ml];
-            bi[r] = s_bi[ml];
+            if (a.q8) {
+                qc[r] = s_i[ml];
+                qm1[r] = s_i[BM + ml];
+                qm2[r] = s_i[2 * BM + ml];
+                qsh[r] = s_i[3 * BM + ml];
+            } else {
+                sc[r] = s_sc[ml];
+                bi[r] = s_bi[ml];
+            }
         }
 #pragma unroll
         for (int j = 0; j < TN; j++) {
+            unsigned words[4] = {0u, 0u, 0u, 0u};
             floatx16 v;
-#pragma unroll
-            for (int r = 0; r < 16; r++) v[r] = fmaf(static_cast<float>(acc[i][j][r]), sc[r], bi[r]);
-            if (a.res) {
-                floatx16 rv;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                    rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                          rrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0));
-                }
-                v += rv;
-            }
-            if (a.act == 1) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
-            } else if (a.act == 2) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
-            }
-            if (a.q_out) {
-                // four consecutive channels of the lane -> one dword; channels
-                // past M are written 0 (the padded channels stay zero)
-                unsigned words[4];
+            if (a.q8) {
+                // four consecutive channels per dword: the residual's bytes
+                // of this lane's pixel, then the requantized outputs
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
-                    const unsigned m0 = mrow[i] + 8 * q4;
+                    const unsigned mq = mrow[i] + 8 * q4;
+                    const unsigned rw = a.r8 ? __builtin_amdgcn_raw_buffer_load_b32(r8s, mq < M ? rbase[j] + mq : kOob, 0, 0)
+                                             : 0u;
                     unsigned word = 0;
 #pragma unroll
                     for (int b = 0; b < 4; b++) {
-                        const unsigned m = m0 + b;
-                        const int idx = static_cast<int>(m) * a.OHW + qsp[j];
-                        const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
+                        const int r = 4 * q4 + b;
+                        const int rd = a.r8 ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - a.r_zp : 0;
+                        const int qv = mq + b < M ? q8_requant(acc[i][j][r], qc[r], qm1[r], qm2[r], qsh[r], rd, a.y_zp,
+                                                               a.act == 1)
+                                                  : a.y_zp;
                         word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
                     }
                     words[q4] = word;
                 }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = fmaf(static_cast<float>(acc[i][j][r]), sc[r], bi[r]);
+                if (a.res) {
+                    floatx16 rv;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                        rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                              rrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0));
+                    }
+                    v += rv;
+                }
+                if (a.act == 1) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+                } else if (a.act == 2) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
+                }
+                if (a.q_out) {
+                    // four consecutive channels of the lane -> one dword;
+                    // channels past M are written 0 (the padded channels stay zero)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) {
+                        const unsigned mq = mrow[i] + 8 * q4;
+                        unsigned word = 0;
+#pragma unroll
+                        for (int b = 0; b < 4; b++) {
+                            const unsigned m = mq + b;
+                            const int idx = static_cast<int>(m) * a.OHW + qsp[j];
+                            const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
+                            word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
+                        }
+                        words[q4] = word;
+                    }
+                }
+            }
+            if (a.q_out) {
                 if (stage) {
                     // the tile's pixel row in LDS: 4 channels per dword
                     const int pl = wno + j * 32 + row;
@@ -501,12 +599,12 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
                 } else {
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
-                        const unsigned m0 = mrow[i] + 8 * q4;
-                        __builtin_amdgcn_raw_buffer_store_b32(words[q4], qrs, m0 < M ? qbase[j] + m0 : kOob, 0, 0);
+                        const unsigned mq = mrow[i] + 8 * q4;
+                        __builtin_amdgcn_raw_buffer_store_b32(words[q4], qrs, mq < M ? qbase[j] + mq : kOob, 0, 0);
                     }
                 }
             }
-            if (a.y) {
+            if (a.y && !a.q8) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
@@ -521,7 +619,7 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
     __syncthreads();
     // 16-byte pieces of the staged tile, the BM/16 pieces of one pixel on
     // consecutive threads; a piece is stored when its first channel is below
-    // M (channels from M to the padded pitch hold 0)
+    // M (channels from M to the padded pitch hold 0, or z_y with q8)
     constexpr int PPX = BM / 16;
     for (int t = threadIdx.x; t < BN * PPX; t += 256) {
         const int pl = t / PPX;
@@ -560,7 +658,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
     // the operand buffers, reused by the epilogue's staging area
     constexpr int SMEM = 2 * BN * LDK > i8_stage_bytes(BM, BN) ? 2 * BN * LDK : i8_stage_bytes(BM, BN);
     __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
-    __shared__ float s_par[2 * BM];
+    __shared__ float s_par[4 * BM];  // per-row epilogue constants
     int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem);
 
     const int tid = threadIdx.x;
@@ -662,7 +760,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     if (kt0 >= kt1) return;  // empty split-K slice
-    i8_load_row_params<BM>(a, mt * BM, s_par, s_par + BM);  // read after the loop's barriers
+    i8_load_row_params<BM>(a, mt * BM, s_par);  // read after the loop's barriers
     I8X_LOAD_B(kt0, br0);
     I8X_LOAD_B(kt0 + 1, br1);
     I8X_LOAD_A(kt0, a0);
@@ -684,7 +782,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
 #undef I8X_STORE_B
 #undef I8X_LOAD_B
 #undef I8X_LOAD_A
-    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, s_par + BM, smem);
+    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
 }
 
 // Sums the int32 split-K partials (exact in any order), then dequantizes or
@@ -714,6 +812,28 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
 #pragma unroll
             for (int t = 0; t < 16; t++)
                 if (s + t < splitk) v += p[t];
+        }
+        if (q.q8) {
+            // the INT8 configuration: raw accumulators corrected for the
+            // input zero point, or the fixed-point requantization into the
+            // output int8 tensor (one byte per output)
+#pragma unroll
+            for (int e = 0; e < VEC; e++) {
+                const int img = (n + e) / OHW;
+                const int sp = n + e - img * OHW;
+                if (raw) {
+                    raw[(static_cast<size_t>(img) * M + m) * OHW + sp] = v[e] + q.qrow[m];
+                    continue;
+                }
+                const int oh = sp / q.OW, ow = sp - (sp / q.OW) * q.OW;
+                const int rd = q.r8 ? static_cast<int>(q.r8[(static_cast<size_t>(img * q.r_Hp + oh + q.r_pt) * q.r_Wp +
+                                                             ow + q.r_pl) * q.r_Cp + m]) - q.r_zp
+                                    : 0;
+                q.q_out[(static_cast<size_t>(img * q.q_Hp + oh + q.q_pt) * q.q_Wp + ow + q.q_pl) * q.q_Cp + m] =
+                    static_cast<int8_t>(q8_requant(v[e], q.qrow[M + m], q.qrow[2 * M + m], q.qrow[3 * M + m],
+                                                   q.qrow[4 * M + m], rd, q.y_zp, act == 1));
+            }
+            continue;
         }
         const float sm = scales[m];
         const float bm = bias ? bias[m] : 0.0f;
@@ -777,7 +897,28 @@ struct I8Layout {
     int run_groups;  // groups per kernel row (runs) or per tap
     int groups;    // total 16-byte groups of K
     int Hp, Wp, pt, pl;
+    // bytes from a column's window origin to where xq's padding puts it:
+    // 0 for a buffer padded for this conv; an int8 tensor padded for a wider
+    // reader (pt > ph or pl > pw) shifts every window by the difference
+    int origin = 0;
 };
+
+// The layout of a conv reading an int8 activation tensor in place: the
+// tensor's padded NHWC buffer (its halo at least this conv's padding and
+// wide enough for its windows, as setup_q8_tensors sizes it).
+I8Layout i8_layout_q8(const ConvGeom &g, const Spkv2Q8Tensor &t) {
+    I8Layout L{};
+    L.runs = g.dw == 1;
+    L.Cp = t.Cp;
+    L.run_groups = L.runs ? static_cast<int>((static_cast<size_t>(g.KW) * L.Cp + 15) / 16) : L.Cp / 16;
+    L.groups = L.runs ? g.KH * L.run_groups : g.KH * g.KW * L.run_groups;
+    L.Hp = t.Hp;
+    L.Wp = t.Wp;
+    L.pt = t.pt;
+    L.pl = t.pl;
+    L.origin = ((t.pt - g.ph) * t.Wp + (t.pl - g.pw)) * t.Cp;
+    return L;
+}
 
 I8Layout i8_layout(const ConvGeom &g) {
     I8Layout L{};
@@ -939,7 +1080,7 @@ std::vector<int> build_i8_koff(const ConvGeom &g, const I8Layout &L, int k_tiles
     // two extra tiles of out-of-range entries: the pipeline prefetches up to
     // two tiles past the last one
     std::vector<int> koff(static_cast<size_t>((k_tiles + 2) * per_tile), kOob);
-    for (int q = 0; q < L.groups; q++) koff[q] = i8_group_offset(g, L, q);
+    for (int q = 0; q < L.groups; q++) koff[q] = L.origin + i8_group_offset(g, L, q);
     return koff;
 }
 
@@ -962,10 +1103,12 @@ struct DevBufs {
 
 // Times the candidates the model keeps on zero-filled scratch buffers of the
 // layer's shape and returns the fastest (cfg, split); cached per shape.
-bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out, int *split_out) {
+// q8: the INT8 configuration's epilogue (int8 output and residual) is timed,
+// and the choice is kept under its own key.
+bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out, int *split_out, bool q8 = false) {
     char key[256];
-    snprintf(key, sizeof(key), "i8|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d", g.N, g.C, g.H, g.W, g.M, g.KH, g.KW,
-             g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, g.has_bias ? 1 : 0, g.has_res ? 1 : 0, g.act);
+    snprintf(key, sizeof(key), "i8|%d,%d,%d,%d|%d,%d,%d,%d,%d,%d,%d,%d,%d|%d,%d,%d%s", g.N, g.C, g.H, g.W, g.M, g.KH,
+             g.KW, g.OH, g.OW, g.sh, g.sw, g.dh, g.dw, g.has_bias ? 1 : 0, g.has_res ? 1 : 0, g.act, q8 ? "|q8" : "");
     // a stored choice is taken only if this layer's K layout allows it (a
     // tune DB written by another build may name another configuration)
     if (tuned_lookup(key, cfg_out, split_out) && *cfg_out >= 0 && *cfg_out < kNumI8Cfgs && i8_cfg_fits(L, *cfg_out))
@@ -1015,6 +1158,26 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     float *res = g.has_res ? static_cast<float *>(db.get(ybytes)) : nullptr;
     int32_t *part = static_cast<int32_t *>(db.get(pbytes));
     if (!xq || !wp || !ko || !sc || !y || (g.has_res && !res) || !part) return false;
+    // q8: an int8 output (and residual) of the layer's shape, unpadded, and
+    // constant rows whose values do not matter for the timing
+    const int q_Cp = static_cast<int>(align_up(static_cast<size_t>(g.M), 16));
+    const size_t q_bytes = static_cast<size_t>(g.N) * g.OH * g.OW * q_Cp;
+    int8_t *q_out = q8 ? static_cast<int8_t *>(db.get(q_bytes)) : nullptr;
+    int8_t *q_res = q8 && g.has_res ? static_cast<int8_t *>(db.get(q_bytes)) : nullptr;
+    int *qrow = q8 ? static_cast<int *>(db.get(static_cast<size_t>(5) * g.M * sizeof(int))) : nullptr;
+    if (q8 && (!q_out || (g.has_res && !q_res) || !qrow)) return false;
+    if (qrow) {
+        std::vector<int> rows(static_cast<size_t>(5) * g.M, 0);
+        for (int m = 0; m < g.M; m++) {
+            rows[2 * g.M + m] = 1 << 30;  // m1: multiplier 1/2 at shift 31
+            rows[4 * g.M + m] = 31;
+        }
+        if (hipMemcpy(qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipGetLastError();
+            return false;
+        }
+    }
+    if (q_res) (void)hipMemsetAsync(q_res, 0, q_bytes, st);
     (void)hipMemsetAsync(xq, 0, xbytes, st);
     (void)hipMemsetAsync(wp, 0, wbytes, st);
     (void)hipMemsetAsync(sc, 0, static_cast<size_t>(g.M) * 4, st);
@@ -1044,6 +1207,24 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
         a.bias = g.has_bias ? sc : nullptr;
         a.res = res;
         a.y = y;
+        if (q8) {
+            a.q8 = 1;
+            a.qrow = qrow;
+            a.scales = nullptr;
+            a.bias = nullptr;
+            a.res = nullptr;
+            a.y = nullptr;
+            a.q_out = q_out;
+            a.q_bytes = static_cast<int>(q_bytes);
+            a.q_Hp = g.OH;
+            a.q_Wp = g.OW;
+            a.q_Cp = q_Cp;
+            a.r8 = q_res;
+            a.r_bytes = q_res ? static_cast<int>(q_bytes) : 0;
+            a.r_Hp = g.OH;
+            a.r_Wp = g.OW;
+            a.r_Cp = q_Cp;
+        }
         if (hipEventRecord(e0, st) != hipSuccess) return 1e300;
         for (int r = 0; r < reps; r++)
             if (launch_i8(st, cd.cfg, cd.tc, a, part, nullptr) != 0) return 1e300;
@@ -1160,9 +1341,64 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
     return join_handoff(pp, plan, L, readers, is_output);
 }
 
+// The INT8 configuration's per-channel requantization constants (the same
+// definition as the oracle's restatement): bias_q = round_half_away(b /
+// (s_x s_w)) clamped to +-2^30; m1 ~ (s_x s_w / s_y) 2^S and m2 ~ (s_r /
+// s_y) 2^S with S = 31 - e for max(ratio) = f 2^e, f in [0.5, 1), one less
+// if a multiplier rounds to 2^31.  Rows of qrow: -z_x sum(w), that plus
+// bias_q, m1, m2, S.  False when a shift leaves [1, 62].
+bool q8_requant_rows(const ConvGeom &g, const int8_t *w, const float *ws, float sx, int zx, float sy, float sr,
+                     const float *bias, std::vector<int> &rows) {
+    const int M = g.M;
+    const size_t K = static_cast<size_t>(g.C) * g.KH * g.KW;
+    rows.assign(static_cast<size_t>(5) * M, 0);
+    for (int m = 0; m < M; m++) {
+        int64_t wsum = 0;
+        for (size_t k = 0; k < K; k++) wsum += w[m * K + k];
+        const double r1 = (static_cast<double>(sx) * static_cast<double>(ws[m])) / static_cast<double>(sy);
+        const double r2 = sr > 0.0f ? static_cast<double>(sr) / static_cast<double>(sy) : 0.0;
+        int e = 0;
+        (void)std::frexp(std::max(r1, r2), &e);
+        int sh = 31 - e;
+        double a1 = std::floor(std::ldexp(r1, sh) + 0.5), a2 = std::floor(std::ldexp(r2, sh) + 0.5);
+        if (a1 >= 2147483648.0 || a2 >= 2147483648.0) {
+            sh -= 1;
+            a1 = std::floor(std::ldexp(r1, sh) + 0.5);
+            a2 = std::floor(std::ldexp(r2, sh) + 0.5);
+        }
+        if (sh < 1 || sh > 62) return false;
+        double bq = 0.0;
+        if (bias) {
+            const double v = static_cast<double>(bias[m]) / (static_cast<double>(sx) * static_cast<double>(ws[m]));
+            bq = v >= 0.0 ? std::floor(v + 0.5) : -std::floor(-v + 0.5);
+            bq = std::min(std::max(bq, -1073741824.0), 1073741824.0);
+        }
+        const int zw = static_cast<int>(-static_cast<int64_t>(zx) * wsum);
+        rows[m] = zw;
+        rows[M + m] = zw + static_cast<int>(bq);
+        rows[2 * M + m] = static_cast<int>(a1);
+        rows[3 * M + m] = static_cast<int>(a2);
+        rows[4 * M + m] = sh;
+    }
+    return true;
+}
+
 int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *plan) {
     const ConvGeom &g = plan->g;
-    if (g.group != 1 || g.x_dtype != SPKV2_DTYPE_FP32) return SPKV2_E_UNSUPPORTED;
+    // the INT8 configuration with int8 tensors between nodes: the input is
+    // an int8 tensor (or fp32, quantized asymmetrically on load), the output
+    // an int8 tensor, the residual (if any) an int8 tensor
+    const Spkv2Q8Tensor *tx = q8_tensor(ctx, node->inputs[0]);
+    const Spkv2Q8Tensor *ty = q8_tensor(ctx, node->outputs[0]);
+    const Spkv2Q8Tensor *tr = g.has_res ? q8_tensor(ctx, node->inputs[3]) : nullptr;
+    const bool q8 = tx || ty;
+    if (g.group != 1 || (!tx && g.x_dtype != SPKV2_DTYPE_FP32)) return SPKV2_E_UNSUPPORTED;
+    if (q8 && (!ty || (g.has_res && !tr) || (g.act != 0 && g.act != 1))) {
+        set_last_error_text("conv node " + std::to_string(node->id) +
+                            ": int8 tensors between nodes need an int8 output, an int8 residual and no SiLU");
+        return SPKV2_E_UNSUPPORTED;
+    }
+    if (tr && (tr->N != g.N || tr->C != g.M || tr->H != g.OH || tr->W != g.OW)) return -11;
     const Spkv2QuantParamRecord *wq = spkv2_ctx_find_quant_param(ctx, node->inputs[1]);
     const Spkv2QuantParamRecord *xq = spkv2_ctx_find_quant_param(ctx, node->inputs[0]);
     if (!wq || !xq) return SPKV2_E_QUANT;
@@ -1171,11 +1407,18 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     if (!ws || !xs || static_cast<int>(wq->num_channels) < g.M || xq->num_channels < 1) return SPKV2_E_QUANT;
     const int8_t *w = reinterpret_cast<const int8_t *>(host_weight_data(ctx, node->inputs[1]));
     if (!w) return SPKV2_E_UNSUPPORTED;
+    int zx = 0;
+    if (q8) {
+        float sx = 0.0f;
+        if (int rc = q8_params(ctx, node->inputs[0], &sx, &zx)) return rc;
+    }
 
-    const I8Layout L = i8_layout(g);
+    const I8Layout L = tx ? i8_layout_q8(g, *tx) : i8_layout(g);
+    // an int8 input is read in place: only the fp32 input needs the workspace copy
     const size_t xq_bytes = static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp;
     if (xq_bytes >= 0x7fff0000ULL) return SPKV2_E_UNSUPPORTED;  // byte offsets are 31-bit
-    plan->path = CONV_IGEMM_I8;
+    plan->path = q8 ? CONV_Q8 : CONV_IGEMM_I8;
+    plan->x_zp = zx;
     plan->x_scale = xs[0];
     plan->Hp = L.Hp;
     plan->Wp = L.Wp;
@@ -1186,7 +1429,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
 
     int cfg = 0, split = 1;
     const char *tune_env = getenv("SPKV2_CONV_TUNE");
-    if ((tune_env && tune_env[0] == '0') || !tune_i8(ctx->stream, g, L, &cfg, &split)) {
+    if ((tune_env && tune_env[0] == '0') || !tune_i8(ctx->stream, g, L, &cfg, &split, q8)) {
         double best = 1e300;
         for (int c = 0; c < kNumI8Cfgs; c++)
             for (int s : kI8Splits) {
@@ -1232,7 +1475,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
     const size_t part_bytes = i8_partial_bytes(tc, g.M, Ntot);
     // partial offsets (slice, row, out-of-range column) must stay below 2^32
     if (part_bytes >= 0x40000000ULL) return SPKV2_E_UNSUPPORTED;
-    plan->pad_bytes = align_up(xq_bytes + 64, 256);
+    plan->pad_bytes = tx ? 0 : align_up(xq_bytes + 64, 256);
     plan->workspace = plan->pad_bytes + part_bytes;
 
     // activation quantization constants (reference conv_int8.c:22-23)
@@ -1264,6 +1507,28 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
                            "hipMemcpy"))
         return rc;
 
+    if (q8) {
+        float sy = 0.0f, sr = 0.0f;
+        int zy = 0, zr = 0;
+        if (int rc = q8_params(ctx, node->outputs[0], &sy, &zy)) return rc;
+        if (tr)
+            if (int rc = q8_params(ctx, node->inputs[3], &sr, &zr)) return rc;
+        const float *bias = g.has_bias ? reinterpret_cast<const float *>(host_weight_data(ctx, node->inputs[2])) : nullptr;
+        if (g.has_bias && (!bias || rec(ctx, node->inputs[2])->dtype != SPKV2_DTYPE_FP32)) return SPKV2_E_UNSUPPORTED;
+        std::vector<int> rows;
+        if (!q8_requant_rows(g, w, ws, plan->x_scale, zx, sy, sr, bias, rows)) {
+            set_last_error_text("conv node " + std::to_string(node->id) + ": requantization shift out of range");
+            return SPKV2_E_QUANT;
+        }
+        if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->qrow), rows.size() * sizeof(int)), "hipMalloc"))
+            return rc;
+        if (int rc = hip_check(hipMemcpy(plan->qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice),
+                               "hipMemcpy"))
+            return rc;
+        set_kernel_name(ctx, node, std::string("conv_igemm_q8<") + t.name + (L.runs ? ",runs" : ",taps") +
+                                       ",splitk=" + std::to_string(plan->splitk) + ">");
+        return 0;
+    }
     std::vector<float> comb(static_cast<size_t>(g.M));
     for (int m = 0; m < g.M; m++) comb[m] = ws[m] * plan->x_scale;  // reference conv_int8.c:93
     if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->scales), comb.size() * 4), "hipMalloc")) return rc;
@@ -1277,9 +1542,14 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
 
 int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *plan, int32_t *raw_acc_out) {
     const ConvGeom &g = plan->g;
+    const bool q8 = plan->path == CONV_Q8;
+    const Spkv2Q8Tensor *tx = q8 ? q8_tensor(ctx, node->inputs[0]) : nullptr;
+    const Spkv2Q8Tensor *ty = q8 ? q8_tensor(ctx, node->outputs[0]) : nullptr;
+    const Spkv2Q8Tensor *tr = q8 && g.has_res ? q8_tensor(ctx, node->inputs[3]) : nullptr;
+    if (q8 && (!ty || (g.has_res && !tr))) return SPKV2_E_UNSUPPORTED;
     uint8_t *wsb = plan_workspace(ctx, plan);
-    if (!wsb) return SPKV2_E_UNSUPPORTED;
-    const I8Layout L = i8_layout(g);
+    if (!wsb && plan->workspace > 0) return SPKV2_E_UNSUPPORTED;
+    const I8Layout L = tx ? i8_layout_q8(g, *tx) : i8_layout(g);
     int8_t *xq = reinterpret_cast<int8_t *>(wsb);
     int32_t *part = reinterpret_cast<int32_t *>(wsb + plan->pad_bytes);
     const float inv_scale = 1.0f / plan->x_scale;  // reference conv_int8.c:23
@@ -1287,19 +1557,22 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     // with the handoffs not live (a fault event armed, or the kernel registry
     // changed since prepare) every tensor is materialized and quantized here
     const bool handoff = handoffs_live(ctx);
-    if ((plan->q_in || plan->q_shared) && handoff) {
+    if (tx) {
+        xq = tx->buf;  // an int8 tensor, read in place
+    } else if ((plan->q_in || plan->q_shared) && handoff) {
         xq = plan->q_in ? plan->q_in : plan->q_shared;  // written by the producer's epilogue
     } else if (L.Cp <= 16) {
         const size_t pixels = static_cast<size_t>(g.N) * L.Hp * L.Wp;
         hipLaunchKernelGGL(quantize_pad_nhwc_narrow, dim3(grid_for(pixels, 256)), dim3(256), 0, ctx->stream,
                            dptr<const float>(ctx, node->inputs[0]), xq, g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl,
-                           inv_scale, plan->quant_split, g.N);
+                           inv_scale, plan->quant_split, g.N, q8 ? plan->x_zp : 0, q8 ? 1 : 0);
         if (int rc = launch_status("quantize_pad_nhwc_narrow")) return rc;
     } else {
         dim3 qgrid(static_cast<unsigned>((L.Hp * L.Wp + 63) / 64), static_cast<unsigned>((L.Cp + 63) / 64),
                    static_cast<unsigned>(g.N));
         hipLaunchKernelGGL(quantize_pad_nhwc, qgrid, dim3(256), 0, ctx->stream, dptr<const float>(ctx, node->inputs[0]),
-                           xq, g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl, inv_scale, plan->quant_split);
+                           xq, g.C, g.H, g.W, L.Hp, L.Wp, L.Cp, L.pt, L.pl, inv_scale, plan->quant_split,
+                           q8 ? plan->x_zp : 0, q8 ? 1 : 0);
         if (int rc = launch_status("quantize_pad_nhwc")) return rc;
     }
 
@@ -1309,21 +1582,44 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     a.xq = xq;
     a.wp = static_cast<const int8_t *>(plan->wpack);
     a.koff = static_cast<const int *>(plan->ktab);
-    a.scales = plan->scales;
-    a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
-    a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
-    a.y = dptr<float>(ctx, node->outputs[0]);
-    if (plan->q_out && handoff) {
-        a.q_out = plan->q_out;
-        a.q_bytes = static_cast<int>(static_cast<size_t>(g.N) * plan->q_Hp * plan->q_Wp * plan->q_Cp);
-        a.q_Hp = plan->q_Hp;
-        a.q_Wp = plan->q_Wp;
-        a.q_Cp = plan->q_Cp;
-        a.q_pt = plan->q_pt;
-        a.q_pl = plan->q_pl;
-        a.q_split = plan->q_split;
-        a.q_inv = plan->q_inv_scale;
-        if (!plan->y_needed) a.y = nullptr;
+    if (q8) {
+        a.q8 = 1;
+        a.qrow = plan->qrow;
+        a.q_out = ty->buf;
+        a.q_bytes = static_cast<int>(ty->bytes);
+        a.q_Hp = ty->Hp;
+        a.q_Wp = ty->Wp;
+        a.q_Cp = ty->Cp;
+        a.q_pt = ty->pt;
+        a.q_pl = ty->pl;
+        a.y_zp = ty->zp;
+        if (tr) {
+            a.r8 = tr->buf;
+            a.r_bytes = static_cast<int>(tr->bytes);
+            a.r_Hp = tr->Hp;
+            a.r_Wp = tr->Wp;
+            a.r_Cp = tr->Cp;
+            a.r_pt = tr->pt;
+            a.r_pl = tr->pl;
+            a.r_zp = tr->zp;
+        }
+    } else {
+        a.scales = plan->scales;
+        a.bias = g.has_bias ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
+        a.res = g.has_res ? dptr<const float>(ctx, node->inputs[3]) : nullptr;
+        a.y = dptr<float>(ctx, node->outputs[0]);
+        if (plan->q_out && handoff) {
+            a.q_out = plan->q_out;
+            a.q_bytes = static_cast<int>(static_cast<size_t>(g.N) * plan->q_Hp * plan->q_Wp * plan->q_Cp);
+            a.q_Hp = plan->q_Hp;
+            a.q_Wp = plan->q_Wp;
+            a.q_Cp = plan->q_Cp;
+            a.q_pt = plan->q_pt;
+            a.q_pl = plan->q_pl;
+            a.q_split = plan->q_split;
+            a.q_inv = plan->q_inv_scale;
+            if (!plan->y_needed) a.y = nullptr;
+        }
     }
     if (int rc = launch_i8(ctx->stream, plan->cfg, tc, a, part, raw_acc_out)) return rc;
     // accumulator capture: the same GEMM again on the same quantized input,

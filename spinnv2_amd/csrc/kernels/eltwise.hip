@@ -1016,6 +1016,7 @@ int setup_pool_int8_inputs(Spkv2Context *ctx) {
 }
 
 int maxpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    if (q8_tensor(ctx, node->inputs[0])) return maxpool_q8_run(ctx, node);
     PoolArgs p;
     if (int rc = pool_args(ctx, node, &p)) return rc;
     const size_t total = static_cast<size_t>(p.N) * p.C * p.OH * p.OW;
@@ -1089,6 +1090,7 @@ int avgpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
 }
 
 int global_avgpool_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
+    if (q8_tensor(ctx, node->inputs[0])) return mean_q8_run(ctx, node);
     const Spkv2TensorRecord *xr = rec(ctx, node->inputs[0]);
     if (xr->rank != 4) return -11;
     const size_t rows = static_cast<size_t>(xr->shape[0]) * xr->shape[1];
@@ -1159,6 +1161,12 @@ int reduce_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     } else {
         for (int i = 0; i < rank; i++) reduced[i] = true;
         naxes = rank;
+    }
+    if (q8_tensor(ctx, node->inputs[0])) {
+        // an int8 activation: ReduceMean over H, W only
+        if (node->op_type != SPKV2_OP_REDUCEMEAN || rank != 4 || naxes != 2 || !reduced[2] || !reduced[3])
+            return SPKV2_E_UNSUPPORTED;
+        return mean_q8_run(ctx, node);
     }
     float denom = 1.0f;
     for (int i = 0; i < rank; i++)

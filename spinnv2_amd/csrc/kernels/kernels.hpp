@@ -58,6 +58,16 @@ int setup_concat_views(Spkv2Context *ctx);
 // int8 conv -> MaxPool -> int8 convs: the conv hands the pool int8 (eltwise.hip)
 int setup_pool_int8_inputs(Spkv2Context *ctx);
 
+// INT8 configuration with int8 tensors between nodes (q8.hip): the int8
+// activation tensors' buffers (before the node prepares), the check that
+// built-in kernels run every node touching one (after them), and the
+// MaxPool / spatial-mean kernels over them
+int setup_q8_tensors(Spkv2Context *ctx);
+int check_q8_winners(const Spkv2Context *ctx);
+int q8_params(const Spkv2Context *ctx, uint32_t tensor_id, float *scale, int *zp);
+int maxpool_q8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node);
+int mean_q8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node);
+
 // reliability helpers used by the executor
 int flip_bit(hipStream_t s, void *data, uint64_t element, uint32_t bit);
 int minmax(hipStream_t s, const float *x, size_t n, float *dev_out4);

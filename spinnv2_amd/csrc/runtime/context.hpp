@@ -31,6 +31,23 @@ struct Spkv2TensorView {
     int64_t ch_elems = 0;   // elements between channels (0: the tensor's own plane size)
 };
 
+// An int8 activation tensor of the INT8 configuration with int8 tensors
+// between nodes (package dtype int8, role activation): it lives in its own
+// device buffer as zero-point-padded NHWC, [N][Hp][Wp][Cp] bytes, the image
+// at rows pt.. and columns pl.., channels 0..C-1 of a Cp = 16k pitch.  The
+// halo (the widest padding of the convs that read it) and the pitch's extra
+// channels hold the zero point, written once at prepare: a padded tap then
+// reads the real value 0.  Not in the arena: nothing but the built-in int8
+// kernels reads it.
+struct Spkv2Q8Tensor {
+    int8_t *buf = nullptr;
+    size_t bytes = 0;
+    int N = 0, C = 0, H = 0, W = 0;
+    int Hp = 0, Wp = 0, Cp = 0, pt = 0, pl = 0;
+    float scale = 1.0f;
+    int zp = 0;
+};
+
 struct Spkv2Context {
     // ---- the package (host memory, zero-copy views into the blob) ----
     uint8_t *owned_model = nullptr;
@@ -129,6 +146,11 @@ struct Spkv2Context {
     std::vector<uint8_t> view_split;
     std::vector<uint8_t> view_elide;  // nodes whose output the views already hold: nothing to run
     std::vector<void *> view_buffers;
+    // int8 activation tensors (per tensor id; buf null for every other
+    // tensor) and the nodes that read or write one
+    std::vector<Spkv2Q8Tensor> q8;
+    std::vector<uint8_t> q8_node;
+    bool has_q8 = false;
 };
 
 // ---- internal helpers shared by the runtime translation units ----
@@ -170,6 +192,11 @@ inline bool view_elided(const Spkv2Context *ctx, uint32_t node_id) {
 void set_last_error(const char *what, hipError_t err);
 void set_last_error_text(const std::string &text);
 int hip_check(hipError_t err, const char *what);
+
+// The int8 activation tensor record of a tensor id, or null.
+inline const Spkv2Q8Tensor *q8_tensor(const Spkv2Context *ctx, uint32_t tensor_id) {
+    return tensor_id < ctx->q8.size() && ctx->q8[tensor_id].buf ? &ctx->q8[tensor_id] : nullptr;
+}
 
 inline const uint8_t *host_weight_data(const Spkv2Context *ctx, uint32_t tensor_id) {
     const Spkv2TensorRecord *r = &ctx->tensor_records[tensor_id];

@@ -418,6 +418,9 @@ extern "C" int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t
             return rc;
         if (int rc = alloc_zeroed(reinterpret_cast<uint8_t **>(&ctx->dev_flag), 4 * sizeof(uint32_t), ctx->stream))
             return rc;
+        // int8 activation tensors (the INT8 configuration with int8 tensors
+        // between nodes) get their buffers before the nodes plan against them
+        if (int rc = spk::kern::setup_q8_tensors(ctx)) return rc;
         size_t workspace = 0;
         for (uint32_t i = 0; i < ctx->header.num_nodes; i++) {
             size_t ws = 0;
@@ -425,6 +428,7 @@ extern "C" int spkv2_prepare_with_scratch(Spkv2Context *ctx, void *arena, size_t
             if (rc != 0) return rc;
             if (ws > workspace) workspace = ws;
         }
+        if (int rc = spk::kern::check_q8_winners(ctx)) return rc;
         if (int rc = spk::kern::setup_concat_views(ctx)) return rc;
         if (int rc = spk::kern::setup_pool_int8_inputs(ctx)) return rc;
         if (workspace > 0) {
@@ -512,6 +516,13 @@ extern "C" int spkv2_run(Spkv2Context *ctx) {
     for (uint32_t i = 0; i < ctx->header.num_tensors; i++)
         if (ctx->tensor_records[i].role != SPKV2_ROLE_WEIGHT && !ctx->tensors[i].data) return -5;
     spk::refresh_winners(ctx);
+    if (ctx->has_q8 && !ctx->winners_match) {
+        // a user kernel registered since prepare would now run a node whose
+        // int8 tensors live in the built-in kernels' own buffers
+        spk::set_last_error_text("the kernel registry changed since prepare: int8 tensors between nodes need the "
+                                 "built-in kernels that prepared them");
+        return SPKV2_E_UNSUPPORTED;
+    }
     const bool can_graph =
         ctx->graph_mode && !ctx->profiling && spk::handoffs_live(ctx) && ctx->protection_count == 0;
     if (can_graph) return run_graph(ctx);
@@ -650,6 +661,12 @@ extern "C" const float *spkv2_ctx_quant_scales(const Spkv2Context *ctx, const Sp
     return reinterpret_cast<const float *>(ctx->quant_data + qp->data_offset);
 }
 
+extern "C" const int32_t *spkv2_ctx_quant_zero_points(const Spkv2Context *ctx, const Spkv2QuantParamRecord *qp) {
+    if (!ctx || !qp || !ctx->quant_data) return nullptr;
+    if (qp->data_offset + static_cast<uint64_t>(qp->num_channels) * 8 > ctx->quant_data_size) return nullptr;
+    return reinterpret_cast<const int32_t *>(ctx->quant_data + qp->data_offset + static_cast<uint64_t>(qp->num_channels) * 4);
+}
+
 extern "C" int spkv2_ctx_node_cache(Spkv2Context *ctx, uint32_t node_id, void ***slot, void (***dtor)(void *)) {
     if (!ctx || node_id >= ctx->node_count) return -1;
     if (slot) *slot = &ctx->node_cache[node_id];
@@ -723,6 +740,13 @@ extern "C" int spkv2_mi355x_node_kernel_name(Spkv2Context *ctx, uint32_t node_id
     return 0;
 }
 
+// Bytes of a conv node's int32 accumulators: four per output element.
+static size_t acc_bytes(const Spkv2TensorRecord *y) {
+    size_t n = 1;
+    for (uint16_t i = 0; i < y->rank; i++) n *= y->shape[i];
+    return n * sizeof(int32_t);
+}
+
 extern "C" int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable) {
     if (!ctx) return -1;
     if (!ctx->prepared) return SPKV2_E_NO_DEVICE;
@@ -739,7 +763,9 @@ extern "C" int spkv2_mi355x_set_int8_capture(Spkv2Context *ctx, int enable) {
         const Spkv2NodeRecord *node = &ctx->node_records[i];
         if (node->op_type != SPKV2_OP_CONV || node->input_count < 2) continue;
         if (ctx->tensor_records[node->inputs[1]].dtype != SPKV2_DTYPE_INT8) continue;
-        const size_t bytes = ctx->tensor_records[node->outputs[0]].size_bytes;
+        // int32 per output element, whatever the output's own dtype (an int8
+        // tensor in the INT8 configuration with int8 tensors between nodes)
+        const size_t bytes = acc_bytes(&ctx->tensor_records[node->outputs[0]]);
         if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&ctx->acc_capture[node->id]), bytes),
                                "hipMalloc accumulator capture"))
             return rc;
@@ -754,7 +780,7 @@ extern "C" int spkv2_mi355x_conv_int8_accumulators(Spkv2Context *ctx, uint32_t n
     const Spkv2NodeRecord *node = &ctx->node_records[node_id];
     if (node->op_type != SPKV2_OP_CONV) return -1;
     const Spkv2TensorRecord *y = &ctx->tensor_records[node->outputs[0]];
-    if (size != y->size_bytes) return -2;
+    if (size != acc_bytes(y)) return -2;
     if (node_id < ctx->acc_capture.size() && ctx->acc_capture[node_id]) {
         // captured during the last spkv2_run
         if (int rc = hip_check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize")) return rc;
@@ -812,7 +838,7 @@ extern "C" int spkv2_mi355x_conv_int8_accumulators_noalloc(Spkv2Context *ctx, ui
     const Spkv2NodeRecord *node = &ctx->node_records[node_id];
     if (node->op_type != SPKV2_OP_CONV) return -1;
     const Spkv2TensorRecord *y = &ctx->tensor_records[node->outputs[0]];
-    if (size != y->size_bytes) return -2;
+    if (size != acc_bytes(y)) return -2;
     if (size > kAccScratchBytes) {
         spk::set_last_error_text("int8 accumulators of " + std::to_string(size) +
                                  " bytes exceed the 16 MiB allocation-free staging array");

@@ -170,6 +170,8 @@ void destroy(Spkv2Context *ctx) {
         for (int32_t *p : ctx->acc_capture)
             if (p) (void)hipFree(p);
         for (void *p : ctx->view_buffers) (void)hipFree(p);
+        for (Spkv2Q8Tensor &t : ctx->q8)
+            if (t.buf) (void)hipFree(t.buf);
         if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     }
     spkv2_platform_free(ctx->node_cache);

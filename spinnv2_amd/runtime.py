@@ -82,6 +82,7 @@ SIGNATURES = {
     "spkv2_ctx_stream": (VP, [VP]),
     "spkv2_ctx_find_quant_param": (VP, [VP, U32]),
     "spkv2_ctx_quant_scales": (VP, [VP, VP]),
+    "spkv2_ctx_quant_zero_points": (VP, [VP, VP]),
     "spkv2_ctx_node_cache": (I, [VP, U32, VP, VP]),
     "spkv2_device_malloc": (I, [ctypes.POINTER(VP), SZ]),
     "spkv2_device_free": (I, [VP]),
@@ -100,6 +101,7 @@ SIGNATURES = {
     "spkv2_mi355x_conv_int8_accumulators": (I, [VP, U32, VP, SZ]),
     "spkv2_mi355x_set_int8_capture": (I, [VP, I]),
     "spkv2_mi355x_conv_int8_accumulators_noalloc": (I, [VP, U32, VP, SZ]),
+    "spkv2_mi355x_read_int8_tensor": (I, [VP, U32, VP, SZ]),
 }
 
 _LIB = None
@@ -251,6 +253,14 @@ class Model:
         out = np.empty(nbytes // 4, dtype=np.int32)
         _check(self.lib, self.lib.spkv2_mi355x_conv_int8_accumulators(self.ctx, node_id, out.ctypes.data, nbytes),
                "int8 accumulators")
+        return out
+
+    def read_int8_tensor(self, tensor_id: int, shape) -> np.ndarray:
+        """An int8 activation tensor (the INT8 configuration with int8
+        tensors between nodes) after a run, as an NCHW int8 array."""
+        out = np.empty(tuple(int(d) for d in shape), dtype=np.int8)
+        _check(self.lib, self.lib.spkv2_mi355x_read_int8_tensor(self.ctx, tensor_id, out.ctypes.data, out.nbytes),
+               "read int8 tensor")
         return out
 
     def set_fault_event(self, event: FaultEvent | dict | None) -> int:

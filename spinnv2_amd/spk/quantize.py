@@ -216,13 +216,15 @@ def int8_tensor_plan(g: Graph) -> tuple[set[int], list]:
     return cand, convs
 
 
-def quantize_int8_activations(g: Graph, samples: list) -> list[QuantParam]:
+def quantize_int8_activations(g: Graph, samples: list, calibrate_on: Graph | None = None) -> list[QuantParam]:
     """Turns a fused fp32 graph into the INT8 configuration's package form:
     calibrates min/max of every tensor the mode stores as int8 (and of the
     fp32 inputs its Convs quantize on load) on the samples with the fp32
     forward, quantizes those Convs' weights per channel, marks the int8
     tensors, and returns the quantization records (per-tensor scale and
-    zero point; MaxPool outputs take their input's)."""
+    zero point; MaxPool outputs take their input's).  `calibrate_on` runs
+    the samples through another graph of the same structure and weights
+    (e.g. the batch-1 graph for a batch-64 package: tensor ids agree)."""
     cand, convs = int8_tensor_plan(g)
     if not convs:
         raise ValueError("no Conv of this graph can run with int8 tensors between nodes")
@@ -234,7 +236,7 @@ def quantize_int8_activations(g: Graph, samples: list) -> list[QuantParam]:
     lo: dict[int, float] = {}
     hi: dict[int, float] = {}
     for smp in samples:
-        vals = forward_fp32(g, smp if isinstance(smp, (list, tuple)) else [smp], want)
+        vals = forward_fp32(calibrate_on or g, smp if isinstance(smp, (list, tuple)) else [smp], want)
         for t in want:
             v = vals[t]
             lo[t] = min(lo.get(t, np.inf), float(np.min(v)))

@@ -258,3 +258,31 @@ def test_oracle_q8_resnet_tracks_fp32():
     got = OracleExecutor(blob).run(x)[0].ravel()
     want = forward_fp32(ref_g, [x], {ref_g.outputs[0]})[ref_g.outputs[0]].ravel()
     assert np.abs(got - want).max() <= 0.1 * np.abs(want).max()
+
+
+def test_q8_package_records_and_loader():
+    """The mode's package: int8 activation tensors (dtype 2, role
+    activation) of numel bytes in the memory plan, a per-tensor record with
+    a zero point for each, and the runtime loader accepts it."""
+    import ctypes as ct
+
+    from oracle.spk_exec import Package
+    from spinnv2_amd.runtime import load_library
+    from spinnv2_amd.spk import models, write_spk
+
+    g = models.resnet(50, 1, image=32, classes=10)
+    samples = [models.make_input(g.tensors[g.inputs[0]].shape, 1000 + i) for i in range(2)]
+    from spinnv2_amd.spk.quantize import quantize_int8_activations
+
+    blob = write_spk(g, "mi355x", quant_params=quantize_int8_activations(g, samples))
+    pkg = Package(blob)
+    q8 = [t for t in pkg.tensors if t.dtype == 2 and t.role == 4]
+    assert len(q8) == 54
+    for t in q8:
+        assert t.size == int(np.prod(t.shape))
+        assert len(pkg.quant[t.id]) == 1 and -128 <= int(pkg.zero_points[t.id][0]) <= 127
+    lib = load_library()
+    buf = ct.create_string_buffer(blob, len(blob))
+    ctx = ct.c_void_p()
+    assert lib.spkv2_load_memory(buf, len(blob), ct.byref(ctx)) == 0
+    lib.spkv2_free(ctx)
