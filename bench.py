@@ -22,7 +22,10 @@ Reported:
   cpu_baseline   the reference runtime (cpu_generic package: naive conv on
                  x86) on one batch-1 image, timed on the host;
   int8, elementwise, yolo   INT8 ResNet-50, the memory-bound ops against
-                 the HBM peak, YOLOv10n 640 images/s (sections of their own).
+                 the HBM peak, YOLOv10n 640 images/s (sections of their own);
+  int8_config_mode  INT8 ResNet-50 in BASELINE configs[4]'s own semantics
+                 (asymmetric activations, int8 tensors between nodes,
+                 fixed-point requantization), against the int8 MFMA peak.
 
     python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--batch 64] [--no-cpu-baseline]
 """
@@ -386,6 +389,125 @@ def int8_resnet50(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, 
     return out
 
 
+def int8_config_mode(lib, steps: int, warmup: int, b1_steps: int, batch: int = 64, node_report: bool = False,
+                     eager: bool = False) -> dict:
+    """INT8 ResNet-50 224x224 in BASELINE configs[4]'s own semantics (no
+    reference counterpart): per-channel symmetric int8 weights, per-tensor
+    asymmetric activation scales and zero points from min/max over 16
+    seeded calibration batches, int8 tensors between nodes, int32
+    accumulation, fixed-point requantization with round-half-away and a
+    fused Relu clamp.  images/s at `batch` (graph replay), batch-1 latency,
+    and the int8 conv launches against the int8 MFMA peak."""
+    from spinnv2_amd.runtime import DeviceBuffer, Model
+    from spinnv2_amd.spk import models, write_spk
+    from spinnv2_amd.spk.quantize import quantize_int8_activations
+
+    t0 = time.time()
+    cal = models.resnet(50, 1)
+    samples = [models.make_input(cal.tensors[cal.inputs[0]].shape, 1000 + i) for i in range(16)]
+
+    def build(b):
+        g = models.resnet(50, b)
+        qp = quantize_int8_activations(g, samples, calibrate_on=cal)
+        return g, write_spk(g, "mi355x", quant_params=qp)
+
+    g, blob = build(batch)
+    log(f"int8 config mode: calibrated and quantized in {time.time() - t0:.1f}s")
+    ops, in_bytes = {}, 0
+    for n in g.nodes:
+        if n.op_type == "Conv":
+            y = g.shape(n.outputs[0])
+            w = g.tensors[n.inputs[1]].shape
+            ops[n.id] = 2 * y[0] * y[1] * y[2] * y[3] * w[1] * w[2] * w[3]
+    total_ops = sum(ops.values())
+    x = models.make_input(g.tensors[g.inputs[0]].shape)
+    m = Model(blob, lib=lib)
+    xin = DeviceBuffer(x.nbytes, lib)
+    xin.upload(x)
+    m.bind_input(0, xin)
+    m.set_profiling(True)
+    for _ in range(warmup):
+        m.run()
+    m.reset_node_times()
+    lib.spkv2_device_synchronize()
+    for _ in range(steps):
+        m.run()
+    lib.spkv2_device_synchronize()
+    m.set_profiling(False)
+    eager_out = m.get_output(0)
+    m.set_graph_mode(not eager)
+    for _ in range(warmup):
+        m.run()
+    lib.spkv2_device_synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        m.run()
+    lib.spkv2_device_synchronize()
+    elapsed = time.perf_counter() - t0
+    graph_same = bit_identical(m.get_output(0), eager_out)
+    m.set_graph_mode(False)
+    conv_ms = 0.0
+    for nid in ops:
+        ms, cnt = m.node_time(nid)
+        conv_ms += ms / max(cnt, 1)
+        if node_report:
+            n = g.nodes[nid]
+            xs_, ws_ = g.shape(n.inputs[0]), g.tensors[n.inputs[1]].shape
+            t_ms = ms / max(cnt, 1)
+            log(f"q8 node {nid:3d} {xs_[1]}x{xs_[2]}->{ws_[0]} k{ws_[2]} s{n.attrs['strides'][0]} "
+                f"{m.kernel_name(nid):52s} {t_ms * 1e3:8.1f} us {ops[nid] / t_ms / 1e9:7.1f} TOP/s")
+    m.close()
+    xin.free()
+    # roofline time basis as the fp32 headline's: the summed kernel-trace
+    # durations of the conv launches per step from the committed summary
+    k8 = pmc_traffic("conv_igemm_q8_resnet50_b64_kernel_stats.txt") if batch == 64 else None
+    kms = k8.get("q8_conv_kernels_ms_per_run") if k8 else None
+    t8 = pmc_traffic("conv_igemm_q8_resnet50_b64_traffic.txt") if batch == 64 else None
+    traffic_b = t8.get("conv_hbm_bytes_per_step") if t8 else None
+    basis_ms = kms if kms else conv_ms
+    tops = total_ops / (basis_ms * 1e-3) / 1e12
+    out = {"workload": "resnet50_int8_config_224", "batch": batch, "images_per_sec": batch * steps / elapsed,
+           "ms_per_step": elapsed * 1e3 / steps, "timed_mode": "eager" if eager else "hip_graph",
+           "graph_matches_eager": graph_same,
+           "semantics": "BASELINE configs[4]: per-channel symmetric int8 weights, per-tensor asymmetric int8 "
+                        "activations (min/max over 16 calibration batches), int8 tensors between nodes, int32 "
+                        "accumulate, fixed-point requantize (round half away), fused Relu clamp; no reference "
+                        "counterpart (checked against the oracle's restatement)",
+           "conv_gop_per_image": total_ops / batch / 1e9,
+           "roofline": {"bound": "mfma", "achieved": tops, "peak": INT8_MFMA_PEAK_TOPS, "unit": "TOP/s",
+                        "frac": tops / INT8_MFMA_PEAK_TOPS, "traffic": traffic_b,
+                        "kernel_ms_per_step": kms,
+                        "basis": ("summed kernel-trace durations of the conv launches per step "
+                                  "(profiles/conv_igemm_q8_resnet50_b64_kernel_stats.txt)" if kms
+                                  else "HIP events around every conv node, eager pass (upper bound of the time)"),
+                        "event_basis": {"conv_ms_per_step": conv_ms,
+                                        "tops": total_ops / (conv_ms * 1e-3) / 1e12,
+                                        "frac": total_ops / (conv_ms * 1e-3) / 1e12 / INT8_MFMA_PEAK_TOPS}},
+           "hbm_frac_of_traffic": (traffic_b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBPS) if traffic_b and kms else None}
+    if b1_steps > 0:
+        g1, blob1 = build(1)
+        m1 = Model(blob1, lib=lib)
+        x1 = models.make_input(g1.tensors[g1.inputs[0]].shape)
+        b1 = DeviceBuffer(x1.nbytes, lib)
+        b1.upload(x1)
+        m1.bind_input(0, b1)
+        m1.run()
+        eager1 = m1.get_output(0)
+        m1.set_graph_mode(not eager)
+        for _ in range(5):
+            m1.run()
+        lib.spkv2_device_synchronize()
+        t0 = time.perf_counter()
+        for _ in range(b1_steps):
+            m1.run()
+        lib.spkv2_device_synchronize()
+        out["b1_ms_per_image"] = (time.perf_counter() - t0) * 1e3 / b1_steps
+        out["b1_graph_matches_eager"] = bit_identical(m1.get_output(0), eager1)
+        m1.close()
+        b1.free()
+    return out
+
+
 def yolo_v10n(lib, steps: int, node_report: bool = False, eager: bool = False, batches=(1, 16)) -> dict:
     """YOLOv10n-style detector at 640x640, batch 1 and
     16: images/s from HIP-graph replays of the node loop (the whole YOLO op
@@ -490,6 +612,9 @@ def main() -> None:
     ap.add_argument("--no-host-io", action="store_true", help="skip the host-buffer (PCIe) pass")
     ap.add_argument("--no-int8", action="store_true", help="skip the INT8 ResNet-50 section")
     ap.add_argument("--int8-only", action="store_true", help="run only the INT8 ResNet-50 section")
+    ap.add_argument("--int8-config-only", action="store_true",
+                    help="run only the INT8 ResNet-50 section in BASELINE configs[4]'s own semantics")
+    ap.add_argument("--no-int8-config", action="store_true", help="skip the INT8 configuration-semantics section")
     ap.add_argument("--no-elementwise", action="store_true", help="skip the memory-bound op section")
     ap.add_argument("--no-yolo", action="store_true", help="skip the YOLOv10n section")
     ap.add_argument("--yolo-only", action="store_true", help="run only the YOLOv10n section")
@@ -522,6 +647,10 @@ def main() -> None:
     if args.yolo_only:
         batches = (args.yolo_batch,) if args.yolo_batch else (1, 16)
         print(json.dumps(yolo_v10n(lib, max(args.steps, 10), args.node_report, args.eager, batches)), flush=True)
+        return
+    if args.int8_config_only:
+        print(json.dumps(int8_config_mode(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
+                                          args.eager)), flush=True)
         return
     if args.int8_only:
         print(json.dumps(int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, args.batch, args.node_report,
@@ -635,6 +764,8 @@ def main() -> None:
     b1_ms, b1_same = batch1_latency(args.depth, args.b1_steps, lib, args.eager) if args.b1_steps > 0 else (None, None)
 
     int8 = None if args.no_int8 else int8_resnet50(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager)
+    int8_cfg = (None if args.no_int8_config
+                else int8_config_mode(lib, args.steps, args.warmup, args.b1_steps, eager=args.eager))
     ew = None if args.no_elementwise else elementwise(lib)
     yolo = None if args.no_yolo else yolo_v10n(lib, max(args.steps, 10), eager=args.eager)
 
@@ -684,6 +815,7 @@ def main() -> None:
         "cpu_baseline": base,
         "cpu_baseline_simd": base_simd,
         "int8": int8,
+        "int8_config_mode": int8_cfg,
         "elementwise": ew,
         "yolo": yolo,
         "top1_image0": int(logits[0].argmax()),

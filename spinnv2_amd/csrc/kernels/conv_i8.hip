@@ -217,13 +217,19 @@ __device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even)
 }
 
 constexpr int i8_stage_bytes(int BM, int BN);
-template <int BM>
+template <int BM, int Q8>
 __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par);
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
                                             int lane, const float *s_par, int8_t *s_q);
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
+                                            int lane, const float *s_par, int8_t *s_q);
 
-template <int BM, int BN, int BK, int BMAP>
+// Q8: the INT8 configuration's epilogue (q8_epilogue) instead of i8_epilogue,
+// a separate instantiation so that neither epilogue's registers weigh on the
+// other's kernels.
+template <int BM, int BN, int BK, int BMAP, int Q8>
 __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int TM = BM / 64, TN = BN / 64;  // 2x2 waves, each (32*TM) x (32*TN)
     constexpr int LDK = BK + 16;               // bytes per LDS row
@@ -355,7 +361,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     if (kt0 >= kt1) return;  // empty split-K slice
-    i8_load_row_params<BM>(a, mt * BM, s_par);  // read after the loop's barriers
+    i8_load_row_params<BM, Q8>(a, mt * BM, s_par);  // read after the loop's barriers
     I8_LOAD_TILE(kt0, ar0, br0);
     I8_LOAD_TILE(kt0 + 1, ar1, br1);
     I8_STORE_TILE(0, ar0, br0);
@@ -373,7 +379,10 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #undef I8_COMPUTE
 #undef I8_LOAD_TILE
 #undef I8_STORE_TILE
-    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    if constexpr (Q8)
+        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    else
+        i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
 }
 
 // Workgroup-shared memory of the int8 GEMM kernels' epilogue: the tile's
@@ -384,9 +393,9 @@ constexpr int i8_stage_bytes(int BM, int BN) { return BN * (BM + 16); }
 
 // s_par: [BM] combined scales and [BM] biases, or with q8 four [BM] int32
 // rows (c, m1, m2, shift), each a row of the plan's qrow table.
-template <int BM>
+template <int BM, int Q8>
 __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par) {
-    if (a.q8) {
+    if constexpr (Q8) {
         int *s_i = reinterpret_cast<int *>(s_par);
         for (int i = threadIdx.x; i < BM; i += 256) {
             const int m = mt0 + i;
@@ -407,13 +416,13 @@ __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, flo
 // tile at (mt0, nt0) (blockIdx.y is the split-K slice).  mode 1 stores int32
 // partials, mode 2 the raw accumulators as NCHW, mode 0 dequantizes (+ bias,
 // residual, activation) into y and/or requantizes into the consumer's padded
-// NHWC int8 buffer -- or with q8 requantizes in fixed point into the output
-// int8 tensor -- through the LDS staging area when its channel pitch is a
+// NHWC int8 buffer: through the LDS staging area when its channel pitch is a
 // multiple of 16, so each pixel's channels of the tile leave as contiguous
 // 16-byte pieces (the other waves' channels of the same pixel beside them).
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
                                             int lane, const float *s_par, int8_t *s_q) {
+    const float *s_sc = s_par, *s_bi = s_par + BM;
     const int m0 = mt0 + wmo, n0 = nt0 + wno;
     const int row = lane & 31;
     // 32x32 accumulator layout: lane holds column (lane & 31) and rows
@@ -464,27 +473,19 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                    // q8: the halo holds z_x, so sum(w x) - z_x sum(w) = sum(w (x - z_x))
-                    const int v = acc[i][j][r] + (a.q8 && m < M ? a.qrow[m] : 0);
-                    __builtin_amdgcn_raw_buffer_store_b32(v, wrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(acc[i][j][r], wrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0);
                 }
         return;
     }
-    const int8_t *dummy = reinterpret_cast<const int8_t *>(a.wp);  // base of the unused resources (0 records)
-    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(
-        a.y ? static_cast<void *>(a.y) : const_cast<int8_t *>(dummy), static_cast<short>(0), a.y ? a.y_bytes : 0,
-        kBufWord3);
+    const __amdgpu_buffer_rsrc_t yrs = __builtin_amdgcn_make_buffer_rsrc(a.y ? a.y : const_cast<float *>(a.scales), static_cast<short>(0),
+                                                                         a.y ? a.y_bytes : 0, kBufWord3);
     const __amdgpu_buffer_rsrc_t rrs = __builtin_amdgcn_make_buffer_rsrc(
-        a.res ? const_cast<float *>(a.res) : const_cast<float *>(reinterpret_cast<const float *>(dummy)),
-        static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
+        const_cast<float *>(a.res ? a.res : a.scales), static_cast<short>(0), a.res ? a.y_bytes : 0, kBufWord3);
     const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
         a.q_out ? a.q_out : const_cast<int8_t *>(a.xq), static_cast<short>(0), a.q_out ? a.q_bytes : 0, kBufWord3);
-    const __amdgpu_buffer_rsrc_t r8s = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t *>(a.r8 ? a.r8 : dummy), static_cast<short>(0), a.r8 ? a.r_bytes : 0, kBufWord3);
-    // handoff / q8 output: byte offset of this lane's pixel in the padded
-    // NHWC int8 buffer, and its spatial index (for the NCHW rounding split);
-    // q8 residual: the pixel's offset in the residual's padded NHWC buffer
-    unsigned qbase[TN], rbase[TN];
+    // handoff: byte offset of this lane's pixel in the consumer's padded NHWC
+    // buffer, and its spatial index (for the NCHW rounding split)
+    unsigned qbase[TN];
     int qsp[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++) {
@@ -496,98 +497,61 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
         qsp[j] = sp;
         qbase[j] = n < a.Ntot ? static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp)
                               : static_cast<unsigned>(kOob);
-        rbase[j] = n < a.Ntot && a.r8
-                       ? static_cast<unsigned>(((img * a.r_Hp + oh + a.r_pt) * a.r_Wp + ow + a.r_pl) * a.r_Cp)
-                       : static_cast<unsigned>(kOob);
     }
-    // staged int8 stores (workgroup-uniform): the staging area aliases the
+    // staged handoff (workgroup-uniform): the staging area aliases the
     // k-loop's LDS operands, so every wave must be past its last read
     const bool stage = a.q_out && a.q_Cp % 16 == 0;
     constexpr int SQ = BM + 16;  // staging row pitch: an odd multiple of 16 bytes
     if (stage) __syncthreads();
-    const float *s_sc = s_par, *s_bi = s_par + BM;
-    const int *s_i = reinterpret_cast<const int *>(s_par);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         // per-row constants of this block (LDS), for all TN blocks
         floatx16 sc, bi;
-        intx16 qc, qm1, qm2, qsh;
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * (r >> 2) + (r & 3);
-            if (a.q8) {
-                qc[r] = s_i[ml];
-                qm1[r] = s_i[BM + ml];
-                qm2[r] = s_i[2 * BM + ml];
-                qsh[r] = s_i[3 * BM + ml];
-            } else {
-                sc[r] = s_sc[ml];
-                bi[r] = s_bi[ml];
-            }
+            sc[r] = s_sc[ml];
+            bi[r] = s_bi[ml];
         }
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            unsigned words[4] = {0u, 0u, 0u, 0u};
             floatx16 v;
-            if (a.q8) {
-                // four consecutive channels per dword: the residual's bytes
-                // of this lane's pixel, then the requantized outputs
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = fmaf(static_cast<float>(acc[i][j][r]), sc[r], bi[r]);
+            if (a.res) {
+                floatx16 rv;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
+                    rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                          rrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0));
+                }
+                v += rv;
+            }
+            if (a.act == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
+            } else if (a.act == 2) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
+            }
+            if (a.q_out) {
+                // four consecutive channels of the lane -> one dword; channels
+                // past M are written 0 (the padded channels stay zero)
+                unsigned words[4];
 #pragma unroll
                 for (int q4 = 0; q4 < 4; q4++) {
-                    const unsigned mq = mrow[i] + 8 * q4;
-                    const unsigned rw = a.r8 ? __builtin_amdgcn_raw_buffer_load_b32(r8s, mq < M ? rbase[j] + mq : kOob, 0, 0)
-                                             : 0u;
+                    const unsigned m0 = mrow[i] + 8 * q4;
                     unsigned word = 0;
 #pragma unroll
                     for (int b = 0; b < 4; b++) {
-                        const int r = 4 * q4 + b;
-                        const int rd = a.r8 ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - a.r_zp : 0;
-                        const int qv = mq + b < M ? q8_requant(acc[i][j][r], qc[r], qm1[r], qm2[r], qsh[r], rd, a.y_zp,
-                                                               a.act == 1)
-                                                  : a.y_zp;
+                        const unsigned m = m0 + b;
+                        const int idx = static_cast<int>(m) * a.OHW + qsp[j];
+                        const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
                         word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
                     }
                     words[q4] = word;
                 }
-            } else {
-#pragma unroll
-                for (int r = 0; r < 16; r++) v[r] = fmaf(static_cast<float>(acc[i][j][r]), sc[r], bi[r]);
-                if (a.res) {
-                    floatx16 rv;
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
-                        rv[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                              rrs, m < M ? obase[j] + m * ohw4 : kOob, 0, 0));
-                    }
-                    v += rv;
-                }
-                if (a.act == 1) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) v[r] = v[r] > 0.0f ? v[r] : 0.0f;
-                } else if (a.act == 2) {
-#pragma unroll
-                    for (int r = 0; r < 16; r++) v[r] = apply_act(v[r], 2);
-                }
-                if (a.q_out) {
-                    // four consecutive channels of the lane -> one dword;
-                    // channels past M are written 0 (the padded channels stay zero)
-#pragma unroll
-                    for (int q4 = 0; q4 < 4; q4++) {
-                        const unsigned mq = mrow[i] + 8 * q4;
-                        unsigned word = 0;
-#pragma unroll
-                        for (int b = 0; b < 4; b++) {
-                            const unsigned m = mq + b;
-                            const int idx = static_cast<int>(m) * a.OHW + qsp[j];
-                            const int qv = m < M ? quantize_one(v[4 * q4 + b], a.q_inv, idx < a.q_split) : 0;
-                            word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
-                        }
-                        words[q4] = word;
-                    }
-                }
-            }
-            if (a.q_out) {
                 if (stage) {
                     // the tile's pixel row in LDS: 4 channels per dword
                     const int pl = wno + j * 32 + row;
@@ -599,12 +563,12 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
                 } else {
 #pragma unroll
                     for (int q4 = 0; q4 < 4; q4++) {
-                        const unsigned mq = mrow[i] + 8 * q4;
-                        __builtin_amdgcn_raw_buffer_store_b32(words[q4], qrs, mq < M ? qbase[j] + mq : kOob, 0, 0);
+                        const unsigned m0 = mrow[i] + 8 * q4;
+                        __builtin_amdgcn_raw_buffer_store_b32(words[q4], qrs, m0 < M ? qbase[j] + m0 : kOob, 0, 0);
                     }
                 }
             }
-            if (a.y && !a.q8) {
+            if (a.y) {
 #pragma unroll
                 for (int r = 0; r < 16; r++) {
                     const unsigned m = mrow[i] + 8 * (r >> 2) + (r & 3);
@@ -619,8 +583,131 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
     __syncthreads();
     // 16-byte pieces of the staged tile, the BM/16 pieces of one pixel on
     // consecutive threads; a piece is stored when its first channel is below
-    // M (channels from M to the padded pitch hold 0, or z_y with q8)
+    // M (channels from M to the padded pitch hold 0)
     constexpr int PPX = BM / 16;
+    for (int t = threadIdx.x; t < BN * PPX; t += 256) {
+        const int pl = t / PPX;
+        const int c16 = (t - pl * PPX) * 16;
+        const int n = nt0 + pl;
+        if (n >= a.Ntot || mt0 + c16 >= a.M) continue;
+        const int img = n / a.OHW;
+        const int sp = n - img * a.OHW;
+        const int oh = sp / a.OW;
+        const int ow = sp - oh * a.OW;
+        const unsigned off =
+            static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp + mt0 + c16);
+        const uintx4 val = *reinterpret_cast<const uintx4 *>(&s_q[pl * SQ + c16]);
+        __builtin_amdgcn_raw_buffer_store_b128(val, qrs, off, 0, 0);
+    }
+}
+
+// The epilogue of the INT8 configuration with int8 tensors between nodes
+// (conv_igemm_i8* with Q8): mode 1 and mode 2 as in i8_epilogue (mode 2
+// adds -z_x sum(w) per row, giving sum(w (x - z_x))); mode 0 requantizes in
+// fixed point into the output int8 tensor.  The tile goes through the LDS
+// staging area ([BN pixels][BM + 16 bytes]): the residual tile, when there
+// is one, is first loaded into it as 16-byte pieces of each pixel's
+// channels; each lane then replaces its residual dwords (four channels of a
+// pixel) with its four requantized outputs; the tile leaves as 16-byte
+// pieces.  Per-row constants (c, m1, m2, shift) come from LDS four rows at a
+// time, so only the accumulators stay live.
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
+                                            int lane, const float *s_par, int8_t *s_q) {
+    const int m0 = mt0 + wmo, n0 = nt0 + wno;
+    const int row = lane & 31;
+    const unsigned M = a.M;
+    const unsigned rsub = 4 * (lane >> 5);
+    if (a.mode == 1 || a.mode == 2) {
+        const __amdgpu_buffer_rsrc_t wrs =
+            __builtin_amdgcn_make_buffer_rsrc(a.ws, static_cast<short>(0), a.ws_bytes, kBufWord3);
+        const unsigned nt4 = static_cast<unsigned>(a.Ntot) * 4u;
+        const unsigned ohw4 = static_cast<unsigned>(a.OHW) * 4u;
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + j * 32 + row;
+            const int img = n / a.OHW;
+            const int sp = n - img * a.OHW;
+            // mode 1: partials [split][M][Ntot]; mode 2: NCHW accumulators
+            const unsigned col = n >= a.Ntot ? static_cast<unsigned>(kOob)
+                                 : a.mode == 1
+                                     ? static_cast<unsigned>(n) * 4u
+                                     : (static_cast<unsigned>(img) * M * static_cast<unsigned>(a.OHW) + sp) * 4u;
+            const unsigned mstride = a.mode == 1 ? nt4 : ohw4;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const unsigned m = m0 + i * 32 + rsub + 8 * (r >> 2) + (r & 3);
+                    const int v = acc[i][j][r] + (a.mode == 2 && m < M ? a.qrow[m] : 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(v, wrs, m < M ? col + m * mstride : kOob,
+                                                          a.mode == 1 ? blockIdx.y * M * nt4 : 0u, 0);
+                }
+        }
+        return;
+    }
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc(a.q_out, static_cast<short>(0), a.q_bytes, kBufWord3);
+    constexpr int SQ = BM + 16;  // staging row pitch: an odd multiple of 16 bytes
+    constexpr int PPX = BM / 16;
+    // the staging area aliases the k-loop's LDS operands: every wave must be
+    // past its last read
+    __syncthreads();
+    if (a.r8) {
+        const __amdgpu_buffer_rsrc_t r8s = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<int8_t *>(a.r8), static_cast<short>(0), a.r_bytes, kBufWord3);
+        for (int t = threadIdx.x; t < BN * PPX; t += 256) {
+            const int pl = t / PPX;
+            const int c16 = (t - pl * PPX) * 16;
+            const int n = nt0 + pl;
+            unsigned off = static_cast<unsigned>(kOob);
+            if (n < a.Ntot && mt0 + c16 < a.M) {
+                const int img = n / a.OHW;
+                const int sp = n - img * a.OHW;
+                const int oh = sp / a.OW;
+                const int ow = sp - oh * a.OW;
+                off = static_cast<unsigned>(((img * a.r_Hp + oh + a.r_pt) * a.r_Wp + ow + a.r_pl) * a.r_Cp + mt0 + c16);
+            }
+            *reinterpret_cast<uintx4 *>(&s_q[pl * SQ + c16]) = __builtin_amdgcn_raw_buffer_load_b128(r8s, off, 0, 0);
+        }
+        __syncthreads();
+    }
+    const int *s_i = reinterpret_cast<const int *>(s_par);
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            // rows ml .. ml + 3 of the tile: four consecutive channels
+            const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * q4;
+            int c[4], m1[4], m2[4], sh[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                c[b] = s_i[ml + b];
+                m1[b] = s_i[BM + ml + b];
+                m2[b] = s_i[2 * BM + ml + b];
+                sh[b] = s_i[3 * BM + ml + b];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                unsigned *cell = reinterpret_cast<unsigned *>(&s_q[(wno + j * 32 + row) * SQ + ml]);
+                const unsigned rw = a.r8 ? *cell : 0u;
+                unsigned word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int rd = a.r8 ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - a.r_zp : 0;
+                    const int qv = static_cast<unsigned>(m0 - wmo + ml + b) < M
+                                       ? q8_requant(acc[i][j][4 * q4 + b], c[b], m1[b], m2[b], sh[b], rd, a.y_zp,
+                                                    a.act == 1)
+                                       : a.y_zp;
+                    word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
+                }
+                *cell = word;
+            }
+        }
+    __syncthreads();
+    // 16-byte pieces of the staged tile, the BM/16 pieces of one pixel on
+    // consecutive threads; a piece is stored when its first channel is below
+    // M (channels from M to the padded pitch hold z_y)
     for (int t = threadIdx.x; t < BN * PPX; t += 256) {
         const int pl = t / PPX;
         const int c16 = (t - pl * PPX) * 16;
@@ -645,7 +732,7 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 // by all its workgroups) into registers, two k-tiles ahead, and only the
 // gathered activations go through LDS (pixel-major gather, as BMAP 1 of
 // conv_igemm_i8).  WAVES_M x WAVES_N waves, each (32*TM) x (32*TN).
-template <int BM, int BN, int BK, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int Q8>
 __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
     constexpr int TM = BM / (32 * WAVES_M), TN = BN / (32 * WAVES_N);
     constexpr int K32 = BK / 32;       // 32-byte k steps per tile
@@ -760,7 +847,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
 
     if (kt0 >= kt1) return;  // empty split-K slice
-    i8_load_row_params<BM>(a, mt * BM, s_par);  // read after the loop's barriers
+    i8_load_row_params<BM, Q8>(a, mt * BM, s_par);  // read after the loop's barriers
     I8X_LOAD_B(kt0, br0);
     I8X_LOAD_B(kt0 + 1, br1);
     I8X_LOAD_A(kt0, a0);
@@ -782,7 +869,10 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
 #undef I8X_STORE_B
 #undef I8X_LOAD_B
 #undef I8X_LOAD_A
-    i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    if constexpr (Q8)
+        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    else
+        i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
 }
 
 // Sums the int32 split-K partials (exact in any order), then dequantizes or
@@ -866,14 +956,18 @@ struct I8Cfg {
     int bmap;     // B gather lane map (see conv_igemm_i8)
     int adirect;  // 1: conv_igemm_i8x, weights packed in MFMA fragment order and loaded straight to registers
     const char *name;
-    I8Kernel kernel;
+    I8Kernel kernel;     // reference semantics (i8_epilogue)
+    I8Kernel kernel_q8;  // the INT8 configuration (q8_epilogue)
 };
 
 // New configurations go at the end: the tune tables store indices.
-#define I8CFG(BM, BN, BK) {BM, BN, BK, 0, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0>}
-#define I8CFGP(BM, BN, BK) {BM, BN, BK, 1, 0, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1>}
-#define I8CFGX(BM, BN, BK, WM, WN) \
-    {BM, BN, BK, 1, 1, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN, conv_igemm_i8x<BM, BN, BK, WM, WN>}
+#define I8CFG(BM, BN, BK) \
+    {BM, BN, BK, 0, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0, 0>, conv_igemm_i8<BM, BN, BK, 0, 1>}
+#define I8CFGP(BM, BN, BK) \
+    {BM, BN, BK, 1, 0, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1, 0>, conv_igemm_i8<BM, BN, BK, 1, 1>}
+#define I8CFGX(BM, BN, BK, WM, WN)                                                                                  \
+    {BM, BN, BK, 1, 1, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN, conv_igemm_i8x<BM, BN, BK, WM, WN, 0>,             \
+     conv_igemm_i8x<BM, BN, BK, WM, WN, 1>}
 const I8Cfg kI8Cfgs[] = {
     I8CFG(128, 128, 64),  I8CFG(128, 128, 128),  I8CFG(128, 64, 64),  I8CFG(128, 64, 128),
     I8CFG(64, 128, 64),   I8CFG(64, 64, 64),     I8CFG(64, 64, 128),
@@ -1060,7 +1154,7 @@ int launch_i8(hipStream_t st, int c, const I8Counts &tc, I8Args a, int32_t *part
         a.mode = 0;
     }
     dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
-    kI8Cfgs[c].kernel<<<grid, dim3(256), 0, st>>>(a);
+    (a.q8 ? kI8Cfgs[c].kernel_q8 : kI8Cfgs[c].kernel)<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_i8")) return rc;
     if (split) {
         const size_t total = static_cast<size_t>(a.M) * a.Ntot;
