@@ -73,6 +73,7 @@ struct ConvPlan {
     // and the shift (requantization constants computed at prepare)
     int *qrow;
     int x_zp;            // CONV_Q8: the input's zero point
+    bool q8_hi;          // CONV_Q8: every row's shift is at least 33 (the 32-bit rounding tail)
     float x_scale;       // int8 path: activation scale
     int quant_split;     // int8 path: first element index of the per-image tail (round half away)
     size_t workspace;    // bytes of device workspace needed per run

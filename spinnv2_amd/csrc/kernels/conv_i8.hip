@@ -38,6 +38,7 @@
 
 #include "conv.hpp"
 #include "kernels.hpp"
+#include "q8_math.hpp"
 
 namespace spk::kern {
 
@@ -170,6 +171,10 @@ struct I8Args {
     int x_bytes, y_bytes, ws_bytes;
     int img_stride;                     // bytes per padded image
     int Wp, Cp, M, OW, OHW, Ntot;
+    // n / OHW and n / OW as a multiply and shift (div_fast), for column
+    // indices below 2^31: most of the per-pixel address arithmetic
+    unsigned ohw_m, ow_m;
+    int ohw_s, ow_s;
     int sh, sw;
     int m_tiles, k_tiles, kt_per_split;
     int act;
@@ -186,23 +191,14 @@ struct I8Args {
     // residual is the int8 tensor r8 (zero point r_zp); mode 2 adds the
     // first row, giving sum(w (x - z_x)).
     int q8;
+    int q8_hi;  // every row's shift is at least 33: q8_requant_hi
     const int *__restrict__ qrow;
     const int8_t *__restrict__ r8;
     int r_bytes, r_Hp, r_Wp, r_Cp, r_pt, r_pl, r_zp;
     int y_zp;
 };
 
-// Fixed-point requantization of one output (the INT8 configuration):
-// t = (acc + c) m1 + rd m2 in int64, rounded to nearest with ties away from
-// zero by the shift, plus the output zero point, Relu as a clamp at it,
-// saturated.  (t + half - [t < 0]) >> sh equals sign(t) ((|t| + half) >> sh).
-__device__ __forceinline__ int q8_requant(int acc, int c, int m1, int m2, int sh, int rd, int zy, bool relu) {
-    const int64_t t = (static_cast<int64_t>(acc) + c) * m1 + static_cast<int64_t>(rd) * m2;
-    const int64_t half = int64_t(1) << (sh - 1);
-    int v = static_cast<int>((t + half - (t < 0 ? 1 : 0)) >> sh) + zy;
-    if (relu) v = max(v, zy);
-    return min(max(v, -128), 127);
-}
+
 
 // The reference's activation quantization of one value (conv_int8.c:26-55):
 // round half to even below `split` (the 16-wide vector body), half away
@@ -216,15 +212,30 @@ __device__ __forceinline__ int quantize_one(float v, float inv_scale, bool even)
     return static_cast<int>(r);
 }
 
+// n / d for 0 <= n < 2^31 with (m, s) from div_magic(d): m = ceil(2^s / d),
+// s = 31 + ceil(log2 d), so n m / 2^s is within 2^-ceil(log2 d) <= 1/d of
+// n / d and its floor is exact.  One 32 x 32 -> 64 multiply and a shift
+// instead of a division sequence.
+__device__ __forceinline__ int div_fast(int n, unsigned m, int s) {
+    return static_cast<int>((static_cast<uint64_t>(static_cast<unsigned>(n)) * m) >> s);
+}
+
 constexpr int i8_stage_bytes(int BM, int BN);
 template <int BM, int Q8>
 __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par);
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
                                             int lane, const float *s_par, int8_t *s_q);
+// 16-byte pieces of a BM x BN tile's int8 channels (BM/16 per pixel) each
+// thread of a 256-thread workgroup stages
+template <int BM, int BN>
+constexpr int q8_pieces() { return (BN * (BM / 16) + 255) / 256; }
+template <int BM, int BN>
+__device__ __forceinline__ void q8_residual_load(const I8Args &a, int mt0, int nt0, uintx4 (&rr)[q8_pieces<BM, BN>()]);
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
-                                            int lane, const float *s_par, int8_t *s_q);
+                                            int lane, const float *s_par, int8_t *s_q,
+                                            const uintx4 (&rr)[q8_pieces<BM, BN>()]);
 
 // Q8: the INT8 configuration's epilogue (q8_epilogue) instead of i8_epilogue,
 // a separate instantiation so that neither epilogue's registers weigh on the
@@ -266,9 +277,9 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     // byte offset of output column n's receptive-field origin in xq
     auto col_of = [&](int n) -> int {
         if (n >= a.Ntot) return kOob;
-        const int img = n / a.OHW;
+        const int img = div_fast(n, a.ohw_m, a.ohw_s);
         const int sp = n - img * a.OHW;
-        const int oh = sp / a.OW;
+        const int oh = div_fast(sp, a.ow_m, a.ow_s);
         const int ow = sp - oh * a.OW;
         return img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
     };
@@ -379,10 +390,13 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 #undef I8_COMPUTE
 #undef I8_LOAD_TILE
 #undef I8_STORE_TILE
-    if constexpr (Q8)
-        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
-    else
+    if constexpr (Q8) {
+        uintx4 rr[q8_pieces<BM, BN>()];
+        if (a.mode == 0 && a.r8) q8_residual_load<BM, BN>(a, mt * BM, nt * BN, rr);
+        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem, rr);
+    } else {
         i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    }
 }
 
 // Workgroup-shared memory of the int8 GEMM kernels' epilogue: the tile's
@@ -391,8 +405,9 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
 // that aliases the k-loop's operand buffers (free once the loop is done).
 constexpr int i8_stage_bytes(int BM, int BN) { return BN * (BM + 16); }
 
-// s_par: [BM] combined scales and [BM] biases, or with q8 four [BM] int32
-// rows (c, m1, m2, shift), each a row of the plan's qrow table.
+// s_par: [BM] combined scales and [BM] biases, or with q8 [BM][4] int32
+// (c, m1, m2, shift of each row: rows 1-4 of the plan's qrow table), one
+// 16-byte LDS read per row in the epilogue.
 template <int BM, int Q8>
 __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par) {
     if constexpr (Q8) {
@@ -400,7 +415,7 @@ __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, flo
         for (int i = threadIdx.x; i < BM; i += 256) {
             const int m = mt0 + i;
 #pragma unroll
-            for (int r = 0; r < 4; r++) s_i[r * BM + i] = m < a.M ? a.qrow[(r + 1) * a.M + m] : 1;
+            for (int r = 0; r < 4; r++) s_i[4 * i + r] = m < a.M ? a.qrow[(r + 1) * a.M + m] : (r == 3 ? 33 : 0);
         }
         return;
     }
@@ -457,7 +472,7 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int n = n0 + j * 32 + row;
-        const int img = n / a.OHW;
+        const int img = div_fast(n, a.ohw_m, a.ohw_s);
         const int sp = n - img * a.OHW;
         obase[j] = n < a.Ntot
                        ? (static_cast<unsigned>(img) * M * static_cast<unsigned>(a.OHW) + static_cast<unsigned>(sp)) * 4u
@@ -490,9 +505,9 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         const int n = n0 + j * 32 + row;
-        const int img = n / a.OHW;
+        const int img = div_fast(n, a.ohw_m, a.ohw_s);
         const int sp = n - img * a.OHW;
-        const int oh = sp / a.OW;
+        const int oh = div_fast(sp, a.ow_m, a.ow_s);
         const int ow = sp - oh * a.OW;
         qsp[j] = sp;
         qbase[j] = n < a.Ntot ? static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp)
@@ -590,9 +605,9 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
         const int c16 = (t - pl * PPX) * 16;
         const int n = nt0 + pl;
         if (n >= a.Ntot || mt0 + c16 >= a.M) continue;
-        const int img = n / a.OHW;
+        const int img = div_fast(n, a.ohw_m, a.ohw_s);
         const int sp = n - img * a.OHW;
-        const int oh = sp / a.OW;
+        const int oh = div_fast(sp, a.ow_m, a.ow_s);
         const int ow = sp - oh * a.OW;
         const unsigned off =
             static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp + mt0 + c16);
@@ -611,9 +626,37 @@ __device__ __forceinline__ void i8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 // pixel) with its four requantized outputs; the tile leaves as 16-byte
 // pieces.  Per-row constants (c, m1, m2, shift) come from LDS four rows at a
 // time, so only the accumulators stay live.
+// The residual tile's 16-byte pieces for this thread (the BM/16 pieces of
+// one pixel on consecutive threads), loaded into registers; pieces past the
+// output's pixels or channels read 0 (out-of-range offsets).
+template <int BM, int BN>
+__device__ __forceinline__ void q8_residual_load(const I8Args &a, int mt0, int nt0, uintx4 (&rr)[q8_pieces<BM, BN>()]) {
+    constexpr int PPX = BM / 16;
+    const __amdgpu_buffer_rsrc_t r8s = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int8_t *>(a.r8 ? a.r8 : reinterpret_cast<const int8_t *>(a.wp)), static_cast<short>(0),
+        a.r8 ? a.r_bytes : 0, kBufWord3);
+#pragma unroll
+    for (int k = 0; k < q8_pieces<BM, BN>(); k++) {
+        const int t = threadIdx.x + 256 * k;
+        const int pl = t / PPX;
+        const int c16 = (t - pl * PPX) * 16;
+        const int n = nt0 + pl;
+        unsigned off = static_cast<unsigned>(kOob);
+        if (t < BN * PPX && n < a.Ntot && mt0 + c16 < a.M) {
+            const int img = div_fast(n, a.ohw_m, a.ohw_s);
+            const int sp = n - img * a.OHW;
+            const int oh = div_fast(sp, a.ow_m, a.ow_s);
+            const int ow = sp - oh * a.OW;
+            off = static_cast<unsigned>(((img * a.r_Hp + oh + a.r_pt) * a.r_Wp + ow + a.r_pl) * a.r_Cp + mt0 + c16);
+        }
+        rr[k] = __builtin_amdgcn_raw_buffer_load_b128(r8s, off, 0, 0);
+    }
+}
+
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
-                                            int lane, const float *s_par, int8_t *s_q) {
+                                            int lane, const float *s_par, int8_t *s_q,
+                                            const uintx4 (&rr)[q8_pieces<BM, BN>()]) {
     const int m0 = mt0 + wmo, n0 = nt0 + wno;
     const int row = lane & 31;
     const unsigned M = a.M;
@@ -626,7 +669,7 @@ __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
         for (int j = 0; j < TN; j++) {
             const int n = n0 + j * 32 + row;
-            const int img = n / a.OHW;
+            const int img = div_fast(n, a.ohw_m, a.ohw_s);
             const int sp = n - img * a.OHW;
             // mode 1: partials [split][M][Ntot]; mode 2: NCHW accumulators
             const unsigned col = n >= a.Ntot ? static_cast<unsigned>(kOob)
@@ -654,39 +697,28 @@ __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
     // past its last read
     __syncthreads();
     if (a.r8) {
-        const __amdgpu_buffer_rsrc_t r8s = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<int8_t *>(a.r8), static_cast<short>(0), a.r_bytes, kBufWord3);
-        for (int t = threadIdx.x; t < BN * PPX; t += 256) {
+        // the residual tile (loaded by the caller) into the staging area
+#pragma unroll
+        for (int k = 0; k < q8_pieces<BM, BN>(); k++) {
+            const int t = threadIdx.x + 256 * k;
             const int pl = t / PPX;
             const int c16 = (t - pl * PPX) * 16;
-            const int n = nt0 + pl;
-            unsigned off = static_cast<unsigned>(kOob);
-            if (n < a.Ntot && mt0 + c16 < a.M) {
-                const int img = n / a.OHW;
-                const int sp = n - img * a.OHW;
-                const int oh = sp / a.OW;
-                const int ow = sp - oh * a.OW;
-                off = static_cast<unsigned>(((img * a.r_Hp + oh + a.r_pt) * a.r_Wp + ow + a.r_pl) * a.r_Cp + mt0 + c16);
-            }
-            *reinterpret_cast<uintx4 *>(&s_q[pl * SQ + c16]) = __builtin_amdgcn_raw_buffer_load_b128(r8s, off, 0, 0);
+            if (t < BN * PPX) *reinterpret_cast<uintx4 *>(&s_q[pl * SQ + c16]) = rr[k];
         }
         __syncthreads();
     }
-    const int *s_i = reinterpret_cast<const int *>(s_par);
+    const intx4 *s_row = reinterpret_cast<const intx4 *>(s_par);
+    const int lo = a.act == 1 ? a.y_zp : -128;  // Relu clamps at the zero point
+    const bool hi_only = a.q8_hi != 0;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int q4 = 0; q4 < 4; q4++) {
             // rows ml .. ml + 3 of the tile: four consecutive channels
             const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * q4;
-            int c[4], m1[4], m2[4], sh[4];
+            intx4 p[4];
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                c[b] = s_i[ml + b];
-                m1[b] = s_i[BM + ml + b];
-                m2[b] = s_i[2 * BM + ml + b];
-                sh[b] = s_i[3 * BM + ml + b];
-            }
+            for (int b = 0; b < 4; b++) p[b] = s_row[ml + b];
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 unsigned *cell = reinterpret_cast<unsigned *>(&s_q[(wno + j * 32 + row) * SQ + ml]);
@@ -695,10 +727,10 @@ __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
 #pragma unroll
                 for (int b = 0; b < 4; b++) {
                     const int rd = a.r8 ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - a.r_zp : 0;
-                    const int qv = static_cast<unsigned>(m0 - wmo + ml + b) < M
-                                       ? q8_requant(acc[i][j][4 * q4 + b], c[b], m1[b], m2[b], sh[b], rd, a.y_zp,
-                                                    a.act == 1)
-                                       : a.y_zp;
+                    const int x = acc[i][j][4 * q4 + b];
+                    int qv = hi_only ? q8_requant_hi(x, p[b][0], p[b][1], p[b][2], p[b][3] - 32, rd, a.y_zp, lo)
+                                     : q8_requant(x, p[b][0], p[b][1], p[b][2], p[b][3], rd, a.y_zp, lo);
+                    if (static_cast<unsigned>(m0 - wmo + ml + b) >= M) qv = a.y_zp;
                     word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
                 }
                 *cell = word;
@@ -713,9 +745,9 @@ __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
         const int c16 = (t - pl * PPX) * 16;
         const int n = nt0 + pl;
         if (n >= a.Ntot || mt0 + c16 >= a.M) continue;
-        const int img = n / a.OHW;
+        const int img = div_fast(n, a.ohw_m, a.ohw_s);
         const int sp = n - img * a.OHW;
-        const int oh = sp / a.OW;
+        const int oh = div_fast(sp, a.ow_m, a.ow_s);
         const int ow = sp - oh * a.OW;
         const unsigned off =
             static_cast<unsigned>(((img * a.q_Hp + oh + a.q_pt) * a.q_Wp + ow + a.q_pl) * a.q_Cp + mt0 + c16);
@@ -771,9 +803,9 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
         const int n = nt * BN + p * PPP + bpix;
         int c = kOob;
         if (n < a.Ntot) {
-            const int img = n / a.OHW;
+            const int img = div_fast(n, a.ohw_m, a.ohw_s);
             const int sp = n - img * a.OHW;
-            const int oh = sp / a.OW;
+            const int oh = div_fast(sp, a.ow_m, a.ow_s);
             const int ow = sp - oh * a.OW;
             c = img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
         }
@@ -869,10 +901,190 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
 #undef I8X_STORE_B
 #undef I8X_LOAD_B
 #undef I8X_LOAD_A
-    if constexpr (Q8)
-        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
-    else
+    if constexpr (Q8) {
+        uintx4 rr[q8_pieces<BM, BN>()];
+        if (a.mode == 0 && a.r8) q8_residual_load<BM, BN>(a, mt * BM, nt * BN, rr);
+        q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem, rr);
+    } else {
         i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+    }
+}
+
+// Persistent form of conv_igemm_i8x (no split-K): a grid of at most the
+// workgroups the GPU holds at once (a multiple of 8), workgroup b walking the
+// tiles of XCD b % 8's contiguous share (m fastest) with a stride of the
+// workgroups on that XCD.  Before a tile's epilogue the next tile's first two
+// B k-tiles, its first A k-tile and (Q8) its residual tile are loaded into
+// registers, so their memory latency overlaps the epilogue's arithmetic and
+// stores; short-K layers (1x1 convs: one or two k-tiles) are otherwise a
+// chain of dependent round trips per tile.
+template <int BM, int BN, int BK, int WAVES_M, int WAVES_N, int Q8>
+__global__ void __launch_bounds__(256) conv_igemm_i8p(I8Args a) {
+    constexpr int TM = BM / (32 * WAVES_M), TN = BN / (32 * WAVES_N);
+    constexpr int K32 = BK / 32;
+    constexpr int LDK = BK + 16;
+    constexpr int G = BK / 16;
+    constexpr int PPP = 256 / G;
+    constexpr int GPT = BN / PPP;
+    constexpr int RP = q8_pieces<BM, BN>();
+    static_assert(WAVES_M * WAVES_N == 4 && TM >= 1 && TN >= 1 && BK % 32 == 0, "tile shape");
+    static_assert(GPT >= 1 && BN % PPP == 0 && (LDK / 16) % 2 == 1, "B gather shape");
+    constexpr int SMEM = 2 * BN * LDK > i8_stage_bytes(BM, BN) ? 2 * BN * LDK : i8_stage_bytes(BM, BN);
+    __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
+    __shared__ float s_par[4 * BM];
+    int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem);
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int row = lane & 31;
+    const int khalf = 16 * (lane >> 5);
+    const int bpix = tid / G, bgrp = tid % G;
+
+    const int n_tiles = (a.Ntot + BN - 1) / BN;
+    const int T = a.m_tiles * n_tiles;
+    const int xcd = blockIdx.x & 7, per = gridDim.x >> 3;
+    const int t_end = static_cast<int>((static_cast<int64_t>(xcd) + 1) * T / 8);
+    int t = static_cast<int>(static_cast<int64_t>(xcd) * T / 8) + (blockIdx.x >> 3);
+    if (t >= t_end) return;  // workgroup-uniform
+
+    const __amdgpu_buffer_rsrc_t xrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t *>(a.xq), static_cast<short>(0), a.x_bytes, kBufWord3);
+    // byte offsets of this thread's B pixels of tile column nt (+ its group)
+    auto columns = [&](int nt, int (&cp)[GPT]) {
+#pragma unroll
+        for (int p = 0; p < GPT; p++) {
+            const int n = nt * BN + p * PPP + bpix;
+            int c = kOob;
+            if (n < a.Ntot) {
+                const int img = div_fast(n, a.ohw_m, a.ohw_s);
+                const int sp = n - img * a.OHW;
+                const int oh = div_fast(sp, a.ow_m, a.ow_s);
+                const int ow = sp - oh * a.OW;
+                c = img * a.img_stride + (oh * a.sh * a.Wp + ow * a.sw) * a.Cp;
+            }
+            cp[p] = c + bgrp * 16;
+        }
+    };
+
+    intx4 a0[TM][K32], a1[TM][K32], br0[GPT], br1[GPT];
+    int colp[GPT];
+    uintx4 rr[RP];
+
+#define I8P_LOAD_A(MT, KT, AX)                                                                                       \
+    {                                                                                                                \
+        const int kt_ = min((KT), a.k_tiles - 1);                                                                    \
+        const intx4 *src =                                                                                           \
+            reinterpret_cast<const intx4 *>(a.wp + (static_cast<size_t>(MT) * a.k_tiles + kt_) * (BM * BK));        \
+        _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int q = 0; q < K32; q++) AX[i][q] =     \
+            src[((wm * TM + i) * K32 + q) * 64 + lane];                                                              \
+    }
+#define I8P_LOAD_B(CP, KT, BR)                                                                                       \
+    {                                                                                                                \
+        const int kbase = a.koff[(KT) * G];                                                                          \
+        _Pragma("unroll") for (int p = 0; p < GPT; p++) BR[p] =                                                      \
+            __builtin_bit_cast(intx4, __builtin_amdgcn_raw_buffer_load_b128(xrs, CP[p], kbase, 0));                  \
+    }
+#define I8P_STORE_B(BUF, BR)                                                                                         \
+    {                                                                                                                \
+        _Pragma("unroll") for (int p = 0; p < GPT; p++) * reinterpret_cast<intx4 *>(                                 \
+            &Bs[BUF][(p * PPP + bpix) * LDK + bgrp * 16]) = BR[p];                                                   \
+    }
+#define I8P_FRAG_B(BUF, Q, BF)                                                                                       \
+    {                                                                                                                \
+        _Pragma("unroll") for (int j = 0; j < TN; j++) BF[j] =                                                       \
+            *reinterpret_cast<const intx4 *>(&Bs[BUF][((wn * TN + j) * 32 + row) * LDK + (Q) * 32 + khalf]);        \
+    }
+#define I8P_MMA(AX, Q, BF)                                                                                           \
+    _Pragma("unroll") for (int i = 0; i < TM; i++) _Pragma("unroll") for (int j = 0; j < TN; j++) acc[i][j] =        \
+        __builtin_amdgcn_mfma_i32_32x32x32_i8(AX[i][Q], BF[j], acc[i][j], 0, 0, 0);
+#define I8P_COMPUTE(BUF, AX)                                                                                         \
+    {                                                                                                                \
+        intx4 fb0[TN], fb1[TN];                                                                                      \
+        I8P_FRAG_B(BUF, 0, fb0);                                                                                     \
+        _Pragma("unroll") for (int q = 0; q < K32; q += 2) {                                                         \
+            if (q + 1 < K32) I8P_FRAG_B(BUF, q + 1, fb1);                                                            \
+            I8P_MMA(AX, q, fb0);                                                                                     \
+            if (q + 2 < K32) I8P_FRAG_B(BUF, q + 2, fb0);                                                            \
+            if (q + 1 < K32) { I8P_MMA(AX, q + 1, fb1); }                                                            \
+        }                                                                                                            \
+    }
+#define I8P_STEP(KT, BUF, AC, AN, BNX, BF)                                                                           \
+    {                                                                                                                \
+        I8P_LOAD_B(colp, (KT) + 2, BF);                                                                              \
+        I8P_LOAD_A(mt, (KT) + 1, AN);                                                                                \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8P_COMPUTE(BUF, AC);                                                                                        \
+        __builtin_amdgcn_sched_barrier(0);                                                                           \
+        I8P_STORE_B((BUF) ^ 1, BNX);                                                                                 \
+        __syncthreads();                                                                                             \
+    }
+
+    // the first tile's prologue loads
+    int mt = t % a.m_tiles, nt = t / a.m_tiles;
+    columns(nt, colp);
+    I8P_LOAD_B(colp, 0, br0);
+    I8P_LOAD_B(colp, 1, br1);
+    I8P_LOAD_A(mt, 0, a0);
+    if constexpr (Q8)
+        if (a.r8) q8_residual_load<BM, BN>(a, mt * BM, nt * BN, rr);
+    for (;;) {
+        i8_load_row_params<BM, Q8>(a, mt * BM, s_par);  // read after the loop's barriers
+        I8P_STORE_B(0, br0);
+        __syncthreads();
+        intx16 acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][j][r] = 0;
+        int kt = 0;
+        for (; kt + 1 < a.k_tiles; kt += 2) {
+            I8P_STEP(kt, 0, a0, a1, br1, br0);
+            I8P_STEP(kt + 1, 1, a1, a0, br0, br1);
+        }
+        if (kt < a.k_tiles) {
+            I8P_COMPUTE(0, a0);
+        }
+        // the next tile's prologue loads, in flight during this epilogue
+        const int tn = t + per;
+        const bool more = tn < t_end;
+        const int mt_n = more ? tn % a.m_tiles : mt, nt_n = more ? tn / a.m_tiles : nt;
+        uintx4 rr_n[RP];
+        if (more) {
+            int cp[GPT];
+            columns(nt_n, cp);
+#pragma unroll
+            for (int p = 0; p < GPT; p++) colp[p] = cp[p];
+            I8P_LOAD_B(cp, 0, br0);
+            I8P_LOAD_B(cp, 1, br1);
+            I8P_LOAD_A(mt_n, 0, a0);
+            if constexpr (Q8)
+                if (a.r8) q8_residual_load<BM, BN>(a, mt_n * BM, nt_n * BN, rr_n);
+        }
+        if constexpr (Q8)
+            q8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem, rr);
+        else
+            i8_epilogue<BM, BN, TM, TN>(acc, a, mt * BM, nt * BN, wm * TM * 32, wn * TN * 32, lane, s_par, smem);
+        if (!more) break;
+        t = tn;
+        mt = mt_n;
+        nt = nt_n;
+#pragma unroll
+        for (int k = 0; k < RP; k++) rr[k] = rr_n[k];
+        // every wave is past this tile's epilogue (its LDS staging and row
+        // constants) before the next tile writes them
+        __syncthreads();
+    }
+#undef I8P_STEP
+#undef I8P_COMPUTE
+#undef I8P_MMA
+#undef I8P_FRAG_B
+#undef I8P_STORE_B
+#undef I8P_LOAD_B
+#undef I8P_LOAD_A
 }
 
 // Sums the int32 split-K partials (exact in any order), then dequantizes or
@@ -909,19 +1121,19 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
             // output int8 tensor (one byte per output)
 #pragma unroll
             for (int e = 0; e < VEC; e++) {
-                const int img = (n + e) / OHW;
+                const int img = div_fast(n + e, q.ohw_m, q.ohw_s);
                 const int sp = n + e - img * OHW;
                 if (raw) {
                     raw[(static_cast<size_t>(img) * M + m) * OHW + sp] = v[e] + q.qrow[m];
                     continue;
                 }
-                const int oh = sp / q.OW, ow = sp - (sp / q.OW) * q.OW;
+                const int oh = div_fast(sp, q.ow_m, q.ow_s), ow = sp - oh * q.OW;
                 const int rd = q.r8 ? static_cast<int>(q.r8[(static_cast<size_t>(img * q.r_Hp + oh + q.r_pt) * q.r_Wp +
                                                              ow + q.r_pl) * q.r_Cp + m]) - q.r_zp
                                     : 0;
                 q.q_out[(static_cast<size_t>(img * q.q_Hp + oh + q.q_pt) * q.q_Wp + ow + q.q_pl) * q.q_Cp + m] =
                     static_cast<int8_t>(q8_requant(v[e], q.qrow[M + m], q.qrow[2 * M + m], q.qrow[3 * M + m],
-                                                   q.qrow[4 * M + m], rd, q.y_zp, act == 1));
+                                                   q.qrow[4 * M + m], rd, q.y_zp, act == 1 ? q.y_zp : -128));
             }
             continue;
         }
@@ -929,7 +1141,7 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
         const float bm = bias ? bias[m] : 0.0f;
 #pragma unroll
         for (int e = 0; e < VEC; e++) {
-            const int img = (n + e) / OHW;
+            const int img = div_fast(n + e, q.ohw_m, q.ohw_s);
             const int sp = n + e - img * OHW;
             const size_t yi = (static_cast<size_t>(img) * M + m) * OHW + sp;
             if (raw) {
@@ -940,7 +1152,7 @@ __global__ void __launch_bounds__(256) splitk_i8_epilogue(const int32_t *__restr
             if (res) f += res[yi];
             f = apply_act(f, act);
             if (q.q_out) {
-                const int oh = sp / q.OW, ow = sp - (sp / q.OW) * q.OW;
+                const int oh = div_fast(sp, q.ow_m, q.ow_s), ow = sp - oh * q.OW;
                 q.q_out[(static_cast<size_t>(img * q.q_Hp + oh + q.q_pt) * q.q_Wp + ow + q.q_pl) * q.q_Cp + m] =
                     static_cast<int8_t>(quantize_one(f, q.q_inv, m * OHW + sp < q.q_split));
             }
@@ -954,7 +1166,8 @@ using I8Kernel = void (*)(I8Args);
 struct I8Cfg {
     int BM, BN, BK;
     int bmap;     // B gather lane map (see conv_igemm_i8)
-    int adirect;  // 1: conv_igemm_i8x, weights packed in MFMA fragment order and loaded straight to registers
+    int adirect;  // 1: conv_igemm_i8x / i8p, weights packed in MFMA fragment order and loaded straight to registers
+    int persist;  // 1: conv_igemm_i8p, a resident grid walking the tiles (no split-K)
     const char *name;
     I8Kernel kernel;     // reference semantics (i8_epilogue)
     I8Kernel kernel_q8;  // the INT8 configuration (q8_epilogue)
@@ -962,12 +1175,16 @@ struct I8Cfg {
 
 // New configurations go at the end: the tune tables store indices.
 #define I8CFG(BM, BN, BK) \
-    {BM, BN, BK, 0, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0, 0>, conv_igemm_i8<BM, BN, BK, 0, 1>}
-#define I8CFGP(BM, BN, BK) \
-    {BM, BN, BK, 1, 0, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1, 0>, conv_igemm_i8<BM, BN, BK, 1, 1>}
+    {BM, BN, BK, 0, 0, 0, #BM "x" #BN "x" #BK, conv_igemm_i8<BM, BN, BK, 0, 0>, conv_igemm_i8<BM, BN, BK, 0, 1>}
+#define I8CFGP(BM, BN, BK)                                                                                          \
+    {BM, BN, BK, 1, 0, 0, #BM "x" #BN "x" #BK ",px", conv_igemm_i8<BM, BN, BK, 1, 0>,                             \
+     conv_igemm_i8<BM, BN, BK, 1, 1>}
 #define I8CFGX(BM, BN, BK, WM, WN)                                                                                  \
-    {BM, BN, BK, 1, 1, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN, conv_igemm_i8x<BM, BN, BK, WM, WN, 0>,             \
+    {BM, BN, BK, 1, 1, 0, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN, conv_igemm_i8x<BM, BN, BK, WM, WN, 0>,          \
      conv_igemm_i8x<BM, BN, BK, WM, WN, 1>}
+#define I8CFGR(BM, BN, BK, WM, WN)                                                                                  \
+    {BM, BN, BK, 1, 1, 1, #BM "x" #BN "x" #BK ",ax" #WM "x" #WN ",persist", conv_igemm_i8p<BM, BN, BK, WM, WN, 0>, \
+     conv_igemm_i8p<BM, BN, BK, WM, WN, 1>}
 const I8Cfg kI8Cfgs[] = {
     I8CFG(128, 128, 64),  I8CFG(128, 128, 128),  I8CFG(128, 64, 64),  I8CFG(128, 64, 128),
     I8CFG(64, 128, 64),   I8CFG(64, 64, 64),     I8CFG(64, 64, 128),
@@ -976,10 +1193,14 @@ const I8Cfg kI8Cfgs[] = {
     I8CFGX(128, 128, 128, 2, 2), I8CFGX(128, 64, 128, 2, 2), I8CFGX(64, 128, 128, 2, 2),
     I8CFGX(64, 64, 128, 2, 2),   I8CFGX(128, 128, 64, 2, 2),  I8CFGX(128, 64, 64, 2, 2),
     I8CFGX(64, 64, 64, 2, 2),    I8CFGX(256, 64, 64, 4, 1),   I8CFGX(256, 64, 128, 4, 1),
+    I8CFGR(64, 64, 64, 2, 2),    I8CFGR(128, 64, 64, 2, 2),   I8CFGR(64, 128, 64, 2, 2),
+    I8CFGR(128, 128, 64, 2, 2),  I8CFGR(64, 64, 128, 2, 2),   I8CFGR(128, 64, 128, 2, 2),
+    I8CFGR(256, 64, 64, 4, 1),   I8CFGR(256, 64, 128, 4, 1),
 };
 #undef I8CFG
 #undef I8CFGP
 #undef I8CFGX
+#undef I8CFGR
 constexpr int kNumI8Cfgs = sizeof(kI8Cfgs) / sizeof(kI8Cfgs[0]);
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -1121,6 +1342,14 @@ size_t i8_partial_bytes(const I8Counts &tc, int M, int Ntot) {
     return tc.splitk > 1 ? static_cast<size_t>(tc.splitk) * M * Ntot * sizeof(int32_t) : 0;
 }
 
+// (m, s) of div_fast for divisor d >= 1 (dividends below 2^31)
+void div_magic(unsigned d, unsigned *m, int *s) {
+    int l = 0;
+    while ((uint64_t(1) << l) < d) l++;
+    *s = 31 + l;
+    *m = static_cast<unsigned>(((uint64_t(1) << *s) + d - 1) / d);
+}
+
 void fill_i8_args(I8Args &a, const ConvGeom &g, const I8Layout &L, const I8Counts &tc) {
     a.x_bytes = static_cast<int>(static_cast<size_t>(g.N) * L.Hp * L.Wp * L.Cp);
     a.y_bytes = static_cast<int>(g.y_elems * 4);
@@ -1131,6 +1360,8 @@ void fill_i8_args(I8Args &a, const ConvGeom &g, const I8Layout &L, const I8Count
     a.OW = g.OW;
     a.OHW = g.OH * g.OW;
     a.Ntot = g.N * a.OHW;
+    div_magic(static_cast<unsigned>(a.OHW), &a.ohw_m, &a.ohw_s);
+    div_magic(static_cast<unsigned>(a.OW), &a.ow_m, &a.ow_s);
     a.sh = g.sh;
     a.sw = g.sw;
     a.m_tiles = tc.m_tiles;
@@ -1140,6 +1371,31 @@ void fill_i8_args(I8Args &a, const ConvGeom &g, const I8Layout &L, const I8Count
 }
 
 // Launches the GEMM (and the split-K epilogue) of configuration c.
+// Workgroups of a persistent kernel: as many as the GPU holds at once (the
+// occupancy calculator's figure per CU times the CUs), a multiple of 8 (one
+// share per XCD), and no more than the tiles need.
+unsigned persistent_grid(I8Kernel kern, int tiles) {
+    static std::mutex mu;
+    static std::map<I8Kernel, int> per_cu;
+    int occ = 0;
+    {
+        std::lock_guard<std::mutex> lk(mu);
+        auto it = per_cu.find(kern);
+        if (it == per_cu.end()) {
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, 256, 0) != hipSuccess || occ < 1) {
+                (void)hipGetLastError();
+                occ = 1;
+            }
+            per_cu[kern] = occ;
+        } else {
+            occ = it->second;
+        }
+    }
+    const long resident = static_cast<long>(cu_count()) * occ;
+    const long need = (static_cast<long>(tiles) + 7) / 8 * 8;
+    return static_cast<unsigned>(std::max(8L, std::min(resident / 8 * 8, need)));
+}
+
 int launch_i8(hipStream_t st, int c, const I8Counts &tc, I8Args a, int32_t *part, int32_t *raw) {
     const bool split = tc.splitk > 1;
     if (split) {
@@ -1153,8 +1409,13 @@ int launch_i8(hipStream_t st, int c, const I8Counts &tc, I8Args a, int32_t *part
     } else {
         a.mode = 0;
     }
+    const I8Kernel kern = a.q8 ? kI8Cfgs[c].kernel_q8 : kI8Cfgs[c].kernel;
     dim3 grid(static_cast<unsigned>(tc.m_tiles * tc.n_tiles), static_cast<unsigned>(tc.splitk));
-    (a.q8 ? kI8Cfgs[c].kernel_q8 : kI8Cfgs[c].kernel)<<<grid, dim3(256), 0, st>>>(a);
+    if (kI8Cfgs[c].persist) {
+        if (split) return SPKV2_E_UNSUPPORTED;  // the persistent kernels take whole tiles
+        grid = dim3(persistent_grid(kern, tc.m_tiles * tc.n_tiles), 1);
+    }
+    kern<<<grid, dim3(256), 0, st>>>(a);
     if (int rc = launch_status("conv_igemm_i8")) return rc;
     if (split) {
         const size_t total = static_cast<size_t>(a.M) * a.Ntot;
@@ -1220,6 +1481,7 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
         if (!i8_cfg_fits(L, c)) continue;
         int last = -1;
         for (int s : kI8Splits) {
+            if (s > 1 && kI8Cfgs[c].persist) break;  // whole tiles only
             const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
             if (tc.splitk == last) continue;
             if (s > 1 && tc.kt_per_split < 2) break;
@@ -1263,8 +1525,8 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     if (qrow) {
         std::vector<int> rows(static_cast<size_t>(5) * g.M, 0);
         for (int m = 0; m < g.M; m++) {
-            rows[2 * g.M + m] = 1 << 30;  // m1: multiplier 1/2 at shift 31
-            rows[4 * g.M + m] = 31;
+            rows[2 * g.M + m] = 1 << 30;  // m1: multiplier 2^-10 at shift 40 (the high-word path)
+            rows[4 * g.M + m] = 40;
         }
         if (hipMemcpy(qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
             (void)hipGetLastError();
@@ -1303,6 +1565,7 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
         a.y = y;
         if (q8) {
             a.q8 = 1;
+            a.q8_hi = 1;
             a.qrow = qrow;
             a.scales = nullptr;
             a.bias = nullptr;
@@ -1527,7 +1790,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
         double best = 1e300;
         for (int c = 0; c < kNumI8Cfgs; c++)
             for (int s : kI8Splits) {
-                if (!i8_cfg_fits(L, c)) break;
+                if (!i8_cfg_fits(L, c) || (s > 1 && kI8Cfgs[c].persist)) break;
                 const I8Counts tc = i8_counts(c, g.M, Ntot, Kbytes, s);
                 if (s > 1 && tc.kt_per_split < 2) break;
                 const double m = i8_model_us(c, tc, g.M, Ntot);
@@ -1552,6 +1815,7 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
         const int s = atoi(e);
         if (s >= 1 && s <= 64) split = s;
     }
+    if (kI8Cfgs[cfg].persist) split = 1;  // the persistent kernels take whole tiles
     const I8Cfg &t = kI8Cfgs[cfg];
     const I8Counts tc = i8_counts(cfg, g.M, Ntot, Kbytes, split);
     plan->cfg = cfg;
@@ -1609,11 +1873,19 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
             if (int rc = q8_params(ctx, node->inputs[3], &sr, &zr)) return rc;
         const float *bias = g.has_bias ? reinterpret_cast<const float *>(host_weight_data(ctx, node->inputs[2])) : nullptr;
         if (g.has_bias && (!bias || rec(ctx, node->inputs[2])->dtype != SPKV2_DTYPE_FP32)) return SPKV2_E_UNSUPPORTED;
+        // |acc + c| < 2^31 (the kernels add them in 32 bits): |sum w x| and
+        // |z_x sum w| are each below 2^14 K, |bias_q| <= 2^30
+        if (static_cast<int64_t>(g.C) * g.KH * g.KW > 32768) {
+            set_last_error_text("conv node " + std::to_string(node->id) + ": K above 32768 in the INT8 configuration");
+            return SPKV2_E_UNSUPPORTED;
+        }
         std::vector<int> rows;
         if (!q8_requant_rows(g, w, ws, plan->x_scale, zx, sy, sr, bias, rows)) {
             set_last_error_text("conv node " + std::to_string(node->id) + ": requantization shift out of range");
             return SPKV2_E_QUANT;
         }
+        plan->q8_hi = true;
+        for (int m = 0; m < g.M; m++) plan->q8_hi = plan->q8_hi && rows[4 * g.M + m] >= 33;
         if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->qrow), rows.size() * sizeof(int)), "hipMalloc"))
             return rc;
         if (int rc = hip_check(hipMemcpy(plan->qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice),
@@ -1679,6 +1951,7 @@ int conv_i8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, const ConvPlan *
     if (q8) {
         a.q8 = 1;
         a.qrow = plan->qrow;
+        a.q8_hi = plan->q8_hi ? 1 : 0;
         a.q_out = ty->buf;
         a.q_bytes = static_cast<int>(ty->bytes);
         a.q_Hp = ty->Hp;

@@ -10,6 +10,7 @@ times its candidates and appends its choice to the output file
 
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8 | --missing] [--no-int8]
     python -m spinnv2_amd.tune_table --int8-network [--b1 | --splitk] [table.tune]
+    python -m spinnv2_amd.tune_table --q8-network [--b1 | --splitk] [table.tune]
     python -m spinnv2_amd.tune_table --f32-network [--yolo] [--b1] [--thin | --rows96] [table.tune]
 
 With --missing every entry of the committed table is kept and only layer
@@ -32,7 +33,9 @@ its nodes beats the current one by more than 2%.  --f32-network does the
 same for ResNet-101 b=64 (with --yolo YOLOv10n b=16, with --b1 batch 1)
 over the fp32 tile configurations and schedules (F32_SWEEP, F32_SWEEP_B1),
 or with --thin / --rows96 over the thin or the 96-row tiles alone (F32_THIN,
-F32_ROWS96).
+F32_ROWS96).  --q8-network does it for the INT8 configuration with int8
+tensors between nodes (ResNet-50, keys ending in |q8) over every int8 tile
+configuration, the persistent ones included.
 """
 
 from __future__ import annotations
@@ -61,6 +64,9 @@ def networks(int8: bool = True):
             yield f"int8 resnet50 b={batch}", g, quantize_conv_weights(g) + act
     for batch in (16, 1):
         yield f"yolov10n b={batch}", models.yolo_v10n(batch), None
+    if int8:
+        for batch in (64, 1):
+            yield f"int8 configuration resnet50 b={batch}", *q8_resnet50(batch)
 
 
 def main() -> None:
@@ -86,7 +92,8 @@ def main() -> None:
 
     lib = load_library()
     for label, g, qp in networks(int8="--no-int8" not in sys.argv[1:]):
-        with Model(write_spk(g, "mi355x", quant_params=qp), lib=lib):
+        blob = qp if isinstance(qp, bytes) else write_spk(g, "mi355x", quant_params=qp)
+        with Model(blob, lib=lib):
             pass
         print(f"tuned {label}", flush=True)
     lines = {}
@@ -100,12 +107,26 @@ def main() -> None:
     print(f"{len(lines)} layer shapes -> {out}")
 
 
-def int8_key(g, n) -> str:
-    """The INT8 tuner's key of a conv node (conv_i8.hip, tune_i8)."""
+def int8_key(g, n, q8: bool = False) -> str:
+    """The INT8 tuner's key of a conv node (conv_i8.hip, tune_i8); q8: the
+    INT8 configuration with int8 tensors between nodes."""
     x, w, y = g.shape(n.inputs[0]), g.tensors[n.inputs[1]].shape, g.shape(n.outputs[0])
     st, dl = n.attrs.get("strides", [1, 1]), n.attrs.get("dilations", [1, 1])
     return (f"i8|{x[0]},{x[1]},{x[2]},{x[3]}|{w[0]},{w[2]},{w[3]},{y[2]},{y[3]},{st[0]},{st[1]},{dl[0]},{dl[1]}|"
-            f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}")
+            f"{1 if len(n.inputs) > 2 else 0},{1 if len(n.inputs) > 3 else 0},{_act(n)}" + ("|q8" if q8 else ""))
+
+
+def q8_resnet50(batch: int):
+    """INT8 ResNet-50 224x224 in the INT8 configuration with int8 tensors
+    between nodes, calibrated as bench.py does (16 seeded single-image
+    batches through the batch-1 fp32 graph): (graph, package)."""
+    from .spk import models, write_spk
+    from .spk.quantize import quantize_int8_activations
+
+    cal = models.resnet(50, 1)
+    samples = [models.make_input(cal.tensors[cal.inputs[0]].shape, 1000 + i) for i in range(16)]
+    g = models.resnet(50, batch)
+    return g, write_spk(g, "mi355x", quant_params=quantize_int8_activations(g, samples, calibrate_on=cal))
 
 
 def _padded_extent(g, n):
@@ -256,6 +277,20 @@ def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: st
             t = sum(r["times"][i] for i in nodes)
             if t < best:
                 best, pick = t, cand
+        if key not in current:
+            # not in the table yet (the live tuner ran for it): the best
+            # explicit candidate, so the choice becomes reproducible
+            best, pick = 1e300, None
+            for cand, r in runs.items():
+                if key in r["fell_back"]:
+                    continue
+                t = sum(r["times"][i] for i in nodes)
+                if t < best:
+                    best, pick = t, cand
+            if pick:
+                changed[key] = pick
+                print(f"{key}: new -> {pick} ({now:.1f} us with the live tuner, {best:.1f} us)")
+            continue
         if pick and tuple(map(int, pick.split())) != current.get(key) and best < 0.98 * now:
             changed[key] = pick
             print(f"{key}: {current.get(key)} -> {pick} ({now:.1f} -> {best:.1f} us over {len(nodes)} nodes)")
@@ -263,6 +298,8 @@ def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: st
     for line in table.read_text().splitlines():
         p = line.split()
         lines.append(f"{p[0]} {changed[p[0]]}" if p and p[0] in changed else line)
+    lines += [f"{k} {v}" for k, v in changed.items() if k not in current]
+    lines = sorted(set(lines), key=lambda l: l.split()[0] if l.split() else "")
     table.write_text("".join(l + "\n" for l in lines))
     print(f"{label}: {len(changed)} entries changed -> {table}")
 
@@ -284,6 +321,20 @@ def int8_network(table: Path, batch: int = 64) -> None:
         network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (2, 3, 4)], table, "int8 resnet50 b=64")
     else:
         network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
+
+
+def q8_network(table: Path, batch: int = 64) -> None:
+    """In-network sweep of the INT8 configuration's layers (keys ending in
+    |q8): every int8 tile configuration, whole tiles (and at batch 1 with
+    split-K)."""
+    g, blob = q8_resnet50(batch)
+    keys = {n.id: int8_key(g, n, q8=True) for n in g.nodes if n.op_type == "Conv"}
+    if batch == 1:
+        cands = [(c, s) for c in range(31) for s in (1, 2, 3, 4, 6, 8, 12, 16) if s == 1 or c < 23]
+    else:
+        cands = [(c, 1) for c in range(31)] + ([(c, s) for c in range(23) for s in (2, 3, 4)]
+                                               if "--splitk" in sys.argv[1:] else [])
+    network_sweep(g, blob, keys, cands, table, f"int8 configuration resnet50 b={batch}")
 
 
 # fp32 candidates: every configuration but the skinny ones (batch-1 tiles)
@@ -322,10 +373,12 @@ def f32_network(table: Path, net: str = "resnet101", thin: bool = False, rows96:
 if __name__ == "__main__":
     if len(sys.argv) == 5 and sys.argv[1] == "--sweep-child":
         _sweep_child(sys.argv[2], sys.argv[3], sys.argv[4])
-    elif "--int8-network" in sys.argv[1:] or "--f32-network" in sys.argv[1:]:
+    elif any(f in sys.argv[1:] for f in ("--int8-network", "--f32-network", "--q8-network")):
         rest = [a for a in sys.argv[1:] if not a.startswith("--")]
         table = Path(rest[0]) if rest else DEFAULT_OUT
-        if "--int8-network" in sys.argv[1:]:
+        if "--q8-network" in sys.argv[1:]:
+            q8_network(table, 1 if "--b1" in sys.argv[1:] else 64)
+        elif "--int8-network" in sys.argv[1:]:
             int8_network(table, 1 if "--b1" in sys.argv[1:] else 64)
         else:
             yolo, b1 = "--yolo" in sys.argv[1:], "--b1" in sys.argv[1:]

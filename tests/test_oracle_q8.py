@@ -286,3 +286,52 @@ def test_q8_package_records_and_loader():
     ctx = ct.c_void_p()
     assert lib.spkv2_load_memory(buf, len(blob), ct.byref(ctx)) == 0
     lib.spkv2_free(ctx)
+
+
+def test_device_requant_math_equals_oracle(tmp_path, lib):
+    """spinnv2_amd/csrc/kernels/q8_math.hpp (the device epilogue's
+    requantization, built here for the host with g++): the general form and
+    the high-word form (shift >= 33) equal the oracle's single rounding on
+    random values and on constructed ties of both signs, where the high-word
+    form's borrow rule decides."""
+    import subprocess
+    from pathlib import Path
+
+    hdr = Path(__file__).resolve().parent.parent / "spinnv2_amd" / "csrc" / "kernels"
+    src = tmp_path / "shim.cpp"
+    src.write_text('#include "q8_math.hpp"\n'
+                   'extern "C" int rq(int a, int c, int m1, int m2, int sh, int rd, int zy, int lo) '
+                   '{ return spk::kern::q8_requant(a, c, m1, m2, sh, rd, zy, lo); }\n'
+                   'extern "C" int rq_hi(int a, int c, int m1, int m2, int k, int rd, int zy, int lo) '
+                   '{ return spk::kern::q8_requant_hi(a, c, m1, m2, k, rd, zy, lo); }\n')
+    so = tmp_path / "shim.so"
+    subprocess.run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", f"-I{hdr}", str(src), "-o", str(so)], check=True)
+    shim = ctypes.CDLL(str(so))
+    for f in (shim.rq, shim.rq_hi):
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_int] * 8
+    rng = np.random.default_rng(21)
+    cases = []
+    for _ in range(20000):
+        S = int(rng.integers(33, 60))
+        cases.append((int(rng.integers(-(1 << 27), 1 << 27)), int(rng.integers(-(1 << 29), 1 << 29)),
+                      int(rng.integers(1 << 29, 1 << 31)), int(rng.integers(0, 1 << 31)), S,
+                      int(rng.integers(-255, 256)), int(rng.integers(-128, 128)), int(rng.integers(0, 2))))
+    # ties: t = (2j + 1) 2^(S-1) exactly, both signs, with and without a low word
+    for S in (33, 34, 40, 47):
+        for j in (0, 1, 5, 100):
+            for sign in (1, -1):
+                # m1 = 2^(S-1-e) times an odd A gives t = A 2^(S-1-e); choose A = (2j+1) 2^e
+                m1 = 1 << 30
+                e = S - 1 - 30
+                if e < 0:
+                    continue
+                A = sign * (2 * j + 1) * (1 << e)
+                cases.append((A, 0, m1, 0, S, 0, 0, 0))
+                cases.append((A + sign, 0, m1, 0, S, 0, 0, 0))  # just past the tie
+                cases.append((A - sign, 0, m1, 0, S, 0, 0, 0))  # just before it
+    for acc, c, m1, m2, S, rd, zy, relu in cases:
+        lo = zy if relu else -128
+        want = lib.oracle_q8_requant_one(acc, c, m1, m2, S, rd, zy, relu)
+        assert shim.rq(acc, c, m1, m2, S, rd, zy, lo) == want, (acc, c, m1, m2, S, rd, zy, relu)
+        assert shim.rq_hi(acc, c, m1, m2, S - 32, rd, zy, lo) == want, (acc, c, m1, m2, S, rd, zy, relu)
