@@ -68,9 +68,10 @@ struct ConvPlan {
     bool padded;         // fp32 path: the input is copied into a padded workspace buffer first
     size_t pad_bytes;    // fp32 path: workspace bytes of that padded copy
     float *scales;       // device, int8 path: w_scale[m] * x_scale
-    // device, CONV_Q8: per output channel, five int32 rows of M:
-    // -z_x * sum(w[m]), that plus bias_q[m], the multipliers m1[m], m2[m]
-    // and the shift (requantization constants computed at prepare)
+    // device, CONV_Q8: per output channel, seven int32 rows of M:
+    // -z_x * sum(w[m]), that plus bias_q[m], the multipliers m1[m], m2[m],
+    // the shift S, and 2^(S-33), S - 32 (requantization constants computed
+    // at prepare)
     int *qrow;
     int x_zp;            // CONV_Q8: the input's zero point
     bool q8_hi;          // CONV_Q8: every row's shift is at least 33 (the 32-bit rounding tail)

@@ -252,7 +252,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8(I8Args a) {
     constexpr int OPS = 2 * (BM + BN) * LDK;
     constexpr int SMEM = OPS > i8_stage_bytes(BM, BN) ? OPS : i8_stage_bytes(BM, BN);
     __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
-    __shared__ float s_par[4 * BM];  // per-row epilogue constants
+    __shared__ float s_par[5 * BM];  // per-row epilogue constants
     int8_t(*As)[BM * LDK] = reinterpret_cast<int8_t(*)[BM * LDK]>(smem);
     int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem + 2 * BM * LDK);
 
@@ -411,11 +411,16 @@ constexpr int i8_stage_bytes(int BM, int BN) { return BN * (BM + 16); }
 template <int BM, int Q8>
 __device__ __forceinline__ void i8_load_row_params(const I8Args &a, int mt0, float *s_par) {
     if constexpr (Q8) {
+        // [BM][4] (c, m1, m2, S or with q8_hi 2^(S-33)), then [BM] S - 32
         int *s_i = reinterpret_cast<int *>(s_par);
         for (int i = threadIdx.x; i < BM; i += 256) {
             const int m = mt0 + i;
-#pragma unroll
-            for (int r = 0; r < 4; r++) s_i[4 * i + r] = m < a.M ? a.qrow[(r + 1) * a.M + m] : (r == 3 ? 33 : 0);
+            const bool in = m < a.M;
+            s_i[4 * i] = in ? a.qrow[a.M + m] : 0;
+            s_i[4 * i + 1] = in ? a.qrow[2 * a.M + m] : 0;
+            s_i[4 * i + 2] = in ? a.qrow[3 * a.M + m] : 0;
+            s_i[4 * i + 3] = in ? a.qrow[(a.q8_hi ? 5 : 4) * a.M + m] : (a.q8_hi ? 1 : 33);
+            s_i[4 * BM + i] = in ? a.qrow[6 * a.M + m] : 1;
         }
         return;
     }
@@ -653,6 +658,63 @@ __device__ __forceinline__ void q8_residual_load(const I8Args &a, int mt0, int n
     }
 }
 
+// clamp(v, lo) to [lo, 127] (lo <= 127) in one instruction: the median of
+// v, lo and 127
+__device__ __forceinline__ int med3_127(int v, int lo) {
+    int r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "v"(lo), "v"(127));
+    return r;
+}
+
+// The requantization of one wave's TM x TN accumulator blocks in the LDS
+// staging area ([pixel][BM + 16 bytes]): each lane's four consecutive
+// channels of a pixel are one dword there, holding the residual's bytes on
+// entry (RES) and the int8 outputs on exit.  HI: every row's shift is at
+// least 33 (q8_requant_hi).  Rows past M get z_y.
+template <int BM, int TM, int TN, bool HI, bool RES>
+__device__ __forceinline__ void q8_requant_tile(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int wmo, int wno,
+                                                int lane, const float *s_par, int8_t *s_q) {
+    constexpr int SQ = BM + 16;
+    const int row = lane & 31;
+    const int rsub = 4 * (lane >> 5);
+    const intx4 *s_row = reinterpret_cast<const intx4 *>(s_par);
+    const int *s_k = reinterpret_cast<const int *>(s_par) + 4 * BM;
+    const int lo = a.act == 1 ? a.y_zp : -128;  // Relu clamps at the zero point
+    const int zy = a.y_zp, zr = a.r_zp;
+    (void)mt0;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            // rows ml .. ml + 3 of the tile: four consecutive channels (rows
+            // past M compute from zero constants; the channels they land in
+            // are never read)
+            const int ml = wmo + i * 32 + rsub + 8 * q4;
+            intx4 p[4];
+            int k[4];
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                p[b] = s_row[ml + b];
+                if (HI) k[b] = s_k[ml + b];
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                unsigned *cell = reinterpret_cast<unsigned *>(&s_q[(wno + j * 32 + row) * SQ + ml]);
+                const unsigned rw = RES ? *cell : 0u;
+                unsigned word = 0;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const int rd = RES ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - zr : 0;
+                    const int x = acc[i][j][4 * q4 + b];
+                    const int qv = HI ? q8_requant_hi(x, p[b][0], p[b][1], p[b][2], p[b][3], k[b], rd, lo, med3_127)
+                                      : q8_requant(x, p[b][0], p[b][1], p[b][2], p[b][3], rd, zy, lo);
+                    word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
+                }
+                *cell = word;
+            }
+        }
+}
+
 template <int BM, int BN, int TM, int TN>
 __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args &a, int mt0, int nt0, int wmo, int wno,
                                             int lane, const float *s_par, int8_t *s_q,
@@ -707,35 +769,15 @@ __device__ __forceinline__ void q8_epilogue(intx16 (&acc)[TM][TN], const I8Args 
         }
         __syncthreads();
     }
-    const intx4 *s_row = reinterpret_cast<const intx4 *>(s_par);
-    const int lo = a.act == 1 ? a.y_zp : -128;  // Relu clamps at the zero point
-    const bool hi_only = a.q8_hi != 0;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int q4 = 0; q4 < 4; q4++) {
-            // rows ml .. ml + 3 of the tile: four consecutive channels
-            const int ml = wmo + i * 32 + static_cast<int>(rsub) + 8 * q4;
-            intx4 p[4];
-#pragma unroll
-            for (int b = 0; b < 4; b++) p[b] = s_row[ml + b];
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                unsigned *cell = reinterpret_cast<unsigned *>(&s_q[(wno + j * 32 + row) * SQ + ml]);
-                const unsigned rw = a.r8 ? *cell : 0u;
-                unsigned word = 0;
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const int rd = a.r8 ? static_cast<int>(static_cast<int8_t>(rw >> (8 * b))) - a.r_zp : 0;
-                    const int x = acc[i][j][4 * q4 + b];
-                    int qv = hi_only ? q8_requant_hi(x, p[b][0], p[b][1], p[b][2], p[b][3] - 32, rd, a.y_zp, lo)
-                                     : q8_requant(x, p[b][0], p[b][1], p[b][2], p[b][3], rd, a.y_zp, lo);
-                    if (static_cast<unsigned>(m0 - wmo + ml + b) >= M) qv = a.y_zp;
-                    word |= (static_cast<unsigned>(qv) & 0xffu) << (8 * b);
-                }
-                *cell = word;
-            }
-        }
+    // one copy of the loop per (shift form, residual) pair, chosen once per
+    // tile, so no per-element branch remains
+    if (a.q8_hi) {
+        if (a.r8) q8_requant_tile<BM, TM, TN, true, true>(acc, a, m0 - wmo, wmo, wno, lane, s_par, s_q);
+        else q8_requant_tile<BM, TM, TN, true, false>(acc, a, m0 - wmo, wmo, wno, lane, s_par, s_q);
+    } else {
+        if (a.r8) q8_requant_tile<BM, TM, TN, false, true>(acc, a, m0 - wmo, wmo, wno, lane, s_par, s_q);
+        else q8_requant_tile<BM, TM, TN, false, false>(acc, a, m0 - wmo, wmo, wno, lane, s_par, s_q);
+    }
     __syncthreads();
     // 16-byte pieces of the staged tile, the BM/16 pieces of one pixel on
     // consecutive threads; a piece is stored when its first channel is below
@@ -777,7 +819,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8x(I8Args a) {
     // the operand buffers, reused by the epilogue's staging area
     constexpr int SMEM = 2 * BN * LDK > i8_stage_bytes(BM, BN) ? 2 * BN * LDK : i8_stage_bytes(BM, BN);
     __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
-    __shared__ float s_par[4 * BM];  // per-row epilogue constants
+    __shared__ float s_par[5 * BM];  // per-row epilogue constants
     int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem);
 
     const int tid = threadIdx.x;
@@ -931,7 +973,7 @@ __global__ void __launch_bounds__(256) conv_igemm_i8p(I8Args a) {
     static_assert(GPT >= 1 && BN % PPP == 0 && (LDK / 16) % 2 == 1, "B gather shape");
     constexpr int SMEM = 2 * BN * LDK > i8_stage_bytes(BM, BN) ? 2 * BN * LDK : i8_stage_bytes(BM, BN);
     __shared__ __attribute__((aligned(16))) int8_t smem[SMEM];
-    __shared__ float s_par[4 * BM];
+    __shared__ float s_par[5 * BM];
     int8_t(*Bs)[BN * LDK] = reinterpret_cast<int8_t(*)[BN * LDK]>(smem);
 
     const int tid = threadIdx.x;
@@ -1520,13 +1562,15 @@ bool tune_i8(hipStream_t st, const ConvGeom &g, const I8Layout &L, int *cfg_out,
     const size_t q_bytes = static_cast<size_t>(g.N) * g.OH * g.OW * q_Cp;
     int8_t *q_out = q8 ? static_cast<int8_t *>(db.get(q_bytes)) : nullptr;
     int8_t *q_res = q8 && g.has_res ? static_cast<int8_t *>(db.get(q_bytes)) : nullptr;
-    int *qrow = q8 ? static_cast<int *>(db.get(static_cast<size_t>(5) * g.M * sizeof(int))) : nullptr;
+    int *qrow = q8 ? static_cast<int *>(db.get(static_cast<size_t>(7) * g.M * sizeof(int))) : nullptr;
     if (q8 && (!q_out || (g.has_res && !q_res) || !qrow)) return false;
     if (qrow) {
-        std::vector<int> rows(static_cast<size_t>(5) * g.M, 0);
+        std::vector<int> rows(static_cast<size_t>(7) * g.M, 0);
         for (int m = 0; m < g.M; m++) {
             rows[2 * g.M + m] = 1 << 30;  // m1: multiplier 2^-10 at shift 40 (the high-word path)
             rows[4 * g.M + m] = 40;
+            rows[5 * g.M + m] = 1 << 7;
+            rows[6 * g.M + m] = 8;
         }
         if (hipMemcpy(qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
             (void)hipGetLastError();
@@ -1703,12 +1747,13 @@ static int setup_handoff(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPla
 // (s_x s_w)) clamped to +-2^30; m1 ~ (s_x s_w / s_y) 2^S and m2 ~ (s_r /
 // s_y) 2^S with S = 31 - e for max(ratio) = f 2^e, f in [0.5, 1), one less
 // if a multiplier rounds to 2^31.  Rows of qrow: -z_x sum(w), that plus
-// bias_q, m1, m2, S.  False when a shift leaves [1, 62].
-bool q8_requant_rows(const ConvGeom &g, const int8_t *w, const float *ws, float sx, int zx, float sy, float sr,
-                     const float *bias, std::vector<int> &rows) {
+// bias_q, m1, m2, S, and for q8_requant_hi 2^(S-33) and S - 32.  False when
+// a shift leaves [1, 62].
+bool q8_requant_rows(const ConvGeom &g, const int8_t *w, const float *ws, float sx, int zx, float sy, int zy,
+                     float sr, const float *bias, std::vector<int> &rows) {
     const int M = g.M;
     const size_t K = static_cast<size_t>(g.C) * g.KH * g.KW;
-    rows.assign(static_cast<size_t>(5) * M, 0);
+    rows.assign(static_cast<size_t>(7) * M, 0);
     for (int m = 0; m < M; m++) {
         int64_t wsum = 0;
         for (size_t k = 0; k < K; k++) wsum += w[m * K + k];
@@ -1736,6 +1781,9 @@ bool q8_requant_rows(const ConvGeom &g, const int8_t *w, const float *ws, float 
         rows[2 * M + m] = static_cast<int>(a1);
         rows[3 * M + m] = static_cast<int>(a2);
         rows[4 * M + m] = sh;
+        // the high-word form's rounding constant with z_y folded in, and shift
+        rows[5 * M + m] = sh >= 33 && sh <= 55 ? (1 << (sh - 33)) + zy * (1 << (sh - 32)) : 0;
+        rows[6 * M + m] = sh - 32;
     }
     return true;
 }
@@ -1880,12 +1928,12 @@ int conv_i8_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, ConvPlan *pl
             return SPKV2_E_UNSUPPORTED;
         }
         std::vector<int> rows;
-        if (!q8_requant_rows(g, w, ws, plan->x_scale, zx, sy, sr, bias, rows)) {
+        if (!q8_requant_rows(g, w, ws, plan->x_scale, zx, sy, zy, sr, bias, rows)) {
             set_last_error_text("conv node " + std::to_string(node->id) + ": requantization shift out of range");
             return SPKV2_E_QUANT;
         }
         plan->q8_hi = true;
-        for (int m = 0; m < g.M; m++) plan->q8_hi = plan->q8_hi && rows[4 * g.M + m] >= 33;
+        for (int m = 0; m < g.M; m++) plan->q8_hi = plan->q8_hi && rows[4 * g.M + m] >= 33 && rows[4 * g.M + m] <= 55;
         if (int rc = hip_check(hipMalloc(reinterpret_cast<void **>(&plan->qrow), rows.size() * sizeof(int)), "hipMalloc"))
             return rc;
         if (int rc = hip_check(hipMemcpy(plan->qrow, rows.data(), rows.size() * sizeof(int), hipMemcpyHostToDevice),

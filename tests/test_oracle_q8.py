@@ -291,7 +291,8 @@ def test_q8_package_records_and_loader():
 def test_device_requant_math_equals_oracle(tmp_path, lib):
     """spinnv2_amd/csrc/kernels/q8_math.hpp (the device epilogue's
     requantization, built here for the host with g++): the general form and
-    the high-word form (shift >= 33) equal the oracle's single rounding on
+    the high-word form (shift 33..55, output zero point folded into the
+    rounding constant) equal the oracle's single rounding on
     random values and on constructed ties of both signs, where the high-word
     form's borrow rule decides."""
     import subprocess
@@ -303,7 +304,8 @@ def test_device_requant_math_equals_oracle(tmp_path, lib):
                    'extern "C" int rq(int a, int c, int m1, int m2, int sh, int rd, int zy, int lo) '
                    '{ return spk::kern::q8_requant(a, c, m1, m2, sh, rd, zy, lo); }\n'
                    'extern "C" int rq_hi(int a, int c, int m1, int m2, int k, int rd, int zy, int lo) '
-                   '{ return spk::kern::q8_requant_hi(a, c, m1, m2, k, rd, zy, lo); }\n')
+                   '{ return spk::kern::q8_requant_hi(a, c, m1, m2, (1 << (k - 1)) + zy * (1 << k), k, rd, lo, '
+                   'spk::kern::q8_clamp); }\n')
     so = tmp_path / "shim.so"
     subprocess.run(["g++", "-std=c++17", "-O2", "-shared", "-fPIC", f"-I{hdr}", str(src), "-o", str(so)], check=True)
     shim = ctypes.CDLL(str(so))
@@ -313,12 +315,12 @@ def test_device_requant_math_equals_oracle(tmp_path, lib):
     rng = np.random.default_rng(21)
     cases = []
     for _ in range(20000):
-        S = int(rng.integers(33, 60))
+        S = int(rng.integers(33, 56))
         cases.append((int(rng.integers(-(1 << 27), 1 << 27)), int(rng.integers(-(1 << 29), 1 << 29)),
                       int(rng.integers(1 << 29, 1 << 31)), int(rng.integers(0, 1 << 31)), S,
                       int(rng.integers(-255, 256)), int(rng.integers(-128, 128)), int(rng.integers(0, 2))))
     # ties: t = (2j + 1) 2^(S-1) exactly, both signs, with and without a low word
-    for S in (33, 34, 40, 47):
+    for S in (33, 34, 40, 47, 55):
         for j in (0, 1, 5, 100):
             for sign in (1, -1):
                 # m1 = 2^(S-1-e) times an odd A gives t = A 2^(S-1-e); choose A = (2j+1) 2^e
