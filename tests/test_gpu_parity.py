@@ -152,6 +152,8 @@ FLOAT_OPS = [
     ("Softmax", [4, 1000], dict(axis=-1)),
     ("Softmax", [2, 16, 50], dict(axis=1)),
     ("Softmax", [5, 2048], dict(axis=-1)),     # register-resident rows at their limit
+    ("Softmax", [4099, 1000], dict(axis=-1)),  # many rows
+    ("Softmax", [2048, 36], dict(axis=-1)),    # many short rows
     ("Softmax", [3, 2052], dict(axis=-1)),     # longer rows: three passes
     ("Softmax", [3, 6, 7], dict(axis=-1)),     # rows not a multiple of 4
     ("Softmax", [2, 16, 4, 300], dict(axis=1)),  # DFL-like: 16 strided bins in registers
@@ -1281,3 +1283,4 @@ def test_fp32_pad_handoff_with_other_readers(gpu, monkeypatch):
         np.testing.assert_array_equal(u, v)
     for u, v in zip(outs["1"], run_oracle(blob, xs)):
         assert tnorm_err(u, v) <= FP32_TOL
+
