@@ -4,6 +4,7 @@
            [--group NAME --include SUBSTR [--include ...] [--exclude SUBSTR ...]]
     python -m spinnv2_amd.rocprof_summary traffic --fetch <pmc.csv> --write <pmc.csv>
            --copy-fetch <pmc.csv> --copy-write <pmc.csv> --copy-bytes B --runs N --match conv_igemm
+           [--group NAME --include SUBSTR [--include ...] [--exclude SUBSTR ...]]
     python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
            [--mops SQ_INSTS_VALU_MFMA_MOPS_I8 --peak 5000]
 
@@ -13,8 +14,9 @@ spkv2_run calls the profiled command made (N), giving per-run kernel time;
 the --exclude substrings (e.g. every launch of the conv nodes: the GEMM,
 split-K epilogue and padding kernels, without the classifier Gemm's).
 `traffic` sums FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the
-kernels whose name contains --match, per run, and scales each counter by
-bytes / counter of a plain copy kernel of known size profiled the same way;
+kernels whose name contains --match (or the --group members), per run, and
+scales each counter by bytes / counter of a plain copy kernel of known size
+profiled the same way;
 per kernel it also gives the HBM GB/s those bytes make over the dispatches'
 own durations (timestamps of the FETCH_SIZE pass).
 `mfma` reads a --pmc pass of an MFMA work counter (--mops, default
@@ -99,7 +101,17 @@ def _copy_scale(path: str, copy_bytes: int) -> float:
     return copy_bytes / (sum(vals) / len(vals) * 1024.0)
 
 
+def _member(name: str, match: str | None, include: list[str], exclude: list[str]) -> bool:
+    """A kernel of the totalled set: any --include (and no --exclude) when
+    includes are given, else a name containing --match."""
+    n = short_name(name)
+    if include:
+        return any(s in n for s in include) and not any(s in n for s in exclude)
+    return bool(match) and match in name
+
+
 def traffic(args) -> str:
+    include, exclude = getattr(args, "include", None) or [], getattr(args, "exclude", None) or []
     fs = _copy_scale(args.copy_fetch, args.copy_bytes)
     ws = _copy_scale(args.copy_write, args.copy_bytes)
     fetch = _counter_per_kernel(args.fetch)
@@ -117,13 +129,16 @@ def traffic(args) -> str:
         gbps = (rd + wr) / ns if ns > 0 else 0.0
         out.append(f"{short_name(name)[:48]:48s} {fetch.get(name, [0])[0] / args.runs:8.1f} {rd / 1e6:12.1f} "
                    f"{wr / 1e6:12.1f} {gbps:9.0f}")
-        if args.match in name:
+        if _member(name, args.match, include, exclude):
             tot_r += rd
             tot_w += wr
             disp += fetch.get(name, [0])[0]
+    label = getattr(args, "group", None) or args.match
     out.append("")
-    out.append(f"result {args.match}_read_bytes_per_step = {tot_r:.0f}")
-    out.append(f"result {args.match}_write_bytes_per_step = {tot_w:.0f}")
+    if include:
+        out.append(f"group {label}: names containing any of {include}" + (f", none of {exclude}" if exclude else ""))
+    out.append(f"result {label}_read_bytes_per_step = {tot_r:.0f}")
+    out.append(f"result {label}_write_bytes_per_step = {tot_w:.0f}")
     out.append(f"result conv_hbm_bytes_per_step = {tot_r + tot_w:.0f}")
     out.append(f"result conv_dispatches_per_step = {disp / args.runs:.0f}")
     return "\n".join(out)
@@ -182,6 +197,9 @@ def main() -> None:
     t.add_argument("--copy-bytes", type=int, required=True)
     t.add_argument("--runs", type=int, required=True)
     t.add_argument("--match", default="conv_igemm")
+    t.add_argument("--group", default=None, help="label of the kernels totalled from --include / --exclude")
+    t.add_argument("--include", action="append", default=[], help="totalled: name contains this")
+    t.add_argument("--exclude", action="append", default=[], help="not totalled: name contains this")
     m = sub.add_parser("mfma")
     m.add_argument("csv")
     m.add_argument("--runs", type=int, required=True)

@@ -62,6 +62,28 @@ def test_traffic_copy_scaled(tmp_path):
     assert float(row[-1]) == pytest.approx(2500 * 1024 / 1000, rel=1e-3)
 
 
+def test_traffic_group_include_exclude(tmp_path):
+    """--group totals the --include kernels minus --exclude, under its own label."""
+    mib = 1 << 20
+    cf = _write(tmp_path / "cf.csv", PMC_COLS, [[1, "copy_kernel(float*)", "FETCH_SIZE", 2048, 0, 1000]])
+    cw = _write(tmp_path / "cw.csv", PMC_COLS, [[1, "copy_kernel(float*)", "WRITE_SIZE", 4096, 0, 1000]])
+    names = ["void spk::kern::conv_igemm_i8<64>(A)", "spk::kern::quantize_pad_nhwc_narrow(float const*)",
+             "void spk::kern::conv_igemm_f32<64, 64, 16, 2, 2, 1>(B)"]
+    f = _write(tmp_path / "f.csv", PMC_COLS, [[i + 1, n, "FETCH_SIZE", 100 * (i + 1), 0, 1000]
+                                             for i, n in enumerate(names)])
+    w = _write(tmp_path / "w.csv", PMC_COLS, [[i + 1, n, "WRITE_SIZE", 10 * (i + 1), 0, 1000]
+                                             for i, n in enumerate(names)])
+    args = SimpleNamespace(fetch=f, write=w, copy_fetch=cf, copy_write=cw, copy_bytes=4 * mib, runs=1,
+                           match="conv_igemm", group="q8", include=["conv_igemm", "quantize_pad"],
+                           exclude=["conv_igemm_f32"])
+    out = rs.traffic(args)
+    # members: the int8 conv (100 KiB x2 read, 10 KiB written) and the quantize pass (200 x2, 20)
+    assert _result(out, "q8_read_bytes_per_step") == pytest.approx(600 * 1024)
+    assert _result(out, "q8_write_bytes_per_step") == pytest.approx(30 * 1024)
+    assert _result(out, "conv_hbm_bytes_per_step") == pytest.approx(630 * 1024)
+    assert _result(out, "conv_dispatches_per_step") == 2
+
+
 def test_mfma_work_and_busy(tmp_path):
     rows = []
     # two dispatches of 100 us; each counts 1e6 MOPS (x512 FLOP); GUI_ACTIVE sums 8 XCDs
