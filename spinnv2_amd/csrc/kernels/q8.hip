@@ -7,7 +7,7 @@
 // The reference runtime has no such mode; the package marks the tensors
 // (dtype int8, role activation) and carries each one's per-tensor scale and
 // zero point in its quantization section (the record's zero-point array,
-// reference runtime/include/spkv2_format.h:205-213).  Semantics:
+// reference runtime/include/spkv2_format.h:211-226).  Semantics:
 //   MaxPool: the maximum of the in-bounds taps, input and output sharing one
 //            scale and zero point;
 //   ReduceMean over H, W / GlobalAveragePool: y = (float)((double)sum(q - z)
