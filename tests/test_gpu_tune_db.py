@@ -10,6 +10,7 @@ import subprocess
 import sys
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
@@ -92,3 +93,73 @@ def test_tune_db_reuses_hybrid_choice(gpu, tmp_path):
     assert ",dp=" in second["name"], second
     assert abs(second["sum"] - first["sum"]) <= 1e-4 * first["sum"]
     assert db.read_text() == f"{key} {cfg} 1004\n"  # a hit stores nothing new
+
+
+# entries of conv_f32.hip's tile table that run the implicit-GEMM kernel
+# (64- and 128-row tiles, BK 16 to 128, the 32- and 96-row tiles); the
+# skinny (12, 13) and thin (17, 18) kernels sum in orders of their own
+IGEMM_CFGS = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16, 19, 20]
+
+
+def test_igemm_tiles_share_one_summation_order(gpu, monkeypatch):
+    """The deterministic tuner's premise: every implicit-GEMM tile shape
+    gives the same fp32 bits for the same split-K cut (k = 1024: one slice,
+    or four slices of 256 k, as 16 k-tiles of 16, 8 of 32 or 4 of 64), so
+    timing may choose among them freely."""
+    from spinnv2_amd.runtime import Model
+    from spinnv2_amd.spk import models, write_spk
+
+    from .helpers import rng_inputs
+
+    g = models.single_conv(2, 1024, 14, 14, 96, 1, act=None, residual=True)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    monkeypatch.setenv("SPKV2_CONV_TUNE", "0")
+    for split, cfgs in ((1, IGEMM_CFGS), (4, [6, 7, 8])):
+        outs = []
+        for c in cfgs:
+            monkeypatch.setenv("SPKV2_CONV_CFG", str(c))
+            monkeypatch.setenv("SPKV2_CONV_SPLITK", str(split))
+            with Model(blob) as m:
+                for i, x in enumerate(xs):
+                    m.set_input(i, x)
+                m.run()
+                outs.append((m.kernel_name(0), m.get_output(0)))
+        names = [n for n, _ in outs]
+        assert len(set(names)) == len(cfgs) and all(f"splitk={split}>" in n for n in names), names
+        for n, y in outs[1:]:
+            np.testing.assert_array_equal(y.view(np.uint32), outs[0][1].view(np.uint32), err_msg=f"{n} vs {names[0]}")
+
+
+DET_CHILD = r"""
+import hashlib, json, sys
+sys.path.insert(0, %r)
+from spinnv2_amd.runtime import Model
+from spinnv2_amd.spk import models, write_spk
+g = models.resnet(18, 3, image=72)
+x = models.make_input(g.tensors[g.inputs[0]].shape, 9)
+with Model(write_spk(g, "mi355x")) as m:
+    m.set_input(0, x)
+    m.run()
+    y = m.get_output(0)
+    names = [m.kernel_name(n.id) for n in g.nodes if n.op_type in ("Conv", "Gemm")]
+print(json.dumps({"sha": hashlib.sha256(y.tobytes()).hexdigest(), "names": names}))
+""" % str(ROOT)
+
+
+def test_deterministic_tuner_is_bit_reproducible_outside_the_table(gpu):
+    """SPKV2_TUNE_DETERMINISTIC=1 on layer shapes the committed table does
+    not hold (ResNet-18 at 72x72, batch 3), tuned live in two fresh
+    processes with different tie bands (0% and 50%: different tile picks
+    within a summation order): the model fixes each layer's summation order,
+    so the logits are bit-identical whatever the timings."""
+    runs = []
+    for tie in ("0", "50"):
+        env = dict(os.environ, SPKV2_TUNE_TABLE="0", SPKV2_TUNE_TIE=tie, SPKV2_TUNE_DETERMINISTIC="1")
+        for k in ("SPKV2_TUNE_DB", "SPKV2_CONV_CFG", "SPKV2_CONV_SPLITK", "SPKV2_CONV_HYBRID", "SPKV2_CONV_TUNE"):
+            env.pop(k, None)
+        out = subprocess.run([sys.executable, "-c", DET_CHILD], env=env, capture_output=True, text=True, timeout=100)
+        assert out.returncode == 0, out.stderr[-2000:]
+        runs.append(json.loads(out.stdout.strip().splitlines()[-1]))
+    print("tile picks that differ:", [(a, b) for a, b in zip(runs[0]["names"], runs[1]["names"]) if a != b])
+    assert runs[0]["sha"] == runs[1]["sha"]
