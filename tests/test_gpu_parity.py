@@ -152,7 +152,8 @@ FLOAT_OPS = [
     ("Softmax", [4, 1000], dict(axis=-1)),
     ("Softmax", [2, 16, 50], dict(axis=1)),
     ("Softmax", [5, 2048], dict(axis=-1)),     # register-resident rows at their limit
-    ("Softmax", [4099, 1000], dict(axis=-1)),  # many rows
+    ("Softmax", [4099, 1000], dict(axis=-1)),  # many rows (non-temporal stores)
+    ("Softmax", [1100, 2048], dict(axis=-1)),  # many long rows (non-temporal stores)
     ("Softmax", [2048, 36], dict(axis=-1)),    # many short rows
     ("Softmax", [3, 2052], dict(axis=-1)),     # longer rows: three passes
     ("Softmax", [3, 6, 7], dict(axis=-1)),     # rows not a multiple of 4
