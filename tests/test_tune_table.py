@@ -3,8 +3,8 @@ benchmark networks' layer shapes, on the CPU: every fp32 implicit-GEMM conv
 and every INT8 conv of them has an entry under the key the runtime computes
 (conv_f32.hip shape_key with the shared padded geometry, conv_i8.hip
 tune_i8), so no process tunes them at prepare and fp32 results stay
-bit-reproducible across processes; and no conv entry is left over from a
-shape the networks no longer have."""
+bit-reproducible across processes (INT8 ResNet-50 in both INT8 modes); and
+no conv entry is left over from a shape the networks no longer have."""
 
 from __future__ import annotations
 
@@ -29,6 +29,9 @@ def _keys():
     for b in (64, 1):
         g = models.resnet(50, b)
         i8.update(T.int8_key(g, n) for n in g.nodes if n.op_type == "Conv")
+        # the INT8 configuration with int8 tensors between nodes: the same
+        # layers under keys of their own (the key depends on shapes only)
+        i8.update(T.int8_key(g, n, q8=True) for n in g.nodes if n.op_type == "Conv")
     return f32, i8
 
 
