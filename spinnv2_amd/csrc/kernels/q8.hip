@@ -60,22 +60,42 @@ __global__ void __launch_bounds__(256) maxpool_q8(const int8_t *__restrict__ x, 
     }
 }
 
-// One thread per (image, channel): consecutive threads read consecutive
-// channels of a pixel.
-__global__ void __launch_bounds__(256) plane_mean_q8(const int8_t *__restrict__ x, float *__restrict__ y, int N, int C,
-                                                     int H, int W, int Hp, int Wp, int Cp, int pt, int pl, float scale,
-                                                     int zp) {
-    const size_t total = static_cast<size_t>(N) * C;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
-         i += static_cast<size_t>(gridDim.x) * 256) {
-        const int c = static_cast<int>(i % C);
-        const size_t img = i / C;
-        int sum = 0;  // |q - z| <= 255 per element: exact for H*W < 2^23
-        for (int h = 0; h < H; h++) {
-            const int8_t *row = x + ((img * Hp + h + pt) * Wp + pl) * static_cast<size_t>(Cp) + c;
-            for (int w = 0; w < W; w++) sum += static_cast<int>(row[static_cast<size_t>(w) * Cp]) - zp;
-        }
-        y[i] = static_cast<float>((static_cast<double>(sum) * static_cast<double>(scale)) / static_cast<double>(H * W));
+// One wave per (image, 16 channels): lane l sums pixels l, l + 64, ... of
+// the image, 16 channels at a time from one 16-byte load (the channel pitch
+// is a multiple of 16), and the 64 lanes' sums are added through LDS.  The
+// sums are integers, so any order gives the same total; lane c < 16 then
+// subtracts the zero point's share and writes channel c.
+__global__ void __launch_bounds__(64) plane_mean_q8(const int8_t *__restrict__ x, float *__restrict__ y, int C, int H,
+                                                    int W, int Hp, int Wp, int Cp, int pt, int pl, float scale,
+                                                    int zp) {
+    typedef signed char char16 __attribute__((ext_vector_type(16)));
+    __shared__ int part[64][17];
+    const int groups = (C + 15) / 16;
+    const int img = static_cast<int>(blockIdx.x) / groups;
+    const int g = static_cast<int>(blockIdx.x) - img * groups;
+    const int lane = threadIdx.x;
+    const int HW = H * W;
+    int sum[16];
+#pragma unroll
+    for (int b = 0; b < 16; b++) sum[b] = 0;
+    // |sum| <= 128 * H * W: exact for H * W < 2^23
+    for (int p = lane; p < HW; p += 64) {
+        const int h = p / W, w = p - h * W;
+        const char16 v = *reinterpret_cast<const char16 *>(
+            x + ((static_cast<size_t>(img) * Hp + h + pt) * Wp + w + pl) * static_cast<size_t>(Cp) + g * 16);
+#pragma unroll
+        for (int b = 0; b < 16; b++) sum[b] += static_cast<int>(v[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < 16; b++) part[lane][b] = sum[b];
+    __syncthreads();
+    const int c = g * 16 + lane;
+    if (lane < 16 && c < C) {
+        int total = 0;
+        for (int l = 0; l < 64; l++) total += part[l][lane];
+        const int centered = total - zp * HW;  // sum(q - z)
+        y[static_cast<size_t>(img) * C + c] =
+            static_cast<float>((static_cast<double>(centered) * static_cast<double>(scale)) / static_cast<double>(HW));
     }
 }
 
@@ -234,10 +254,11 @@ int mean_q8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node) {
     }
     if (static_cast<int64_t>(x->H) * x->W >= (int64_t(1) << 23)) return SPKV2_E_UNSUPPORTED;
     set_kernel_name(ctx, node, "plane_mean_q8");
-    const size_t total = static_cast<size_t>(x->N) * x->C;
-    if (total == 0) return 0;
-    hipLaunchKernelGGL(plane_mean_q8, dim3(grid_for(total, 256)), dim3(256), 0, ctx->stream, x->buf,
-                       dptr<float>(ctx, node->outputs[0]), x->N, x->C, x->H, x->W, x->Hp, x->Wp, x->Cp, x->pt, x->pl,
+    const size_t waves = static_cast<size_t>(x->N) * ((x->C + 15) / 16);  // one per (image, 16 channels)
+    if (waves == 0) return 0;
+    if (waves >= 0x80000000ULL) return SPKV2_E_UNSUPPORTED;
+    hipLaunchKernelGGL(plane_mean_q8, dim3(static_cast<unsigned>(waves)), dim3(64), 0, ctx->stream, x->buf,
+                       dptr<float>(ctx, node->outputs[0]), x->C, x->H, x->W, x->Hp, x->Wp, x->Cp, x->pt, x->pl,
                        x->scale, x->zp);
     return launch_status("plane_mean_q8");
 }

@@ -111,6 +111,7 @@ CHAINS = [
     dict(batch=2, hw=11, pool=True, residual=False),
     dict(batch=1, c=20, hw=10, widths=(36, 52), relu_last=False),
     dict(batch=2, hw=8, k=5),
+    dict(batch=2, hw=40, k=1, residual=False),  # a 40 x 40 spatial mean: 25 pixels per lane
 ]
 
 
