@@ -29,35 +29,61 @@ namespace {
 // One thread per (output pixel, 16 channels): the in-bounds taps' 16-byte
 // pieces, byte-wise maxima, one 16-byte store into the output's padded NHWC
 // buffer.  Both buffers have a channel pitch that is a multiple of 16.
-__global__ void __launch_bounds__(256) maxpool_q8(const int8_t *__restrict__ x, int8_t *__restrict__ y,
-                                                  unsigned pixels, int C16, int H, int W, int xHp, int xWp, int xCp,
-                                                  int xpt, int xpl, int OH, int OW, int yHp, int yWp, int yCp, int ypt,
-                                                  int ypl, int kh, int kw, int sh, int sw, int ph, int pw) {
+// Workgroup b (after the XCD remap below) covers chunk b % chunks of output
+// row b / chunks (one wave-uniform division per workgroup; threads along the
+// row's OW x C16 pieces).  K > 0: a K x K window, unrolled, every tap's load in
+// flight before the first maximum; K = 0: any window.
+template <int K>
+__global__ void __launch_bounds__(256) maxpool_q8(const int8_t *__restrict__ x, int8_t *__restrict__ y, int chunks,
+                                                  int C16, int H, int W, int xHp, int xWp, int xCp, int xpt, int xpl,
+                                                  int OH, int OW, int yHp, int yWp, int yCp, int ypt, int ypl, int kh,
+                                                  int kw, int sh, int sw, int ph, int pw) {
     typedef signed char char16 __attribute__((ext_vector_type(16)));
-    const size_t total = static_cast<size_t>(pixels) * C16;
-    for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
-         i += static_cast<size_t>(gridDim.x) * 256) {
-        const int c16 = static_cast<int>(i % C16);
-        const size_t pix = i / C16;
-        const int ow = static_cast<int>(pix % OW);
-        const size_t t = pix / OW;
-        const int oh = static_cast<int>(t % OH);
-        const size_t img = t / OH;
-        char16 m = static_cast<char16>(static_cast<signed char>(-128));
+    // consecutive workgroups land on different XCDs: give each XCD a
+    // contiguous range of rows, so the input row two neighbouring output
+    // rows share is fetched into one L2
+    int bid = static_cast<int>(blockIdx.x);
+    const int nb = static_cast<int>(gridDim.x);
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    const int row = bid / chunks;  // image * OH + oh
+    const int t = (bid - row * chunks) * 256 + static_cast<int>(threadIdx.x);
+    if (t >= OW * C16) return;
+    const int img = row / OH;
+    const int oh = row - img * OH;
+    const int ow = t / C16;
+    const int c16 = t - ow * C16;
+    const int8_t *xi = x + static_cast<size_t>(img) * xHp * xWp * xCp + c16 * 16;
+    char16 m = static_cast<char16>(static_cast<signed char>(-128));
+    if constexpr (K > 0) {
+        char16 v[K][K];
+#pragma unroll
+        for (int a = 0; a < K; a++)
+#pragma unroll
+            for (int b = 0; b < K; b++) {
+                const int ih = oh * sh - ph + a, iw = ow * sw - pw + b;
+                const bool in = static_cast<unsigned>(ih) < static_cast<unsigned>(H) &&
+                                static_cast<unsigned>(iw) < static_cast<unsigned>(W);
+                v[a][b] = in ? *reinterpret_cast<const char16 *>(
+                                   xi + (static_cast<size_t>(ih + xpt) * xWp + iw + xpl) * xCp)
+                             : m;
+            }
+#pragma unroll
+        for (int a = 0; a < K; a++)
+#pragma unroll
+            for (int b = 0; b < K; b++) m = __builtin_elementwise_max(m, v[a][b]);
+    } else {
         for (int a = 0; a < kh; a++) {
             const int ih = oh * sh - ph + a;
             if (ih < 0 || ih >= H) continue;
             for (int b = 0; b < kw; b++) {
                 const int iw = ow * sw - pw + b;
                 if (iw < 0 || iw >= W) continue;
-                const char16 v = *reinterpret_cast<const char16 *>(
-                    x + ((img * xHp + ih + xpt) * xWp + iw + xpl) * static_cast<size_t>(xCp) + c16 * 16);
-                m = __builtin_elementwise_max(m, v);
+                m = __builtin_elementwise_max(
+                    m, *reinterpret_cast<const char16 *>(xi + (static_cast<size_t>(ih + xpt) * xWp + iw + xpl) * xCp));
             }
         }
-        *reinterpret_cast<char16 *>(y + ((img * yHp + oh + ypt) * yWp + ow + ypl) * static_cast<size_t>(yCp) +
-                                    c16 * 16) = m;
     }
+    *reinterpret_cast<char16 *>(y + ((static_cast<size_t>(img) * yHp + oh + ypt) * yWp + ow + ypl) * yCp + c16 * 16) = m;
 }
 
 // One wave per (image, 16 channels): lane l sums pixels l, l + 64, ... of
@@ -234,14 +260,17 @@ int maxpool_q8_run(Spkv2Context *ctx, const Spkv2NodeRecord *node) {
     Spkv2AttrRecord attr;
     if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
     set_kernel_name(ctx, node, "maxpool_q8");
-    const size_t pixels = static_cast<size_t>(y->N) * y->H * y->W;
-    if (pixels == 0) return 0;
-    if (pixels > 0xffffffffULL) return SPKV2_E_UNSUPPORTED;
     const int C16 = x->Cp / 16;
-    hipLaunchKernelGGL(maxpool_q8, dim3(grid_for(pixels * C16, 256)), dim3(256), 0, ctx->stream, x->buf, y->buf,
-                       static_cast<unsigned>(pixels), C16, x->H, x->W, x->Hp, x->Wp, x->Cp, x->pt, x->pl, y->H, y->W,
-                       y->Hp, y->Wp, y->Cp, y->pt, y->pl, attr.kernel_shape[0], attr.kernel_shape[1], attr.strides[0],
-                       attr.strides[1], attr.pads[0], attr.pads[1]);
+    const size_t rows = static_cast<size_t>(y->N) * y->H;
+    const size_t per_row = static_cast<size_t>(y->W) * C16;  // 16-byte pieces of one output row
+    if (rows == 0 || per_row == 0) return 0;
+    const size_t chunks = (per_row + 255) / 256;
+    if (per_row > 0x7fffffffULL || rows * chunks >= 0x80000000ULL) return SPKV2_E_UNSUPPORTED;
+    const bool k3 = attr.kernel_shape[0] == 3 && attr.kernel_shape[1] == 3;
+    hipLaunchKernelGGL(k3 ? maxpool_q8<3> : maxpool_q8<0>, dim3(static_cast<unsigned>(rows * chunks)), dim3(256), 0,
+                       ctx->stream, x->buf, y->buf, static_cast<int>(chunks), C16, x->H, x->W, x->Hp, x->Wp, x->Cp,
+                       x->pt, x->pl, y->H, y->W, y->Hp, y->Wp, y->Cp, y->pt, y->pl, attr.kernel_shape[0],
+                       attr.kernel_shape[1], attr.strides[0], attr.strides[1], attr.pads[0], attr.pads[1]);
     return launch_status("maxpool_q8");
 }
 

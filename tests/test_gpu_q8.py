@@ -90,7 +90,7 @@ def _chain(batch=2, c=16, hw=9, widths=(24, 40), k=3, stride=1, residual=True, r
     x = g.input("x", [batch, in_ch, hw, hw])
     a = g.relu(g.conv(x, p.he((c, in_ch, k0, k0)), p.normal(c, 0.05), pad=k0 // 2))
     if pool:
-        a = g.maxpool(a, 3, 2, 1)
+        a = g.maxpool(a, *(pool if isinstance(pool, tuple) else (3, 2, 1)))
     b = g.relu(g.conv(a, p.he((widths[0], c, k, k)), p.normal(widths[0], 0.05), stride=stride, pad=k // 2))
     y = g.conv(b, p.he((widths[1], widths[0], 1, 1)), p.normal(widths[1], 0.05))
     if residual:
@@ -112,6 +112,7 @@ CHAINS = [
     dict(batch=1, c=20, hw=10, widths=(36, 52), relu_last=False),
     dict(batch=2, hw=8, k=5),
     dict(batch=2, hw=40, k=1, residual=False),  # a 40 x 40 spatial mean: 25 pixels per lane
+    dict(batch=2, hw=12, pool=(2, 2, 0), residual=False),  # a 2 x 2 window: the generic pooling loop
 ]
 
 
