@@ -174,10 +174,10 @@ def _int8_capable_reader(g: Graph, n, idx: int) -> bool:
 
 
 def int8_tensor_plan(g: Graph) -> tuple[set[int], list]:
-    """The tensors the mode stores as int8 and the Convs it runs: a Conv's
-    output or a MaxPool's output becomes int8 when it is not a graph output
-    and every reader takes int8 (a group-1 Conv as input or residual, a
-    MaxPool, a spatial mean); a Conv runs in the mode only when its output is
+    """The tensors the mode stores as int8 and the Convs it runs: the output
+    of a group-1 Conv without SiLU, or of a MaxPool, becomes int8 when it is
+    not a graph output and every reader takes int8 (a group-1 Conv as input
+    or residual, a MaxPool, a spatial mean); a Conv runs in the mode only when its output is
     int8, so its int8 inputs and residual must be too, and a MaxPool keeps
     int8 only with int8 on both sides.  Iterated to a fixed point."""
     readers: dict[int, list] = {}
@@ -186,7 +186,11 @@ def int8_tensor_plan(g: Graph) -> tuple[set[int], list]:
             readers.setdefault(t, []).append((n, i))
     cand = set()
     for n in g.nodes:
-        if n.op_type == "Conv" and int(n.attrs.get("group", 1)) == 1 or n.op_type == "MaxPool":
+        # the requantizing epilogue applies Relu as a clamp; a SiLU conv keeps
+        # its fp32 output
+        q8_conv = (n.op_type == "Conv" and int(n.attrs.get("group", 1)) == 1 and
+                   n.attrs.get("fused_activation") in (None, "Relu"))
+        if q8_conv or n.op_type == "MaxPool":
             t = n.outputs[0]
             if t not in g.outputs and readers.get(t) and all(_int8_capable_reader(g, r, i) for r, i in readers[t]):
                 cand.add(t)

@@ -217,3 +217,79 @@ def test_q8_resnet50_224_b64_images_equal_batch1_oracle(gpu):
             m.set_input(0, x)
             m.run()
             np.testing.assert_array_equal(m.get_output(1).view(np.uint32), eager.view(np.uint32))
+
+
+def test_q8_refuses_user_kernels_and_protection_on_int8_tensors(gpu, monkeypatch):
+    """Nodes that read or write int8 tensors between nodes run only on the
+    built-in kernels that hold those tensors' device buffers.  A user kernel
+    registered for them after prepare makes spkv2_run refuse (-32) without
+    calling it, and clearing the registry restores the bit-identical run;
+    registered before prepare, prepare refuses.  A protection plan naming an
+    int8 tensor (its guards read fp32 tensors) is refused at prepare (this
+    repository's writer never writes one; the package here is forced)."""
+    import ctypes
+
+    from spinnv2_amd.runtime import Model, RuntimeError_, load_library
+    from spinnv2_amd.spk import format as F
+    from spinnv2_amd.spk import writer
+    from spinnv2_amd.spk.writer import Protection
+
+    lib = load_library()
+    g = _chain()
+    blob = _q8_package(g)
+    xs = rng_inputs(g)
+    calls = []
+    kernel = ctypes.CFUNCTYPE(ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p)(
+        lambda ctx, node, scratch: calls.append(1) or -99)
+    register = lambda: lib.spkv2_register_kernel(F.OP["Conv"], F.BACKEND["mi355x"], F.KIND["implicit_gemm_i8"],
+                                                 ctypes.cast(kernel, ctypes.c_void_p), 5)
+    try:
+        lib.spkv2_clear_user_kernels()
+        with Model(blob) as m:
+            m.set_input(0, xs[0])
+            m.run()
+            base = m.get_output(0)
+            assert register() == 0
+            m.set_input(0, xs[0])
+            assert m.run_rc() == -32 and not calls
+            lib.spkv2_clear_user_kernels()
+            # the memory plan may reuse the input's arena region once its
+            # last reader ran: inputs are set before every run
+            m.set_input(0, xs[0])
+            m.run()
+            np.testing.assert_array_equal(m.get_output(0).view(np.uint32), base.view(np.uint32))
+        assert register() == 0
+        m = Model(blob, prepare=False)
+        try:
+            with pytest.raises(RuntimeError_) as err:
+                m.prepare()
+            assert err.value.code == -32 and not calls
+        finally:
+            m.close()
+    finally:
+        lib.spkv2_clear_user_kernels()
+    # a range guard on a conv whose output is an int8 tensor
+    h = _chain()
+    conv = next(n for n in h.nodes if n.op_type == "Conv")
+    samples = [[models.make_input(h.tensors[h.inputs[0]].shape, 1000 + i)] for i in range(4)]
+    qp = quantize_int8_activations(h, samples)
+    t = h.tensors[conv.outputs[0]]
+    assert t.dtype == "int8"
+    strict = writer._protection_section
+
+    def forced(g_, entries, offset):  # the writer's own check refuses int8 outputs
+        t.dtype = "fp32"
+        try:
+            return strict(g_, entries, offset)
+        finally:
+            t.dtype = "int8"
+
+    monkeypatch.setattr(writer, "_protection_section", forced)
+    prot = write_spk(h, "mi355x", quant_params=qp, protection=[Protection(conv.id, "range_guard_rerun", -1e3, 1e3)])
+    m = Model(prot, prepare=False)
+    try:
+        with pytest.raises(RuntimeError_) as err:
+            m.prepare()
+        assert err.value.code == -32
+    finally:
+        m.close()

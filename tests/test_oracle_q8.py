@@ -240,6 +240,20 @@ def test_int8_tensor_plan_resnet_and_fallback():
     run_default_pipeline(h)
     cand, convs = int8_tensor_plan(h)
     assert cand == set() and convs == []
+    # a SiLU conv keeps its fp32 output (the requantizing epilogue clamps
+    # Relu only), so the tensor it reads stays fp32 too; the conv after it
+    # quantizes that fp32 input on load
+    s = Graph("silu")
+    x = s.input("x", [1, 3, 8, 8])
+    a = s.relu(s.conv(x, p.he((8, 3, 3, 3)), p.normal(8, 0.01), pad=1))
+    b = s.silu(s.conv(a, p.he((8, 8, 3, 3)), p.normal(8, 0.01), pad=1))
+    c = s.relu(s.conv(b, p.he((16, 8, 1, 1)), p.normal(16, 0.01)))
+    s.mark_output(s.flatten(s.reduce_mean(c, [2, 3], keepdims=1), 1))
+    run_default_pipeline(s)
+    convs_all = [n for n in s.nodes if n.op_type == "Conv"]
+    assert [n.attrs.get("fused_activation") for n in convs_all] == ["Relu", "Silu", "Relu"]
+    cand, convs = int8_tensor_plan(s)
+    assert convs == [convs_all[2]] and cand == {convs_all[2].outputs[0]}
 
 
 def test_oracle_q8_resnet_tracks_fp32():
