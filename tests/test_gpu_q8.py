@@ -293,3 +293,14 @@ def test_q8_refuses_user_kernels_and_protection_on_int8_tensors(gpu, monkeypatch
         assert err.value.code == -32
     finally:
         m.close()
+
+
+def test_q8_resnet18_basic_blocks(gpu):
+    """ResNet-18's basic blocks in the mode (3x3 convs carrying the residual,
+    1x1 stride-2 projections, the 7x7 stem and its MaxPool) at 64x64, batch
+    2: every int8 tensor and every conv's accumulators bit-exact; the spatial
+    mean (a second graph output) bit-exact, the logits within tolerance."""
+    g = models.resnet(18, 2, image=64)
+    blob = _q8_package(g, mark=[[n for n in g.nodes if n.op_type == "ReduceMean"][0].outputs[0]])
+    assert len(_int8_tensors(g)) == 21  # 20 conv outputs and the stem MaxPool's
+    _check_all(g, blob, rng_inputs(g), exact_outputs={1})
