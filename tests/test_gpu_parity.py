@@ -135,6 +135,12 @@ EXACT_OPS = [
     ("Sub", [2, 3, 40, 40], dict(b_shape=[1], swap=True)),
     ("Div", [2, 8, 10, 10], dict(b_shape=[1], swap=True)),
     ("Mul", [3, 5, 7], dict(b_shape=[1])),
+    # the unrolled-window pools: SPPF's 5x5/1/2, a 3x3/1/1 and a 5x5/2/2 on odd sizes; a 4x4 window
+    # stays on the generic loop
+    ("MaxPool", [2, 16, 20, 20], dict(k=5, s=1, p=2)),
+    ("MaxPool", [1, 8, 13, 11], dict(k=3, s=1, p=1)),
+    ("MaxPool", [1, 8, 17, 15], dict(k=5, s=2, p=2)),
+    ("MaxPool", [1, 4, 12, 12], dict(k=4, s=2, p=1)),
 ]
 
 
@@ -145,6 +151,22 @@ def test_exact_ops_bitwise(gpu, op, shape, kw):
     xs = rng_inputs(g)
     got = run_gpu(blob, xs)[0]
     want = run_oracle(blob, xs)[0]
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("k,s,p", [(2, 2, 0), (3, 1, 1), (5, 1, 2), (3, 2, 1), (4, 2, 1)])
+def test_maxpool_signed_zero_order(gpu, k, s, p):
+    """Windows of -0.0, +0.0 and negatives (and a NaN): the maximum of a
+    window holding both zeros is whichever comes first in the reference's
+    order (rows, then columns, strict >), NaN is never taken; every pooling
+    kernel gives the oracle's bits."""
+    g = models.single_op("MaxPool", [2, 3, 16, 16], k=k, s=s, p=p)
+    blob = write_spk(g, "mi355x")
+    rng = np.random.default_rng(k * 10 + s)
+    x = rng.choice(np.array([-0.0, 0.0, -1.5, -0.25], np.float32), size=(2, 3, 16, 16))
+    x[0, 0, 3, 5] = np.nan
+    got = run_gpu(blob, [x])[0]
+    want = run_oracle(blob, [x])[0]
     np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
