@@ -931,7 +931,9 @@ int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     }
     size_t axis_off = 0;
     set_kernel_name(ctx, node, ov ? "concat_views" : "concat");
-    for (uint16_t i = 0; i < node->input_count; i++) {
+    CopySeg segs[8];  // a node record has at most eight inputs
+    int count = 0;
+    for (uint16_t i = 0; i < node->input_count && i < 8; i++) {
         const Spkv2TensorRecord *xr = rec(ctx, node->inputs[i]);
         const float *x = dptr<const float>(ctx, node->inputs[i]);
         const size_t block = static_cast<size_t>(xr->shape[axis]) * inner;
@@ -942,10 +944,10 @@ int concat_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         }
         float *dst = y + axis_off * inner;
         if (!((outer == 1 || x_stride == y_stride) && dst == x) && outer * block > 0)
-            if (int rc = strided_block_copy(ctx->stream, x, dst, outer, block, x_stride, 0, y_stride)) return rc;
+            segs[count++] = CopySeg{x, dst, block, x_stride, 0, y_stride};
         axis_off += xr->shape[axis];
     }
-    return 0;
+    return multi_block_copy(ctx->stream, segs, count, outer);  // one launch for the aligned inputs
 }
 
 static int pool_args(Spkv2Context *ctx, const Spkv2NodeRecord *node, PoolArgs *p) {

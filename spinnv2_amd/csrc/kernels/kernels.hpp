@@ -51,6 +51,15 @@ int topk_run(Spkv2Context *, const Spkv2NodeRecord *, void *);
 // (float elements; Concat, Split, Slice)
 int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, size_t block, size_t x_stride,
                        size_t x_base, size_t y_stride);
+// The copies of several blocks with the same `outer` (a Split's outputs, a
+// Concat's inputs) in one launch: segment k copies
+// y_k[o * y_stride_k + j] = x_k[x_base_k + o * x_stride_k + j], j < block_k.
+struct CopySeg {
+    const float *x;
+    float *y;
+    size_t block, x_stride, x_base, y_stride;
+};
+int multi_block_copy(hipStream_t s, const CopySeg *segs, int count, size_t outer);
 
 // channel-slice views of Concats at batch > 1 (views.cpp), after every
 // node's prepare

@@ -140,6 +140,25 @@ __global__ void __launch_bounds__(256) block_copy4(const floatx4 *__restrict__ x
             y[o * y_stride4 + j] = x[o * x_stride4 + j];
 }
 
+// Several block copies in one launch: grid.z is the segment, grid.y walks
+// its blocks, grid.x the float4s of a block.
+constexpr int kMaxCopySegs = 8;
+struct CopySegs4 {
+    const floatx4 *x[kMaxCopySegs];
+    floatx4 *y[kMaxCopySegs];
+    size_t block4[kMaxCopySegs], x_stride4[kMaxCopySegs], y_stride4[kMaxCopySegs];
+};
+__global__ void __launch_bounds__(256) block_copy4_multi(CopySegs4 c, size_t outer) {
+    const int k = static_cast<int>(blockIdx.z);
+    const floatx4 *x = c.x[k];
+    floatx4 *y = c.y[k];
+    const size_t block4 = c.block4[k], xs = c.x_stride4[k], ys = c.y_stride4[k];
+    for (size_t o = blockIdx.y; o < outer; o += gridDim.y)
+        for (size_t j = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; j < block4;
+             j += static_cast<size_t>(gridDim.x) * 256)
+            y[o * ys + j] = x[o * xs + j];
+}
+
 // Slice with a step: y[(o*out + s)*inner + t] = x[(o*dim + start + s*step)*inner + t]
 __global__ void __launch_bounds__(256) slice_kernel(const float *__restrict__ x, float *__restrict__ y, size_t outer,
                                                     int64_t out, int64_t dim, int64_t start, int64_t step, size_t inner) {
@@ -621,6 +640,40 @@ int strided_block_copy(hipStream_t s, const float *x, float *y, size_t outer, si
     return launch_status("block_copy");
 }
 
+int multi_block_copy(hipStream_t s, const CopySeg *segs, int count, size_t outer) {
+    CopySegs4 c = {};
+    int k = 0;
+    size_t max4 = 0;
+    auto flush = [&]() -> int {
+        if (k == 0) return 0;
+        const unsigned gx = static_cast<unsigned>(std::min<size_t>((max4 + 255) / 256, 1024));
+        const unsigned gy = static_cast<unsigned>(std::min<size_t>(outer, 65535));
+        hipLaunchKernelGGL(block_copy4_multi, dim3(gx, gy, static_cast<unsigned>(k)), dim3(256), 0, s, c, outer);
+        k = 0;
+        max4 = 0;
+        return launch_status("block_copy");
+    };
+    for (int i = 0; i < count; i++) {
+        const CopySeg &g = segs[i];
+        if (outer * g.block == 0) continue;
+        const bool vec = g.block % 4 == 0 && g.x_stride % 4 == 0 && g.x_base % 4 == 0 && g.y_stride % 4 == 0 &&
+                         reinterpret_cast<uintptr_t>(g.x) % 16 == 0 && reinterpret_cast<uintptr_t>(g.y) % 16 == 0;
+        if (!vec) {
+            if (int rc = strided_block_copy(s, g.x, g.y, outer, g.block, g.x_stride, g.x_base, g.y_stride)) return rc;
+            continue;
+        }
+        c.x[k] = reinterpret_cast<const floatx4 *>(g.x + g.x_base);
+        c.y[k] = reinterpret_cast<floatx4 *>(g.y);
+        c.block4[k] = g.block / 4;
+        c.x_stride4[k] = g.x_stride / 4;
+        c.y_stride4[k] = g.y_stride / 4;
+        max4 = std::max(max4, g.block / 4);
+        if (++k == kMaxCopySegs)
+            if (int rc = flush()) return rc;
+    }
+    return flush();
+}
+
 int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     Spkv2AttrRecord attr;
     if (int rc = spkv2_ctx_get_attr(ctx, node, &attr)) return rc;
@@ -648,17 +701,16 @@ int split_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
         x = reinterpret_cast<const float *>(v->base);
     }
     set_kernel_name(ctx, node, "split");
-    for (uint16_t k = 0; k < node->output_count; k++) {
+    CopySeg segs[4];  // a node record has at most four outputs
+    int count = 0;
+    for (uint16_t k = 0; k < node->output_count && k < 4; k++) {
         const Spkv2TensorRecord *yr = rec(ctx, node->outputs[k]);
         const size_t block = static_cast<size_t>(yr->shape[axis]) * inner;
         if (axis_offset + yr->shape[axis] > x_axis) return -11;
-        if (int rc = strided_block_copy(ctx->stream, x,
-                                        dptr<float>(ctx, node->outputs[k]), outer, block, x_axis * inner,
-                                        axis_offset * inner, block))
-            return rc;
+        segs[count++] = CopySeg{x, dptr<float>(ctx, node->outputs[k]), block, x_axis * inner, axis_offset * inner, block};
         axis_offset += yr->shape[axis];
     }
-    return 0;
+    return multi_block_copy(ctx->stream, segs, count, outer);  // one launch for the aligned outputs
 }
 
 int slice_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
