@@ -509,13 +509,18 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 // values are channels 16g..16g+15 of the chunk at its column n, loaded with
 // voffset = col(n) + chunk base and soffset = t * channel stride.  Columns
 // past N use an out-of-range voffset and load 0.
-template <int W>
+//
+// P chunks are in flight per wave (4 x 20 loads at most, within the 63
+// vmcnt allows); the launch takes P = 1 or 2 when no wave has more chunks
+// than that, so the unused load buffers do not cost registers (and
+// workgroups per CU).  P does not change the summation order.
+template <int W, int P>
 __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
-    constexpr int P = 4;  // chunks in flight per wave: 4 x 20 loads, within the 63 vmcnt allows
     __shared__ float red[W][256];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // wave-uniform in a scalar register: a chunk's tap arithmetic is scalar
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4;
     const int l16 = lane & 15;
     int bid = blockIdx.x;
@@ -539,9 +544,14 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
     const int cs4 = a.sk_cstride * 4;
-    // packed weights [m_tiles][KC][4 slots][16 rows][16 k]
-    const floatx4 *wsrc = reinterpret_cast<const floatx4 *>(a.wp) +
-                          (static_cast<size_t>(mt) * KC * 1024 + (g * 16 + l16) * 16) / 4;
+    // the lane's column and its k slot's channel offset within a chunk
+    const int colg = col == kOobOffset ? kOobOffset : col + 16 * g * cs4;
+    // packed weights [m_tiles][KC][4 slots][16 rows][16 k] (fewer than 2^31
+    // bytes, checked at launch); a lane's 16 values of a chunk are one 64-byte
+    // run at wbase + chunk * 4096
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.wp), static_cast<short>(0), a.m_tiles * KC * 4096, kBufferWord3);
+    const int wbase = (mt * KC * 1024 + (g * 16 + l16) * 16) * 4;
     const int nch = wave < KC ? (KC - wave + W - 1) / W : 0;
 
     // the epilogue's element of this thread (tid < 256): its bias and
@@ -560,20 +570,26 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     float bv[P][16];
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 
-    // loads chunk I of this wave into register set S; past the wave's last
-    // chunk it loads a valid chunk that is never used
+    // loads chunk I of this wave into register set S.  Past the wave's last
+    // chunk (the pipeline's tail) every offset is out of range: the loads
+    // return zeros without a memory access, and stay unconditional so the
+    // compiler keeps exact counts of the loads in flight (a branch around
+    // them makes it wait for all of them before each chunk's MFMAs).
 #define SK_LOAD(I, S)                                                                                             \
     {                                                                                                             \
-        const int kc_ = min(wave + W * (I), KC - 1);                                                              \
-        const floatx4 *src_ = wsrc + static_cast<size_t>(kc_) * 256;                                              \
-        _Pragma("unroll") for (int q = 0; q < 4; q++) av[S][q] = src_[q];                                         \
+        const int kr_ = wave + W * (I);                                                                           \
+        const bool own_ = kr_ < KC;                                                                               \
+        const int kc_ = own_ ? kr_ : 0;                                                                           \
+        const int ao_ = own_ ? wbase + kc_ * 4096 : kOobOffset;                                                   \
+        _Pragma("unroll") for (int q = 0; q < 4; q++) av[S][q] =                                                  \
+            __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ao_, q * 16, 0));              \
         const int k0_ = kc_ * 64;                                                                                 \
         const int tap_ = k0_ / a.sk_C;                                                                            \
-        const int c0_ = k0_ - tap_ * a.sk_C + 16 * g;                                                             \
+        const int c0_ = k0_ - tap_ * a.sk_C;                                                                      \
         const int kh_ = tap_ / a.sk_KW;                                                                           \
         const int kw_ = tap_ - kh_ * a.sk_KW;                                                                     \
-        const int vo_ =                                                                                           \
-            col == kOobOffset ? kOobOffset : col + (kh_ * a.sk_tap_h + kw_ * a.sk_tap_w + c0_ * a.sk_cstride) * 4; \
+        const int uo_ = (kh_ * a.sk_tap_h + kw_ * a.sk_tap_w + c0_ * a.sk_cstride) * 4;                           \
+        const int vo_ = colg == kOobOffset || !own_ ? kOobOffset : colg + uo_;                                    \
         _Pragma("unroll") for (int t = 0; t < 16; t++) bv[S][t] =                                                 \
             __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(xrs, vo_, t * cs4, 0));                \
     }
@@ -581,7 +597,23 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     _Pragma("unroll") for (int t = 0; t < 16; t++) acc =                                                          \
         __builtin_amdgcn_mfma_f32_16x16x4f32(av[S][t >> 2][t & 3], bv[S][t], acc, 0, 0, 0);
 
-    if (nch > 0) {
+    if constexpr (P < 4) {
+        // groups of P chunks, all loads of a group before its MFMAs (one
+        // group when no wave has more than P chunks, as the launch arranges).
+        // The MFMAs are unconditional (a branch around them lets the compiler
+        // sink each load next to its MFMA, one round trip per load): past the
+        // wave's last chunk both operands are zeros, which leave acc
+        // bit-identical, as acc starts at +0 and a sum that starts at +0 is
+        // never -0.
+        for (int i0 = 0; i0 < nch; i0 += P) {
+#pragma unroll
+            for (int p = 0; p < P; p++) SK_LOAD(i0 + p, p);
+#pragma unroll
+            for (int p = 0; p < P; p++) { SK_MMA(p); }
+        }
+    } else if (nch > 0) {
+        // a ring of P register sets: chunk i + P - 1 loads while chunk i
+        // multiplies
 #pragma unroll
         for (int p = 0; p < P - 1; p++) SK_LOAD(p, p);
         for (int i0 = 0; i0 < nch; i0 += P) {
@@ -1137,8 +1169,10 @@ const TileCfg kCfgs[] = {
     // latency per 16 k
     CFG(64, 64, 64, 0.95),   CFG(64, 64, 128, 0.95), CFG(128, 64, 64, 0.95),  CFG(64, 128, 64, 0.90),
     // 16 x 16 tiles, k over 4 or 8 waves: small outputs without split-K
-    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4>, conv_skinny_f32<4>, conv_skinny_f32<4>, 1.0, 4},
-    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8>, conv_skinny_f32<8>, conv_skinny_f32<8>, 1.0, 8},
+    // (kernel: the four-chunk pipeline; the launch picks a shallower one
+    // by the chunks per wave, skinny_kernel)
+    {16, 16, 64, "skinny16x16w4", conv_skinny_f32<4, 4>, conv_skinny_f32<4, 4>, conv_skinny_f32<4, 4>, 1.0, 4},
+    {16, 16, 64, "skinny16x16w8", conv_skinny_f32<8, 4>, conv_skinny_f32<8, 4>, conv_skinny_f32<8, 4>, 1.0, 8},
     // 32-row tiles, the four waves side by side along n: layers with 16-48
     // output channels (YOLO) fill half or more of the MFMA rows instead of
     // a quarter to three quarters of a 64-row tile
@@ -1157,6 +1191,14 @@ constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // threads per workgroup of configuration c
 int cfg_threads(int c) { return kCfgs[c].skinny_waves > 0 ? 64 * kCfgs[c].skinny_waves : 256; }
+
+// The skinny kernel of W waves for k_tiles 64-k chunks: chunks in flight
+// per wave no more than the busiest wave has
+IgemmKernel skinny_kernel(int W, int k_tiles) {
+    const int per_wave = (k_tiles + W - 1) / W;
+    if (W == 4) return per_wave <= 1 ? conv_skinny_f32<4, 1> : per_wave <= 2 ? conv_skinny_f32<4, 2> : conv_skinny_f32<4, 4>;
+    return per_wave <= 1 ? conv_skinny_f32<8, 1> : per_wave <= 2 ? conv_skinny_f32<8, 2> : conv_skinny_f32<8, 4>;
+}
 
 int device_cu_count() {
     static int cus = 0;
@@ -1409,13 +1451,19 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
             set_last_error_text("conv_skinny_f32: layer without whole 64-channel chunks per tap");
             return SPKV2_E_UNSUPPORTED;
         }
+        // the packed weights are addressed with 32-bit buffer offsets
+        if (static_cast<long long>(tc.m_tiles) * tc.k_tiles * 4096 >= kOobOffset) {
+            set_last_error_text("conv_skinny_f32: packed weights of 2 GiB or more");
+            return SPKV2_E_UNSUPPORTED;
+        }
         a.sk_C = gg.C;
         a.sk_cstride = gg.cstride;
         a.sk_KW = gg.KW;
         a.sk_tap_h = gg.tap_h;
         a.sk_tap_w = gg.tap_w;
         a.ws = nullptr;
-        t.kernel<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0, st>>>(a);
+        skinny_kernel(t.skinny_waves, tc.k_tiles)<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0,
+                                                    st>>>(a);
         return launch_status("conv_skinny_f32");
     }
     if (t.thin_mb > 0) {

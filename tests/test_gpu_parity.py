@@ -596,6 +596,9 @@ def test_gemm_every_tile_config(gpu, monkeypatch, cfg, k):
 SKINNY_CASES = [
     ("conv3x3_res", lambda: models.single_conv(2, 128, 11, 13, 150, 3, 1, 1, act="Relu", residual=True)),
     ("conv1x1_s2", lambda: models.single_conv(1, 256, 14, 14, 72, 1, 2, 0, act=None)),
+    # 6 chunks of 64 k: with 4 waves two chunks in flight per wave and two
+    # waves multiplying one chunk of zeros; with 8 waves two waves idle
+    ("conv1x1_c384", lambda: models.single_conv(1, 384, 9, 10, 50, 1, 1, 0, act="Relu")),
     ("conv3x3_s2_dil2", lambda: models.single_conv(1, 64, 15, 15, 40, 3, 2, 2, dilation=2, act="Relu")),
     ("gemm_alpha", lambda: models.single_gemm(3, 192, 70, alpha=0.5)),
     ("gemm_trans_a", lambda: models.single_gemm(5, 128, 33, trans_a=1)),
