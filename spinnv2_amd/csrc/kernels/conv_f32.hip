@@ -144,6 +144,8 @@ struct IgemmArgs {
     const int *__restrict__ ktap;
     int chk_H, chk_W, chk_ph, chk_pw;
     int th_steps;  // thin kernel: K / 4 MFMA steps (k' = tap * sk_C + c)
+    // row-window kernel: the input window's geometry (GatherGeom's win_*)
+    int win_KH, win_len, win_pitch, win_shift, win_owb, win_OH, win_dw;
 };
 
 
@@ -526,8 +528,11 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     int bid = blockIdx.x;
     const int nb = gridDim.x;
     if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-    const int mt = bid % a.m_tiles;
-    const int nt = bid / a.m_tiles;
+    // n-tiles of one m-tile consecutive: each XCD fetches only its m-tiles'
+    // weights into its L2
+    const int ntiles = nb / a.m_tiles;
+    const int mt = bid / ntiles;
+    const int nt = bid - mt * ntiles;
     const int KC = a.k_tiles;  // chunks of 64 k
 
     int col = kOobOffset;
@@ -645,6 +650,174 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
             a.yp[(static_cast<size_t>(eimg) * a.yp_C + em - a.yp_m0) * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + ow +
                  a.yp_pl] = v;
         }
+        if (a.y) a.y[eyi] = v;
+    }
+}
+
+// Row-window implicit GEMM: the skinny kernel's arithmetic (16 x 16 output
+// tile, 64-k chunks dealt round robin to W waves, 16 MFMAs per chunk, the
+// wave partials summed in wave order: the same k order and sums, so the same
+// bits as conv_skinny_f32<W>) with the B operand staged once per workgroup.
+// A workgroup takes 16 output channels by 16 consecutive pixels of one output
+// row; the input those pixels read -- C x KH rows of win_len columns, each
+// element once, against once per tap in the skinny kernel -- is loaded into
+// LDS first (dynamic LDS of C x KH x win_pitch floats), every load of a
+// thread in flight together, so only the weights stream through the k loop:
+// four 16-byte loads per chunk, R chunks in flight, and the next chunk's 16
+// LDS reads issued before the current chunk's MFMAs.  Pixels past the row's
+// end read column 0 of the window and are not stored.
+constexpr int kWinFloats = 24576;  // most LDS a window may take: 96 KB
+
+template <int W, int R, int KH>
+__global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
+    extern __shared__ float win[];
+    __shared__ float red[W][256];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4;
+    const int l16 = lane & 15;
+    int bid = blockIdx.x;
+    const int nb = gridDim.x;
+    if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+    // the n-tiles of one m-tile are consecutive, so each XCD (a contiguous
+    // range after the remap) fetches only its m-tiles' weights, the larger
+    // operand at batch 1, into its L2 (stage-4 3x3 conv: 23.8 -> 20.4 us)
+    const int ntiles = nb / a.m_tiles;
+    const int mt = bid / ntiles;
+    const int nt = bid - mt * ntiles;  // (output row, 16-pixel segment)
+    const int row = nt / a.win_owb;
+    const int ow0 = (nt - row * a.win_owb) * 16;
+    const int img = row / a.win_OH;
+    const int oh = row - img * a.win_OH;
+    const int KC = a.k_tiles;
+    const int C = a.sk_C;
+    const int pitch = a.win_pitch;
+    const int cst = KH * pitch;  // LDS floats between channels
+
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.wp), static_cast<short>(0), a.m_tiles * KC * 4096, kBufferWord3);
+    const int wbase = (mt * KC * 1024 + (g * 16 + l16) * 16) * 4;
+    const int nch = wave < KC ? (KC - wave + W - 1) / W : 0;
+    floatx4 av[R][4];
+    // weights of chunk I of this wave into register set S (out-of-range
+    // offsets past the wave's last chunk: zeros, no memory access)
+#define WN_LOAD(I, S)                                                                                             \
+    {                                                                                                             \
+        const int kr_ = wave + W * (I);                                                                           \
+        const int ao_ = kr_ < KC ? wbase + kr_ * 4096 : kOobOffset;                                               \
+        _Pragma("unroll") for (int q = 0; q < 4; q++) av[S][q] =                                                  \
+            __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ao_, q * 16, 0));              \
+    }
+    // the ring's first R - 1 chunks go out before the window, so the
+    // window's barrier waits for nothing the k loop has not yet needed
+    if (nch > 0) {
+#pragma unroll
+        for (int p = 0; p < R - 1; p++) WN_LOAD(p, p);
+    }
+
+    // the epilogue's element of this thread (tid < 256): bias and residual
+    // loaded now
+    const int em = mt * 16 + (tid >> 4);
+    const int eow = ow0 + (tid & 15);
+    const bool eown = tid < 256 && em < a.M && eow < a.OW;
+    const int esp = oh * a.OW + eow;
+    const size_t eyi = static_cast<size_t>(img) * a.y_img_stride + static_cast<size_t>(em) * a.y_cstride + esp;
+    const float ebias = eown && a.bias ? a.bias[em] : 0.0f;
+    const float eres = eown && a.res ? a.res[eyi] : 0.0f;
+
+    // the window: LDS row c * KH + kh holds input row oh * sh + kh * dh of
+    // channel c from column ow0 * sw on.  A wave instruction loads rpi = 64
+    // >> win_shift rows of one kh, one lane per column; a thread's channels
+    // are c_first + u * cstep, their KH rows each, up to 48 loads in flight.
+    {
+        const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
+        const int rpi = 64 >> a.win_shift;
+        const int q = lane >> a.win_shift;
+        const int j = lane & ((1 << a.win_shift) - 1);
+        const int cstep = W * rpi;
+        const int c_first = wave * rpi + q;
+        const bool jload = j < a.win_len;
+        const bool jstore = j < pitch;
+        const int xb = (img * a.x_img_stride + oh * a.sh * a.Wp + ow0 * a.sw + j + c_first * a.sk_cstride) * 4;
+        const int xstep = cstep * a.sk_cstride * 4;
+        const int tap4 = a.sk_tap_h * 4;
+        constexpr int UC = 48 / KH;  // channels per thread in flight
+        for (int u0 = 0; c_first + u0 * cstep < C; u0 += UC) {
+            float v[UC][KH];
+#pragma unroll
+            for (int u = 0; u < UC; u++) {
+                const bool ok = c_first + (u0 + u) * cstep < C && jload;
+#pragma unroll
+                for (int kh = 0; kh < KH; kh++)
+                    v[u][kh] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(
+                                   xrs, ok ? xb + (u0 + u) * xstep + kh * tap4 : kOobOffset, 0, 0));
+            }
+#pragma unroll
+            for (int u = 0; u < UC; u++) {
+                const int c = c_first + (u0 + u) * cstep;
+                if (c < C && jstore) {
+#pragma unroll
+                    for (int kh = 0; kh < KH; kh++) win[(c * KH + kh) * pitch + j] = v[u][kh];
+                }
+            }
+        }
+    }
+    __syncthreads();
+
+    // a lane's column in the window (pixels past the row's end: column 0)
+    const int jcol = ow0 + l16 < a.OW ? l16 * a.sw : 0;
+    const int gbase = 16 * g * cst + jcol;
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float bv[2][16];
+    // the 16 LDS values of chunk I of this wave into B set S
+#define WN_BREAD(I, S)                                                                                            \
+    {                                                                                                             \
+        const int k0_ = min(wave + W * (I), KC - 1) * 64;                                                         \
+        const int tap_ = k0_ / C;                                                                                 \
+        const int c0_ = k0_ - tap_ * C;                                                                           \
+        const int kh_ = tap_ / a.sk_KW;                                                                           \
+        const int kw_ = tap_ - kh_ * a.sk_KW;                                                                     \
+        const float *b_ = win + gbase + (c0_ * KH + kh_) * pitch + kw_ * a.win_dw;                                \
+        _Pragma("unroll") for (int t = 0; t < 16; t++) bv[S][t] = b_[t * cst];                                    \
+    }
+#define WN_MMA(A, S)                                                                                              \
+    _Pragma("unroll") for (int t = 0; t < 16; t++) acc =                                                          \
+        __builtin_amdgcn_mfma_f32_16x16x4f32(av[A][t >> 2][t & 3], bv[S][t], acc, 0, 0, 0);
+    if (nch > 0) {
+        WN_BREAD(0, 0);
+        for (int i0 = 0; i0 < nch; i0 += R) {
+#pragma unroll
+            for (int p = 0; p < R; p++) {
+                WN_LOAD(i0 + p + R - 1, (p + R - 1) % R);
+                if (i0 + p < nch) {
+                    if (i0 + p + 1 < nch) { WN_BREAD(i0 + p + 1, (p + 1) & 1); }
+                    WN_MMA(p, p & 1);
+                }
+            }
+        }
+    }
+#undef WN_LOAD
+#undef WN_BREAD
+#undef WN_MMA
+
+    // 16x16 accumulator layout: lane (g, l16) holds rows 4g..4g+3 of column l16
+#pragma unroll
+    for (int i = 0; i < 4; i++) red[wave][(4 * g + i) * 16 + l16] = acc[i];
+    __syncthreads();
+    if (eown) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) v += red[w][tid];
+        if (a.alpha != 1.0f) v *= a.alpha;
+        if (a.bias) v += ebias;
+        if (a.res) v += eres;
+        v = apply_act(v, a.act);
+        if (a.yp && static_cast<unsigned>(em - a.yp_m0) < static_cast<unsigned>(a.yp_C))
+            a.yp[(static_cast<size_t>(img) * a.yp_C + em - a.yp_m0) * a.yp_plane + (oh + a.yp_pt) * a.yp_Wp + eow +
+                 a.yp_pl] = v;
         if (a.y) a.y[eyi] = v;
     }
 }
@@ -1155,6 +1328,9 @@ struct TileCfg {
     double eff;  // relative per-CU MFMA efficiency of the shape (measured on ResNet layers)
     int skinny_waves = 0;  // > 0: conv_skinny_f32 with this many waves (no split-K)
     int thin_mb = 0;       // > 0: conv_thin_f32 with this many 16-row blocks (no split-K)
+    // with skinny_waves: conv_window_f32 instead (the skinny kernel's sums,
+    // the input window in LDS; convolutions only)
+    bool window = false;
 };
 
 #define CFGW(BM, BN, BK, WM, WN, EFF)                                                                        \
@@ -1184,6 +1360,14 @@ const TileCfg kCfgs[] = {
     // 96-row tiles, the four waves side by side along n, each three 32x32
     // blocks: 65-96 output channels (YOLO's 80-class head) in one m-tile
     CFGW(96, 128, 16, 1, 4, 0.90), CFGW(96, 128, 32, 1, 4, 0.90),
+    // row-window tiles: the skinny tiles' arithmetic (the same bits as
+    // entries 12 and 13), one output row segment per workgroup, the input
+    // window in LDS (kernel: the eight-chunk ring; the launch picks a
+    // shallower one by the chunks per wave, window_kernel)
+    {16, 16, 64, "win16x16w4", conv_window_f32<4, 8, 3>, conv_window_f32<4, 8, 3>, conv_window_f32<4, 8, 3>, 1.0, 4, 0,
+     true},
+    {16, 16, 64, "win16x16w8", conv_window_f32<8, 4, 3>, conv_window_f32<8, 4, 3>, conv_window_f32<8, 4, 3>, 1.0, 8, 0,
+     true},
 };
 #undef CFG
 #undef CFGW
@@ -1191,6 +1375,22 @@ constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // threads per workgroup of configuration c
 int cfg_threads(int c) { return kCfgs[c].skinny_waves > 0 ? 64 * kCfgs[c].skinny_waves : 256; }
+
+// The row-window kernel of W waves for k_tiles 64-k chunks and KH (1 or 3)
+// window rows per channel: a ring of weight chunks no deeper than the
+// busiest wave's chunks
+template <int KH>
+IgemmKernel window_kernel_kh(int W, int per_wave) {
+    if (W == 4)
+        return per_wave <= 2 ? conv_window_f32<4, 2, KH> : per_wave <= 4 ? conv_window_f32<4, 4, KH>
+                                                                        : conv_window_f32<4, 8, KH>;
+    // eight waves: two per SIMD, 256 registers each, room for a ring of four
+    return per_wave <= 2 ? conv_window_f32<8, 2, KH> : conv_window_f32<8, 4, KH>;
+}
+IgemmKernel window_kernel(int W, int k_tiles, int KH) {
+    const int per_wave = (k_tiles + W - 1) / W;
+    return KH == 1 ? window_kernel_kh<1>(W, per_wave) : window_kernel_kh<3>(W, per_wave);
+}
 
 // The skinny kernel of W waves for k_tiles 64-k chunks: chunks in flight
 // per wave no more than the busiest wave has
@@ -1370,10 +1570,14 @@ bool skinny_fits(const GatherSpec &gs) { return gs.gather.C > 0 && gs.gather.C %
 // its 4-k MFMA step.
 bool thin_fits(const GatherSpec &gs) { return gs.gather.C > 0 && gs.gather.C % 4 == 0 && gs.K % 4 == 0; }
 
+// The row-window kernel takes a skinny layer that is a convolution whose
+// input window fits its LDS (win_len set at planning).
+bool window_fits(const GatherSpec &gs) { return skinny_fits(gs) && gs.gather.win_len > 0; }
+
 // Configuration c can run the layer.
 bool cfg_fits(int c, const GatherSpec &gs) {
     return resident_wgs(c) > 0 && (kCfgs[c].skinny_waves == 0 || skinny_fits(gs)) &&
-           (kCfgs[c].thin_mb == 0 || thin_fits(gs));
+           (!kCfgs[c].window || window_fits(gs)) && (kCfgs[c].thin_mb == 0 || thin_fits(gs));
 }
 
 std::vector<int> build_koff(const GatherSpec &gs, int BK) {
@@ -1462,6 +1666,30 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
         a.sk_tap_h = gg.tap_h;
         a.sk_tap_w = gg.tap_w;
         a.ws = nullptr;
+        if (t.window) {
+            // the window's rows and columns: checked here as well as at
+            // planning, since the kernel's LDS holds kWinFloats floats
+            if (gg.win_len <= 0 || gg.win_len > 64 || gg.win_pitch < gg.win_len || (1 << gg.win_shift) < gg.win_len ||
+                gg.win_shift > 6 || (gg.win_KH != 1 && gg.win_KH != 3) ||
+                static_cast<long long>(gg.C) * gg.win_KH * gg.win_pitch > kWinFloats ||
+                gg.win_KH != g.KH || gg.win_rows != g.N * g.OH || gg.win_owb != (g.OW + 15) / 16) {
+                set_last_error_text("conv_window_f32: layer without a row window that fits the kernel's LDS");
+                return SPKV2_E_UNSUPPORTED;
+            }
+            a.win_KH = gg.win_KH;
+            a.win_len = gg.win_len;
+            a.win_pitch = gg.win_pitch;
+            a.win_shift = gg.win_shift;
+            a.win_owb = gg.win_owb;
+            a.win_OH = g.OH;
+            a.win_dw = gg.win_dw;
+            const long long wgs = static_cast<long long>(tc.m_tiles) * gg.win_rows * gg.win_owb;
+            if (wgs >= (1LL << 31)) return SPKV2_E_UNSUPPORTED;
+            const size_t lds = static_cast<size_t>(gg.C) * gg.win_KH * gg.win_pitch * 4;
+            window_kernel(t.skinny_waves, tc.k_tiles, gg.win_KH)<<<dim3(static_cast<unsigned>(wgs)),
+                                                                    dim3(64 * t.skinny_waves), lds, st>>>(a);
+            return launch_status("conv_window_f32");
+        }
         skinny_kernel(t.skinny_waves, tc.k_tiles)<<<dim3(static_cast<unsigned>(tiles)), dim3(64 * t.skinny_waves), 0,
                                                     st>>>(a);
         return launch_status("conv_skinny_f32");
@@ -1994,6 +2222,25 @@ int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvP
     gs.gather.KW = g.KW;
     gs.gather.tap_h = g.dh * Wp;
     gs.gather.tap_w = g.dw;
+    {
+        // the row window of a 16-pixel output segment (conv_window_f32):
+        // KH rows of wlen columns per channel, rows padded to an odd KH x
+        // pitch (the four 16-channel k slots then fall on distinct LDS banks)
+        const int wlen = (std::min(16, g.OW) - 1) * g.sw + (g.KW - 1) * g.dw + 1;
+        int pitch = wlen;
+        if ((g.KH * pitch) % 2 == 0) pitch++;
+        if ((g.KH == 1 || g.KH == 3) && wlen <= 64 && static_cast<long long>(g.C) * g.KH * pitch <= kWinFloats) {
+            gs.gather.win_KH = g.KH;
+            gs.gather.win_len = wlen;
+            gs.gather.win_pitch = pitch;
+            while ((1 << gs.gather.win_shift) < wlen) gs.gather.win_shift++;
+            gs.gather.win_rows = g.N * g.OH;
+            gs.gather.win_owb = (g.OW + 15) / 16;
+            gs.gather.win_OH = g.OH;
+            gs.gather.win_dh = g.dh;
+            gs.gather.win_dw = g.dw;
+        }
+    }
     if (int rc = plan_tiles_and_weights(st, g, gs, w_host, plan)) return rc;
     plan->workspace = plan->pad_bytes + partial_bytes(plan);
     return 0;
@@ -2023,6 +2270,9 @@ int plan_igemm_gemm(hipStream_t st, const ConvGeom &g, const float *w_host, int 
 std::string igemm_name(const ConvPlan *p) {
     if (kCfgs[p->cfg].thin_mb > 0)
         return std::string("conv_thin_f32<") + kCfgs[p->cfg].name + (p->padded ? ",pad" : "") + ">";
+    if (kCfgs[p->cfg].window)
+        return std::string("conv_window_f32<16x16,w") + std::to_string(kCfgs[p->cfg].skinny_waves) +
+               (p->padded ? ",pad" : "") + ">";
     if (kCfgs[p->cfg].skinny_waves > 0)
         return std::string("conv_skinny_f32<16x16,w") + std::to_string(kCfgs[p->cfg].skinny_waves) +
                (p->padded ? ",pad" : "") + ">";

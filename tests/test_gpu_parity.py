@@ -625,6 +625,65 @@ def test_skinny_configs(gpu, monkeypatch, cfg, name, build):
     assert tnorm_err(got, want) <= FP32_TOL
 
 
+# The row-window configurations (entries 21 and 22: the skinny kernels'
+# arithmetic, one output row segment per workgroup, the input window in LDS)
+# on convolutions: several images and rows, rows narrower and wider than a
+# 16-pixel segment (a partial last segment), stride 2, dilation, residual, a
+# 1x1 layer whose waves hold unequal chunk counts, and a 512-channel window.
+F32_WINDOW_CFGS = [21, 22]
+WINDOW_CASES = [
+    ("conv3x3_res", lambda: models.single_conv(2, 128, 11, 13, 150, 3, 1, 1, act="Relu", residual=True)),
+    ("conv3x3_s2", lambda: models.single_conv(1, 128, 29, 29, 40, 3, 2, 1, act="Relu")),
+    ("conv3x3_dil2_wide", lambda: models.single_conv(1, 64, 20, 40, 24, 3, 1, 2, dilation=2, act=None)),
+    ("conv1x1_c384", lambda: models.single_conv(1, 384, 9, 10, 50, 1, 1, 0, act="Relu")),
+    ("conv1x1_s2", lambda: models.single_conv(1, 256, 14, 14, 72, 1, 2, 0, act=None)),
+    ("conv3x3_c512_res", lambda: models.single_conv(1, 512, 7, 7, 64, 3, 1, 1, act="Relu", residual=True)),
+]
+
+
+def _run_named(blob, xs):
+    from spinnv2_amd.runtime import Model
+
+    with Model(blob) as m:
+        for i, x in enumerate(xs):
+            m.set_input(i, x)
+        m.run()
+        return m.get_output(0), m.kernel_name(0)
+
+
+@pytest.mark.parametrize("wi", [0, 1], ids=["w4", "w8"])
+@pytest.mark.parametrize("name,build", WINDOW_CASES, ids=[c[0] for c in WINDOW_CASES])
+def test_window_configs_match_skinny_bit_for_bit(gpu, monkeypatch, wi, name, build):
+    """Against the oracle within the fp32 tolerance, and bit for bit against
+    the skinny kernel of the same wave count: both sum the same products in
+    the same order (64-k chunks round robin over the waves, 16 MFMAs per
+    chunk, the wave partials in wave order)."""
+    g = build()
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_WINDOW_CFGS[wi]))
+    got, kname = _run_named(blob, xs)
+    assert f"conv_window_f32<16x16,w{4 * (wi + 1)}" in kname, kname
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_SKINNY_CFGS[wi]))
+    ref, kname = _run_named(blob, xs)
+    assert f"conv_skinny_f32<16x16,w{4 * (wi + 1)}" in kname, kname
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_window_config_refused_where_it_does_not_fit(gpu, monkeypatch):
+    """A window larger than the kernel's LDS (1024 channels x 3 rows x 19
+    columns) and a Gemm (no rows) do not take a forced row-window
+    configuration; both still match the oracle."""
+    monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_WINDOW_CFGS[0]))
+    for g in (models.single_conv(1, 1024, 16, 16, 32, 3, 1, 1), models.single_gemm(3, 192, 70, alpha=0.5)):
+        blob = write_spk(g, "mi355x")
+        xs = rng_inputs(g)
+        got, kname = _run_named(blob, xs)
+        assert "window" not in kname, kname
+        assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
     """A layer whose channels per tap are not a multiple of 64 does not take
     a forced skinny configuration (its chunks would straddle taps)."""
@@ -731,6 +790,7 @@ def test_split_k_graph_replays_match_eager(gpu, monkeypatch):
     the captured graph), so its replays give the eager result every time."""
     from spinnv2_amd.runtime import Model
 
+    monkeypatch.setenv("SPKV2_CONV_CFG", "7")  # 64x64x32 (the table's choice for the shape takes no split-K)
     monkeypatch.setenv("SPKV2_CONV_SPLITK", "6")
     g = models.single_conv(1, 256, 14, 14, 256, 3, 1, 1, act="Relu")
     blob = write_spk(g, "mi355x")
