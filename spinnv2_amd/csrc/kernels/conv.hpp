@@ -52,12 +52,11 @@ struct GatherGeom {
     const int *ktap = nullptr;
     // row-window kernel (a conv over the padded input; win_len 0 when the
     // layer has no such form): per output row segment of 16 pixels the
-    // input window is C x KH rows of win_len columns, kept in LDS with
-    // win_pitch floats per row (KH * win_pitch odd); win_shift = log2 of the
-    // lanes one window row takes when loading it; win_rows = N * OH output
-    // rows of win_owb 16-pixel segments; kh steps win_dh input rows.
-    int win_KH = 0, win_len = 0, win_pitch = 0, win_shift = 0, win_rows = 0, win_owb = 0, win_OH = 0, win_dh = 1,
-        win_dw = 1;
+    // input window is KH rows of win_len columns of C channels, kept in LDS
+    // channel-minor; win_shift = log2 of the lanes one window row takes when
+    // loading it; win_rows = N * OH output rows of win_owb 16-pixel
+    // segments; kh steps win_dh input rows, kw win_dw columns.
+    int win_KH = 0, win_len = 0, win_shift = 0, win_rows = 0, win_owb = 0, win_OH = 0, win_dh = 1, win_dw = 1;
 };
 
 struct ConvPlan {

@@ -145,7 +145,7 @@ struct IgemmArgs {
     int chk_H, chk_W, chk_ph, chk_pw;
     int th_steps;  // thin kernel: K / 4 MFMA steps (k' = tap * sk_C + c)
     // row-window kernel: the input window's geometry (GatherGeom's win_*)
-    int win_KH, win_len, win_pitch, win_shift, win_owb, win_OH, win_dw;
+    int win_KH, win_len, win_shift, win_owb, win_OH, win_dw;
 };
 
 
@@ -515,7 +515,8 @@ __global__ void __launch_bounds__(256) conv_igemm_f32(IgemmArgs a) {
 // P chunks are in flight per wave (4 x 20 loads at most, within the 63
 // vmcnt allows); the launch takes P = 1 or 2 when no wave has more chunks
 // than that, so the unused load buffers do not cost registers (and
-// workgroups per CU).  P does not change the summation order.
+// workgroups per CU), and P = 2 for sixteen waves, whatever their chunks
+// (128 registers a wave).  P does not change the summation order.
 template <int W, int P>
 __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
     __shared__ float red[W][256];
@@ -659,13 +660,15 @@ __global__ void __launch_bounds__(64 * W) conv_skinny_f32(IgemmArgs a) {
 // wave partials summed in wave order: the same k order and sums, so the same
 // bits as conv_skinny_f32<W>) with the B operand staged once per workgroup.
 // A workgroup takes 16 output channels by 16 consecutive pixels of one output
-// row; the input those pixels read -- C x KH rows of win_len columns, each
-// element once, against once per tap in the skinny kernel -- is loaded into
-// LDS first (dynamic LDS of C x KH x win_pitch floats), every load of a
-// thread in flight together, so only the weights stream through the k loop:
-// four 16-byte loads per chunk, R chunks in flight, and the next chunk's 16
-// LDS reads issued before the current chunk's MFMAs.  Pixels past the row's
-// end read column 0 of the window and are not stored.
+// row; the input those pixels read -- C channels of KH rows of win_len
+// columns, each element once, against once per tap in the skinny kernel --
+// is loaded into LDS first, every load of a thread in flight together, so
+// only the weights stream through the k loop: four 16-byte loads per chunk,
+// R chunks in flight.  The window is channel-minor, [kh][column][C + 4]
+// floats (dynamic LDS): a lane's 16 channels of a chunk are four 16-byte
+// LDS reads, the rows of 16 lanes 16 bytes apart mod 256 (no bank
+// conflicts), issued before the previous chunk's MFMAs.  Pixels past the
+// row's end read column 0 of the window and are not stored.
 constexpr int kWinFloats = 24576;  // most LDS a window may take: 96 KB
 
 template <int W, int R, int KH>
@@ -692,8 +695,7 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
     const int oh = row - img * a.win_OH;
     const int KC = a.k_tiles;
     const int C = a.sk_C;
-    const int pitch = a.win_pitch;
-    const int cst = KH * pitch;  // LDS floats between channels
+    const int CP = C + 4;  // LDS floats per window column
 
     const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.wp), static_cast<short>(0), a.m_tiles * KC * 4096, kBufferWord3);
@@ -709,13 +711,6 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
         _Pragma("unroll") for (int q = 0; q < 4; q++) av[S][q] =                                                  \
             __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(wrs, ao_, q * 16, 0));              \
     }
-    // the ring's first R - 1 chunks go out before the window, so the
-    // window's barrier waits for nothing the k loop has not yet needed
-    if (nch > 0) {
-#pragma unroll
-        for (int p = 0; p < R - 1; p++) WN_LOAD(p, p);
-    }
-
     // the epilogue's element of this thread (tid < 256): bias and residual
     // loaded now
     const int em = mt * 16 + (tid >> 4);
@@ -726,10 +721,12 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
     const float ebias = eown && a.bias ? a.bias[em] : 0.0f;
     const float eres = eown && a.res ? a.res[eyi] : 0.0f;
 
-    // the window: LDS row c * KH + kh holds input row oh * sh + kh * dh of
-    // channel c from column ow0 * sw on.  A wave instruction loads rpi = 64
-    // >> win_shift rows of one kh, one lane per column; a thread's channels
+    // the window: element (kh, j, c) is input row oh * sh + kh * dh, column
+    // ow0 * sw + j of channel c.  A wave instruction loads rpi = 64 >>
+    // win_shift channels of one kh, one lane per column; a thread's channels
     // are c_first + u * cstep, their KH rows each, up to 48 loads in flight.
+    // The ring's first R - 1 weight chunks go out after the window's loads
+    // (which the barrier waits for) and before its LDS writes.
     {
         const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<float *>(a.x), static_cast<short>(0), a.x_bytes, kBufferWord3);
@@ -739,11 +736,10 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
         const int cstep = W * rpi;
         const int c_first = wave * rpi + q;
         const bool jload = j < a.win_len;
-        const bool jstore = j < pitch;
         const int xb = (img * a.x_img_stride + oh * a.sh * a.Wp + ow0 * a.sw + j + c_first * a.sk_cstride) * 4;
         const int xstep = cstep * a.sk_cstride * 4;
         const int tap4 = a.sk_tap_h * 4;
-        constexpr int UC = 48 / KH;  // channels per thread in flight
+        constexpr int UC = (W >= 16 ? 24 : 48) / KH;  // channels per thread in flight
         for (int u0 = 0; c_first + u0 * cstep < C; u0 += UC) {
             float v[UC][KH];
 #pragma unroll
@@ -755,12 +751,16 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
                         float, __builtin_amdgcn_raw_buffer_load_b32(
                                    xrs, ok ? xb + (u0 + u) * xstep + kh * tap4 : kOobOffset, 0, 0));
             }
+            if (u0 == 0 && nch > 0) {
+#pragma unroll
+                for (int p = 0; p < R - 1; p++) WN_LOAD(p, p);
+            }
 #pragma unroll
             for (int u = 0; u < UC; u++) {
                 const int c = c_first + (u0 + u) * cstep;
-                if (c < C && jstore) {
+                if (c < C && jload) {
 #pragma unroll
-                    for (int kh = 0; kh < KH; kh++) win[(c * KH + kh) * pitch + j] = v[u][kh];
+                    for (int kh = 0; kh < KH; kh++) win[(kh * a.win_len + j) * CP + c] = v[u][kh];
                 }
             }
         }
@@ -769,7 +769,7 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
 
     // a lane's column in the window (pixels past the row's end: column 0)
     const int jcol = ow0 + l16 < a.OW ? l16 * a.sw : 0;
-    const int gbase = 16 * g * cst + jcol;
+    const int gbase = jcol * CP + 16 * g;
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     float bv[2][16];
     // the 16 LDS values of chunk I of this wave into B set S
@@ -780,8 +780,11 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
         const int c0_ = k0_ - tap_ * C;                                                                           \
         const int kh_ = tap_ / a.sk_KW;                                                                           \
         const int kw_ = tap_ - kh_ * a.sk_KW;                                                                     \
-        const float *b_ = win + gbase + (c0_ * KH + kh_) * pitch + kw_ * a.win_dw;                                \
-        _Pragma("unroll") for (int t = 0; t < 16; t++) bv[S][t] = b_[t * cst];                                    \
+        const float *b_ = win + gbase + (kh_ * a.win_len + kw_ * a.win_dw) * CP + c0_;                            \
+        _Pragma("unroll") for (int t4 = 0; t4 < 4; t4++) {                                                        \
+            const floatx4 v4_ = *reinterpret_cast<const floatx4 *>(b_ + 4 * t4);                                  \
+            _Pragma("unroll") for (int e = 0; e < 4; e++) bv[S][4 * t4 + e] = v4_[e];                             \
+        }                                                                                                         \
     }
 #define WN_MMA(A, S)                                                                                              \
     _Pragma("unroll") for (int t = 0; t < 16; t++) acc =                                                          \
@@ -1368,6 +1371,11 @@ const TileCfg kCfgs[] = {
      true},
     {16, 16, 64, "win16x16w8", conv_window_f32<8, 4, 3>, conv_window_f32<8, 4, 3>, conv_window_f32<8, 4, 3>, 1.0, 8, 0,
      true},
+    // sixteen waves (four per SIMD, 128 registers each): the skinny tile and
+    // its row-window form, the same bits as each other
+    {16, 16, 64, "skinny16x16w16", conv_skinny_f32<16, 2>, conv_skinny_f32<16, 2>, conv_skinny_f32<16, 2>, 1.0, 16},
+    {16, 16, 64, "win16x16w16", conv_window_f32<16, 2, 3>, conv_window_f32<16, 2, 3>, conv_window_f32<16, 2, 3>, 1.0,
+     16, 0, true},
 };
 #undef CFG
 #undef CFGW
@@ -1384,8 +1392,10 @@ IgemmKernel window_kernel_kh(int W, int per_wave) {
     if (W == 4)
         return per_wave <= 2 ? conv_window_f32<4, 2, KH> : per_wave <= 4 ? conv_window_f32<4, 4, KH>
                                                                         : conv_window_f32<4, 8, KH>;
-    // eight waves: two per SIMD, 256 registers each, room for a ring of four
-    return per_wave <= 2 ? conv_window_f32<8, 2, KH> : conv_window_f32<8, 4, KH>;
+    // eight waves: two per SIMD, 256 registers each, room for a ring of four;
+    // sixteen: 128 registers, a ring of two
+    if (W == 8) return per_wave <= 2 ? conv_window_f32<8, 2, KH> : conv_window_f32<8, 4, KH>;
+    return conv_window_f32<16, 2, KH>;
 }
 IgemmKernel window_kernel(int W, int k_tiles, int KH) {
     const int per_wave = (k_tiles + W - 1) / W;
@@ -1397,7 +1407,9 @@ IgemmKernel window_kernel(int W, int k_tiles, int KH) {
 IgemmKernel skinny_kernel(int W, int k_tiles) {
     const int per_wave = (k_tiles + W - 1) / W;
     if (W == 4) return per_wave <= 1 ? conv_skinny_f32<4, 1> : per_wave <= 2 ? conv_skinny_f32<4, 2> : conv_skinny_f32<4, 4>;
-    return per_wave <= 1 ? conv_skinny_f32<8, 1> : per_wave <= 2 ? conv_skinny_f32<8, 2> : conv_skinny_f32<8, 4>;
+    if (W == 8) return per_wave <= 1 ? conv_skinny_f32<8, 1> : per_wave <= 2 ? conv_skinny_f32<8, 2> : conv_skinny_f32<8, 4>;
+    // sixteen waves (128 registers): groups of at most two chunks
+    return per_wave <= 1 ? conv_skinny_f32<16, 1> : conv_skinny_f32<16, 2>;
 }
 
 int device_cu_count() {
@@ -1669,23 +1681,22 @@ static int launch_igemm(hipStream_t st, int cfg, const TileCounts &tc, const Con
         if (t.window) {
             // the window's rows and columns: checked here as well as at
             // planning, since the kernel's LDS holds kWinFloats floats
-            if (gg.win_len <= 0 || gg.win_len > 64 || gg.win_pitch < gg.win_len || (1 << gg.win_shift) < gg.win_len ||
-                gg.win_shift > 6 || (gg.win_KH != 1 && gg.win_KH != 3) ||
-                static_cast<long long>(gg.C) * gg.win_KH * gg.win_pitch > kWinFloats ||
+            if (gg.win_len <= 0 || gg.win_len > 64 || (1 << gg.win_shift) < gg.win_len || gg.win_shift > 6 ||
+                (gg.win_KH != 1 && gg.win_KH != 3) ||
+                static_cast<long long>(gg.C + 4) * gg.win_KH * gg.win_len > kWinFloats ||
                 gg.win_KH != g.KH || gg.win_rows != g.N * g.OH || gg.win_owb != (g.OW + 15) / 16) {
                 set_last_error_text("conv_window_f32: layer without a row window that fits the kernel's LDS");
                 return SPKV2_E_UNSUPPORTED;
             }
             a.win_KH = gg.win_KH;
             a.win_len = gg.win_len;
-            a.win_pitch = gg.win_pitch;
             a.win_shift = gg.win_shift;
             a.win_owb = gg.win_owb;
             a.win_OH = g.OH;
             a.win_dw = gg.win_dw;
             const long long wgs = static_cast<long long>(tc.m_tiles) * gg.win_rows * gg.win_owb;
             if (wgs >= (1LL << 31)) return SPKV2_E_UNSUPPORTED;
-            const size_t lds = static_cast<size_t>(gg.C) * gg.win_KH * gg.win_pitch * 4;
+            const size_t lds = static_cast<size_t>(gg.C + 4) * gg.win_KH * gg.win_len * 4;
             window_kernel(t.skinny_waves, tc.k_tiles, gg.win_KH)<<<dim3(static_cast<unsigned>(wgs)),
                                                                     dim3(64 * t.skinny_waves), lds, st>>>(a);
             return launch_status("conv_window_f32");
@@ -2224,15 +2235,11 @@ int plan_igemm_f32(hipStream_t st, const ConvGeom &g, const float *w_host, ConvP
     gs.gather.tap_w = g.dw;
     {
         // the row window of a 16-pixel output segment (conv_window_f32):
-        // KH rows of wlen columns per channel, rows padded to an odd KH x
-        // pitch (the four 16-channel k slots then fall on distinct LDS banks)
+        // KH rows of wlen columns of C + 4 floats
         const int wlen = (std::min(16, g.OW) - 1) * g.sw + (g.KW - 1) * g.dw + 1;
-        int pitch = wlen;
-        if ((g.KH * pitch) % 2 == 0) pitch++;
-        if ((g.KH == 1 || g.KH == 3) && wlen <= 64 && static_cast<long long>(g.C) * g.KH * pitch <= kWinFloats) {
+        if ((g.KH == 1 || g.KH == 3) && wlen <= 64 && static_cast<long long>(g.C + 4) * g.KH * wlen <= kWinFloats) {
             gs.gather.win_KH = g.KH;
             gs.gather.win_len = wlen;
-            gs.gather.win_pitch = pitch;
             while ((1 << gs.gather.win_shift) < wlen) gs.gather.win_shift++;
             gs.gather.win_rows = g.N * g.OH;
             gs.gather.win_owb = (g.OW + 15) / 16;

@@ -346,8 +346,8 @@ F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16)]
 
 # batch 1: every configuration but the thin and 96-row ones, whole tiles and
 # split-K (the skinny and row-window ones split k over their waves instead)
-F32_SWEEP_B1 = [(c, s) for c in (*range(17), 21, 22) for s in (1, 2, 3, 4, 6, 8, 12, 16)
-                if s == 1 or c not in (12, 13, 21, 22)]
+F32_SWEEP_B1 = [(c, s) for c in (*range(17), 21, 22, 23, 24) for s in (1, 2, 3, 4, 6, 8, 12, 16)
+                if s == 1 or c not in (12, 13, 21, 22, 23, 24)]
 
 # the thin tiles alone (16 and 32 rows by 256 columns, whole tiles), against
 # the table as it is

@@ -368,7 +368,8 @@ def test_graph_mode_matches_eager(gpu):
 # splitk_epilogue sums them in slice order and applies the epilogue), on a
 # ragged residual conv; forced through the tuning overrides.
 F32_IGEMM_CFGS = [*range(12), 14, 15, 16, 19, 20]
-F32_SKINNY_CFGS = [12, 13]
+F32_SKINNY_CFGS = [12, 13, 23]  # 4, 8 and 16 waves
+SKINNY_WAVES = {12: 4, 13: 8, 23: 16}
 SPLIT_CASES = [(cfg, split) for cfg in F32_IGEMM_CFGS for split in (1, 3, 8)]
 
 
@@ -589,8 +590,8 @@ def test_gemm_every_tile_config(gpu, monkeypatch, cfg, k):
     assert tnorm_err(run_gpu(blob, xs)[0], run_oracle(blob, xs)[0]) <= FP32_TOL
 
 
-# The skinny configurations (16 x 16 tiles, k over 4 or 8 waves summed in
-# LDS; entries 12 and 13 of the fp32 table) on layers whose channels per tap
+# The skinny configurations (16 x 16 tiles, k over 4, 8 or 16 waves summed
+# in LDS; entries 12, 13 and 23 of the fp32 table) on layers whose channels per tap
 # are multiples of 64: ragged M and N, padding, stride, dilation, residual,
 # and Gemm with alpha and with transA.
 SKINNY_CASES = [
@@ -620,17 +621,18 @@ def test_skinny_configs(gpu, monkeypatch, cfg, name, build):
         m.run()
         got = m.get_output(0)
         name = m.kernel_name(0)
-    assert f"conv_skinny_f32<16x16,w{4 if cfg == F32_SKINNY_CFGS[0] else 8}" in name, name
+    assert f"conv_skinny_f32<16x16,w{SKINNY_WAVES[cfg]}," in name or f"conv_skinny_f32<16x16,w{SKINNY_WAVES[cfg]}>" in name, name
     want = run_oracle(blob, xs)[0]
     assert tnorm_err(got, want) <= FP32_TOL
 
 
-# The row-window configurations (entries 21 and 22: the skinny kernels'
-# arithmetic, one output row segment per workgroup, the input window in LDS)
+# The row-window configurations (entries 21, 22 and 24: the skinny kernels'
+# arithmetic with 4, 8 and 16 waves, one output row segment per workgroup,
+# the input window in LDS)
 # on convolutions: several images and rows, rows narrower and wider than a
 # 16-pixel segment (a partial last segment), stride 2, dilation, residual, a
 # 1x1 layer whose waves hold unequal chunk counts, and a 512-channel window.
-F32_WINDOW_CFGS = [21, 22]
+F32_WINDOW_CFGS = [21, 22, 24]
 WINDOW_CASES = [
     ("conv3x3_res", lambda: models.single_conv(2, 128, 11, 13, 150, 3, 1, 1, act="Relu", residual=True)),
     ("conv3x3_s2", lambda: models.single_conv(1, 128, 29, 29, 40, 3, 2, 1, act="Relu")),
@@ -651,7 +653,7 @@ def _run_named(blob, xs):
         return m.get_output(0), m.kernel_name(0)
 
 
-@pytest.mark.parametrize("wi", [0, 1], ids=["w4", "w8"])
+@pytest.mark.parametrize("wi", [0, 1, 2], ids=["w4", "w8", "w16"])
 @pytest.mark.parametrize("name,build", WINDOW_CASES, ids=[c[0] for c in WINDOW_CASES])
 def test_window_configs_match_skinny_bit_for_bit(gpu, monkeypatch, wi, name, build):
     """Against the oracle within the fp32 tolerance, and bit for bit against
@@ -663,11 +665,12 @@ def test_window_configs_match_skinny_bit_for_bit(gpu, monkeypatch, wi, name, bui
     xs = rng_inputs(g)
     monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_WINDOW_CFGS[wi]))
     got, kname = _run_named(blob, xs)
-    assert f"conv_window_f32<16x16,w{4 * (wi + 1)}" in kname, kname
+    waves = SKINNY_WAVES[F32_SKINNY_CFGS[wi]]
+    assert f"conv_window_f32<16x16,w{waves}," in kname or f"conv_window_f32<16x16,w{waves}>" in kname, kname
     assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
     monkeypatch.setenv("SPKV2_CONV_CFG", str(F32_SKINNY_CFGS[wi]))
     ref, kname = _run_named(blob, xs)
-    assert f"conv_skinny_f32<16x16,w{4 * (wi + 1)}" in kname, kname
+    assert f"conv_skinny_f32<16x16,w{waves}," in kname or f"conv_skinny_f32<16x16,w{waves}>" in kname, kname
     np.testing.assert_array_equal(got, ref)
 
 
