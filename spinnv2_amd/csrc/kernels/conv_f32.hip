@@ -740,30 +740,36 @@ __global__ void __launch_bounds__(64 * W) conv_window_f32(IgemmArgs a) {
         const int xstep = cstep * a.sk_cstride * 4;
         const int tap4 = a.sk_tap_h * 4;
         constexpr int UC = (W >= 16 ? 24 : 48) / KH;  // channels per thread in flight
-        for (int u0 = 0; c_first + u0 * cstep < C; u0 += UC) {
-            float v[UC][KH];
+        float v[UC][KH];
+#define WN_FILL_LOADS(U0)                                                                                         \
+    _Pragma("unroll") for (int u = 0; u < UC; u++) {                                                              \
+        const bool ok_ = c_first + ((U0) + u) * cstep < C && jload;                                               \
+        _Pragma("unroll") for (int kh = 0; kh < KH; kh++) v[u][kh] = __builtin_bit_cast(                          \
+            float, __builtin_amdgcn_raw_buffer_load_b32(xrs, ok_ ? xb + ((U0) + u) * xstep + kh * tap4 : kOobOffset,  \
+                                                         0, 0));                                                  \
+    }
+#define WN_FILL_STORES(U0)                                                                                        \
+    _Pragma("unroll") for (int u = 0; u < UC; u++) {                                                              \
+        const int c_ = c_first + ((U0) + u) * cstep;                                                              \
+        if (c_ < C && jload) {                                                                                    \
+            _Pragma("unroll") for (int kh = 0; kh < KH; kh++) win[(kh * a.win_len + j) * CP + c_] = v[u][kh];     \
+        }                                                                                                         \
+    }
+        // the first batch runs in every thread (lanes with no channel load
+        // out-of-range offsets): the weight prologue after it must run in
+        // every wave, also in waves with no window channels
+        WN_FILL_LOADS(0);
+        if (nch > 0) {
 #pragma unroll
-            for (int u = 0; u < UC; u++) {
-                const bool ok = c_first + (u0 + u) * cstep < C && jload;
-#pragma unroll
-                for (int kh = 0; kh < KH; kh++)
-                    v[u][kh] = __builtin_bit_cast(
-                        float, __builtin_amdgcn_raw_buffer_load_b32(
-                                   xrs, ok ? xb + (u0 + u) * xstep + kh * tap4 : kOobOffset, 0, 0));
-            }
-            if (u0 == 0 && nch > 0) {
-#pragma unroll
-                for (int p = 0; p < R - 1; p++) WN_LOAD(p, p);
-            }
-#pragma unroll
-            for (int u = 0; u < UC; u++) {
-                const int c = c_first + (u0 + u) * cstep;
-                if (c < C && jload) {
-#pragma unroll
-                    for (int kh = 0; kh < KH; kh++) win[(kh * a.win_len + j) * CP + c] = v[u][kh];
-                }
-            }
+            for (int p = 0; p < R - 1; p++) WN_LOAD(p, p);
         }
+        WN_FILL_STORES(0);
+        for (int u0 = UC; c_first + u0 * cstep < C; u0 += UC) {
+            WN_FILL_LOADS(u0);
+            WN_FILL_STORES(u0);
+        }
+#undef WN_FILL_LOADS
+#undef WN_FILL_STORES
     }
     __syncthreads();
 

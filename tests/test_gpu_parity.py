@@ -640,6 +640,11 @@ WINDOW_CASES = [
     ("conv1x1_c384", lambda: models.single_conv(1, 384, 9, 10, 50, 1, 1, 0, act="Relu")),
     ("conv1x1_s2", lambda: models.single_conv(1, 256, 14, 14, 72, 1, 2, 0, act=None)),
     ("conv3x3_c512_res", lambda: models.single_conv(1, 512, 7, 7, 64, 3, 1, 1, act="Relu", residual=True)),
+    # windows narrow enough that whole waves load no window channel (16
+    # waves x 8 rows, and 8 waves x 16 rows, against 64 channels): those
+    # waves still load their weights
+    ("conv3x3_c64_5x5", lambda: models.single_conv(2, 64, 5, 5, 64, 3, 1, 1, act="Relu")),
+    ("conv1x1_c64_4x4", lambda: models.single_conv(1, 64, 4, 4, 32, 1, 1, 0, act=None)),
 ]
 
 

@@ -84,10 +84,13 @@ def test_c2f_views_bit_identical_to_copies(gpu, monkeypatch, split):
     assert tnorm_err(on, want) <= FP32_TOL
 
 
-def test_c2f_views_skinny_kernel(gpu, monkeypatch):
-    """The skinny 16x16 kernel (layers of 64-channel multiples) reading and
-    writing through views: every conv that can take it is forced onto it."""
-    monkeypatch.setenv("SPKV2_CONV_CFG", "12")
+@pytest.mark.parametrize("cfg,kind", [("12", "skinny"), ("21", "window"), ("24", "window")],
+                         ids=["skinny4", "window4", "window16"])
+def test_c2f_views_skinny_kernel(gpu, monkeypatch, cfg, kind):
+    """The skinny 16x16 kernel and its row-window form (layers of 64-channel
+    multiples) reading and writing through views and padded-input handoffs:
+    every conv that can take it is forced onto it."""
+    monkeypatch.setenv("SPKV2_CONV_CFG", cfg)
     g = _c2f_graph(batch=2, c_in=64, hw=12, widths=(128, 128))
     blob = write_spk(g, "mi355x")
     xs = rng_inputs(g)
@@ -95,7 +98,7 @@ def test_c2f_views_skinny_kernel(gpu, monkeypatch):
     monkeypatch.setenv("SPKV2_CONCAT_VIEWS", "0")
     off, _ = _run(blob, xs, len(g.nodes))
     np.testing.assert_array_equal(on.view(np.uint32), off.view(np.uint32))
-    assert any("skinny" in n for n in names), names
+    assert any(kind in n for n in names), names
     assert "concat_views" in names
 
 
@@ -178,13 +181,15 @@ def test_yolo_v10n_views_against_oracle(gpu, monkeypatch, batch):
         check_detections([a.reshape(w.shape)[n] for a, w in zip(got, want)], [w[n] for w in want])
 
 
-@pytest.mark.parametrize("force", [("SPKV2_CONV_SPLITK", "3"), ("SPKV2_CONV_CFG", "18"), ("SPKV2_CONV_CFG", "12")],
-                         ids=["splitk3", "thin32", "skinny"])
+@pytest.mark.parametrize("force", [("SPKV2_CONV_SPLITK", "3"), ("SPKV2_CONV_CFG", "18"), ("SPKV2_CONV_CFG", "12"),
+                                   ("SPKV2_CONV_CFG", "24")],
+                         ids=["splitk3", "thin32", "skinny", "window16"])
 def test_yolo_head_views_every_epilogue(gpu, monkeypatch, force):
     """The detection head's convs write the [N, 144, L] buffer with channel
     stride L through every epilogue that can take them (split-K partials
-    summed by splitk_epilogue, the thin and the skinny kernels): outputs
-    equal the copying path bit for bit."""
+    summed by splitk_epilogue, the thin and the skinny kernels and the
+    skinny kernel's row-window form): outputs equal the copying path bit for
+    bit."""
     from spinnv2_amd.runtime import Model
 
     monkeypatch.setenv(*force)
