@@ -33,6 +33,10 @@ struct GemmPlan {
     int trans_a;
     float alpha;
     int x_stride;
+    // at most four rows of A (a classifier at batch 1-4), A not transposed,
+    // K a multiple of 4: the matrix-vector kernel over these weights, W[n][k]
+    // row-major (device); null otherwise
+    float *wrow;
 };
 
 void gemm_plan_free(void *p) {
@@ -40,7 +44,57 @@ void gemm_plan_free(void *p) {
     if (!g) return;
     if (g->conv.wpack) (void)hipFree(g->conv.wpack);
     if (g->conv.ktab) (void)hipFree(g->conv.ktab);
+    if (g->wrow) (void)hipFree(g->wrow);
     delete g;
+}
+
+// Matrix-vector form of a Gemm with R <= 4 rows of A: y[r][n] = alpha *
+// sum_k A[r][k] W[n][k] + c[n].  One wave per output n reads row n of W in
+// 16-byte pieces (lane l takes k = 4 (l + 64 j) .. + 3, j = 0, 1, ...), all
+// of a lane's pieces in flight together with the matching pieces of the R
+// rows of A; each lane sums its products in k order, then the 64 lane sums
+// are added in a fixed butterfly.  Bound by the HBM reads of W (4 K bytes per
+// output), where the 16 x 16 MFMA tiles leave most CUs idle and each tile's
+// k chain serial.
+template <int R>
+__global__ void __launch_bounds__(256) gemv_f32(const float *__restrict__ W, const float *__restrict__ A,
+                                                const float *__restrict__ c, float *__restrict__ Y, int K, int Nout,
+                                                float alpha) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= Nout) return;  // the whole wave (n is per wave)
+    const floatx4 *w4 = reinterpret_cast<const floatx4 *>(W + static_cast<size_t>(n) * K);
+    const floatx4 *a4 = reinterpret_cast<const floatx4 *>(A);
+    const int K4 = K / 4;
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    constexpr int U = 8;  // pieces per lane in flight
+    for (int j0 = lane; j0 < K4; j0 += 64 * U) {
+        floatx4 wv[U], av[U][R];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int j = j0 + 64 * u;
+            const bool ok = j < K4;
+            wv[u] = ok ? w4[j] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < R; r++) av[u][r] = ok ? a4[r * K4 + j] : floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int r = 0; r < R; r++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[r] = fmaf(wv[u][e], av[u][r][e], acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) acc[r] += __shfl_xor(acc[r], off, 64);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) Y[static_cast<size_t>(r) * Nout + n] = alpha * acc[r] + (c ? c[n] : 0.0f);
+    }
 }
 
 // Batched MatMul y[b] = A[a(b)] x B[b(b)] (reference kernels/reference/mm/
@@ -253,8 +307,22 @@ int gemm_prepare(Spkv2Context *ctx, const Spkv2NodeRecord *node, size_t *ws) {
     // byte offsets inside the kernels are 32-bit signed
     if (g.x_elems * 4 >= (int64_t(1) << 31) || g.y_elems * 4 >= (int64_t(1) << 31)) return SPKV2_E_UNSUPPORTED;
     gp->conv.g = g;
+    // (also the fallback of the matrix-vector kernel: an A not 16-byte aligned)
     if (int rc = plan_igemm_gemm(ctx->stream, g, w.data(), attr.trans_a ? gp->rows : 1, &gp->conv)) return rc;
-    set_kernel_name(ctx, node, "gemm:" + igemm_name(&gp->conv));
+    // a forced tile configuration (SPKV2_CONV_CFG) keeps the tiles
+    if (gp->rows >= 1 && gp->rows <= 4 && !attr.trans_a && gp->K % 4 == 0 && !getenv("SPKV2_CONV_CFG")) {
+        const size_t wb = w.size() * sizeof(float);
+        if (hipMalloc(reinterpret_cast<void **>(&gp->wrow), wb) != hipSuccess) {
+            (void)hipGetLastError();
+            gp->wrow = nullptr;
+        } else if (hipMemcpy(gp->wrow, w.data(), wb, hipMemcpyHostToDevice) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(gp->wrow);
+            gp->wrow = nullptr;
+        }
+    }
+    set_kernel_name(ctx, node, gp->wrow ? "gemm:gemv_f32<" + std::to_string(gp->rows) + ">"
+                                        : "gemm:" + igemm_name(&gp->conv));
     *ws = claim_spec_scratch(ctx, node, &gp->conv);
     return 0;
 }
@@ -269,6 +337,16 @@ int gemm_run(Spkv2Context *ctx, const Spkv2NodeRecord *node, void *) {
     const float *a = dptr<const float>(ctx, node->inputs[0]);
     const float *c = node->input_count > 2 ? dptr<const float>(ctx, node->inputs[2]) : nullptr;
     float *y = dptr<float>(ctx, node->outputs[0]);
+    if (gp->wrow && (reinterpret_cast<uintptr_t>(a) & 15) == 0) {
+        const dim3 grid(static_cast<unsigned>((gp->Nout + 3) / 4));
+        switch (gp->rows) {
+            case 1: gemv_f32<1><<<grid, 256, 0, ctx->stream>>>(gp->wrow, a, c, y, gp->K, gp->Nout, gp->alpha); break;
+            case 2: gemv_f32<2><<<grid, 256, 0, ctx->stream>>>(gp->wrow, a, c, y, gp->K, gp->Nout, gp->alpha); break;
+            case 3: gemv_f32<3><<<grid, 256, 0, ctx->stream>>>(gp->wrow, a, c, y, gp->K, gp->Nout, gp->alpha); break;
+            default: gemv_f32<4><<<grid, 256, 0, ctx->stream>>>(gp->wrow, a, c, y, gp->K, gp->Nout, gp->alpha); break;
+        }
+        return launch_status("gemv_f32");
+    }
     // A is [rows][K] (one "image" of K channels per row), or [K][rows] with trans_a
     return run_igemm_f32_strided(ctx, &gp->conv, a, c, y, gp->alpha, gp->trans_a ? 1 : gp->K);
 }

@@ -692,6 +692,30 @@ def test_window_config_refused_where_it_does_not_fit(gpu, monkeypatch):
         assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
 
 
+@pytest.mark.parametrize("rows,k,n", [(1, 2048, 1000), (2, 132, 37), (3, 516, 70), (4, 64, 1)])
+def test_gemm_matrix_vector_kernel(gpu, rows, k, n):
+    """A Gemm of 1-4 rows (a classifier at batch 1-4) runs as a matrix-vector
+    product (one wave per output, 16-byte weight pieces): the oracle within
+    the fp32 tolerance, with alpha and bias, ragged K and outputs."""
+    g = models.single_gemm(rows, k, n, alpha=0.75)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got, kname = _run_named(blob, xs)
+    assert f"gemv_f32<{rows}>" in kname, kname
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
+@pytest.mark.parametrize("rows,k,trans_a", [(2, 130, 0), (3, 128, 1), (5, 128, 0)], ids=["k130", "trans_a", "rows5"])
+def test_gemm_matrix_vector_kernel_not_taken(gpu, rows, k, trans_a):
+    """K not a multiple of 4, a transposed A and five rows keep the tiles."""
+    g = models.single_gemm(rows, k, 20, trans_a=trans_a)
+    blob = write_spk(g, "mi355x")
+    xs = rng_inputs(g)
+    got, kname = _run_named(blob, xs)
+    assert "gemv" not in kname, kname
+    assert tnorm_err(got, run_oracle(blob, xs)[0]) <= FP32_TOL
+
+
 def test_skinny_config_refused_off_64_channel_layers(gpu, monkeypatch):
     """A layer whose channels per tap are not a multiple of 64 does not take
     a forced skinny configuration (its chunks would straddle taps)."""
