@@ -11,7 +11,7 @@ times its candidates and appends its choice to the output file
     python -m spinnv2_amd.tune_table [out.tune] [--retune-int8 | --missing] [--no-int8]
     python -m spinnv2_amd.tune_table --int8-network [--b1 | --splitk] [table.tune]
     python -m spinnv2_amd.tune_table --q8-network [--b1 | --splitk] [table.tune]
-    python -m spinnv2_amd.tune_table --f32-network [--yolo] [--b1] [--thin | --rows96] [table.tune]
+    python -m spinnv2_amd.tune_table --f32-network [--yolo] [--b1] [--thin | --rows96 | --skinny] [table.tune]
 
 With --missing every entry of the committed table is kept and only layer
 shapes it lacks are tuned (the table stays in force, so the tuner runs for
@@ -32,8 +32,8 @@ shape's entry changes when another configuration's summed node time over
 its nodes beats the current one by more than 2%.  --f32-network does the
 same for ResNet-101 b=64 (with --yolo YOLOv10n b=16, with --b1 batch 1)
 over the fp32 tile configurations and schedules (F32_SWEEP, F32_SWEEP_B1),
-or with --thin / --rows96 over the thin or the 96-row tiles alone (F32_THIN,
-F32_ROWS96).  --q8-network does it for the INT8 configuration with int8
+or with --thin / --rows96 / --skinny over the thin, the 96-row or the skinny
+and row-window tiles alone (F32_THIN, F32_ROWS96, F32_SKINNY).  --q8-network does it for the INT8 configuration with int8
 tensors between nodes (ResNet-50, keys ending in |q8) over every int8 tile
 configuration, the persistent ones included.
 """
@@ -356,8 +356,12 @@ F32_THIN = [(17, 1), (18, 1)]
 # the 96-row tiles (whole tiles and hybrid schedules), against the table as it is
 F32_ROWS96 = [(c, s) for c in (19, 20) for s in (1, 1004, 1008)]
 
+# the skinny and row-window tiles (4, 8 and 16 waves), against the table as it is
+F32_SKINNY = [(c, 1) for c in (12, 13, 23, 21, 22, 24)]
 
-def f32_network(table: Path, net: str = "resnet101", thin: bool = False, rows96: bool = False) -> None:
+
+def f32_network(table: Path, net: str = "resnet101", thin: bool = False, rows96: bool = False,
+                skinny: bool = False) -> None:
     from .spk import models, write_spk
 
     g = {"yolo": lambda: models.yolo_v10n(16), "yolo_b1": lambda: models.yolo_v10n(1),
@@ -365,7 +369,8 @@ def f32_network(table: Path, net: str = "resnet101", thin: bool = False, rows96:
     blob = write_spk(g, "mi355x")
     keys = {n.id: f32_key(g, n) for n in g.nodes
             if n.op_type == "Conv" and n.attrs.get("group", 1) == 1 and not _smallk(g, n)}
-    cands = F32_ROWS96 if rows96 else F32_THIN if thin else F32_SWEEP_B1 if net in ("resnet101_b1", "yolo_b1") else \
+    cands = F32_SKINNY if skinny else F32_ROWS96 if rows96 else F32_THIN if thin else \
+        F32_SWEEP_B1 if net in ("resnet101_b1", "yolo_b1") else \
         F32_SWEEP + ([(c, s) for c in (14, 15, 16) for s in (1004, 1008, 1016)] if net == "yolo" else [])
     network_sweep(g, blob, keys, cands, table, {"yolo": "yolov10n b=16", "yolo_b1": "yolov10n b=1",
                                                 "resnet101_b1": "resnet101 b=1"}.get(net, "resnet101 b=64"))
@@ -384,6 +389,7 @@ if __name__ == "__main__":
         else:
             yolo, b1 = "--yolo" in sys.argv[1:], "--b1" in sys.argv[1:]
             f32_network(table, ("yolo_b1" if b1 else "yolo") if yolo else "resnet101_b1" if b1 else "resnet101",
-                        thin="--thin" in sys.argv[1:], rows96="--rows96" in sys.argv[1:])
+                        thin="--thin" in sys.argv[1:], rows96="--rows96" in sys.argv[1:],
+                        skinny="--skinny" in sys.argv[1:])
     else:
         main()
