@@ -7,6 +7,7 @@
            [--group NAME --include SUBSTR [--include ...] [--exclude SUBSTR ...]]
     python -m spinnv2_amd.rocprof_summary mfma <pmc.csv> --runs N --match conv_igemm --cus 256 --xcds 8
            [--mops SQ_INSTS_VALU_MFMA_MOPS_I8 --peak 5000]
+    python -m spinnv2_amd.rocprof_summary launches <kernel_trace.csv> --runs N [--match conv_igemm_i8]
 
 `stats` divides rocprofv3 --kernel-trace --stats totals by the number of
 spkv2_run calls the profiled command made (N), giving per-run kernel time;
@@ -27,6 +28,10 @@ durations against --peak (T ops/s of the counted type; 157.3 for fp32, 5000
 for int8), and MFMA busy cycles (per SIMD) over the
 active cycles of all SIMDs: GRBM_GUI_ACTIVE / XCDs x CUs x 4 (on MI355X
 GRBM_GUI_ACTIVE sums the 8 XCDs' counts: about 8 x duration x clock).
+`launches` reads a --kernel-trace dispatch list and splits each kernel (name
+containing --match) by its launch shape (workgroups x grid y x grid z, and
+the workgroup size): the layers that share one tile configuration apart,
+with dispatches per run, the median dispatch duration and time per run.
 """
 
 from __future__ import annotations
@@ -181,6 +186,25 @@ def mfma(args) -> str:
     return "\n".join(out)
 
 
+def launches(path: str, runs: int, match: str | None = None) -> str:
+    per: dict[tuple, list[float]] = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        name = short_name(r["Kernel_Name"])
+        if match and match not in r["Kernel_Name"]:
+            continue
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+        shape = (int(r["Grid_Size_X"]) // max(int(r["Workgroup_Size_X"]), 1), int(r["Grid_Size_Y"]),
+                 int(r["Grid_Size_Z"]), wg)
+        per[(name, shape)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [f"{'kernel':44s} {'workgroups':>16s} {'threads':>7s} {'disp/run':>8s} {'median us':>9s} {'ms/run':>8s}"]
+    for (name, (gx, gy, gz, wg)), d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        d = sorted(d)
+        med = d[len(d) // 2] if len(d) % 2 else (d[len(d) // 2 - 1] + d[len(d) // 2]) / 2
+        out.append(f"{name[:44]:44s} {f'{gx}x{gy}x{gz}':>16s} {wg:7d} {len(d) / runs:8.1f} {med:9.2f} "
+                   f"{sum(d) / runs / 1e3:8.3f}")
+    return "\n".join(out)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -208,9 +232,13 @@ def main() -> None:
     m.add_argument("--xcds", type=int, default=8)
     m.add_argument("--peak", type=float, default=157.3, help="T ops/s of the counted MFMA type (fp32: 157.3)")
     m.add_argument("--mops", default="SQ_INSTS_VALU_MFMA_MOPS_F32", help="MFMA work counter (units of 512 ops)")
+    ln = sub.add_parser("launches")
+    ln.add_argument("csv")
+    ln.add_argument("--runs", type=int, required=True)
+    ln.add_argument("--match", default=None, help="only kernels whose name contains this")
     a = ap.parse_args()
     print({"stats": lambda: stats(a.csv, a.runs, a.match, a.group, a.include, a.exclude), "traffic": lambda: traffic(a),
-           "mfma": lambda: mfma(a)}[a.cmd]())
+           "mfma": lambda: mfma(a), "launches": lambda: launches(a.csv, a.runs, a.match)}[a.cmd]())
 
 
 if __name__ == "__main__":

@@ -126,3 +126,23 @@ def test_stats_group_include_exclude(tmp_path):
     # 2.0 ms + 0.5 ms over 10 runs; the KVEC Gemm and the pool are not members
     assert _result(out, "conv_kernels_ms_per_run") == pytest.approx(0.25)
     assert _result(out, "conv_kernels_calls_per_run") == pytest.approx(3.0)
+
+
+def test_launches_by_grid(tmp_path):
+    cols = ["Kernel_Name", "Start_Timestamp", "End_Timestamp", "Workgroup_Size_X", "Workgroup_Size_Y",
+            "Workgroup_Size_Z", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z"]
+    k = "void spk::kern::conv_igemm_i8x<128, 64, 64, 2, 2, 0>(spk::kern::I8Args)"
+    # two runs: a 6272-workgroup launch (90 and 100 us) and two 1568-workgroup
+    # launches per run (20, 22, 24, 30 us); another kernel left out by --match
+    rows = [[k, 0, 90_000, 256, 1, 1, 6272 * 256, 1, 1], [k, 0, 100_000, 256, 1, 1, 6272 * 256, 1, 1],
+            [k, 0, 20_000, 256, 1, 1, 1568 * 256, 1, 1], [k, 0, 22_000, 256, 1, 1, 1568 * 256, 1, 1],
+            [k, 0, 24_000, 256, 1, 1, 1568 * 256, 1, 1], [k, 0, 30_000, 256, 1, 1, 1568 * 256, 1, 1],
+            ["copy_kernel(float*)", 0, 5_000, 256, 1, 1, 256, 1, 1]]
+    out = rs.launches(_write(tmp_path / "t.csv", cols, rows), runs=2, match="conv_igemm_i8")
+    lines = out.splitlines()
+    assert len(lines) == 3 and "copy_kernel" not in out
+    # one dispatch per run, median of 90 and 100 us, 190 us over two runs
+    assert lines[1].split()[-5:] == ["6272x1x1", "256", "1.0", "95.00", "0.095"]
+    small = lines[2].split()
+    # four dispatches over two runs: 2 per run, median of 20, 22, 24, 30 is 23, 96 us / 2 runs
+    assert small[-5:] == ["1568x1x1", "256", "2.0", "23.00", "0.048"]
