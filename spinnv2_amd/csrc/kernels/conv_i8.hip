@@ -1238,6 +1238,8 @@ const I8Cfg kI8Cfgs[] = {
     I8CFGR(64, 64, 64, 2, 2),    I8CFGR(128, 64, 64, 2, 2),   I8CFGR(64, 128, 64, 2, 2),
     I8CFGR(128, 128, 64, 2, 2),  I8CFGR(64, 64, 128, 2, 2),   I8CFGR(128, 64, 128, 2, 2),
     I8CFGR(256, 64, 64, 4, 1),   I8CFGR(256, 64, 128, 4, 1),
+    I8CFGX(128, 64, 64, 4, 1),   I8CFGX(128, 64, 128, 4, 1),  I8CFGX(128, 128, 64, 4, 1),
+    I8CFGX(128, 128, 128, 4, 1), I8CFGR(128, 64, 64, 4, 1),   I8CFGR(128, 64, 128, 4, 1),
 };
 #undef I8CFG
 #undef I8CFGP

@@ -304,6 +304,12 @@ def network_sweep(g, blob: bytes, keys: dict, candidates, table: Path, label: st
     print(f"{label}: {len(changed)} entries changed -> {table}")
 
 
+# conv_i8.hip's tile configurations (kI8Cfgs): how many, and those that
+# take split-K (the persistent ones, 23-30, 35 and 36, take whole tiles only)
+I8_CONFIGS = 37
+I8_SPLITTABLE = [*range(23), 31, 32, 33, 34]
+
+
 def int8_network(table: Path, batch: int = 64) -> None:
     from .spk import models, write_spk
     from .spk.quantize import calibrate_activation_scales, quantize_conv_weights
@@ -314,11 +320,11 @@ def int8_network(table: Path, batch: int = 64) -> None:
     g = models.resnet(50, batch)
     blob = write_spk(g, "mi355x", quant_params=quantize_conv_weights(g) + act)
     keys = {n.id: int8_key(g, n) for n in g.nodes if n.op_type == "Conv"}
-    if batch == 1:  # every configuration with split-K too (23 configurations)
-        network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (1, 2, 3, 4, 6, 8, 12, 16)], table,
+    if batch == 1:  # every configuration with split-K too
+        network_sweep(g, blob, keys, [(c, s) for c in I8_SPLITTABLE for s in (1, 2, 3, 4, 6, 8, 12, 16)], table,
                       "int8 resnet50 b=1")
-    elif "--splitk" in sys.argv[1:]:  # the 23 configurations with split-K 2, 3, 4
-        network_sweep(g, blob, keys, [(c, s) for c in range(23) for s in (2, 3, 4)], table, "int8 resnet50 b=64")
+    elif "--splitk" in sys.argv[1:]:  # the configurations with split-K 2, 3, 4
+        network_sweep(g, blob, keys, [(c, s) for c in I8_SPLITTABLE for s in (2, 3, 4)], table, "int8 resnet50 b=64")
     else:
         network_sweep(g, blob, keys, [(c, 1) for c in range(64)], table, "int8 resnet50 b=64", open_ended=True)
 
@@ -330,10 +336,11 @@ def q8_network(table: Path, batch: int = 64) -> None:
     g, blob = q8_resnet50(batch)
     keys = {n.id: int8_key(g, n, q8=True) for n in g.nodes if n.op_type == "Conv"}
     if batch == 1:
-        cands = [(c, s) for c in range(31) for s in (1, 2, 3, 4, 6, 8, 12, 16) if s == 1 or c < 23]
+        cands = [(c, s) for c in range(I8_CONFIGS) for s in (1, 2, 3, 4, 6, 8, 12, 16)
+                 if s == 1 or c in I8_SPLITTABLE]
     else:
-        cands = [(c, 1) for c in range(31)] + ([(c, s) for c in range(23) for s in (2, 3, 4)]
-                                               if "--splitk" in sys.argv[1:] else [])
+        cands = [(c, 1) for c in range(I8_CONFIGS)] + ([(c, s) for c in I8_SPLITTABLE for s in (2, 3, 4)]
+                                                       if "--splitk" in sys.argv[1:] else [])
     network_sweep(g, blob, keys, cands, table, f"int8 configuration resnet50 b={batch}")
 
 

@@ -313,14 +313,16 @@ def test_int8_every_tile_config_and_split(gpu, monkeypatch, cfg, split):
 
 
 # Pixel-major gather configurations (7-13, the direct-weight kernel
-# conv_igemm_i8x: 14-22, and its persistent form conv_igemm_i8p: 23-30, which
-# takes whole tiles only): every one on a 1x1 conv (one kernel row: always
-# eligible) and on a 3x3 conv with 64 channels (12 groups per kernel row:
-# eligible for BK = 64 only), with split-K, ragged M and N, residual and
-# Relu; ineligible forcings are refused.
+# conv_igemm_i8x: 14-22 and 31-34, and its persistent form conv_igemm_i8p:
+# 23-30 and 35-36, which takes whole tiles only): every one on a 1x1 conv
+# (one kernel row: always eligible) and on a 3x3 conv with 64 channels (12
+# groups per kernel row: eligible for BK = 64 only), with split-K, ragged M
+# and N, residual and Relu; ineligible forcings are refused.
 I8_PX_BK = {7: 64, 8: 128, 9: 64, 10: 128, 11: 64, 12: 64, 13: 128,
             14: 128, 15: 128, 16: 128, 17: 128, 18: 64, 19: 64, 20: 64, 21: 64, 22: 128,
-            23: 64, 24: 64, 25: 64, 26: 64, 27: 128, 28: 128, 29: 64, 30: 128}
+            23: 64, 24: 64, 25: 64, 26: 64, 27: 128, 28: 128, 29: 64, 30: 128,
+            31: 64, 32: 128, 33: 64, 34: 128, 35: 64, 36: 128}
+I8_PERSIST = {*range(23, 31), 35, 36}
 I8_PX = [(cfg, shape, split) for cfg in I8_PX_BK for shape in ("1x1", "3x3") for split in (1, 3)]
 
 
@@ -341,7 +343,7 @@ def test_int8_pixel_gather_configs(gpu, monkeypatch, cfg, shape, split):
         return
     name = _int8_check(g)
     assert (",ax" in name) if cfg >= 14 else (",px," in name), name
-    assert (",persist" in name) == (cfg >= 23), name
+    assert (",persist" in name) == (cfg in I8_PERSIST), name
 
 
 def test_graph_mode_matches_eager(gpu):

@@ -129,8 +129,8 @@ def test_q8_chain_bit_exact(gpu, case):
 # direct-weight kernels (whole tiles), on a chain whose 3x3
 # layer reads a halo; 64-channel tensors so that the pixel-gather kernels
 # with 64-byte k-tiles can read every layer
-Q8_FORCED = [(c, s) for c in (2, 5, 9, 12, 18, 19, 20, 21) for s in (1, 3)] + \
-            [(c, 1) for c in (23, 24, 25, 26, 29)]
+Q8_FORCED = [(c, s) for c in (2, 5, 9, 12, 18, 19, 20, 21, 31, 33) for s in (1, 3)] + \
+            [(c, 1) for c in (23, 24, 25, 26, 29, 35)]
 
 
 @pytest.mark.parametrize("cfg,split", Q8_FORCED, ids=[f"q8cfg{c}_split{s}" for c, s in Q8_FORCED])
