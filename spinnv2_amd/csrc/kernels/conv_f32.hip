@@ -1346,6 +1346,11 @@ struct TileCfg {
     {BM, BN, BK, #BM "x" #BN "x" #BK, conv_igemm_f32<BM, BN, BK, WM, WN, kModePlain>,                          \
      conv_igemm_f32<BM, BN, BK, WM, WN, kModeKvec>, conv_igemm_f32<BM, BN, BK, WM, WN, kModeChk>, EFF}
 #define CFG(BM, BN, BK, EFF) CFGW(BM, BN, BK, 2, 2, EFF)
+// the same with the wave layout in the name (tiles that another entry has
+// with 2 x 2 waves)
+#define CFGWL(BM, BN, BK, WM, WN, EFF)                                                                        \
+    {BM, BN, BK, #BM "x" #BN "x" #BK ",w" #WM "x" #WN, conv_igemm_f32<BM, BN, BK, WM, WN, kModePlain>,       \
+     conv_igemm_f32<BM, BN, BK, WM, WN, kModeKvec>, conv_igemm_f32<BM, BN, BK, WM, WN, kModeChk>, EFF}
 const TileCfg kCfgs[] = {
     CFG(128, 128, 16, 0.85), CFG(128, 128, 32, 0.85), CFG(64, 128, 16, 0.90), CFG(64, 128, 32, 0.88),
     CFG(128, 64, 16, 1.00),  CFG(128, 64, 32, 0.95),  CFG(64, 64, 16, 0.96),  CFG(64, 64, 32, 0.98),
@@ -1382,9 +1387,13 @@ const TileCfg kCfgs[] = {
     {16, 16, 64, "skinny16x16w16", conv_skinny_f32<16, 2>, conv_skinny_f32<16, 2>, conv_skinny_f32<16, 2>, 1.0, 16},
     {16, 16, 64, "win16x16w16", conv_window_f32<16, 2, 3>, conv_window_f32<16, 2, 3>, conv_window_f32<16, 2, 3>, 1.0,
      16, 0, true},
+    // the four waves stacked along M (each 32 rows by the whole tile
+    // width): every weight fragment is loaded by one wave only
+    CFGWL(128, 64, 16, 4, 1, 0.95), CFGWL(128, 64, 32, 4, 1, 0.95),
 };
 #undef CFG
 #undef CFGW
+#undef CFGWL
 constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
 // threads per workgroup of configuration c

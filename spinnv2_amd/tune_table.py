@@ -346,9 +346,10 @@ def q8_network(table: Path, batch: int = 64) -> None:
 
 # fp32 candidates: every configuration but the skinny ones (batch-1 tiles)
 # whole-tile, and the hybrid schedules the tuner picks for ResNet-101 b=64
-# (1000 + slices per remaining tile) on the 64-row ones
-F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16)] + \
-            [(c, s) for c in (2, 6, 7) for s in (1004, 1008, 1016)] + [(6, 3)]
+# (1000 + slices per remaining tile) on the 64-row ones and on the 128 x 64
+# tiles with the waves along M
+F32_SWEEP = [(c, 1) for c in (0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16, 25, 26)] + \
+            [(c, s) for c in (2, 6, 7, 25) for s in (1004, 1008, 1016)] + [(6, 3), (26, 1008)]
 
 
 # batch 1: every configuration but the thin and 96-row ones, whole tiles and

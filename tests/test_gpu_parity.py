@@ -365,11 +365,12 @@ def test_graph_mode_matches_eager(gpu):
 
 # Every implicit-GEMM tile configuration (the fp32 table of conv_f32.hip: 8
 # shallow-k tiles, 4 deep-k ones, then after the two skinny kernels 3 tiles
-# of 32 rows, and after the two thin ones 2 tiles of 96 rows), with and
-# without split-K (each slice writes its partial tile;
-# splitk_epilogue sums them in slice order and applies the epilogue), on a
-# ragged residual conv; forced through the tuning overrides.
-F32_IGEMM_CFGS = [*range(12), 14, 15, 16, 19, 20]
+# of 32 rows, after the two thin ones 2 tiles of 96 rows, and after the
+# row-window and sixteen-wave entries 2 tiles with the waves along M), with
+# and without split-K (each slice writes its partial tile; splitk_epilogue
+# sums them in slice order and applies the epilogue), on a ragged residual
+# conv; forced through the tuning overrides.
+F32_IGEMM_CFGS = [*range(12), 14, 15, 16, 19, 20, 25, 26]
 F32_SKINNY_CFGS = [12, 13, 23]  # 4, 8 and 16 waves
 SKINNY_WAVES = {12: 4, 13: 8, 23: 16}
 SPLIT_CASES = [(cfg, split) for cfg in F32_IGEMM_CFGS for split in (1, 3, 8)]

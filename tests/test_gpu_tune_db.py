@@ -98,7 +98,7 @@ def test_tune_db_reuses_hybrid_choice(gpu, tmp_path):
 # entries of conv_f32.hip's tile table that run the implicit-GEMM kernel
 # (64- and 128-row tiles, BK 16 to 128, the 32- and 96-row tiles); the
 # skinny (12, 13) and thin (17, 18) kernels sum in orders of their own
-IGEMM_CFGS = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16, 19, 20]
+IGEMM_CFGS = [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 14, 15, 16, 19, 20, 25, 26]
 
 
 def test_igemm_tiles_share_one_summation_order(gpu, monkeypatch):
